@@ -1,0 +1,161 @@
+/*
+ * m3s.h -- C ABI of the MI355X (gfx950) Mamba-3 SISO kernels.
+ *
+ * The reference has no FFI for this path: its kernels are Pallas `pallas_call`s
+ * invoked from Python (`mamba3_pallas/kernel_fwd.py`, `kernel_bwd.py`,
+ * `kernel_decode.py`). This header is the boundary that replaces those calls; the
+ * Python layer (`mamba3-siso-tpu_amd/kernels.py`) binds it with ctypes and keeps the
+ * reference's Python signatures above it.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer (hipMalloc / torch CUDA memory), except the
+ *    args structs themselves, which live in host memory.
+ *  - "(B, H, L, P)" tensors are passed as `m3s_bhlp`: a base pointer plus element
+ *    strides for the b, h and t axes; the P axis is contiguous. This lets callers hand
+ *    in views of the fused in_proj output (B, L, H*P) without a transpose.
+ *  - All other tensors are dense row-major in the shape given in the comment.
+ *  - Calls are stream-ordered on `stream` (a hipStream_t, NULL = default stream). No
+ *    call allocates, synchronises, or keeps state between calls; concurrent calls on
+ *    different streams are safe.
+ *  - Return value: M3S_OK (0) or a negative M3S_ERR_*; `m3s_last_error()` then holds
+ *    a message (thread-local).
+ */
+#ifndef M3S_H_
+#define M3S_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M3S_ABI_VERSION 1
+
+#define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
+#define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
+
+#define M3S_OK 0
+#define M3S_ERR_INVALID (-1)     /* null pointer, bad shape or stride, misalignment */
+#define M3S_ERR_UNSUPPORTED (-2) /* (dtype, chunk, N, P) has no compiled kernel     */
+#define M3S_ERR_LAUNCH (-3)      /* the HIP launch itself failed                    */
+
+typedef struct m3s_bhlp {
+  void* ptr;
+  int64_t stride_b, stride_h, stride_t; /* elements */
+} m3s_bhlp;
+
+/* Chunked forward. Replaces `kernel_fwd.siso_forward` (kernel_fwd.py:204-388),
+ * i.e. the `pl.pallas_call(_fwd_kernel, grid=(B, nc, H))` at kernel_fwd.py:367-380. */
+typedef struct m3s_fwd_args {
+  int32_t struct_size; /* sizeof(m3s_fwd_args) */
+  int32_t batch, seqlen, nheads, headdim, state_dim, n_angles, chunk;
+  int32_t dtype; /* M3S_DTYPE_*: dtype of q, k, v, z, y, chunk_states and MFMA operands */
+  int32_t has_d, has_z, has_seed, save_residuals;
+  const void* q;                       /* (B, L, N)                                   */
+  const void* k;                       /* (B, L, N)                                   */
+  m3s_bhlp v;                          /* (B, H, L, P)                                */
+  m3s_bhlp z;                          /* (B, H, L, P), if has_z                      */
+  const float* adt;                    /* (B, H, L)                                   */
+  const float* gamma;                  /* (B, H, L)                                   */
+  const float* scale;                  /* (B, H, L)                                   */
+  const float* phi;                    /* (B, H, L, Nr)                               */
+  const float* q_bias;                 /* (H, N)                                      */
+  const float* k_bias;                 /* (H, N)                                      */
+  const float* d_skip;                 /* (H), if has_d                               */
+  const float* seed_ssm;               /* (B, H, P, N), if has_seed                   */
+  const float* seed_k;                 /* (B, H, N), if has_seed                      */
+  const float* seed_v;                 /* (B, H, P), if has_seed                      */
+  const float* seed_coef;              /* (B, H) = dt_0 (1 - lam_0), if has_seed      */
+  m3s_bhlp y;                          /* out (B, H, L, P)                            */
+  float* ybar;                         /* out (B, H, L, P) pre-gate, if save_residuals */
+  void* chunk_states;                  /* out (B, H, nc, N, P) state at each chunk start,
+                                          stored N-major, if save_residuals           */
+  float* final_ssm;                    /* out (B, H, P, N)                            */
+  float* final_k;                      /* out (B, H, N) rotated, unscaled             */
+  float* final_v;                      /* out (B, H, P)                               */
+} m3s_fwd_args;
+
+/* Reverse-scan backward. Replaces `kernel_bwd.siso_backward_kernel`
+ * (kernel_bwd.py:358-511) plus the dfinal_v injection of `siso_backward`
+ * (kernel_bwd.py:632-637). dq/dk are summed over heads (zeroed by this call). */
+typedef struct m3s_bwd_args {
+  int32_t struct_size; /* sizeof(m3s_bwd_args) */
+  int32_t batch, seqlen, nheads, headdim, state_dim, n_angles, chunk;
+  int32_t dtype;       /* dtype of dy, z, q, k, v, chunk_states, dv, dz */
+  int32_t has_d, has_z;
+  m3s_bhlp dy;                 /* (B, H, L, P) cotangent of the gated output           */
+  const float* ybar;           /* (B, H, L, P) from the forward                        */
+  m3s_bhlp z;                  /* (B, H, L, P), if has_z                               */
+  const void* q;               /* (B, L, N)                                            */
+  const void* k;               /* (B, L, N)                                            */
+  m3s_bhlp v;                  /* (B, H, L, P)                                         */
+  const float* adt;            /* (B, H, L)                                            */
+  const float* gamma;          /* (B, H, L)                                            */
+  const float* scale;          /* (B, H, L)                                            */
+  const float* phi;            /* (B, H, L, Nr)                                        */
+  const float* q_bias;         /* (H, N)                                               */
+  const float* k_bias;         /* (H, N)                                               */
+  const float* d_skip;         /* (H), if has_d                                        */
+  const void* chunk_states;    /* (B, H, nc, N, P) from the forward                    */
+  const float* dfinal_ssm;     /* (B, H, P, N) or NULL                                 */
+  const float* dfinal_v;       /* (B, H, P) or NULL                                    */
+  float* dq;                   /* out (B, L, N), head-summed                           */
+  float* dk;                   /* out (B, L, N), head-summed                           */
+  m3s_bhlp dv;                 /* out (B, H, L, P)                                     */
+  m3s_bhlp dz;                 /* out (B, H, L, P), if has_z                           */
+  float* dadt;                 /* out (B, H, L)                                        */
+  float* dqk_diag;             /* out (B, H, L)                                        */
+  float* dscale;               /* out (B, H, L)                                        */
+  float* uw;                   /* out (B, H, L)  u . w                                 */
+  float* dphi;                 /* out (B, H, L, Nr)                                    */
+  float* dq_bias;              /* out (B, H, N) per-(b, h) partial sums over time      */
+  float* dk_bias;              /* out (B, H, N)                                        */
+  float* k_final;              /* out (B, H, N) rotated k at the last position         */
+  float* dseed_ssm;            /* out (B, H, P, N) adjoint of the seeded state         */
+} m3s_bwd_args;
+
+/* Single-token decode, in place. Replaces `kernel_decode.siso_decode_folded` /
+ * `siso_decode` (kernel_decode.py:252-464), whose state buffers are donated
+ * (`input_output_aliases={9: 1, 10: 2, 11: 3}`): ssm, k_state, v_state and
+ * phi_state are read and overwritten with the next state. */
+typedef struct m3s_decode_args {
+  int32_t struct_size; /* sizeof(m3s_decode_args) */
+  int32_t batch, nheads, headdim, state_dim, n_angles;
+  int32_t dtype;       /* dtype of q, k, v, z, y and of the readout operands */
+  int32_t has_d, has_z;
+  const void* q;          /* (B, N)                        */
+  const void* k;          /* (B, N)                        */
+  const void* v;          /* (B, H, P)                     */
+  const void* z;          /* (B, H, P), if has_z           */
+  const float* adt;       /* (B, H)                        */
+  const float* dt;        /* (B, H)                        */
+  const float* lam;       /* (B, H)                        */
+  const float* angles;    /* (B, Nr) raw, pre-tanh         */
+  const float* q_bias;    /* (H, N)                        */
+  const float* k_bias;    /* (H, N)                        */
+  const float* d_skip;    /* (H), if has_d                 */
+  float* ssm;             /* in/out (B, H, P, N)           */
+  float* k_state;         /* in/out (B, H, N)              */
+  float* v_state;         /* in/out (B, H, P)              */
+  float* phi_state;       /* in/out (B, H, Nr)             */
+  void* y;                /* out (B, H, P)                 */
+} m3s_decode_args;
+
+/* Library identity; no counterpart in the reference. */
+int32_t m3s_abi_version(void);
+/* Message for the last non-zero return on this thread ("" if none). */
+const char* m3s_last_error(void);
+/* 1 if a kernel is compiled for this (dtype, chunk, N, P), else 0. For decode pass
+ * chunk = 0. `which` is 0 = forward, 1 = backward, 2 = decode. */
+int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, int32_t state_dim,
+                      int32_t headdim);
+
+int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
+int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
+int32_t m3s_decode(const m3s_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* M3S_H_ */

@@ -1,0 +1,149 @@
+"""ctypes binding of the C ABI in ``include/m3s.h`` (``csrc/libm3s.so``).
+
+The structs below mirror the header field for field; `m3s_abi_version` and the
+``struct_size`` field of each args struct guard against a stale library.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
+ABI_VERSION = 1
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, -1, -2, -3
+
+i32, i64, vp = C.c_int32, C.c_int64, C.c_void_p
+
+
+class Bhlp(C.Structure):
+    _fields_ = [("ptr", vp), ("stride_b", i64), ("stride_h", i64), ("stride_t", i64)]
+
+
+class FwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("nheads", i32), ("headdim", i32),
+        ("state_dim", i32), ("n_angles", i32), ("chunk", i32),
+        ("dtype", i32),
+        ("has_d", i32), ("has_z", i32), ("has_seed", i32), ("save_residuals", i32),
+        ("q", vp), ("k", vp), ("v", Bhlp), ("z", Bhlp),
+        ("adt", vp), ("gamma", vp), ("scale", vp), ("phi", vp),
+        ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
+        ("seed_ssm", vp), ("seed_k", vp), ("seed_v", vp), ("seed_coef", vp),
+        ("y", Bhlp), ("ybar", vp), ("chunk_states", vp),
+        ("final_ssm", vp), ("final_k", vp), ("final_v", vp),
+    ]
+
+
+class BwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("nheads", i32), ("headdim", i32),
+        ("state_dim", i32), ("n_angles", i32), ("chunk", i32),
+        ("dtype", i32),
+        ("has_d", i32), ("has_z", i32),
+        ("dy", Bhlp), ("ybar", vp), ("z", Bhlp), ("q", vp), ("k", vp), ("v", Bhlp),
+        ("adt", vp), ("gamma", vp), ("scale", vp), ("phi", vp),
+        ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
+        ("chunk_states", vp), ("dfinal_ssm", vp), ("dfinal_v", vp),
+        ("dq", vp), ("dk", vp), ("dv", Bhlp), ("dz", Bhlp),
+        ("dadt", vp), ("dqk_diag", vp), ("dscale", vp), ("uw", vp), ("dphi", vp),
+        ("dq_bias", vp), ("dk_bias", vp), ("k_final", vp), ("dseed_ssm", vp),
+    ]
+
+
+class DecodeArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("nheads", i32), ("headdim", i32), ("state_dim", i32),
+        ("n_angles", i32),
+        ("dtype", i32),
+        ("has_d", i32), ("has_z", i32),
+        ("q", vp), ("k", vp), ("v", vp), ("z", vp),
+        ("adt", vp), ("dt", vp), ("lam", vp), ("angles", vp),
+        ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
+        ("ssm", vp), ("k_state", vp), ("v_state", vp), ("phi_state", vp),
+        ("y", vp),
+    ]
+
+
+#: Every symbol ``include/m3s.h`` declares.
+EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_fwd", "m3s_bwd",
+           "m3s_decode")
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load the library (torch is already imported, so the HIP runtime it loaded is
+    the one the library binds to). Raises if it is missing or stale -- there is no
+    fallback compute path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build it with `python __graft_entry__.py build` "
+            "(the HIP kernels are the only compute path)")
+    lib = C.CDLL(path)
+    lib.m3s_abi_version.restype = i32
+    lib.m3s_last_error.restype = C.c_char_p
+    lib.m3s_supported.restype = i32
+    lib.m3s_supported.argtypes = [i32, i32, i32, i32, i32]
+    lib.m3s_fwd.restype = i32
+    lib.m3s_fwd.argtypes = [C.POINTER(FwdArgs), vp]
+    lib.m3s_bwd.restype = i32
+    lib.m3s_bwd.argtypes = [C.POINTER(BwdArgs), vp]
+    lib.m3s_decode.restype = i32
+    lib.m3s_decode.argtypes = [C.POINTER(DecodeArgs), vp]
+    ver = lib.m3s_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a non-zero ABI return code onto the reference's exception types."""
+    if rc == OK:
+        return
+    msg = load().m3s_last_error().decode(errors="replace")
+    if rc in (ERR_INVALID, ERR_UNSUPPORTED):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def supported(which: int, dtype: int, chunk: int, state_dim: int, headdim: int) -> bool:
+    return bool(load().m3s_supported(which, dtype, chunk, state_dim, headdim))
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float32:
+        return DTYPE_F32
+    raise ValueError(f"kernels run in bf16 or f32, got {dt}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def bhlp(t) -> Bhlp:
+    """A (B, H, L, P) tensor with unit stride on P."""
+    if t is None:
+        return Bhlp(None, 0, 0, 0)
+    if t.stride(3) != 1:
+        raise ValueError("(B, H, L, P) operand must be contiguous along P")
+    return Bhlp(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

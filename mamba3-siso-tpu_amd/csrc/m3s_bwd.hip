@@ -1,0 +1,924 @@
+// Reverse-scan backward of the Mamba-3 SISO chunked scan on gfx950 (MI355X).
+//
+// Replaces `_bwd_kernel` / `siso_backward_kernel` (kernel_bwd.py:103-511) and the
+// dfinal_v injection of `siso_backward` (kernel_bwd.py:632-637). Per chunk, walked in
+// reverse with the adjoint G of the chunk-end state (f32, MFMA registers):
+//
+//   g      = dy * silu(z);  dz = dy * ybar * sig(z) (1 + z (1 - sig(z)))
+//   W      = tril_strict(q~ khat^T * dec),   dM = tril_strict(g v^T * dec),  dec = 2^{min(A_i - A_j, 0)}
+//   dq~    = dM khat + 2^A (g S)
+//   dkhat  = dM^T q~ + 2^{A_last - A} (v G)
+//   dv     = W^T g + 2^{A_last - A} (khat G^T) + (D + gamma u.w) g
+//   dadt   = suffix_sum(q~.dq~ - khat.dkhat) + [2^{A_last} <G, S> + <khat, 2^{A_last-A}(v G)>]
+//   dscale = dkhat . k~,  du = R_{-phi}(dq~) + dqk gamma w,  dw = R_{-phi}(dkhat scale) + dqk gamma u
+//   dphi   = rope_dphi(q~, dq~) + rope_dphi(k~, dk~)
+//   dq += sum_h du, dk += sum_h dw;  G <- 2^{A_last} G + (2^A g)^T q~
+//
+// One workgroup per (b, h). Wave w owns position strip [16w, 16w+16) both as queries
+// (dq~) and as keys (dkhat, dv), which balances the causal triangle across waves.
+// Score-like tiles (W, dM, dM^T) never leave registers: an MFMA accumulator tile is
+// already an operand fragment with its row index as K (see m3s_common.h). Operands
+// whose K is their row index (q~, khat, g over time) are served from transposed LDS
+// copies, built in place by one transpose pass between the two product phases. The
+// elementwise pullback runs row-major on f32 dq~/dkhat staged through LDS, so the
+// head-sum of dq/dk is a coalesced f32 atomic add per row.
+#include "m3s_common.h"
+#include "m3s_internal.h"
+
+namespace m3s {
+
+struct BwdParams {
+  int B, L, H, Nr, nc;
+  int has_d, has_z;
+  const void* dy;
+  int64_t dy_sb, dy_sh, dy_st;
+  const float* ybar;
+  const void* z;
+  int64_t z_sb, z_sh, z_st;
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t v_sb, v_sh, v_st;
+  const float* adt;
+  const float* gamma;
+  const float* scale;
+  const float* phi;
+  const float* qb;
+  const float* kb;
+  const float* dsk;
+  const void* cstates;
+  const float* dfs;
+  const float* dfv;
+  float* dq;
+  float* dk;
+  void* dv;
+  int64_t dv_sb, dv_sh, dv_st;
+  void* dz;
+  int64_t dz_sb, dz_sh, dz_st;
+  float* dadt;
+  float* dqk;
+  float* dscale;
+  float* uw;
+  float* dphi;
+  float* dqb;
+  float* dkb;
+  float* kfin;
+  float* dseed;
+};
+
+template <typename MT> struct BV16;
+template <> struct BV16<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct BV16<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <typename MT, int C, int N, int P, int NW>
+struct BwdCfg {
+  static constexpr int NT = NW * 64;
+  static constexpr int VEC = BV16<MT>::n;
+  static constexpr int H2 = N / 2;
+  static constexpr int PAD = 16 / (int)sizeof(MT);
+  static constexpr int LDQ = N + PAD;   // sQ, sK rows (positions)
+  static constexpr int LDP = P + PAD;   // sG, sV rows (positions), sST / sGT rows (n)
+  static constexpr int LDT = C + PAD;   // sQT, sKT, sGT rows
+  static constexpr int LDF = N + 4;     // f32 staging rows of dq~ / dkhat
+  static constexpr int PB = P / 16, NB = N / 16, CB = C / 16;
+  static constexpr int T4 = PB * NB;
+  static constexpr int SPW = (T4 + NW - 1) / NW;
+  static constexpr int E = C >= 64 ? C / 64 : 1;
+  static constexpr int QKG = H2 / VEC;
+  static constexpr int QKT = (C / 2) * QKG;
+  static constexpr int QKR = (QKT + NT - 1) / NT;
+  static constexpr int VG = P / VEC;
+  static constexpr int VT = (C / 2) * VG;
+  static constexpr int VR = (VT + NT - 1) / NT;
+  static constexpr int SV = N * P / VEC;           // 16-byte pieces of a chunk state
+  static constexpr int SR = (SV + NT - 1) / NT;
+  // transpose-pass tasks: (row pair, column group) over sQ, sK (C x N) and sG (C x P)
+  static constexpr int TQ = (C / 2) * (N / VEC);
+  static constexpr int TG = (C / 2) * (P / VEC);
+  static constexpr int TQR = (TQ + NT - 1) / NT;
+  static constexpr int TGR = (TG + NT - 1) / NT;
+  // ---- LDS layout -----------------------------------------------------------------
+  static constexpr int SZ_QQ = cmax(C * LDQ, N * LDT) * (int)sizeof(MT);  // sQ | sQT
+  static constexpr int SZ_GG = cmax(C * LDP, P * LDT) * (int)sizeof(MT);  // sG | sGT
+  static constexpr int SZ_V = C * LDP * (int)sizeof(MT);
+  static constexpr int SZ_ST = N * LDP * (int)sizeof(MT);                  // S^T [n][p]
+  static constexpr int SZ_X = 2 * SZ_QQ + SZ_GG + SZ_V + SZ_ST;
+  static constexpr int SZ_STAGE = 2 * C * LDF * 4;                         // dq~, dkhat f32
+  static constexpr int SZ_R = cmax(SZ_X, SZ_STAGE);
+  static constexpr int SZ_GAT = N * LDP * (int)sizeof(MT);                 // G^T [n][p]
+  static constexpr int SZ_SC = (8 * C + 4 * N + 16) * 4;
+  static constexpr int LDS_BYTES = SZ_R + SZ_GAT + SZ_SC;
+  static_assert(NW >= CB, "one position strip per wave");
+  static_assert(QKG <= 64 && (QKG & (QKG - 1)) == 0, "row groups must fit a wave");
+  static_assert(VG <= 64 && (VG & (VG - 1)) == 0, "row groups must fit a wave");
+  static_assert(C % 32 == 0 && N % 16 == 0 && P % 16 == 0, "tile shape");
+  static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
+};
+
+template <typename MT>
+__device__ __forceinline__ sub_t<MT> zero_sub() {
+  return sub_from_f32<MT>(f32x4{0.f, 0.f, 0.f, 0.f});
+}
+
+template <typename MT, int C, int N, int P, int NW>
+__global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
+  using F = BwdCfg<MT, C, N, P, NW>;
+  using vec = typename BV16<MT>::type;
+  constexpr int NT = F::NT, VEC = F::VEC, H2 = F::H2;
+  constexpr int LDQ = F::LDQ, LDP = F::LDP, LDT = F::LDT, LDF = F::LDF;
+  constexpr int PB = F::PB, NB = F::NB, CB = F::CB;
+
+  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
+  // Buffer offsets go through an opaque SGPR. Otherwise every access above 64 KiB (the
+  // reach of a ds_read immediate) gets its own address VGPR, and LICM keeps all of them
+  // live across the chunk loop -- enough to spill.
+  auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
+  MT* sQ = reinterpret_cast<MT*>(smem);                       // q~ [t][n]  -> sQT [n][t]
+  MT* sK = reinterpret_cast<MT*>(smem + opq(F::SZ_QQ));            // khat [j][n] -> sKT [n][j]
+  MT* sG = reinterpret_cast<MT*>(smem + opq(2 * F::SZ_QQ));        // g [t][p]  -> sGT [p][t]
+  MT* sV = reinterpret_cast<MT*>(smem + opq(2 * F::SZ_QQ + F::SZ_GG));
+  MT* sST = reinterpret_cast<MT*>(smem + opq(2 * F::SZ_QQ + F::SZ_GG + F::SZ_V));
+  MT* sQT = sQ;
+  MT* sKT = sK;
+  MT* sGT = sG;
+  float* sDQ = reinterpret_cast<float*>(smem);                // staging, after the products
+  float* sDK = reinterpret_cast<float*>(smem + opq(C * LDF * 4));
+  MT* sGaT = reinterpret_cast<MT*>(smem + opq(F::SZ_R));           // adjoint G^T [n][p]
+  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_R + F::SZ_GAT));
+  float* sExpA = sA + C;
+  float* sFac = sExpA + C;
+  float* sGam = sFac + C;
+  float* sScl = sGam + C;
+  float* sDqk = sScl + C;
+  float* sCoef = sDqk + C;
+  float* sDA = sCoef + C;
+  float* sQb = sDA + C;
+  float* sKb = sQb + N;
+  float* sDqb = sKb + N;
+  float* sDkb = sDqb + N;
+  float* sRed = sDkb + N;  // [0]: 2^{A_last}<G,S> + <v, dv_inter> for the current chunk
+
+  const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = wid / p.H, h = wid % p.H;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int L = p.L, Nr = p.Nr, nc = p.nc;
+
+  for (int i = tid; i < N; i += NT) {
+    sQb[i] = p.qb[h * N + i];
+    sKb[i] = p.kb[h * N + i];
+    sDqb[i] = 0.f;
+    sDkb[i] = 0.f;
+  }
+  if (tid == 0) sRed[0] = 0.f;
+  const float dsk = p.has_d ? p.dsk[h] : 0.f;
+
+  const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * L * N;
+  const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * L * N;
+  const MT* vg = static_cast<const MT*>(p.v) + b * p.v_sb + h * p.v_sh;
+  const MT* dyg = static_cast<const MT*>(p.dy) + b * p.dy_sb + h * p.dy_sh;
+  const MT* zg = p.has_z ? static_cast<const MT*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
+  MT* dzg = p.has_z ? static_cast<MT*>(p.dz) + b * p.dz_sb + h * p.dz_sh : nullptr;
+  MT* dvg = static_cast<MT*>(p.dv) + b * p.dv_sb + h * p.dv_sh;
+  const float* ybg = p.ybar + bh * (int64_t)L * P;
+  const float* adtg = p.adt + bh * L;
+  const float* gamg = p.gamma + bh * L;
+  const float* sclg = p.scale + bh * L;
+  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  const MT* csg = static_cast<const MT*>(p.cstates) + bh * (int64_t)nc * N * P;
+  float* dqg = p.dq + (int64_t)b * L * N;
+  float* dkg = p.dk + (int64_t)b * L * N;
+  const bool phi_vec = (Nr % 4) == 0;
+
+  // ---- adjoint G (registers, MFMA layout [p][n]) -----------------------------------
+  f32x4 Gacc[F::SPW];
+#pragma unroll
+  for (int m = 0; m < F::SPW; ++m) {
+    const int s = wave + NW * m;
+    Gacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (s < F::T4 && p.dfs) {
+      const int pb = s % PB, nb = s / PB;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        Gacc[m][i] = p.dfs[(bh * P + pb * 16 + 4 * g4 + i) * N + nb * 16 + l16];
+    }
+  }
+  auto publish_adjoint = [&]() {
+#pragma unroll
+    for (int m = 0; m < F::SPW; ++m) {
+      const int s = wave + NW * m;
+      if (s < F::T4) {
+        const int pb = s % PB, nb = s / PB;
+        *reinterpret_cast<sub_t<MT>*>(sGaT + (nb * 16 + l16) * LDP + pb * 16 + 4 * g4) =
+            sub_from_f32<MT>(Gacc[m]);
+      }
+    }
+  };
+  publish_adjoint();
+
+  // ---- register prefetch of one chunk's raw inputs ----------------------------------
+  vec rq[F::QKR][2][2], rk[F::QKR][2][2];
+  f32x4 rphi[F::QKR][2][VEC / 4];
+  float rscale[F::QKR][2];
+  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2];
+  f32x4 ryb[F::VR][2][VEC / 4];
+  vec rs[F::SR];
+  float radt[F::E], rgam_s, rscl_s;
+
+  auto load_qk = [&](int c, vec (&q_)[F::QKR][2][2], vec (&k_)[F::QKR][2][2],
+                     f32x4 (&ph_)[F::QKR][2][VEC / 4], float (&sc_)[F::QKR][2]) {
+    const int t0 = c * C;
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::QKT) {
+        const int tp = task / F::QKG, j0 = (task % F::QKG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int64_t t = t0 + 2 * tp + e;
+          q_[r][e][0] = *reinterpret_cast<const vec*>(qg + t * N + j0);
+          q_[r][e][1] = *reinterpret_cast<const vec*>(qg + t * N + H2 + j0);
+          k_[r][e][0] = *reinterpret_cast<const vec*>(kg + t * N + j0);
+          k_[r][e][1] = *reinterpret_cast<const vec*>(kg + t * N + H2 + j0);
+          const float* pr = phig + t * Nr;
+#pragma unroll
+          for (int qd = 0; qd < VEC / 4; ++qd) {
+            const int j = j0 + 4 * qd;
+            if (phi_vec && j + 4 <= Nr) {
+              ph_[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ph_[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+            }
+          }
+          sc_[r][e] = sclg[t];
+        }
+      }
+    }
+  };
+  auto prefetch = [&](int c) {
+    const int t0 = c * C;
+    load_qk(c, rq, rk, rphi, rscale);
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int64_t t = t0 + 2 * tp + e;
+          rv[r][e] = *reinterpret_cast<const vec*>(vg + t * p.v_st + p0);
+          rdy[r][e] = *reinterpret_cast<const vec*>(dyg + t * p.dy_st + p0);
+          if (zg) {
+            rz[r][e] = *reinterpret_cast<const vec*>(zg + t * p.z_st + p0);
+#pragma unroll
+            for (int i = 0; i < VEC; i += 4)
+              ryb[r][e][i / 4] = *reinterpret_cast<const f32x4*>(ybg + t * P + p0 + i);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::SR; ++r) {
+      const int f = tid + r * NT;
+      if (f < F::SV) rs[r] = *reinterpret_cast<const vec*>(csg + (int64_t)c * N * P + f * VEC);
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        radt[e] = tt < C ? adtg[t0 + tt] : 0.f;
+      }
+    }
+    if (tid < C) {
+      rgam_s = gamg[t0 + tid];
+      rscl_s = sclg[t0 + tid];
+    }
+  };
+
+  prefetch(nc - 1);
+  __syncthreads();
+
+  for (int c = nc - 1; c >= 0; --c) {
+    const int t0 = c * C;
+    // Lane/wave indices re-derived opaquely each chunk, so the per-lane LDS address
+    // arithmetic is recomputed near its uses instead of being hoisted out of the loop.
+    int lane_v = threadIdx.x;
+    asm volatile("" : "+v"(lane_v));
+    const int tid = lane_v, lane = tid & 63, g4 = lane >> 4, l16 = lane & 15;
+    int wave_s = __builtin_amdgcn_readfirstlane(tid >> 6);
+    asm volatile("" : "+s"(wave_s));
+    const int wave = wave_s;
+
+    // ============ phase L: raw -> LDS (q~, khat, g, v, S^T), dz, dqk, uw ==============
+    if (wave == 0) {
+      float a[F::E];
+      float run = 0.f;
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        run += radt[e] * kLog2e;
+        a[e] = run;
+      }
+      float incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      const float excl = incl - run;
+      const float a_last = __shfl(incl, (C - 1) / F::E, 64);
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        if (tt < C) {
+          const float A = excl + a[e];
+          sA[tt] = A;
+          sExpA[tt] = exp2f(A);
+          sFac[tt] = exp2f(a_last - A);
+        }
+      }
+    }
+    if (tid < C) {
+      sGam[tid] = rgam_s;
+      sScl[tid] = rscl_s;
+    }
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      const bool valid = task < F::QKT;
+      const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
+      float uw[2] = {0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        if (valid) {
+          const int t = 2 * tp + e;
+          vec oq0, oq1, ok0, ok1;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const int j = j0 + i;
+            const float ulo = (float)rq[r][e][0][i] + sQb[j];
+            const float uhi = (float)rq[r][e][1][i] + sQb[H2 + j];
+            const float wlo = (float)rk[r][e][0][i] + sKb[j];
+            const float whi = (float)rk[r][e][1][i] + sKb[H2 + j];
+            uw[e] += ulo * wlo + uhi * whi;
+            float sn = 0.f, cs = 1.f;
+            if (j < Nr) sincosf(rphi[r][e][i / 4][i % 4], &sn, &cs);
+            const float sc = rscale[r][e];
+            oq0[i] = (MT)(ulo * cs - uhi * sn);
+            oq1[i] = (MT)(uhi * cs + ulo * sn);
+            ok0[i] = (MT)((wlo * cs - whi * sn) * sc);
+            ok1[i] = (MT)((whi * cs + wlo * sn) * sc);
+          }
+          *reinterpret_cast<vec*>(sQ + t * LDQ + j0) = oq0;
+          *reinterpret_cast<vec*>(sQ + t * LDQ + H2 + j0) = oq1;
+          *reinterpret_cast<vec*>(sK + t * LDQ + j0) = ok0;
+          *reinterpret_cast<vec*>(sK + t * LDQ + H2 + j0) = ok1;
+        }
+      }
+      uw[0] = group_sum<F::QKG>(uw[0]);
+      uw[1] = group_sum<F::QKG>(uw[1]);
+      if (valid && j0 == 0) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          p.uw[bh * L + t0 + t] = uw[e];
+          sCoef[t] = p.gamma[bh * L + t0 + t] * uw[e] + dsk;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      const bool valid = task < F::VT;
+      const int tp = valid ? task / F::VG : 0, p0 = valid ? (task % F::VG) * VEC : 0;
+      float dqk[2] = {0.f, 0.f};
+      if (valid) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          vec og, odz;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const float dy = (float)rdy[r][e][i];
+            float gv = dy;
+            if (zg) {
+              const float zf = (float)rz[r][e][i];
+              const float sg = sigmoidf_(zf);
+              gv = dy * (zf * sg);
+              odz[i] = (MT)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
+            }
+            dqk[e] += gv * (float)rv[r][e][i];
+            og[i] = (MT)gv;
+          }
+          *reinterpret_cast<vec*>(sG + t * LDP + p0) = og;
+          *reinterpret_cast<vec*>(sV + t * LDP + p0) = rv[r][e];
+          if (dzg) *reinterpret_cast<vec*>(dzg + (int64_t)(t0 + t) * p.dz_st + p0) = odz;
+        }
+      }
+      dqk[0] = group_sum<F::VG>(dqk[0]);
+      dqk[1] = group_sum<F::VG>(dqk[1]);
+      if (valid && p0 == 0) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          sDqk[t] = dqk[e];
+          p.dqk[bh * L + t0 + t] = dqk[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::SR; ++r) {
+      const int f = tid + r * NT;
+      if (f < F::SV) {
+        const int n = (f * VEC) / P, pp = (f * VEC) % P;
+        *reinterpret_cast<vec*>(sST + n * LDP + pp) = rs[r];
+      }
+    }
+    __syncthreads();
+
+    // ============ phase P1: register score tiles, inter-chunk terms ===================
+    const int w = wave;
+    const bool strip = w < CB;
+    sub_t<MT> Wt[CB], dMt[CB], dMT[CB];
+    f32x4 dQ[NB], dKh[NB], dV[PB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      dQ[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dKh[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) dV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float red = 0.f;
+    if (strip) {
+      const int jcol = w * 16 + l16;     // this lane's key position (cols of W, dM)
+      const float Aj = sA[jcol];
+#pragma unroll
+      for (int tb = 0; tb < CB; ++tb) {
+        if (tb >= w) {
+          f32x4 aw = {0.f, 0.f, 0.f, 0.f}, am = {0.f, 0.f, 0.f, 0.f};
+          gemm_nt<MT, N>(aw, sQ, LDQ, tb * 16, sK, LDQ, w * 16);   // W[t][j]
+          gemm_nt<MT, P>(am, sG, LDP, tb * 16, sV, LDP, w * 16);   // dM[t][j]
+          f32x4 vw, vm;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = tb * 16 + 4 * g4 + i;
+            const float dec = (t > jcol) ? exp2f(fminf(sA[t] - Aj, 0.f)) : 0.f;
+            vw[i] = aw[i] * dec;
+            vm[i] = am[i] * dec;
+          }
+          Wt[tb] = sub_from_f32<MT>(vw);
+          dMt[tb] = sub_from_f32<MT>(vm);
+        } else {
+          Wt[tb] = zero_sub<MT>();
+          dMt[tb] = zero_sub<MT>();
+        }
+      }
+      const int tcol = w * 16 + l16;     // this lane's query position (cols of dM^T)
+      const float At = sA[tcol];
+#pragma unroll
+      for (int jb = 0; jb < CB; ++jb) {
+        if (jb <= w) {
+          f32x4 am = {0.f, 0.f, 0.f, 0.f};
+          gemm_nt<MT, P>(am, sV, LDP, jb * 16, sG, LDP, w * 16);   // dM^T[j][t]
+          f32x4 vm;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = jb * 16 + 4 * g4 + i;
+            vm[i] = (tcol > j) ? am[i] * exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+          }
+          dMT[jb] = sub_from_f32<MT>(vm);
+        } else {
+          dMT[jb] = zero_sub<MT>();
+        }
+      }
+      // dq~ inter: 2^{A_t} sum_p g[t][p] S[p][n]   (rows t, cols n)
+      // dkhat inter: 2^{A_last-A_j} sum_p v[j][p] G[p][n]   (rows j, cols n)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        gemm_nt<MT, P>(dQ[nb], sG, LDP, w * 16, sST, LDP, nb * 16);
+        gemm_nt<MT, P>(dKh[nb], sV, LDP, w * 16, sGaT, LDP, nb * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = w * 16 + 4 * g4 + i;
+          dQ[nb][i] *= sExpA[r];
+          dKh[nb][i] *= sFac[r];
+        }
+      }
+      // dv inter: 2^{A_last-A_j} sum_n khat[j][n] G[p][n]   (rows j, cols p)
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += 16) {
+          sub_t<MT> bsub;
+          const int kk = sub_k(k0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bsub[i] = sGaT[(kk + i) * LDP + pb * 16 + l16];
+          mma16(dV[pb], ld_sub<MT>(sK, LDQ, w * 16, k0), bsub);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = w * 16 + 4 * g4 + i;
+          dV[pb][i] *= sFac[j];
+          // <v, dv_inter> == <khat, dk_inter>: the A_last share of the state update
+          red += (float)sV[j * LDP + pb * 16 + l16] * dV[pb][i];
+        }
+      }
+    }
+    // 2^{A_last} <G, S>: this wave's adjoint tiles against the chunk-start state
+    {
+      float gs = 0.f;
+#pragma unroll
+      for (int m = 0; m < F::SPW; ++m) {
+        const int s = wave + NW * m;
+        if (s < F::T4) {
+          const int pb = s % PB, nb = s / PB;
+          const f32x4 sv =
+              sub_to_f32<MT>(*reinterpret_cast<const sub_t<MT>*>(sST + (nb * 16 + l16) * LDP + pb * 16 + 4 * g4));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) gs += Gacc[m][i] * sv[i];
+        }
+      }
+      red += sExpA[C - 1] * gs;
+    }
+    red = group_sum<64>(red);
+    if (lane == 0) atomicAdd(sRed, red);
+    __syncthreads();
+
+    // ============ transpose pass: q~, khat, g to [x][position], one tile at a time =====
+    auto transpose_tile = [&](MT* buf, int ldr, int cols) {
+      // in place: every thread reads its share, barrier, writes it transposed
+      constexpr int MAXR = (C / 2) * (N / VEC) / NT + 1;
+      vec tv[MAXR][2];
+      const int groups = cols / VEC, tasks = (C / 2) * groups;
+#pragma unroll
+      for (int r = 0; r < MAXR; ++r) {
+        const int task = tid + r * NT;
+        if (task < tasks) {
+          const int tp = task / groups, c0 = (task % groups) * VEC;
+          tv[r][0] = *reinterpret_cast<const vec*>(buf + (2 * tp) * ldr + c0);
+          tv[r][1] = *reinterpret_cast<const vec*>(buf + (2 * tp + 1) * ldr + c0);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < MAXR; ++r) {
+        const int task = tid + r * NT;
+        if (task < tasks) {
+          const int tp = task / groups, c0 = (task % groups) * VEC;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i)
+            store_pair<MT>(buf + (c0 + i) * LDT + 2 * tp, (float)tv[r][0][i], (float)tv[r][1][i]);
+        }
+      }
+    };
+    transpose_tile(sQ, LDQ, N);
+    transpose_tile(sK, LDQ, N);
+    transpose_tile(sG, LDP, P);
+    __syncthreads();
+
+    // ============ phase P2: intra-chunk products, adjoint update ======================
+    if (strip) {
+      // dv[j][p] += sum_t W[t][j] g[t][p];  dkhat[j][n] += sum_t dM[t][j] q~[t][n]
+#pragma unroll
+      for (int tb = 0; tb < CB; tb += 2) {
+        if (tb + 1 >= w) {
+#pragma unroll
+          for (int pb = 0; pb < PB; ++pb)
+            mma32(dV[pb], Wt[tb], Wt[tb + 1], ld_sub<MT>(sGT, LDT, pb * 16, tb * 16),
+                  ld_sub<MT>(sGT, LDT, pb * 16, tb * 16 + 16));
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            mma32(dKh[nb], dMt[tb], dMt[tb + 1], ld_sub<MT>(sQT, LDT, nb * 16, tb * 16),
+                  ld_sub<MT>(sQT, LDT, nb * 16, tb * 16 + 16));
+        }
+      }
+      // dq~[t][n] += sum_j dM^T[j][t] khat[j][n]
+#pragma unroll
+      for (int jb = 0; jb < CB; jb += 2) {
+        if (jb <= w) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            mma32(dQ[nb], dMT[jb], dMT[jb + 1], ld_sub<MT>(sKT, LDT, nb * 16, jb * 16),
+                  ld_sub<MT>(sKT, LDT, nb * 16, jb * 16 + 16));
+        }
+      }
+    }
+    // G <- 2^{A_last} G + sum_t (2^{A_t} g[t][p]) q~[t][n]
+    {
+      const float eAl = sExpA[C - 1];
+#pragma unroll
+      for (int m = 0; m < F::SPW; ++m) {
+        const int s = wave + NW * m;
+        if (s < F::T4) {
+          const int pb = s % PB, nb = s / PB;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Gacc[m][i] *= eAl;
+#pragma unroll
+          for (int k0 = 0; k0 < C; k0 += 32) {
+            f32x4 a0 = sub_to_f32<MT>(ld_sub<MT>(sGT, LDT, pb * 16, k0));
+            f32x4 a1 = sub_to_f32<MT>(ld_sub<MT>(sGT, LDT, pb * 16, k0 + 16));
+            const int kk = sub_k(k0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              a0[i] *= sExpA[kk + i];
+              a1[i] *= sExpA[kk + 16 + i];
+            }
+            mma32(Gacc[m], sub_from_f32<MT>(a0), sub_from_f32<MT>(a1),
+                  ld_sub<MT>(sQT, LDT, nb * 16, k0), ld_sub<MT>(sQT, LDT, nb * 16, k0 + 16));
+          }
+        }
+      }
+    }
+    // dv epilogue: + (D + gamma u.w) g, + dfinal_v on the sequence's last row; store
+    if (strip) {
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        const int pcol = pb * 16 + l16;
+        const f32x4 gv = sub_to_f32<MT>(
+            *reinterpret_cast<const sub_t<MT>*>(sGT + pcol * LDT + w * 16 + 4 * g4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = w * 16 + 4 * g4 + i;
+          float d = dV[pb][i] + sCoef[j] * gv[i];
+          if (p.dfv && t0 + j == L - 1) d += p.dfv[bh * P + pcol];
+          dvg[(int64_t)(t0 + j) * p.dv_st + pcol] = (MT)d;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ stage dq~ [t][n] and dkhat [j][n] as f32 rows =======================
+    if (strip) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = w * 16 + 4 * g4 + i;
+          sDQ[r * LDF + nb * 16 + l16] = dQ[nb][i];
+          sDK[r * LDF + nb * 16 + l16] = dKh[nb][i];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ phase R: rotation pullback, per-row reductions, head sum ============
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      const bool valid = task < F::QKT;
+      const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
+      float dA[2] = {0.f, 0.f}, dsc[2] = {0.f, 0.f};
+      float bq[2][VEC], bk[2][VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) bq[0][i] = bq[1][i] = bk[0][i] = bk[1][i] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        if (valid) {
+          const int t = 2 * tp + e;
+          const int64_t tg = t0 + t;
+          const vec q0 = *reinterpret_cast<const vec*>(qg + tg * N + j0);
+          const vec q1 = *reinterpret_cast<const vec*>(qg + tg * N + H2 + j0);
+          const vec k0 = *reinterpret_cast<const vec*>(kg + tg * N + j0);
+          const vec k1 = *reinterpret_cast<const vec*>(kg + tg * N + H2 + j0);
+          const float sc = sScl[t];
+          const float cd = sDqk[t] * sGam[t];
+          const float* pr = phig + tg * Nr;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const int j = j0 + i;
+            const float ulo = (float)q0[i] + sQb[j];
+            const float uhi = (float)q1[i] + sQb[H2 + j];
+            const float wlo = (float)k0[i] + sKb[j];
+            const float whi = (float)k1[i] + sKb[H2 + j];
+            float sn = 0.f, cs = 1.f;
+            if (j < Nr) sincosf(pr[j], &sn, &cs);
+            const float qlo = ulo * cs - uhi * sn, qhi = uhi * cs + ulo * sn;
+            const float klo = wlo * cs - whi * sn, khi = whi * cs + wlo * sn;
+            const float dqlo = sDQ[t * LDF + j], dqhi = sDQ[t * LDF + H2 + j];
+            const float dklo = sDK[t * LDF + j], dkhi = sDK[t * LDF + H2 + j];
+            dA[e] += qlo * dqlo + qhi * dqhi - (klo * sc) * dklo - (khi * sc) * dkhi;
+            dsc[e] += dklo * klo + dkhi * khi;
+            const float dtlo = dklo * sc, dthi = dkhi * sc;   // d k~
+            // R^T = R(-phi): lo' = lo cos + hi sin, hi' = hi cos - lo sin
+            const float dulo = dqlo * cs + dqhi * sn + cd * wlo;
+            const float duhi = dqhi * cs - dqlo * sn + cd * whi;
+            const float dwlo = dtlo * cs + dthi * sn + cd * ulo;
+            const float dwhi = dthi * cs - dtlo * sn + cd * uhi;
+            if (j < Nr)
+              p.dphi[(bh * L + tg) * Nr + j] = (dqhi * qlo - dqlo * qhi) + (dthi * klo - dtlo * khi);
+            if (c == nc - 1 && t == C - 1) {
+              p.kfin[bh * N + j] = klo;
+              p.kfin[bh * N + H2 + j] = khi;
+            }
+            unsafeAtomicAdd(dqg + tg * N + j, dulo);
+            unsafeAtomicAdd(dqg + tg * N + H2 + j, duhi);
+            unsafeAtomicAdd(dkg + tg * N + j, dwlo);
+            unsafeAtomicAdd(dkg + tg * N + H2 + j, dwhi);
+            bq[0][i] += dulo;
+            bq[1][i] += duhi;
+            bk[0][i] += dwlo;
+            bk[1][i] += dwhi;
+          }
+        }
+      }
+      dA[0] = group_sum<F::QKG>(dA[0]);
+      dA[1] = group_sum<F::QKG>(dA[1]);
+      dsc[0] = group_sum<F::QKG>(dsc[0]);
+      dsc[1] = group_sum<F::QKG>(dsc[1]);
+      if (valid && j0 == 0) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          sDA[2 * tp + e] = dA[e];
+          p.dscale[bh * L + t0 + 2 * tp + e] = dsc[e];
+        }
+      }
+      // bias partials: sum over the row pairs of this wave that share the pair group,
+      // then one LDS atomic per element from the first of them
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          float vq = bq[hh][i], vk = bk[hh][i];
+#pragma unroll
+          for (int m = F::QKG; m < 64; m <<= 1) {
+            vq += __shfl_xor(vq, m, 64);
+            vk += __shfl_xor(vk, m, 64);
+          }
+          if (valid && lane < F::QKG) {
+            atomicAdd(sDqb + hh * H2 + j0 + i, vq);
+            atomicAdd(sDkb + hh * H2 + j0 + i, vk);
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
+    if (c > 0) prefetch(c - 1);
+    if (wave == 0) {
+      const float extra = sRed[0];
+      float a[F::E];
+      float run = 0.f;
+#pragma unroll
+      for (int e = F::E - 1; e >= 0; --e) {
+        const int tt = lane * F::E + e;
+        run += (tt < C) ? sDA[tt] : 0.f;
+        a[e] = run;
+      }
+      // suffix scan across lanes: inclusive sum over lanes >= this one
+      float incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_down(incl, off, 64);
+        if (lane + off < 64) incl += o;
+      }
+      const float excl = incl - run;
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        if (tt < C) p.dadt[bh * L + t0 + tt] = excl + a[e] + extra;
+      }
+    }
+    publish_adjoint();
+    __syncthreads();
+    if (tid == 0) sRed[0] = 0.f;
+  }
+
+  // ---- per-(b, h) outputs ------------------------------------------------------------
+#pragma unroll
+  for (int m = 0; m < F::SPW; ++m) {
+    const int s = wave + NW * m;
+    if (s < F::T4) {
+      const int pb = s % PB, nb = s / PB;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        p.dseed[(bh * P + pb * 16 + 4 * g4 + i) * N + nb * 16 + l16] = Gacc[m][i];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < N; i += NT) {
+    p.dqb[bh * N + i] = sDqb[i];
+    p.dkb[bh * N + i] = sDkb[i];
+  }
+}
+
+__global__ void zero_kernel(float4* a, float4* b, int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n4) {
+    a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    b[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+template <typename MT, int C, int N, int P>
+static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
+  constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
+  const int64_t n4 = (int64_t)prm.B * prm.L * N / 4;
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<float4*>(prm.dq), reinterpret_cast<float4*>(prm.dk), n4);
+  int32_t rc = launch_status("m3s_bwd (zero dq/dk)");
+  if (rc != M3S_OK) return rc;
+  hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  return launch_status("m3s_bwd");
+}
+
+#define M3S_BWD_CONFIGS(X) \
+  X(bf16, 128, 128, 64)    \
+  X(bf16, 64, 128, 64)     \
+  X(bf16, 32, 128, 64)     \
+  X(bf16, 64, 64, 64)      \
+  X(bf16, 64, 32, 16)      \
+  X(bf16, 32, 32, 16)      \
+  X(bf16, 64, 16, 16)      \
+  X(bf16, 32, 16, 16)      \
+  X(float, 32, 128, 64)    \
+  X(float, 64, 64, 64)     \
+  X(float, 64, 32, 16)     \
+  X(float, 32, 32, 16)     \
+  X(float, 64, 16, 16)     \
+  X(float, 32, 16, 16)
+
+template <typename MT> constexpr int bcode();
+template <> constexpr int bcode<bf16>() { return M3S_DTYPE_BF16; }
+template <> constexpr int bcode<float>() { return M3S_DTYPE_F32; }
+
+int32_t bwd_supported(int dtype, int chunk, int n, int pdim) {
+#define X(MT, C, N, P) \
+  if (dtype == bcode<MT>() && chunk == C && n == N && pdim == P) return 1;
+  M3S_BWD_CONFIGS(X)
+#undef X
+  return 0;
+}
+
+}  // namespace m3s
+
+extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
+  using namespace m3s;
+  clear_error();
+  M3S_REQUIRE(a != nullptr, "m3s_bwd: args is NULL");
+  M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_bwd_args),
+              "m3s_bwd: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              (int)sizeof(m3s_bwd_args));
+  const int B = a->batch, L = a->seqlen, H = a->nheads, P = a->headdim, N = a->state_dim,
+            Nr = a->n_angles, C = a->chunk;
+  M3S_REQUIRE(B > 0 && L > 0 && H > 0 && P > 0 && N > 0 && C > 0,
+              "m3s_bwd: non-positive dimension");
+  M3S_REQUIRE(L % C == 0, "m3s_bwd: seqlen %d is not a multiple of chunk %d", L, C);
+  M3S_REQUIRE(Nr >= 0 && 2 * Nr <= N, "m3s_bwd: n_angles %d exceeds state_dim/2", Nr);
+  M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32, "m3s_bwd: bad dtype %d",
+              a->dtype);
+  if (!bwd_supported(a->dtype, C, N, P)) {
+    set_error("m3s_bwd: no kernel for dtype=%s chunk=%d state_dim=%d headdim=%d",
+              a->dtype == M3S_DTYPE_BF16 ? "bf16" : "f32", C, N, P);
+    return M3S_ERR_UNSUPPORTED;
+  }
+  const int vec = a->dtype == M3S_DTYPE_BF16 ? 8 : 4;
+  M3S_REQUIRE(bhlp_ok(a->dy, vec) && bhlp_ok(a->v, vec) && bhlp_ok(a->dv, vec),
+              "m3s_bwd: dy/v/dv null, misaligned or strides not multiples of %d", vec);
+  M3S_REQUIRE(!a->has_z || (bhlp_ok(a->z, vec) && bhlp_ok(a->dz, vec) && a->ybar &&
+                            aligned16(a->ybar)),
+              "m3s_bwd: has_z needs z, dz and an aligned ybar");
+  M3S_REQUIRE(a->q && a->k && aligned16(a->q) && aligned16(a->k), "m3s_bwd: q/k null or misaligned");
+  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->phi && a->q_bias && a->k_bias,
+              "m3s_bwd: a required input pointer is NULL");
+  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 || aligned16(a->phi), "m3s_bwd: phi misaligned");
+  M3S_REQUIRE(a->chunk_states && aligned16(a->chunk_states), "m3s_bwd: chunk_states null or misaligned");
+  M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_bwd: has_d but d_skip is NULL");
+  M3S_REQUIRE(a->dq && a->dk && aligned16(a->dq) && aligned16(a->dk) && a->dadt && a->dqk_diag &&
+                  a->dscale && a->uw && a->dq_bias && a->dk_bias && a->k_final && a->dseed_ssm &&
+                  (Nr == 0 || a->dphi),
+              "m3s_bwd: an output pointer is NULL or misaligned");
+  M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_bwd: B*H too large");
+
+  BwdParams prm{};
+  prm.B = B; prm.L = L; prm.H = H; prm.Nr = Nr; prm.nc = L / C;
+  prm.has_d = a->has_d; prm.has_z = a->has_z;
+  prm.dy = a->dy.ptr; prm.dy_sb = a->dy.stride_b; prm.dy_sh = a->dy.stride_h; prm.dy_st = a->dy.stride_t;
+  prm.ybar = a->ybar;
+  prm.z = a->has_z ? a->z.ptr : nullptr;
+  prm.z_sb = a->z.stride_b; prm.z_sh = a->z.stride_h; prm.z_st = a->z.stride_t;
+  prm.q = a->q; prm.k = a->k;
+  prm.v = a->v.ptr; prm.v_sb = a->v.stride_b; prm.v_sh = a->v.stride_h; prm.v_st = a->v.stride_t;
+  prm.adt = a->adt; prm.gamma = a->gamma; prm.scale = a->scale; prm.phi = a->phi;
+  prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
+  prm.cstates = a->chunk_states; prm.dfs = a->dfinal_ssm; prm.dfv = a->dfinal_v;
+  prm.dq = a->dq; prm.dk = a->dk;
+  prm.dv = a->dv.ptr; prm.dv_sb = a->dv.stride_b; prm.dv_sh = a->dv.stride_h; prm.dv_st = a->dv.stride_t;
+  prm.dz = a->has_z ? a->dz.ptr : nullptr;
+  prm.dz_sb = a->dz.stride_b; prm.dz_sh = a->dz.stride_h; prm.dz_st = a->dz.stride_t;
+  prm.dadt = a->dadt; prm.dqk = a->dqk_diag; prm.dscale = a->dscale; prm.uw = a->uw;
+  prm.dphi = a->dphi; prm.dqb = a->dq_bias; prm.dkb = a->dk_bias; prm.kfin = a->k_final;
+  prm.dseed = a->dseed_ssm;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid = B * H;
+#define X(MT, CC, NN, PP)                                              \
+  if (a->dtype == bcode<MT>() && C == CC && N == NN && P == PP)        \
+    return launch_bwd<MT, CC, NN, PP>(prm, grid, s);
+  M3S_BWD_CONFIGS(X)
+#undef X
+  set_error("m3s_bwd: unreachable dispatch");
+  return M3S_ERR_UNSUPPORTED;
+}

@@ -1,0 +1,138 @@
+// Shared device helpers for the gfx950 Mamba-3 SISO kernels.
+//
+// MFMA fragment convention used by every kernel in this library
+// ------------------------------------------------------------
+// All matrix products run on 16x16 output tiles held in the MFMA accumulator layout:
+// lane l owns column (l & 15) and rows 4*(l >> 4) + i, i < 4.
+//
+// Operands are fed as "sub-fragments": a sub-fragment covers a 16-wide slice of the
+// contraction axis K; lane l supplies 4 consecutive K values, k = 4*(l >> 4) + i, for
+// row (A) or column (B) index (l & 15). A 32-wide K block is two sub-fragments
+// (one v_mfma_f32_16x16x32_bf16); a lone 16-wide block is one v_mfma_f32_16x16x16_bf16
+// (or four v_mfma_f32_16x16x4_f32 for f32 operands). The MFMA sums over K slots
+// (lane group, element) and A and B always use the same slot -> k map, so the
+// result is the true product whatever order the hardware assigns to the slots.
+//
+// The payoff: an accumulator tile R[r][c] is *already* a sub-fragment with K = r
+// (as a B operand with N = c, or as an A operand with M = c). A product's output can
+// therefore feed the next product straight from registers -- the within-chunk score
+// matrix never touches LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace m3s {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kPi = 3.14159265358979323846f;
+constexpr float kTwoPi = 6.28318530717958647692f;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---- scalar conversions ---------------------------------------------------------
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// ---- sub-fragment types ---------------------------------------------------------
+template <typename MT> struct Sub;
+template <> struct Sub<bf16> { typedef bf16x4 type; };
+template <> struct Sub<float> { typedef f32x4 type; };
+template <typename MT> using sub_t = typename Sub<MT>::type;
+
+template <typename MT>
+__device__ __forceinline__ sub_t<MT> sub_from_f32(f32x4 v) {
+  sub_t<MT> r;
+  r[0] = (MT)v[0]; r[1] = (MT)v[1]; r[2] = (MT)v[2]; r[3] = (MT)v[3];
+  return r;
+}
+template <typename MT>
+__device__ __forceinline__ f32x4 sub_to_f32(sub_t<MT> v) {
+  f32x4 r;
+  r[0] = (float)v[0]; r[1] = (float)v[1]; r[2] = (float)v[2]; r[3] = (float)v[3];
+  return r;
+}
+
+// ---- MFMA wrappers --------------------------------------------------------------
+// acc += A(16 x 16) * B(16 x 16) over one 16-wide K sub-block.
+__device__ __forceinline__ void mma16(f32x4& acc, bf16x4 a, bf16x4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                   __builtin_bit_cast(s16x4, b), acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma16(f32x4& acc, f32x4 a, f32x4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], acc, 0, 0, 0);
+}
+// acc += A * B over one 32-wide K block given as two sub-fragments each.
+__device__ __forceinline__ void mma32(f32x4& acc, bf16x4 a0, bf16x4 a1, bf16x4 b0, bf16x4 b1) {
+  bf16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+  bf16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma32(f32x4& acc, f32x4 a0, f32x4 a1, f32x4 b0, f32x4 b1) {
+  mma16(acc, a0, b0);
+  mma16(acc, a1, b1);
+}
+
+// ---- sub-fragment loads from LDS ------------------------------------------------
+// Row-contiguous storage: element (r, k) at buf[r * ld + k]. ld and k0 are multiples
+// of 4, so each lane's 4 values are one aligned 8-byte (bf16) / 16-byte (f32) read.
+template <typename MT>
+__device__ __forceinline__ sub_t<MT> ld_sub(const MT* buf, int ld, int r0, int k0) {
+  const int l = lane_id();
+  return *reinterpret_cast<const sub_t<MT>*>(buf + (r0 + (l & 15)) * ld + k0 + 4 * (l >> 4));
+}
+// Same, but only the lane's row index and K offset are returned (for fused scaling).
+__device__ __forceinline__ int sub_row(int r0) { return r0 + (lane_id() & 15); }
+__device__ __forceinline__ int sub_k(int k0) { return k0 + 4 * (lane_id() >> 4); }
+
+// Full product over K (multiple of 16) of two row-contiguous LDS operands:
+// acc += A[rA0 .. rA0+15][0..K) * B[rB0 .. rB0+15][0..K)^T.
+template <typename MT, int K>
+__device__ __forceinline__ void gemm_nt(f32x4& acc, const MT* A, int lda, int rA0,
+                                        const MT* B, int ldb, int rB0) {
+#pragma unroll
+  for (int k0 = 0; k0 + 32 <= K; k0 += 32) {
+    mma32(acc, ld_sub<MT>(A, lda, rA0, k0), ld_sub<MT>(A, lda, rA0, k0 + 16),
+          ld_sub<MT>(B, ldb, rB0, k0), ld_sub<MT>(B, ldb, rB0, k0 + 16));
+  }
+  if constexpr (K % 32 == 16) {
+    mma16(acc, ld_sub<MT>(A, lda, rA0, K - 16), ld_sub<MT>(B, ldb, rB0, K - 16));
+  }
+}
+
+// ---- wave reductions ------------------------------------------------------------
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < W; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// ---- elementwise maths ----------------------------------------------------------
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
+__device__ __forceinline__ float wrap_2pi(float phi) {
+  return phi - kTwoPi * floorf(phi / kTwoPi);
+}
+
+// ---- two adjacent elements as one LDS store ---------------------------------------
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <typename MT> __device__ __forceinline__ void store_pair(MT* dst, float a, float b);
+template <> __device__ __forceinline__ void store_pair<bf16>(bf16* dst, float a, float b) {
+  *reinterpret_cast<bf16x2*>(dst) = bf16x2{(bf16)a, (bf16)b};
+}
+template <> __device__ __forceinline__ void store_pair<float>(float* dst, float a, float b) {
+  *reinterpret_cast<f32x2*>(dst) = f32x2{a, b};
+}
+
+}  // namespace m3s

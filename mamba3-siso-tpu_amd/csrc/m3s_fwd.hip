@@ -1,0 +1,631 @@
+// Chunked forward of the Mamba-3 SISO scan on gfx950 (MI355X).
+//
+// Replaces the reference's `_fwd_kernel` / `siso_forward` (kernel_fwd.py:55-388).
+// Maths per chunk of C tokens, local log2-decay A_t = sum_{s<=t} adt_s * log2(e):
+//
+//   ybar = 2^A (q~ S^T) + tril_strict(q~ khat^T 2^{min(A_i - A_j, 0)}) v + (D + gamma u.w) v
+//   y    = ybar * silu(z)
+//   S   <- 2^{A_last} S + (v 2^{A_last - A})^T khat
+//
+// Design (one workgroup per (b, h), walking the chunks of that sequence in order):
+//  * The carried state S (P x N, f32) lives in MFMA accumulator registers for the
+//    whole sequence; it is never re-read from HBM. Each wave owns a fixed set of its
+//    16x16 tiles.
+//  * Per chunk the raw tiles (q, k, v, z, phi, scalars) are prefetched into registers
+//    one chunk ahead, then bias + rotary + scale are applied on the way into LDS, so
+//    q~/khat exist only as bf16 LDS tiles (no HBM round trip).
+//  * Wave w owns query strip t in [16w, 16w+16): it builds the transposed, masked,
+//    decay-weighted score strip s^T[j][t] with MFMA, keeps it in registers and feeds it
+//    straight into the s.v product (an accumulator tile is already an operand
+//    fragment with its row index as K -- see m3s_common.h), adds the inter-chunk term
+//    2^A (q~ S^T), and stages the result through LDS so the epilogue (diagonal, skip,
+//    gate, stores) runs on contiguous rows with 16-byte global accesses.
+//  * XCD-aware block numbering keeps the H heads of one batch element (which share
+//    q/k) on one XCD's L2.
+#include "m3s_common.h"
+#include "m3s_internal.h"
+
+namespace m3s {
+
+struct FwdParams {
+  int B, L, H, Nr, nc;
+  int has_d, has_z, has_seed, save;
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t v_sb, v_sh, v_st;
+  const void* z;
+  int64_t z_sb, z_sh, z_st;
+  const float* adt;
+  const float* gamma;
+  const float* scale;
+  const float* phi;
+  const float* qb;
+  const float* kb;
+  const float* dsk;
+  const float* seed_ssm;
+  const float* seed_k;
+  const float* seed_v;
+  const float* seed_coef;
+  void* y;
+  int64_t y_sb, y_sh, y_st;
+  float* ybar;
+  void* cstates;
+  float* fssm;
+  float* fk;
+  float* fv;
+};
+
+template <typename MT> struct V16;
+template <> struct V16<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct V16<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+template <typename MT, int C, int N, int P, int NW>
+struct FwdCfg {
+  static constexpr int NT = NW * 64;
+  static constexpr int VEC = V16<MT>::n;          // elements per 16-byte access
+  static constexpr int H2 = N / 2;
+  static constexpr int PAD = 16 / (int)sizeof(MT);
+  static constexpr int LDQ = N + PAD;             // sQ, sK, sS row stride
+  static constexpr int LDT = C + PAD;             // sVT, sKT row stride
+  static constexpr int LDO = P + 4;               // sOut row stride (f32)
+  static constexpr int QKG = H2 / VEC;            // rotary pair groups per row
+  static constexpr int QKT = (C / 2) * QKG;       // q/k tasks: (row pair, pair group)
+  static constexpr int QKR = (QKT + NT - 1) / NT;
+  static constexpr int VG = P / VEC;
+  static constexpr int VT = (C / 2) * VG;         // v / epilogue tasks: (row pair, col group)
+  static constexpr int VR = (VT + NT - 1) / NT;
+  static constexpr int PB = P / 16, NB = N / 16, CB = C / 16;
+  static constexpr int T4 = PB * NB;              // state tiles
+  static constexpr int SPW = (T4 + NW - 1) / NW;  // state tiles per wave
+  static constexpr int E = C >= 64 ? C / 64 : 1;  // scan values per lane of wave 0
+  static constexpr int SZ_Q = C * LDQ * (int)sizeof(MT);
+  static constexpr int SZ_VT = P * LDT * (int)sizeof(MT);
+  static constexpr int SZ_S = P * LDQ * (int)sizeof(MT);
+  static constexpr int SZ_KT = N * LDT * (int)sizeof(MT);
+  static constexpr int SZ_OUT = C * LDO * 4;
+  static constexpr int SZ_U = SZ_KT > SZ_OUT ? SZ_KT : SZ_OUT;
+  static constexpr int SZ_SC = (4 * C + 2 * N) * 4;
+  static constexpr int LDS_BYTES = 2 * SZ_Q + SZ_VT + SZ_S + SZ_U + SZ_SC;
+  static_assert(NW >= CB, "one query strip per wave");
+  static_assert(QKG <= 64 && (QKG & (QKG - 1)) == 0, "row groups must fit a wave");
+  static_assert(C % 32 == 0 && N % 16 == 0 && P % 16 == 0, "tile shape");
+  static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
+};
+
+template <typename MT, int C, int N, int P, int NW>
+__global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
+  using F = FwdCfg<MT, C, N, P, NW>;
+  using vec = typename V16<MT>::type;
+  constexpr int NT = F::NT, VEC = F::VEC, H2 = F::H2;
+  constexpr int LDQ = F::LDQ, LDT = F::LDT, LDO = F::LDO;
+
+  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
+  // Buffer offsets go through an opaque SGPR. Otherwise every access above 64 KiB (the
+  // reach of a ds_read immediate) gets its own address VGPR, and LICM keeps all of them
+  // live across the chunk loop -- enough to spill.
+  auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
+  MT* sQ = reinterpret_cast<MT*>(smem);
+  MT* sK = reinterpret_cast<MT*>(smem + opq(F::SZ_Q));
+  MT* sVT = reinterpret_cast<MT*>(smem + opq(2 * F::SZ_Q));
+  MT* sS = reinterpret_cast<MT*>(smem + opq(2 * F::SZ_Q + F::SZ_VT));
+  unsigned char* uni = smem + opq(2 * F::SZ_Q + F::SZ_VT + F::SZ_S);
+  MT* sKT = reinterpret_cast<MT*>(uni);        // live during the products
+  float* sOut = reinterpret_cast<float*>(uni);  // live during the epilogue
+  float* sA = reinterpret_cast<float*>(smem + opq(2 * F::SZ_Q + F::SZ_VT + F::SZ_S + F::SZ_U));
+  float* sExpA = sA + C;   // 2^{A_t}
+  float* sFac = sExpA + C; // 2^{A_last - A_t}
+  float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
+  float* sQb = sCoef + C;
+  float* sKb = sQb + N;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = wid / p.H, h = wid % p.H;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int L = p.L, Nr = p.Nr, nc = p.nc;
+
+  for (int i = tid; i < N; i += NT) {
+    sQb[i] = p.qb[h * N + i];
+    sKb[i] = p.kb[h * N + i];
+  }
+  const float dsk = p.has_d ? p.dsk[h] : 0.f;
+
+  const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * L * N;
+  const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * L * N;
+  const MT* vg = static_cast<const MT*>(p.v) + b * p.v_sb + h * p.v_sh;
+  const MT* zg = p.has_z ? static_cast<const MT*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
+  MT* yg = static_cast<MT*>(p.y) + b * p.y_sb + h * p.y_sh;
+  const float* adtg = p.adt + bh * L;
+  const float* gamg = p.gamma + bh * L;
+  const float* sclg = p.scale + bh * L;
+  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  MT* csg = p.save ? static_cast<MT*>(p.cstates) + bh * (int64_t)nc * N * P : nullptr;
+
+  // ---- carried state: registers, MFMA layout ------------------------------------
+  f32x4 Sacc[F::SPW];
+#pragma unroll
+  for (int m = 0; m < F::SPW; ++m) {
+    const int s = wave + NW * m;
+    Sacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (s < F::T4 && p.has_seed) {
+      const int pb = s % F::PB, nb = s / F::PB;
+      const int ncol = nb * 16 + (lane & 15);
+      const float coef = p.seed_coef[bh];
+      const float kp = p.seed_k[bh * N + ncol];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int prow = pb * 16 + 4 * (lane >> 4) + i;
+        Sacc[m][i] = p.seed_ssm[(bh * P + prow) * N + ncol] + coef * p.seed_v[bh * P + prow] * kp;
+      }
+    }
+  }
+  auto publish_state = [&](int cidx) {
+    // S (registers) -> sS as the MFMA operand type, and the chunk_states residual.
+#pragma unroll
+    for (int m = 0; m < F::SPW; ++m) {
+      const int s = wave + NW * m;
+      if (s < F::T4) {
+        const int pb = s % F::PB, nb = s / F::PB;
+        const int ncol = nb * 16 + (lane & 15);
+        const int prow0 = pb * 16 + 4 * (lane >> 4);
+        sub_t<MT> sv = sub_from_f32<MT>(Sacc[m]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sS[(prow0 + i) * LDQ + ncol] = sv[i];
+        if (csg && cidx < nc)
+          *reinterpret_cast<sub_t<MT>*>(csg + ((int64_t)cidx * N + ncol) * P + prow0) = sv;
+      }
+    }
+  };
+  publish_state(0);
+
+  // ---- register prefetch of one chunk's raw inputs --------------------------------
+  vec rq[F::QKR][2][2], rk[F::QKR][2][2];
+  f32x4 rphi[F::QKR][2][VEC / 4];
+  float rscale[F::QKR][2], rgam[F::QKR][2];
+  vec rv[F::VR][2], rz[F::VR][2];
+  float radt[F::E];
+
+  const bool phi_vec = (Nr % 4) == 0;
+  auto prefetch = [&](int c) {
+    const int t0 = c * C;
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::QKT) {
+        const int tp = task / F::QKG, j0 = (task % F::QKG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int64_t t = t0 + 2 * tp + e;
+          rq[r][e][0] = *reinterpret_cast<const vec*>(qg + t * N + j0);
+          rq[r][e][1] = *reinterpret_cast<const vec*>(qg + t * N + H2 + j0);
+          rk[r][e][0] = *reinterpret_cast<const vec*>(kg + t * N + j0);
+          rk[r][e][1] = *reinterpret_cast<const vec*>(kg + t * N + H2 + j0);
+          const float* pr = phig + t * Nr;
+#pragma unroll
+          for (int qd = 0; qd < VEC / 4; ++qd) {
+            const int j = j0 + 4 * qd;
+            if (phi_vec && j + 4 <= Nr) {
+              rphi[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) rphi[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+            }
+          }
+          rscale[r][e] = sclg[t];
+          rgam[r][e] = gamg[t];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int64_t t = t0 + 2 * tp + e;
+          rv[r][e] = *reinterpret_cast<const vec*>(vg + t * p.v_st + p0);
+          if (zg) rz[r][e] = *reinterpret_cast<const vec*>(zg + t * p.z_st + p0);
+        }
+      }
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        radt[e] = tt < C ? adtg[t0 + tt] : 0.f;
+      }
+    }
+  };
+
+  prefetch(0);
+  __syncthreads();  // sQb/sKb, sS
+
+  vec cv[F::VR][2], cz[F::VR][2];
+
+  for (int c = 0; c < nc; ++c) {
+    const int t0 = c * C;
+    const bool last_chunk = (c == nc - 1);
+    // Lane/wave indices re-derived opaquely each chunk, so the per-lane LDS address
+    // arithmetic is recomputed near its uses instead of being hoisted out of the loop.
+    int lane_v = threadIdx.x;
+    asm volatile("" : "+v"(lane_v));
+    const int tid = lane_v, lane = tid & 63;
+    int wave_s = __builtin_amdgcn_readfirstlane(tid >> 6);
+    asm volatile("" : "+s"(wave_s));
+    const int wave = wave_s;
+
+    // ================= phase L: raw registers -> LDS tiles ==========================
+    if (wave == 0) {
+      // inclusive prefix sum of adt*log2(e) over the chunk
+      float a[F::E];
+      float run = 0.f;
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        run += radt[e] * kLog2e;
+        a[e] = run;
+      }
+      float incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      const float excl = incl - run;
+      const float a_last = __shfl(incl, (C - 1) / F::E, 64);
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        if (tt < C) {
+          const float A = excl + a[e];
+          sA[tt] = A;
+          sExpA[tt] = exp2f(A);
+          sFac[tt] = exp2f(a_last - A);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      const bool valid = task < F::QKT;
+      const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
+      float khat[2][2][VEC];
+      float uw[2] = {0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        float qt[2][VEC], kt[2][VEC];
+        if (valid) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const int j = j0 + i;
+            const float ulo = (float)rq[r][e][0][i] + sQb[j];
+            const float uhi = (float)rq[r][e][1][i] + sQb[H2 + j];
+            const float wlo = (float)rk[r][e][0][i] + sKb[j];
+            const float whi = (float)rk[r][e][1][i] + sKb[H2 + j];
+            uw[e] += ulo * wlo + uhi * whi;
+            float sn = 0.f, cs = 1.f;
+            if (j < Nr) sincosf(rphi[r][e][i / 4][i % 4], &sn, &cs);
+            qt[0][i] = ulo * cs - uhi * sn;
+            qt[1][i] = uhi * cs + ulo * sn;
+            kt[0][i] = wlo * cs - whi * sn;
+            kt[1][i] = whi * cs + wlo * sn;
+          }
+          const int t = 2 * tp + e;
+          vec oq0, oq1, ok0, ok1;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            khat[e][0][i] = kt[0][i] * rscale[r][e];
+            khat[e][1][i] = kt[1][i] * rscale[r][e];
+            oq0[i] = (MT)qt[0][i];
+            oq1[i] = (MT)qt[1][i];
+            ok0[i] = (MT)khat[e][0][i];
+            ok1[i] = (MT)khat[e][1][i];
+          }
+          *reinterpret_cast<vec*>(sQ + t * LDQ + j0) = oq0;
+          *reinterpret_cast<vec*>(sQ + t * LDQ + H2 + j0) = oq1;
+          *reinterpret_cast<vec*>(sK + t * LDQ + j0) = ok0;
+          *reinterpret_cast<vec*>(sK + t * LDQ + H2 + j0) = ok1;
+          if (last_chunk && t == C - 1) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              p.fk[bh * N + j0 + i] = kt[0][i];
+              p.fk[bh * N + H2 + j0 + i] = kt[1][i];
+            }
+          }
+        }
+      }
+      // u.w per row: reduce over the QKG lanes that share the row pair
+      uw[0] = group_sum<F::QKG>(uw[0]);
+      uw[1] = group_sum<F::QKG>(uw[1]);
+      if (valid) {
+        if (j0 == 0) {
+          sCoef[2 * tp] = rgam[r][0] * uw[0] + dsk;
+          sCoef[2 * tp + 1] = rgam[r][1] * uw[1] + dsk;
+        }
+        // khat^T for the state update: pack rows (2tp, 2tp+1) into one store
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const int n = hh * H2 + j0 + i;
+            store_pair<MT>(sKT + n * LDT + 2 * tp, khat[0][hh][i], khat[1][hh][i]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
+        cv[r][0] = rv[r][0];
+        cv[r][1] = rv[r][1];
+        if (zg) {
+          cz[r][0] = rz[r][0];
+          cz[r][1] = rz[r][1];
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          store_pair<MT>(sVT + (p0 + i) * LDT + 2 * tp, (float)rv[r][0][i], (float)rv[r][1][i]);
+        }
+        if (last_chunk && 2 * tp + 1 == C - 1) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) p.fv[bh * P + p0 + i] = (float)rv[r][1][i];
+        }
+      }
+    }
+    __syncthreads();
+
+    if (c + 1 < nc) prefetch(c + 1);
+
+    // ================= phase G: products ============================================
+    f32x4 out[F::PB];
+#pragma unroll
+    for (int pb = 0; pb < F::PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int tb = wave;
+    const int tcol = tb * 16 + (lane & 15);
+    if (tb < F::CB) {
+      const float At = sA[tcol];
+      sub_t<MT> sT[F::CB];
+#pragma unroll
+      for (int jb = 0; jb < F::CB; ++jb) {
+        if (jb <= tb) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          gemm_nt<MT, N>(acc, sK, LDQ, jb * 16, sQ, LDQ, tb * 16);
+          f32x4 sv;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = jb * 16 + 4 * (lane >> 4) + i;
+            sv[i] = (tcol > j) ? acc[i] * exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+          }
+          sT[jb] = sub_from_f32<MT>(sv);
+        } else {
+          sT[jb] = sub_from_f32<MT>(f32x4{0.f, 0.f, 0.f, 0.f});
+        }
+      }
+      // intra-chunk: out^T[p][t] += sum_j v^T[p][j] s^T[j][t]
+#pragma unroll
+      for (int jb = 0; jb < F::CB; jb += 2) {
+        if (jb <= tb) {
+#pragma unroll
+          for (int pb = 0; pb < F::PB; ++pb) {
+            if (jb + 1 <= tb) {
+              mma32(out[pb], ld_sub<MT>(sVT, LDT, pb * 16, jb * 16),
+                    ld_sub<MT>(sVT, LDT, pb * 16, jb * 16 + 16), sT[jb], sT[jb + 1]);
+            } else {
+              mma16(out[pb], ld_sub<MT>(sVT, LDT, pb * 16, jb * 16), sT[jb]);
+            }
+          }
+        }
+      }
+      // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
+      const float eA = sExpA[tcol];
+#pragma unroll
+      for (int pb = 0; pb < F::PB; ++pb) {
+        f32x4 it = {0.f, 0.f, 0.f, 0.f};
+        gemm_nt<MT, N>(it, sS, LDQ, pb * 16, sQ, LDQ, tb * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[pb][i] += eA * it[i];
+      }
+    }
+    // state: S <- 2^{A_last} S + sum_t (v_t 2^{A_last - A_t}) khat_t^T
+    {
+      const float eAl = sExpA[C - 1];
+#pragma unroll
+      for (int m = 0; m < F::SPW; ++m) {
+        const int s = wave + NW * m;
+        if (s < F::T4) {
+          const int pb = s % F::PB, nb = s / F::PB;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Sacc[m][i] *= eAl;
+#pragma unroll
+          for (int k0 = 0; k0 < C; k0 += 32) {
+            sub_t<MT> a0, a1;
+            {
+              f32x4 v0 = sub_to_f32<MT>(ld_sub<MT>(sVT, LDT, pb * 16, k0));
+              f32x4 v1 = sub_to_f32<MT>(ld_sub<MT>(sVT, LDT, pb * 16, k0 + 16));
+              const int kk = sub_k(k0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                v0[i] *= sFac[kk + i];
+                v1[i] *= sFac[kk + 16 + i];
+              }
+              a0 = sub_from_f32<MT>(v0);
+              a1 = sub_from_f32<MT>(v1);
+            }
+            mma32(Sacc[m], a0, a1, ld_sub<MT>(sKT, LDT, nb * 16, k0),
+                  ld_sub<MT>(sKT, LDT, nb * 16, k0 + 16));
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ================= phase W: out^T -> sOut, new S -> sS ===========================
+    if (tb < F::CB) {
+#pragma unroll
+      for (int pb = 0; pb < F::PB; ++pb)
+        *reinterpret_cast<f32x4*>(sOut + tcol * LDO + pb * 16 + 4 * (lane >> 4)) = out[pb];
+    }
+    publish_state(c + 1);
+    __syncthreads();
+
+    // ================= phase E: diagonal + skip + gate, stores ======================
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          const float coef = sCoef[t];
+          float yb[VEC];
+#pragma unroll
+          for (int i = 0; i < VEC; i += 4) {
+            const f32x4 o = *reinterpret_cast<const f32x4*>(sOut + t * LDO + p0 + i);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) yb[i + u] = o[u] + coef * (float)cv[r][e][i + u];
+          }
+          if (p.save) {
+            float* dst = p.ybar + (bh * L + t0 + t) * (int64_t)P + p0;
+#pragma unroll
+            for (int i = 0; i < VEC; i += 4)
+              *reinterpret_cast<f32x4*>(dst + i) = f32x4{yb[i], yb[i + 1], yb[i + 2], yb[i + 3]};
+          }
+          vec yo;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const float g = zg ? silu((float)cz[r][e][i]) : 1.f;
+            yo[i] = (MT)(yb[i] * g);
+          }
+          *reinterpret_cast<vec*>(yg + (int64_t)(t0 + t) * p.y_st + p0) = yo;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // final state
+#pragma unroll
+  for (int m = 0; m < F::SPW; ++m) {
+    const int s = wave + NW * m;
+    if (s < F::T4) {
+      const int pb = s % F::PB, nb = s / F::PB;
+      const int ncol = nb * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int prow = pb * 16 + 4 * (lane >> 4) + i;
+        p.fssm[(bh * P + prow) * N + ncol] = Sacc[m][i];
+      }
+    }
+  }
+}
+
+// ---- dispatch ---------------------------------------------------------------------
+
+template <typename MT, int C, int N, int P>
+static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
+  constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
+  hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  return launch_status("m3s_fwd");
+}
+
+// The (dtype, chunk, N, P) instantiations compiled into the library.
+// The (dtype, chunk, N, P) instantiations compiled into the library. Every backward
+// configuration (m3s_bwd.hip) is also a forward one.
+#define M3S_FWD_CONFIGS(X)  \
+  X(bf16, 128, 128, 64)     \
+  X(bf16, 64, 128, 64)      \
+  X(bf16, 32, 128, 64)      \
+  X(bf16, 64, 64, 64)       \
+  X(bf16, 64, 32, 16)       \
+  X(bf16, 32, 32, 16)       \
+  X(bf16, 64, 16, 16)       \
+  X(bf16, 32, 16, 16)       \
+  X(float, 64, 128, 64)     \
+  X(float, 32, 128, 64)     \
+  X(float, 64, 64, 64)      \
+  X(float, 64, 32, 16)      \
+  X(float, 32, 32, 16)      \
+  X(float, 64, 16, 16)      \
+  X(float, 32, 16, 16)
+
+template <typename MT> constexpr int dtype_code();
+template <> constexpr int dtype_code<bf16>() { return M3S_DTYPE_BF16; }
+template <> constexpr int dtype_code<float>() { return M3S_DTYPE_F32; }
+
+int32_t fwd_supported(int dtype, int chunk, int n, int pdim) {
+#define X(MT, C, N, P) \
+  if (dtype == dtype_code<MT>() && chunk == C && n == N && pdim == P) return 1;
+  M3S_FWD_CONFIGS(X)
+#undef X
+  return 0;
+}
+
+}  // namespace m3s
+
+extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
+  using namespace m3s;
+  clear_error();
+  M3S_REQUIRE(a != nullptr, "m3s_fwd: args is NULL");
+  M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_fwd_args),
+              "m3s_fwd: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              (int)sizeof(m3s_fwd_args));
+  const int B = a->batch, L = a->seqlen, H = a->nheads, P = a->headdim, N = a->state_dim,
+            Nr = a->n_angles, C = a->chunk;
+  M3S_REQUIRE(B > 0 && L > 0 && H > 0 && P > 0 && N > 0 && C > 0,
+              "m3s_fwd: non-positive dimension");
+  M3S_REQUIRE(L % C == 0, "m3s_fwd: seqlen %d is not a multiple of chunk %d", L, C);
+  M3S_REQUIRE(Nr >= 0 && 2 * Nr <= N, "m3s_fwd: n_angles %d exceeds state_dim/2", Nr);
+  M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32, "m3s_fwd: bad dtype %d",
+              a->dtype);
+  if (!fwd_supported(a->dtype, C, N, P)) {
+    set_error("m3s_fwd: no kernel for dtype=%s chunk=%d state_dim=%d headdim=%d",
+              a->dtype == M3S_DTYPE_BF16 ? "bf16" : "f32", C, N, P);
+    return M3S_ERR_UNSUPPORTED;
+  }
+  const int vec = a->dtype == M3S_DTYPE_BF16 ? 8 : 4;
+  M3S_REQUIRE(a->q && a->k && aligned16(a->q) && aligned16(a->k), "m3s_fwd: q/k null or misaligned");
+  M3S_REQUIRE(bhlp_ok(a->v, vec), "m3s_fwd: v null, misaligned or strides not multiples of %d", vec);
+  M3S_REQUIRE(!a->has_z || bhlp_ok(a->z, vec), "m3s_fwd: z null, misaligned or bad strides");
+  M3S_REQUIRE(bhlp_ok(a->y, vec), "m3s_fwd: y null, misaligned or bad strides");
+  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->phi && a->q_bias && a->k_bias,
+              "m3s_fwd: a required input pointer is NULL");
+  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 || aligned16(a->phi), "m3s_fwd: phi misaligned");
+  M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_fwd: has_d but d_skip is NULL");
+  M3S_REQUIRE(!a->has_seed || (a->seed_ssm && a->seed_k && a->seed_v && a->seed_coef),
+              "m3s_fwd: seed_ssm, seed_k, seed_v and seed_coef must be given together");
+  M3S_REQUIRE(!a->save_residuals || (a->ybar && a->chunk_states && aligned16(a->ybar) &&
+                                     aligned16(a->chunk_states)),
+              "m3s_fwd: residual outputs NULL or misaligned");
+  M3S_REQUIRE(a->final_ssm && a->final_k && a->final_v, "m3s_fwd: final state outputs NULL");
+  M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_fwd: B*H too large");
+
+  FwdParams prm{};
+  prm.B = B; prm.L = L; prm.H = H; prm.Nr = Nr; prm.nc = L / C;
+  prm.has_d = a->has_d; prm.has_z = a->has_z; prm.has_seed = a->has_seed;
+  prm.save = a->save_residuals;
+  prm.q = a->q; prm.k = a->k;
+  prm.v = a->v.ptr; prm.v_sb = a->v.stride_b; prm.v_sh = a->v.stride_h; prm.v_st = a->v.stride_t;
+  prm.z = a->has_z ? a->z.ptr : nullptr;
+  prm.z_sb = a->z.stride_b; prm.z_sh = a->z.stride_h; prm.z_st = a->z.stride_t;
+  prm.adt = a->adt; prm.gamma = a->gamma; prm.scale = a->scale; prm.phi = a->phi;
+  prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
+  prm.seed_ssm = a->seed_ssm; prm.seed_k = a->seed_k; prm.seed_v = a->seed_v;
+  prm.seed_coef = a->seed_coef;
+  prm.y = a->y.ptr; prm.y_sb = a->y.stride_b; prm.y_sh = a->y.stride_h; prm.y_st = a->y.stride_t;
+  prm.ybar = a->ybar; prm.cstates = a->chunk_states;
+  prm.fssm = a->final_ssm; prm.fk = a->final_k; prm.fv = a->final_v;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int grid = B * H;
+#define X(MT, CC, NN, PP)                                                     \
+  if (a->dtype == dtype_code<MT>() && C == CC && N == NN && P == PP)          \
+    return launch_fwd<MT, CC, NN, PP>(prm, grid, s);
+  M3S_FWD_CONFIGS(X)
+#undef X
+  set_error("m3s_fwd: unreachable dispatch");
+  return M3S_ERR_UNSUPPORTED;
+}

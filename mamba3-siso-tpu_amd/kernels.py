@@ -1,0 +1,451 @@
+"""Python entry points over the HIP kernels, with the reference's kernel signatures.
+
+* `siso_forward`   -- ``kernel_fwd.siso_forward``   (kernel_fwd.py:204-388)
+* `siso_backward_kernel` / `siso_backward` -- ``kernel_bwd.py:358-669``
+* `siso_decode`, `siso_decode_folded`, `decode_step`, `decode_scan`, `decode_loop`
+  -- ``kernel_decode.py:252-573``
+
+Each validates shapes with the reference's ``ValueError`` conditions, then calls the
+C ABI (``include/m3s.h``) on the current torch stream. Nothing here computes on the
+CPU: every tensor must already be on the ROCm device, and a missing library raises.
+``interpret`` and ``device_kind`` are accepted for signature compatibility and ignored.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Any, NamedTuple, Optional
+
+import torch
+
+from . import _lib
+from . import layout as LY
+
+Tensor = torch.Tensor
+
+
+class ForwardResiduals(NamedTuple):
+    """``kernel_fwd.py:41-52``. ``chunk_states`` is the logical ``(B, H, nc, P, N)``
+    view of an N-major ``(B, H, nc, N, P)`` buffer (the layout the backward reads)."""
+
+    ybar: Tensor
+    chunk_states: Tensor
+
+
+def _device_of(*ts) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(
+                "the Mamba-3 SISO kernels run on the ROCm device only; got a CPU tensor "
+                "(move inputs to 'cuda' -- there is no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _f32c(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.to(torch.float32).contiguous()
+
+
+def _mt(t: Optional[Tensor], mt: torch.dtype) -> Optional[Tensor]:
+    return None if t is None else t.to(mt).contiguous()
+
+
+def _bhlp_operand(t: Optional[Tensor], mt: torch.dtype) -> Optional[Tensor]:
+    """Keep a strided (B, H, L, P) view if the kernel can read it in place."""
+    if t is None:
+        return None
+    if t.dtype != mt:
+        t = t.to(mt)
+    vec = 16 // t.element_size()
+    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+          and all(t.stride(i) % vec == 0 for i in range(3)))
+    return t if ok else t.contiguous()
+
+
+def siso_forward(
+    q: Tensor, k: Tensor, v: Tensor, adt: Tensor, gamma: Tensor, scale: Tensor,
+    phi: Tensor, q_bias: Tensor, k_bias: Tensor, d_skip: Optional[Tensor] = None,
+    z: Optional[Tensor] = None, seed_ssm: Optional[Tensor] = None,
+    seed_k: Optional[Tensor] = None, seed_v: Optional[Tensor] = None,
+    seed_coef: Optional[Tensor] = None, chunk: int = 128,
+    dtype_policy: LY.DtypePolicy | str = LY.BF16, save_residuals: bool = False,
+    interpret: Any = False, device_kind: str | None = None, *, y_out: Optional[Tensor] = None,
+):
+    """Chunked forward (``kernel_fwd.py:204-248``).
+
+    Returns ``(y, final_ssm, final_k, final_v)`` and, with ``save_residuals``, a
+    `ForwardResiduals`. ``y_out`` (keyword-only) is an optional preallocated
+    ``(B, H, L, P)`` view to write ``y`` into (e.g. a ``(B, L, H*P)`` buffer viewed as
+    ``(B, H, L, P)``), saving a transpose.
+    """
+    pol = LY.policy(dtype_policy)
+    LY.validate_chunk(chunk)
+    batch, seqlen, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[3]
+    n_angles = phi.shape[-1]
+    nc = LY.num_chunks(seqlen, chunk)
+    if q.shape != k.shape:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} must match")
+    if tuple(v.shape) != (batch, nheads, seqlen, headdim):
+        raise ValueError(f"unexpected v shape {tuple(v.shape)}")
+    for name, t in (("adt", adt), ("gamma", gamma), ("scale", scale)):
+        if tuple(t.shape) != (batch, nheads, seqlen):
+            raise ValueError(
+                f"{name} must be (B, H, L) = {(batch, nheads, seqlen)}, got {tuple(t.shape)}")
+    seeds = (seed_ssm, seed_k, seed_v, seed_coef)
+    has_seed = any(s is not None for s in seeds)
+    if has_seed and not all(s is not None for s in seeds):
+        raise ValueError("seed_ssm, seed_k, seed_v and seed_coef must be given together")
+    if tuple(phi.shape) != (batch, nheads, seqlen, n_angles):
+        raise ValueError(
+            f"phi must be (B, H, L, Nr) = {(batch, nheads, seqlen, n_angles)}, got {tuple(phi.shape)}")
+    if z is not None and tuple(z.shape) != tuple(v.shape):
+        raise ValueError(f"z shape {tuple(z.shape)} must match v {tuple(v.shape)}")
+    dev = _device_of(q, k, v, adt, gamma, scale, phi, q_bias, k_bias, d_skip, z, *seeds)
+    mt = pol.matmul
+    dcode = _lib.dtype_code(mt)
+    if not _lib.supported(0, dcode, chunk, state_dim, headdim):
+        raise ValueError(
+            f"no forward kernel for policy={pol.name} chunk={chunk} d_state={state_dim} "
+            f"headdim={headdim} (see layout.SUPPORTED_CHUNKS and the library's config table)")
+
+    qc, kc = _mt(q, mt), _mt(k, mt)
+    vc, zc = _bhlp_operand(v, mt), _bhlp_operand(z, mt)
+    adt_c, gam_c, scl_c, phi_c = _f32c(adt), _f32c(gamma), _f32c(scale), _f32c(phi)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    s_ssm, s_k, s_v, s_c = (_f32c(s) for s in seeds)
+
+    y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
+    if y_out is not None:
+        if tuple(y_out.shape) != (batch, nheads, seqlen, headdim) or y_out.dtype != mt:
+            raise ValueError("y_out must be a (B, H, L, P) tensor of the policy dtype")
+        y = _bhlp_operand(y_out, mt)
+        if y is not y_out:
+            raise ValueError("y_out must be 16-byte aligned with P contiguous")
+    else:
+        y = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
+    f32 = dict(device=dev, dtype=torch.float32)
+    final_ssm = torch.empty(batch, nheads, headdim, state_dim, **f32)
+    final_k = torch.empty(batch, nheads, state_dim, **f32)
+    final_v = torch.empty(batch, nheads, headdim, **f32)
+    if save_residuals:
+        ybar = torch.empty(batch, nheads, seqlen, headdim, **f32)
+        cstates = torch.empty(batch, nheads, nc, state_dim, headdim, device=dev, dtype=mt)
+    else:
+        ybar = cstates = None
+
+    a = _lib.FwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.FwdArgs)
+    a.batch, a.seqlen, a.nheads, a.headdim = batch, seqlen, nheads, headdim
+    a.state_dim, a.n_angles, a.chunk = state_dim, n_angles, chunk
+    a.dtype = dcode
+    a.has_d, a.has_z, a.has_seed = int(d_c is not None), int(zc is not None), int(has_seed)
+    a.save_residuals = int(save_residuals)
+    a.q, a.k = qc.data_ptr(), kc.data_ptr()
+    a.v, a.z = _lib.bhlp(vc), _lib.bhlp(zc)
+    a.adt, a.gamma, a.scale, a.phi = (t.data_ptr() for t in (adt_c, gam_c, scl_c, phi_c))
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.seed_ssm, a.seed_k, a.seed_v, a.seed_coef = (_lib.ptr(s) for s in (s_ssm, s_k, s_v, s_c))
+    a.y = _lib.bhlp(y)
+    a.ybar, a.chunk_states = _lib.ptr(ybar), _lib.ptr(cstates)
+    a.final_ssm, a.final_k, a.final_v = final_ssm.data_ptr(), final_k.data_ptr(), final_v.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_fwd")
+
+    if y_out is None and y.dtype != y_dtype:
+        y = y.to(y_dtype)
+    outs = (y, final_ssm, final_k, final_v)
+    if save_residuals:
+        return outs + (ForwardResiduals(ybar=ybar, chunk_states=cstates.transpose(-1, -2)),)
+    return outs
+
+
+# ======================================================================================
+# Decode (kernel_decode.py:252-573)
+# ======================================================================================
+
+
+def _state_buf(t: Tensor, shape, dev) -> Tensor:
+    """The decode kernel updates the carried state in place; reuse the caller's buffer
+    when it already is f32, contiguous and on the device (the donation of
+    ``kernel_decode.py:350-352``), else work on a converted copy."""
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"state tensor has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if t.dtype == torch.float32 and t.is_contiguous() and t.device == dev:
+        return t
+    return t.to(device=dev, dtype=torch.float32).contiguous()
+
+
+def siso_decode(q: Tensor, k: Tensor, v: Tensor, adt: Tensor, dt: Tensor, lam: Tensor,
+                angles: Tensor, q_bias: Tensor, k_bias: Tensor, state,
+                d_skip: Optional[Tensor] = None, z: Optional[Tensor] = None,
+                dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False):
+    """One decode step (``kernel_decode.py:252-360``).
+
+    q, k ``(B, N)``; v, z ``(B, H, P)``; adt, dt, lam ``(B, H)``; angles ``(B, Nr)`` raw
+    (pre-tanh). Returns ``(y (B, H, P), next_state)``. The state's four buffers are
+    updated **in place** and returned (the reference donates them): the input state is
+    consumed.
+    """
+    from .preprocess import SISOState
+
+    pol = LY.policy(dtype_policy)
+    batch, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[2]
+    n_angles = angles.shape[-1]
+    if tuple(k.shape) != (batch, state_dim):
+        raise ValueError(f"k shape {tuple(k.shape)} must match q {tuple(q.shape)}")
+    for name, t in (("adt", adt), ("dt", dt), ("lam", lam)):
+        if tuple(t.shape) != (batch, nheads):
+            raise ValueError(f"{name} must be (B, H) = {(batch, nheads)}, got {tuple(t.shape)}")
+    if z is not None and tuple(z.shape) != tuple(v.shape):
+        raise ValueError("z must match v")
+    dev = _device_of(q, k, v, adt, dt, lam, angles, q_bias, k_bias, d_skip, z, *state)
+    mt = pol.matmul
+    dcode = _lib.dtype_code(mt)
+    if not _lib.supported(2, dcode, 0, state_dim, headdim):
+        raise ValueError(f"no decode kernel for policy={pol.name} d_state={state_dim} headdim={headdim}")
+    ssm = _state_buf(state.ssm, (batch, nheads, headdim, state_dim), dev)
+    kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
+    vst = _state_buf(state.v, (batch, nheads, headdim), dev)
+    phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
+    qc, kc, vc, zc = _mt(q, mt), _mt(k, mt), _mt(v, mt), _mt(z, mt)
+    adt_c, dt_c, lam_c, ang_c = _f32c(adt), _f32c(dt), _f32c(lam), _f32c(angles)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    y = torch.empty(batch, nheads, headdim, device=dev, dtype=mt)
+
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
+    a.batch, a.nheads, a.headdim, a.state_dim, a.n_angles = batch, nheads, headdim, state_dim, n_angles
+    a.dtype = dcode
+    a.has_d, a.has_z = int(d_c is not None), int(zc is not None)
+    a.q, a.k, a.v, a.z = qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), _lib.ptr(zc)
+    a.adt, a.dt, a.lam, a.angles = adt_c.data_ptr(), dt_c.data_ptr(), lam_c.data_ptr(), ang_c.data_ptr()
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.ssm, a.k_state, a.v_state, a.phi_state = (t.data_ptr() for t in (ssm, kst, vst, phist))
+    a.y = y.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_decode(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_decode")
+    y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
+    if y.dtype != y_dtype:
+        y = y.to(y_dtype)
+    return y, SISOState(ssm=ssm, k=kst, v=vst, phi=phist)
+
+
+def siso_decode_folded(*args, **kw):
+    """``kernel_decode.py:363-464``. Same kernel as `siso_decode`: on MI355X one
+    workgroup per (b, h) state serves both of the reference's grids."""
+    return siso_decode(*args, **kw)
+
+
+def decode_step(*args, folded: bool = True, **kw):
+    """``kernel_decode.py:467-471``."""
+    return siso_decode(*args, **kw)
+
+
+def decode_loop(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip=None, z=None,
+                dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
+                folded: bool = False):
+    """``kernel_decode.py:536-573``: ``L`` decode steps in a Python loop; inputs have a
+    time axis (q, k ``(B, L, N)``; v, z ``(B, H, L, P)``; adt/dt/lam ``(B, H, L)``;
+    angles ``(B, L, Nr)``). Returns ``(y (B, H, L, P), state)``."""
+    outs = []
+    for t in range(q.shape[1]):
+        y, state = decode_step(
+            q[:, t], k[:, t], v[:, :, t], adt[:, :, t], dt[:, :, t], lam[:, :, t], angles[:, t],
+            q_bias, k_bias, state, d_skip=d_skip, z=None if z is None else z[:, :, t],
+            dtype_policy=dtype_policy)
+        outs.append(y)
+    return torch.stack(outs, dim=2), state
+
+
+def decode_scan(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip=None, z=None,
+                dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
+                folded: bool = True):
+    """``kernel_decode.py:474-533``: a known-length run of decode steps. The reference
+    uses one ``lax.scan``; here the steps are stream-ordered kernel launches with no
+    host synchronisation between them, which is the same device-only floor."""
+    return decode_loop(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip, z,
+                       dtype_policy=dtype_policy)
+
+
+# ======================================================================================
+# Backward (kernel_bwd.py:358-669)
+# ======================================================================================
+
+
+class KernelGrads(NamedTuple):
+    """``kernel_bwd.py:63-100``. ``dq``/``dk`` are summed over heads (``(B, L, N)``,
+    f32); ``dv``/``dz`` come back in the dtype policy's operand type (f32 or bf16);
+    ``dq_bias``/``dk_bias`` are already reduced over batch and time."""
+
+    dq: Tensor
+    dk: Tensor
+    dv: Tensor
+    dadt: Tensor
+    dqk_diag: Tensor
+    dscale: Tensor
+    dphi: Tensor
+    dz: Optional[Tensor]
+    uw: Tensor
+    dq_bias: Tensor
+    dk_bias: Tensor
+    k_final: Tensor
+    dseed_ssm: Tensor
+
+
+def _nmajor_states(chunk_states: Tensor, mt: torch.dtype) -> Tensor:
+    """The kernel reads chunk states N-major, ``(B, H, nc, N, P)`` contiguous. The
+    forward's residual is a transposed view of exactly that; anything else is copied."""
+    t = chunk_states.transpose(-1, -2)
+    if t.dtype != mt:
+        t = t.to(mt)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def siso_backward_kernel(
+    dy: Tensor, ybar: Tensor, z: Optional[Tensor], q: Tensor, k: Tensor, v: Tensor,
+    adt: Tensor, gamma: Tensor, scale: Tensor, phi: Tensor, q_bias: Tensor, k_bias: Tensor,
+    chunk_states: Tensor, d_skip: Optional[Tensor] = None,
+    dfinal_ssm: Optional[Tensor] = None, chunk: int = 128,
+    dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
+    device_kind: str | None = None, *, dfinal_v: Optional[Tensor] = None,
+) -> KernelGrads:
+    """Reverse chunk scan (``kernel_bwd.py:358-395``). ``dfinal_v`` (keyword-only) is
+    added to ``dv``'s last row inside the kernel, before the cast to the operand type
+    (the reference does it in its epilogue, ``kernel_bwd.py:632-637``)."""
+    pol = LY.policy(dtype_policy)
+    LY.validate_chunk(chunk)
+    batch, seqlen, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[3]
+    n_angles = phi.shape[-1]
+    nc = LY.num_chunks(seqlen, chunk)
+    if tuple(dy.shape) != tuple(v.shape) or tuple(ybar.shape) != tuple(v.shape):
+        raise ValueError("dy and ybar must be (B, H, L, P) like v")
+    if tuple(chunk_states.shape) != (batch, nheads, nc, headdim, state_dim):
+        raise ValueError(f"chunk_states must be (B, H, nc, P, N) = "
+                         f"{(batch, nheads, nc, headdim, state_dim)}, got {tuple(chunk_states.shape)}")
+    dev = _device_of(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias,
+                     chunk_states, d_skip, dfinal_ssm, dfinal_v)
+    mt = pol.matmul
+    dcode = _lib.dtype_code(mt)
+    if not _lib.supported(1, dcode, chunk, state_dim, headdim):
+        raise ValueError(
+            f"no backward kernel for policy={pol.name} chunk={chunk} d_state={state_dim} "
+            f"headdim={headdim}")
+    dyc, zc, vc = _bhlp_operand(dy, mt), _bhlp_operand(z, mt), _bhlp_operand(v, mt)
+    qc, kc = _mt(q, mt), _mt(k, mt)
+    ybc = _f32c(ybar)
+    adt_c, gam_c, scl_c, phi_c = _f32c(adt), _f32c(gamma), _f32c(scale), _f32c(phi)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    cs = _nmajor_states(chunk_states, mt)
+    dfs, dfv = _f32c(dfinal_ssm), _f32c(dfinal_v)
+
+    f32 = dict(device=dev, dtype=torch.float32)
+    dq = torch.empty(batch, seqlen, state_dim, **f32)
+    dk = torch.empty(batch, seqlen, state_dim, **f32)
+    dv = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
+    dz = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt) if zc is not None else None
+    dadt = torch.empty(batch, nheads, seqlen, **f32)
+    dqk = torch.empty(batch, nheads, seqlen, **f32)
+    dscale = torch.empty(batch, nheads, seqlen, **f32)
+    uw = torch.empty(batch, nheads, seqlen, **f32)
+    dphi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
+    dqb = torch.empty(batch, nheads, state_dim, **f32)
+    dkb = torch.empty(batch, nheads, state_dim, **f32)
+    kfin = torch.empty(batch, nheads, state_dim, **f32)
+    dseed = torch.empty(batch, nheads, headdim, state_dim, **f32)
+
+    a = _lib.BwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.BwdArgs)
+    a.batch, a.seqlen, a.nheads, a.headdim = batch, seqlen, nheads, headdim
+    a.state_dim, a.n_angles, a.chunk = state_dim, n_angles, chunk
+    a.dtype = dcode
+    a.has_d, a.has_z = int(d_c is not None), int(zc is not None)
+    a.dy, a.ybar, a.z = _lib.bhlp(dyc), ybc.data_ptr(), _lib.bhlp(zc)
+    a.q, a.k, a.v = qc.data_ptr(), kc.data_ptr(), _lib.bhlp(vc)
+    a.adt, a.gamma, a.scale, a.phi = (t.data_ptr() for t in (adt_c, gam_c, scl_c, phi_c))
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.chunk_states, a.dfinal_ssm, a.dfinal_v = cs.data_ptr(), _lib.ptr(dfs), _lib.ptr(dfv)
+    a.dq, a.dk, a.dv, a.dz = dq.data_ptr(), dk.data_ptr(), _lib.bhlp(dv), _lib.bhlp(dz)
+    a.dadt, a.dqk_diag, a.dscale, a.uw = (t.data_ptr() for t in (dadt, dqk, dscale, uw))
+    a.dphi, a.dq_bias, a.dk_bias = dphi.data_ptr(), dqb.data_ptr(), dkb.data_ptr()
+    a.k_final, a.dseed_ssm = kfin.data_ptr(), dseed.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_bwd")
+    return KernelGrads(dq=dq, dk=dk, dv=dv, dadt=dadt, dqk_diag=dqk, dscale=dscale, dphi=dphi,
+                       dz=dz, uw=uw, dq_bias=dqb.sum(0), dk_bias=dkb.sum(0), k_final=kfin,
+                       dseed_ssm=dseed)
+
+
+class SISOGrads(NamedTuple):
+    """``kernel_bwd.py:514-531``: gradients w.r.t. everything `siso_forward` takes."""
+
+    dq: Tensor
+    dk: Tensor
+    dv: Tensor
+    dadt: Tensor
+    dgamma: Tensor
+    dscale: Tensor
+    dphi: Tensor
+    dq_bias: Tensor
+    dk_bias: Tensor
+    dd_skip: Optional[Tensor]
+    dz: Optional[Tensor]
+    dseed_ssm: Optional[Tensor]
+    dseed_k: Optional[Tensor]
+    dseed_v: Optional[Tensor]
+    dseed_coef: Optional[Tensor]
+
+
+def siso_backward(
+    dy: Tensor, q: Tensor, k: Tensor, v: Tensor, adt: Tensor, gamma: Tensor, scale: Tensor,
+    phi: Tensor, q_bias: Tensor, k_bias: Tensor, ybar: Tensor, chunk_states: Tensor,
+    d_skip: Optional[Tensor] = None, z: Optional[Tensor] = None,
+    seed_ssm: Optional[Tensor] = None, seed_k: Optional[Tensor] = None,
+    seed_v: Optional[Tensor] = None, seed_coef: Optional[Tensor] = None,
+    dfinal_ssm: Optional[Tensor] = None, dfinal_k: Optional[Tensor] = None,
+    dfinal_v: Optional[Tensor] = None, chunk: int = 128,
+    dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
+    device_kind: str | None = None,
+) -> SISOGrads:
+    """The HIP reverse scan plus the small epilogue of ``kernel_bwd.py:534-669``
+    (dgamma, dD, the dfinal_k rotation pullback, seed gradients), in device torch ops
+    on ``(B, H, L)``-sized tensors or smaller."""
+    batch, seqlen, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[3]
+    n_angles = phi.shape[-1]
+    kg = siso_backward_kernel(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias,
+                              chunk_states, d_skip=d_skip, dfinal_ssm=dfinal_ssm, chunk=chunk,
+                              dtype_policy=dtype_policy, dfinal_v=dfinal_v)
+    dq, dk, dphi = kg.dq, kg.dk, kg.dphi
+    dq_bias, dk_bias = kg.dq_bias, kg.dk_bias
+    dgamma = kg.dqk_diag * kg.uw
+    dd_skip = kg.dqk_diag.sum(dim=(0, 2)) if d_skip is not None else None
+    if dfinal_k is not None:
+        cos_l, sin_l = LY.rope_cos_sin(phi[:, :, -1, :].float(), state_dim)
+        dk_rot = LY.rope_apply(dfinal_k.float(), cos_l, -sin_l)     # (B, H, N)
+        dk = dk.clone()
+        dk[:, -1, :] += dk_rot.sum(dim=1)
+        dk_bias = dk_bias + dk_rot.sum(dim=0)
+        dphi = dphi.clone()
+        dphi[:, :, -1, :] += LY.rope_dphi(kg.k_final, dfinal_k.float(), n_angles)
+    if seed_ssm is not None:
+        adj = kg.dseed_ssm
+        coef = seed_coef.float()[..., None, None]
+        dseed_k = (adj * coef * seed_v.float()[..., :, None]).sum(dim=2)
+        dseed_v = (adj * coef * seed_k.float()[..., None, :]).sum(dim=3)
+        dseed_coef = (adj * (seed_v.float()[..., :, None] * seed_k.float()[..., None, :])).sum(dim=(2, 3))
+        dseed_ssm = adj
+    else:
+        dseed_ssm = dseed_k = dseed_v = dseed_coef = None
+    return SISOGrads(dq=dq, dk=dk, dv=kg.dv, dadt=kg.dadt, dgamma=dgamma, dscale=kg.dscale,
+                     dphi=dphi, dq_bias=dq_bias, dk_bias=dk_bias, dd_skip=dd_skip, dz=kg.dz,
+                     dseed_ssm=dseed_ssm, dseed_k=dseed_k, dseed_v=dseed_v,
+                     dseed_coef=dseed_coef)
