@@ -68,6 +68,17 @@ def _bhlp_operand(t: Optional[Tensor], mt: torch.dtype) -> Optional[Tensor]:
     return t if ok else t.contiguous()
 
 
+def _empty_like_layout(v: Tensor, dtype: torch.dtype) -> Tensor:
+    """A new ``(B, H, L, P)`` tensor laid out like ``v``: if ``v`` is a time-major view
+    (a ``(B, L, H, P)`` buffer, e.g. a slice of the fused in_proj output), the result
+    is the same permuted view of a fresh ``(B, L, H, P)`` buffer, so the layer can
+    reshape it to ``(B, L, H*P)`` for free."""
+    b, h, l, p = v.shape
+    if v.stride(2) > v.stride(1):
+        return torch.empty(b, l, h, p, device=v.device, dtype=dtype).permute(0, 2, 1, 3)
+    return torch.empty(b, h, l, p, device=v.device, dtype=dtype)
+
+
 def siso_forward(
     q: Tensor, k: Tensor, v: Tensor, adt: Tensor, gamma: Tensor, scale: Tensor,
     phi: Tensor, q_bias: Tensor, k_bias: Tensor, d_skip: Optional[Tensor] = None,
@@ -75,14 +86,12 @@ def siso_forward(
     seed_k: Optional[Tensor] = None, seed_v: Optional[Tensor] = None,
     seed_coef: Optional[Tensor] = None, chunk: int = 128,
     dtype_policy: LY.DtypePolicy | str = LY.BF16, save_residuals: bool = False,
-    interpret: Any = False, device_kind: str | None = None, *, y_out: Optional[Tensor] = None,
+    interpret: Any = False, device_kind: str | None = None,
 ):
     """Chunked forward (``kernel_fwd.py:204-248``).
 
     Returns ``(y, final_ssm, final_k, final_v)`` and, with ``save_residuals``, a
-    `ForwardResiduals`. ``y_out`` (keyword-only) is an optional preallocated
-    ``(B, H, L, P)`` view to write ``y`` into (e.g. a ``(B, L, H*P)`` buffer viewed as
-    ``(B, H, L, P)``), saving a transpose.
+    `ForwardResiduals`. ``y`` has ``v``'s memory layout (see `_empty_like_layout`).
     """
     pol = LY.policy(dtype_policy)
     LY.validate_chunk(chunk)
@@ -122,14 +131,7 @@ def siso_forward(
     s_ssm, s_k, s_v, s_c = (_f32c(s) for s in seeds)
 
     y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
-    if y_out is not None:
-        if tuple(y_out.shape) != (batch, nheads, seqlen, headdim) or y_out.dtype != mt:
-            raise ValueError("y_out must be a (B, H, L, P) tensor of the policy dtype")
-        y = _bhlp_operand(y_out, mt)
-        if y is not y_out:
-            raise ValueError("y_out must be 16-byte aligned with P contiguous")
-    else:
-        y = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
+    y = _empty_like_layout(vc, mt)
     f32 = dict(device=dev, dtype=torch.float32)
     final_ssm = torch.empty(batch, nheads, headdim, state_dim, **f32)
     final_k = torch.empty(batch, nheads, state_dim, **f32)
@@ -158,7 +160,7 @@ def siso_forward(
     with torch.cuda.device(dev):
         _lib.check(_lib.load().m3s_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_fwd")
 
-    if y_out is None and y.dtype != y_dtype:
+    if y.dtype != y_dtype:
         y = y.to(y_dtype)
     outs = (y, final_ssm, final_k, final_v)
     if save_residuals:
@@ -193,7 +195,7 @@ def siso_decode(q: Tensor, k: Tensor, v: Tensor, adt: Tensor, dt: Tensor, lam: T
     updated **in place** and returned (the reference donates them): the input state is
     consumed.
     """
-    from .preprocess import SISOState
+    from .scan_prep import SISOState
 
     pol = LY.policy(dtype_policy)
     batch, state_dim = q.shape
@@ -350,8 +352,8 @@ def siso_backward_kernel(
     f32 = dict(device=dev, dtype=torch.float32)
     dq = torch.empty(batch, seqlen, state_dim, **f32)
     dk = torch.empty(batch, seqlen, state_dim, **f32)
-    dv = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
-    dz = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt) if zc is not None else None
+    dv = _empty_like_layout(vc, mt)
+    dz = _empty_like_layout(zc, mt) if zc is not None else None
     dadt = torch.empty(batch, nheads, seqlen, **f32)
     dqk = torch.empty(batch, nheads, seqlen, **f32)
     dscale = torch.empty(batch, nheads, seqlen, **f32)

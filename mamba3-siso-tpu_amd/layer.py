@@ -1,0 +1,188 @@
+"""The Mamba-3 SISO layer: projections around the HIP scan (``layer.py`` surface).
+
+``SISOConfig`` / ``SISOParams`` / ``init_params`` / ``split_in_proj`` / ``rms_norm`` /
+``mamba3_siso_layer`` keep the reference's names, fields, defaults and semantics
+(``layer.py:39-262``). ``mamba3_siso_decode_step`` is the per-token layer step the
+reference inlines in ``model.lm_decode_step`` (``model.py:266-289``), minus the block
+norm, residual and MLP.
+
+Layer structure: ``in_proj -> [z, x, B, C, dd_dt, dd_A, trap, angles]``; B, C ->
+RMSNorm; scan with ``q = C``, ``k = B``, gated by ``silu(z)``; ``out_proj``.
+
+Layout: the scan reads ``x`` and ``z`` in place from the fused projection
+``(B, L, d_in_proj)`` (strided ``(B, H, L, P)`` views) and writes ``y`` as a
+``(B, L, H, P)`` buffer, so no transpose is ever materialised (the reference pays three,
+``layer.py:240,249,258``).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any, NamedTuple, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+from . import layout as LY
+from .scan_prep import SISOState, heavy_tail
+from .siso import siso_segment
+
+Tensor = torch.Tensor
+
+
+@dataclasses.dataclass(frozen=True)
+class SISOConfig:
+    """Shapes and hyperparameters (``layer.py:39-99``); same fields and defaults.
+
+    ``chunk`` follows the GPU rule of `layout.validate_chunk` (32/64/128/256) instead of
+    the reference's Mosaic rule (multiple of 128).
+    """
+
+    d_model: int
+    d_state: int = 128
+    headdim: int = 64
+    expand: int = 2
+    rope_fraction: float = 0.5
+    chunk: int = 128
+    a_floor: float = 1e-4
+    norm_eps: float = 1e-5
+    dt_min: float = 0.001
+    dt_max: float = 0.1
+    dt_init_floor: float = 1e-4
+    policy_name: str = "bf16"
+
+    @property
+    def d_inner(self) -> int:
+        return self.expand * self.d_model
+
+    @property
+    def nheads(self) -> int:
+        if self.d_inner % self.headdim != 0:
+            raise ValueError(f"d_inner {self.d_inner} not divisible by headdim {self.headdim}")
+        return self.d_inner // self.headdim
+
+    @property
+    def n_angles(self) -> int:
+        """Rotary pairs (``layer.py:80-91``): even-floored ``d_state*rope_fraction``/2."""
+        if self.rope_fraction not in (0.5, 1.0):
+            raise ValueError(f"rope_fraction must be 0.5 or 1.0, got {self.rope_fraction}")
+        width = int(self.d_state * self.rope_fraction)
+        if width % 2:
+            width -= 1
+        n = width // 2
+        if n <= 0:
+            raise ValueError("rope_fraction too small: no rotary angles")
+        return n
+
+    @property
+    def d_in_proj(self) -> int:
+        """``layer.py:93-95``; order fixed by `split_in_proj`."""
+        return 2 * self.d_inner + 2 * self.d_state + 3 * self.nheads + self.n_angles
+
+    def __post_init__(self):
+        LY.validate_chunk(self.chunk)
+        LY.policy(self.policy_name)
+        _ = self.nheads, self.n_angles
+
+
+class SISOParams(NamedTuple):
+    """``layer.py:102-124``. in_proj ``(d_model, d_in_proj)``; out_proj
+    ``(d_inner, d_model)``; dt_bias ``(H,)``; b/c_norm_weight ``(N,)`` and b/c_bias
+    ``(H, N)`` in the permuted rotary layout; d_skip ``(H,)``."""
+
+    in_proj: Tensor
+    out_proj: Tensor
+    dt_bias: Tensor
+    b_norm_weight: Tensor
+    c_norm_weight: Tensor
+    b_bias: Tensor
+    c_bias: Tensor
+    d_skip: Tensor
+
+
+def init_params(cfg: SISOConfig, key: Any = 0, dtype=torch.float32, device=None) -> SISOParams:
+    """Fresh weights with upstream's initialisation (``layer.py:127-160``).
+
+    ``key`` is an int seed or a ``torch.Generator`` (the reference takes a JAX PRNG key;
+    JAX's threefry stream is not reproduced, only the distributions): in_proj
+    ``U(+-1/sqrt(d_model))``, out_proj ``U(+-1/sqrt(d_inner))``, ``dt_bias`` the inverse
+    softplus of a log-uniform ``dt`` in ``[dt_min, dt_max]`` floored at ``dt_init_floor``;
+    norm gains, B/C biases and D are ones. Drawn on the CPU, then moved to ``device``.
+    """
+    gen = key if isinstance(key, torch.Generator) else torch.Generator().manual_seed(int(key))
+    s_in = 1.0 / math.sqrt(cfg.d_model)
+    s_out = 1.0 / math.sqrt(cfg.d_inner)
+    in_proj = (torch.rand(cfg.d_model, cfg.d_in_proj, generator=gen) * 2 - 1) * s_in
+    out_proj = (torch.rand(cfg.d_inner, cfg.d_model, generator=gen) * 2 - 1) * s_out
+    dt = torch.exp(torch.rand(cfg.nheads, generator=gen)
+                   * (math.log(cfg.dt_max) - math.log(cfg.dt_min)) + math.log(cfg.dt_min))
+    dt = torch.clamp(dt, min=cfg.dt_init_floor)
+    dt_bias = dt + torch.log(-torch.expm1(-dt))   # inverse softplus
+    ones = lambda *s: torch.ones(*s, dtype=dtype)  # noqa: E731
+    p = SISOParams(
+        in_proj=in_proj.to(dtype), out_proj=out_proj.to(dtype), dt_bias=dt_bias.float(),
+        b_norm_weight=ones(cfg.d_state), c_norm_weight=ones(cfg.d_state),
+        b_bias=ones(cfg.nheads, cfg.d_state), c_bias=ones(cfg.nheads, cfg.d_state),
+        d_skip=ones(cfg.nheads))
+    return SISOParams(*(t.to(device) for t in p)) if device is not None else p
+
+
+def split_in_proj(proj: Tensor, cfg: SISOConfig):
+    """``layer.py:163-187``: ``(z, x, B, C, dt_raw, a_raw, trap_raw, angles)`` with z, x
+    ``(B, L, H, P)``, B, C ``(B, L, N)``, scalars ``(B, L, H)``, angles ``(B, L, Nr)``.
+    All are views of ``proj``."""
+    sizes = (cfg.d_inner, cfg.d_inner, cfg.d_state, cfg.d_state,
+             cfg.nheads, cfg.nheads, cfg.nheads, cfg.n_angles)
+    z, x, b, c, dt_raw, a_raw, trap_raw, angles = torch.split(proj, sizes, dim=-1)
+    z = z.unflatten(-1, (cfg.nheads, cfg.headdim))
+    x = x.unflatten(-1, (cfg.nheads, cfg.headdim))
+    return z, x, b, c, dt_raw, a_raw, trap_raw, angles
+
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """``layer.py:190-198``: RMSNorm in f32, gain, no bias, cast back to x.dtype."""
+    xf = x.float()
+    rstd = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps)
+    return (xf * rstd * weight.float()).to(x.dtype)
+
+
+def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
+                      state: Optional[SISOState] = None, interpret: Any = False,
+                      device_kind: str | None = None):
+    """Forward of one layer (``layer.py:201-262``). ``u`` is ``(B, L, d_model)`` on the
+    ROCm device; returns ``(out (B, L, d_model), SISOState)``. Differentiable w.r.t.
+    ``u`` and every `SISOParams` field through torch autograd."""
+    batch, seqlen, _ = u.shape
+    proj = u @ params.in_proj.to(u.dtype)
+    z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj, cfg)
+    b = rms_norm(b, params.b_norm_weight, cfg.norm_eps)
+    c = rms_norm(c, params.c_norm_weight, cfg.norm_eps)
+    out = siso_segment(
+        q=c, k=b, v=x.permute(0, 2, 1, 3), dt_raw=dt_raw, a_raw=a_raw, trap_raw=trap_raw,
+        angles=angles, dt_bias=params.dt_bias, q_bias=params.c_bias, k_bias=params.b_bias,
+        d_skip=params.d_skip, z=z.permute(0, 2, 1, 3), state=state, a_floor=cfg.a_floor,
+        chunk=cfg.chunk, policy_name=cfg.policy_name)
+    y = out.y.permute(0, 2, 1, 3).reshape(batch, seqlen, cfg.d_inner)
+    return y.to(u.dtype) @ params.out_proj.to(u.dtype), out.state
+
+
+def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,
+                            state: SISOState):
+    """One token through the layer (``model.py:266-289`` without block norm/residual):
+    ``u`` ``(B, d_model)`` -> ``(out (B, d_model), next_state)``. The state is updated in
+    place by the decode kernel (the reference donates it)."""
+    proj = u @ params.in_proj.to(u.dtype)
+    z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[:, None, :], cfg)
+    b = rms_norm(b, params.b_norm_weight, cfg.norm_eps)[:, 0]
+    c = rms_norm(c, params.c_norm_weight, cfg.norm_eps)[:, 0]
+    dt = F.softplus(dt_raw[:, 0].float() + params.dt_bias.float())
+    a = torch.clamp(-heavy_tail(a_raw[:, 0].float()), max=-cfg.a_floor)
+    lam = torch.sigmoid(trap_raw[:, 0].float())
+    y, st = K.decode_step(c, b, x[:, 0], a * dt, dt, lam, angles[:, 0], params.c_bias,
+                          params.b_bias, state, d_skip=params.d_skip, z=z[:, 0],
+                          dtype_policy=cfg.policy_name)
+    out = y.reshape(u.shape[0], cfg.d_inner).to(u.dtype) @ params.out_proj.to(u.dtype)
+    return out, st
+

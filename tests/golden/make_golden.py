@@ -108,10 +108,10 @@ def layer_case(tr, name, d_model, d_state, headdim, expand, rope_fraction, b, se
 def main(argv):
     ref_root = Path(argv[1] if len(argv) > 1 else "/root/reference")
     tr = load_torch_ref(ref_root)
-    kernel_case(tr, "torch_ref_kernel_gated", b=2, seqlen=96, h=3, n=16, p=8, nr=4, seed=7)
-    kernel_case(tr, "torch_ref_kernel_plain", b=1, seqlen=64, h=2, n=32, p=8, nr=16, seed=8,
+    kernel_case(tr, "torch_ref_kernel_gated", b=2, seqlen=96, h=3, n=16, p=16, nr=4, seed=7)
+    kernel_case(tr, "torch_ref_kernel_plain", b=1, seqlen=64, h=2, n=32, p=16, nr=16, seed=8,
                 with_dz=False)
-    layer_case(tr, "torch_ref_layer_half", d_model=32, d_state=16, headdim=8, expand=2,
+    layer_case(tr, "torch_ref_layer_half", d_model=32, d_state=16, headdim=16, expand=2,
                rope_fraction=0.5, b=2, seqlen=64, seed=11)
     layer_case(tr, "torch_ref_layer_full", d_model=32, d_state=16, headdim=16, expand=1,
                rope_fraction=1.0, b=1, seqlen=64, seed=12)

@@ -1,0 +1,82 @@
+"""Shared helpers for the GPU parity tests: identical seeded inputs for the CPU oracle
+(float64) and the device (policy dtype), and the tolerance checks.
+
+Tolerances (stated once, used by every GPU test):
+  * f32 policy vs the float64 oracle: p95 relative error over |ref| >= 1e-2
+    (``tests.py:60-88``) <= 2e-5 for forward/decode outputs and <= 2e-4 for gradients
+    (the reference's own bars, ``tests.py:533, 612``).
+  * bf16 policy: against the oracle's bf16 rounding model (same rounding points as the
+    reference kernel) p95 <= 2e-3 for f32 outputs (ybar, state) and <= 5e-3 for outputs
+    stored in bf16 (one bf16 rounding is up to 2^-8 relative); against the float64
+    maths, max |got - ref| /
+    max |ref| <= 2e-2 on outputs and states and <= 2e-2 on gradients (the north_star
+    bound is 5e-2 relative on gradients), and the reference's bf16 p95 bar of 5e-2 on
+    forward outputs (``tests.py:533``).
+"""
+
+import torch
+
+from oracle import siso_oracle as O
+
+F64 = torch.float64
+F32 = torch.float32
+BF16 = torch.bfloat16
+
+FWD_F32_P95 = 2e-5
+GRAD_F32_P95 = 2e-4
+BF16_MODEL_P95 = 2e-3
+BF16_OUT_MODEL_P95 = 5e-3
+BF16_MAXREL = 2e-2
+BF16_P95 = 5e-2
+
+
+def mt_of(policy):
+    return BF16 if policy == "bf16" else F32
+
+
+def boundary_inputs(b, h, seqlen, n, p, nr, policy, seed=0, seeds=False):
+    """Kernel-boundary inputs. Tensors the kernel reads in the policy dtype are rounded
+    to it first, so oracle and kernel see identical values. Returns (cpu_f64, device)."""
+    x = O.make_inputs(b, h, seqlen, n, p, nr, seed=seed)
+    pre, _ = O.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"])
+    mt = mt_of(policy)
+    cpu = dict(
+        q=x["q"].to(mt).double(), k=x["k"].to(mt).double(), v=x["v"].to(mt).double(),
+        z=x["z"].to(mt).double(), adt=pre.adt.float().double(), gamma=pre.gamma.float().double(),
+        scale=pre.scale.float().double(), phi=pre.phi.float().double(),
+        q_bias=x["q_bias"].float().double(), k_bias=x["k_bias"].float().double(),
+        d_skip=x["d_skip"].float().double(), dy=x["dy"].to(mt).double(),
+        dt=pre.dt.float().double(), lam=pre.lam.float().double(),
+        angles=x["angles"].float().double())
+    if seeds:
+        g = torch.Generator().manual_seed(seed + 1000)
+        cpu.update(
+            seed_ssm=torch.randn(b, h, p, n, generator=g, dtype=F64).float().double(),
+            seed_k=torch.randn(b, h, n, generator=g, dtype=F64).float().double(),
+            seed_v=torch.randn(b, h, p, generator=g, dtype=F64).float().double(),
+            seed_coef=torch.rand(b, h, generator=g, dtype=F64).float().double())
+    dev = {}
+    for k_, v_ in cpu.items():
+        dt_ = mt if k_ in ("q", "k", "v", "z", "dy") else F32
+        dev[k_] = v_.to(dt_).cuda()
+    return cpu, dev
+
+
+def fwd_args(d):
+    return [d["q"], d["k"], d["v"], d["adt"], d["gamma"], d["scale"], d["phi"], d["q_bias"],
+            d["k_bias"], d.get("d_skip"), d.get("z"), d.get("seed_ssm"), d.get("seed_k"),
+            d.get("seed_v"), d.get("seed_coef")]
+
+
+def cpu(t):
+    return t.detach().float().cpu().double()
+
+
+def assert_p95(got, ref, tol, what=""):
+    e = O.rel_error(cpu(got), ref)
+    assert e <= tol, f"{what}: p95 rel error {e:.3e} > {tol:.1e}"
+
+
+def assert_maxrel(got, ref, tol, what=""):
+    e = O.max_rel(cpu(got), ref)
+    assert e <= tol, f"{what}: max-normalised error {e:.3e} > {tol:.1e}"

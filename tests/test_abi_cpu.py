@@ -1,0 +1,112 @@
+"""The C-ABI library: it loads, exports every symbol include/m3s.h declares, agrees with
+the header on struct layouts, and rejects bad arguments before touching the GPU.
+No kernel is launched here."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "m3s.h")
+
+
+@pytest.fixture(scope="module")
+def lib(m3):
+    from mamba3_siso_tpu_amd import _lib
+
+    return _lib
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(m3s_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol(lib):
+    handle = lib.load()
+    names = declared_functions()
+    assert names, "no declarations parsed from include/m3s.h"
+    assert set(names) == set(lib.EXPORTS)
+    for name in names:
+        assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 1
+
+
+def test_struct_layouts_match_the_header(lib):
+    """Compile the header with gcc and compare sizeof/offsetof with the ctypes mirror."""
+    src = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "m3s.h"
+int main(void) {
+  printf("%zu %zu %zu %zu\n", sizeof(m3s_bhlp), sizeof(m3s_fwd_args),
+         sizeof(m3s_bwd_args), sizeof(m3s_decode_args));
+  printf("%zu %zu %zu\n", offsetof(m3s_fwd_args, final_v), offsetof(m3s_bwd_args, dseed_ssm),
+         offsetof(m3s_decode_args, y));
+  return 0;
+}
+"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        exe = os.path.join(d, "t")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    sizes = [int(x) for x in out]
+    assert sizes[:4] == [ctypes.sizeof(lib.Bhlp), ctypes.sizeof(lib.FwdArgs),
+                         ctypes.sizeof(lib.BwdArgs), ctypes.sizeof(lib.DecodeArgs)]
+    assert sizes[4:] == [lib.FwdArgs.final_v.offset, lib.BwdArgs.dseed_ssm.offset,
+                         lib.DecodeArgs.y.offset]
+
+
+def test_null_and_stale_args_are_rejected_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_fwd(None, None) == lib.ERR_INVALID
+    assert b"NULL" in h.m3s_last_error()
+    a = lib.FwdArgs()
+    a.struct_size = 3
+    assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"ABI mismatch" in h.m3s_last_error()
+    b = lib.BwdArgs()
+    b.struct_size = ctypes.sizeof(lib.BwdArgs)
+    assert h.m3s_bwd(ctypes.byref(b), None) == lib.ERR_INVALID   # zero dims
+    d = lib.DecodeArgs()
+    d.struct_size = ctypes.sizeof(lib.DecodeArgs)
+    assert h.m3s_decode(ctypes.byref(d), None) == lib.ERR_INVALID
+
+
+def test_unsupported_shapes_and_bad_dims_are_reported(lib):
+    h = lib.load()
+    a = lib.FwdArgs()
+    a.struct_size = ctypes.sizeof(lib.FwdArgs)
+    a.batch, a.seqlen, a.nheads, a.headdim, a.state_dim, a.n_angles, a.chunk = 1, 128, 1, 24, 128, 32, 128
+    a.dtype = lib.DTYPE_BF16
+    assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_UNSUPPORTED
+    assert b"no kernel" in h.m3s_last_error()
+    a.headdim, a.seqlen = 64, 100
+    assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"multiple of chunk" in h.m3s_last_error()
+    a.seqlen, a.n_angles = 128, 65
+    assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    a.n_angles = 32   # now only the pointers are missing
+    assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"q/k" in h.m3s_last_error()
+
+
+def test_capability_table(lib):
+    assert lib.supported(0, lib.DTYPE_BF16, 128, 128, 64)
+    assert lib.supported(1, lib.DTYPE_BF16, 128, 128, 64)
+    assert lib.supported(2, lib.DTYPE_BF16, 0, 128, 64)
+    assert lib.supported(0, lib.DTYPE_F32, 64, 16, 16) and lib.supported(1, lib.DTYPE_F32, 64, 16, 16)
+    # every backward configuration has a forward
+    for dt in (lib.DTYPE_F32, lib.DTYPE_BF16):
+        for c in (32, 64, 128, 256):
+            for n in (16, 32, 64, 128):
+                for p in (16, 64):
+                    if lib.supported(1, dt, c, n, p):
+                        assert lib.supported(0, dt, c, n, p)
+    assert not lib.supported(0, lib.DTYPE_F32, 128, 128, 64)   # does not fit in LDS

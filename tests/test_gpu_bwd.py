@@ -1,0 +1,144 @@
+"""Reverse-scan backward (m3s_bwd + the epilogue) vs autograd of the float64 oracle --
+the way the reference checks its VJP against ``jax.grad`` (``tests.py:573-612``)."""
+
+import math
+
+import pytest
+import torch
+
+from helpers import (BF16, BF16_MAXREL, GRAD_F32_P95, assert_maxrel, assert_p95,
+                     boundary_inputs, fwd_args)
+from oracle import siso_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("q", "k", "v", "adt", "gamma", "scale", "phi", "q_bias", "k_bias", "d_skip", "z",
+         "seed_ssm", "seed_k", "seed_v", "seed_coef")
+GRAD_FIELD = dict(q="dq", k="dk", v="dv", adt="dadt", gamma="dgamma", scale="dscale",
+                  phi="dphi", q_bias="dq_bias", k_bias="dk_bias", d_skip="dd_skip", z="dz",
+                  seed_ssm="dseed_ssm", seed_k="dseed_k", seed_v="dseed_v",
+                  seed_coef="dseed_coef")
+
+
+def run_case(m3, b, h, L, n, p, nr, chunk, policy, seeds, dfin, seed=0):
+    c, d = boundary_inputs(b, h, L, n, p, nr, policy, seed=seed, seeds=seeds)
+    g = torch.Generator().manual_seed(seed + 77)
+    dfs = dfk = dfv = None
+    if dfin:
+        dfs = torch.randn(b, h, p, n, generator=g, dtype=torch.float64).float().double()
+        dfk = torch.randn(b, h, n, generator=g, dtype=torch.float64).float().double()
+        dfv = torch.randn(b, h, p, generator=g, dtype=torch.float64).float().double()
+    want = O.boundary_grads({k_: c[k_] for k_ in NAMES if k_ in c}, c["dy"], dfs, dfk, dfv,
+                            chunk=chunk)
+    out = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy=policy, save_residuals=True)
+    res = out[4]
+    dev = lambda t: None if t is None else t.float().cuda()  # noqa: E731
+    gr = m3.siso_backward(d["dy"], d["q"], d["k"], d["v"], d["adt"], d["gamma"], d["scale"],
+                          d["phi"], d["q_bias"], d["k_bias"], res.ybar, res.chunk_states,
+                          d["d_skip"], d["z"], d.get("seed_ssm"), d.get("seed_k"),
+                          d.get("seed_v"), d.get("seed_coef"), dev(dfs), dev(dfk), dev(dfv),
+                          chunk=chunk, dtype_policy=policy)
+    return want, gr
+
+
+@pytest.mark.parametrize("b,h,L,n,p,nr,chunk,seeds,dfin", [
+    (1, 4, 512, 16, 16, 4, 64, False, False),    # cfg1 kernel shapes
+    (1, 2, 64, 32, 16, 8, 32, True, True),
+    (2, 3, 128, 32, 16, 8, 64, False, False),
+    (1, 2, 128, 128, 64, 32, 32, True, True),
+    (2, 2, 128, 64, 64, 16, 64, True, False),
+])
+def test_backward_f32_matches_autograd_of_oracle(m3, b, h, L, n, p, nr, chunk, seeds, dfin):
+    want, gr = run_case(m3, b, h, L, n, p, nr, chunk, "f32", seeds, dfin)
+    for name, w in want.items():
+        assert_p95(getattr(gr, GRAD_FIELD[name]), w, GRAD_F32_P95, f"d{name}")
+
+
+@pytest.mark.parametrize("chunk,seeds,dfin", [(128, True, True), (64, False, False), (32, True, False)])
+def test_backward_bf16_matches_autograd_of_oracle(m3, chunk, seeds, dfin):
+    want, gr = run_case(m3, 2, 2, 256, 128, 64, 32, chunk, "bf16", seeds, dfin)
+    assert gr.dv.dtype == BF16 and gr.dz.dtype == BF16
+    for name, w in want.items():
+        assert_maxrel(getattr(gr, GRAD_FIELD[name]), w, BF16_MAXREL, f"d{name}")
+
+
+def test_backward_matches_finite_differences_of_the_kernel_forward(m3):
+    """Central differences of the HIP forward itself (f32, tiny): the VJP is checked
+    against the function it differentiates, as tests.py:614-645 does."""
+    c, d = boundary_inputs(1, 1, 64, 16, 16, 4, "f32", seed=9)
+    dy = d["dy"]
+
+    def loss(args):
+        y, fs, fk, fv = m3.siso_forward(*args, chunk=32, dtype_policy="f32")
+        return float((y.double() * dy.double()).sum())
+
+    out = m3.siso_forward(*fwd_args(d), chunk=32, dtype_policy="f32", save_residuals=True)
+    gr = m3.siso_backward(dy, d["q"], d["k"], d["v"], d["adt"], d["gamma"], d["scale"], d["phi"],
+                          d["q_bias"], d["k_bias"], out[4].ybar, out[4].chunk_states, d["d_skip"],
+                          d["z"], chunk=32, dtype_policy="f32")
+    gen = torch.Generator().manual_seed(3)
+    for idx, name, field, eps in ((0, "q", "dq", 1e-2), (2, "v", "dv", 1e-2), (3, "adt", "dadt", 1e-3),
+                                  (6, "phi", "dphi", 1e-3), (5, "scale", "dscale", 1e-3)):
+        base = fwd_args(d)
+        t = base[idx]
+        for i in torch.randperm(t.numel(), generator=gen)[:3].tolist():
+            plus, minus = list(base), list(base)
+            tp, tm = t.clone().reshape(-1), t.clone().reshape(-1)
+            tp[i] += eps
+            tm[i] -= eps
+            plus[idx], minus[idx] = tp.reshape(t.shape), tm.reshape(t.shape)
+            fd = (loss(plus) - loss(minus)) / (2 * eps)
+            got = float(getattr(gr, field).reshape(-1)[i])
+            assert abs(got - fd) <= 2e-2 * max(1.0, abs(fd)), (name, i, got, fd)
+
+
+def test_backward_full_size_cfg3_head_slices_and_head_sum(m3):
+    """cfg3 shapes (B=8, L=8192, H=32, bf16, chunk 128). Per-head gradients of a head
+    slice match the oracle run on that slice alone (heads only couple through the
+    head-summed dq/dk); the head sum is checked by linearity: the full run's dq/dk
+    equals the sum of the kernel's dq/dk over disjoint head groups."""
+    B, L, H, N, P, Nr = 8, 8192, 32, 128, 64, 32
+    g = torch.Generator(device="cuda").manual_seed(21)
+
+    def rn(*s):
+        return torch.randn(*s, generator=g, device="cuda")
+
+    def norm_rows(t):
+        return t * torch.rsqrt(t.square().mean(-1, keepdim=True) + 1e-6)
+
+    q = norm_rows(rn(B, L, N)).to(BF16)
+    k = norm_rows(rn(B, L, N)).to(BF16)
+    v, z, dy = rn(B, H, L, P).to(BF16), rn(B, H, L, P).to(BF16), rn(B, H, L, P).to(BF16)
+    dt_raw = torch.log(torch.expm1(torch.exp(torch.rand(B, L, H, generator=g, device="cuda")
+                                             * (math.log(0.1) - math.log(0.001)) + math.log(0.001))))
+    pre, _ = m3.preprocess(dt_raw, rn(B, L, H), rn(B, L, H), 0.5 * rn(B, L, Nr),
+                           torch.zeros(H, device="cuda"))
+    qb, kb, dsk = 0.1 * rn(H, N), 0.1 * rn(H, N), rn(H)
+
+    def grads(hs):
+        a = [q, k, v[:, hs], pre.adt[:, hs], pre.gamma[:, hs], pre.scale[:, hs], pre.phi[:, hs],
+             qb[hs], kb[hs], dsk[hs], z[:, hs]]
+        out = m3.siso_forward(*a, chunk=128, save_residuals=True)
+        return m3.siso_backward(dy[:, hs], *a[:9], out[4].ybar, out[4].chunk_states,
+                                d_skip=dsk[hs], z=z[:, hs], chunk=128)
+
+    full = grads(slice(None))
+    parts = [grads(slice(i, i + 8)) for i in range(0, H, 8)]
+    dq_sum = sum(p_.dq for p_ in parts)
+    dk_sum = sum(p_.dk for p_ in parts)
+    assert O.max_rel(full.dq.cpu(), dq_sum.cpu()) <= 1e-5
+    assert O.max_rel(full.dk.cpu(), dk_sum.cpu()) <= 1e-5
+    for name in ("dv", "dz", "dadt", "dscale", "dphi"):
+        assert bool(torch.isfinite(getattr(full, name).float()).all()), name
+    # per-head gradients of one batch element on a 2-head slice vs the oracle
+    b_, hs = 3, [2, 29]
+    sl = lambda t: t[b_:b_ + 1, hs].double().cpu()  # noqa: E731
+    inputs = dict(q=q[b_:b_ + 1].double().cpu(), k=k[b_:b_ + 1].double().cpu(), v=sl(v),
+                  adt=sl(pre.adt), gamma=sl(pre.gamma), scale=sl(pre.scale), phi=sl(pre.phi),
+                  q_bias=qb[hs].double().cpu(), k_bias=kb[hs].double().cpu(),
+                  d_skip=dsk[hs].double().cpu(), z=sl(z))
+    want = O.boundary_grads(inputs, sl(dy), chunk=128)
+    got = dict(v=full.dv, z=full.dz, adt=full.dadt, gamma=full.dgamma, scale=full.dscale,
+               phi=full.dphi)
+    for name, t in got.items():
+        assert_maxrel(t[b_:b_ + 1, hs], want[name], BF16_MAXREL, f"d{name} (slice)")

@@ -1,0 +1,127 @@
+"""Single-token decode kernel (m3s_decode) vs the oracle's three-term step, chains of
+steps vs one chunked prefill, and the prefill -> decode handoff (tests.py:734-877)."""
+
+import pytest
+import torch
+
+from helpers import BF16, BF16_OUT_MODEL_P95, BF16_P95, F32, FWD_F32_P95, assert_maxrel, assert_p95, cpu
+from oracle import siso_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def step_inputs(b, h, n, p, nr, policy, seed):
+    x = O.make_inputs(b, h, 1, n, p, nr, seed=seed)
+    pre, _ = O.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"])
+    mt = BF16 if policy == "bf16" else F32
+    g = torch.Generator().manual_seed(seed + 5)
+    st = O.SISOState(torch.randn(b, h, p, n, generator=g, dtype=torch.float64).float().double() * 0.1,
+                     torch.randn(b, h, n, generator=g, dtype=torch.float64).float().double(),
+                     torch.randn(b, h, p, generator=g, dtype=torch.float64).float().double(),
+                     (torch.rand(b, h, nr, generator=g, dtype=torch.float64) * 6).float().double())
+    c = dict(q=x["q"][:, 0].to(mt).double(), k=x["k"][:, 0].to(mt).double(),
+             v=x["v"][:, :, 0].to(mt).double(), z=x["z"][:, :, 0].to(mt).double(),
+             adt=pre.adt[:, :, 0].float().double(), dt=pre.dt[:, :, 0].float().double(),
+             lam=pre.lam[:, :, 0].float().double(), angles=x["angles"][:, 0].float().double(),
+             q_bias=x["q_bias"].float().double(), k_bias=x["k_bias"].float().double(),
+             d_skip=x["d_skip"].float().double())
+    d = {k_: v_.to(mt if k_ in ("q", "k", "v", "z") else F32).cuda() for k_, v_ in c.items()}
+    return c, d, st
+
+
+def step_args(a, st):
+    return (a["q"], a["k"], a["v"], a["adt"], a["dt"], a["lam"], a["angles"], a["q_bias"],
+            a["k_bias"], st, a["d_skip"], a["z"])
+
+
+@pytest.mark.parametrize("b,h,n,p,nr", [(2, 3, 128, 64, 32), (1, 4, 16, 16, 4), (3, 2, 64, 64, 16)])
+def test_decode_step_f32_matches_oracle_in_place(m3, b, h, n, p, nr):
+    c, d, st = step_inputs(b, h, n, p, nr, "f32", seed=1)
+    yr, sr = O.siso_step(*step_args(c, st))
+    gst = m3.SISOState(*(t.float().cuda() for t in st))
+    ptrs = [t.data_ptr() for t in gst]
+    y, s2 = m3.decode_step(*step_args(d, gst), dtype_policy="f32")
+    assert [t.data_ptr() for t in s2] == ptrs        # donated: updated in place
+    assert_p95(y, yr, FWD_F32_P95, "y")
+    assert_p95(s2.ssm, sr.ssm, FWD_F32_P95, "ssm")
+    assert_p95(s2.k, sr.k, FWD_F32_P95, "k")
+    assert O.max_rel(cpu(s2.v), sr.v) == 0.0
+    assert O.rel_error(cpu(s2.phi), sr.phi, angle=True) <= 1e-4
+
+
+def test_decode_step_bf16_matches_rounding_model(m3):
+    c, d, st = step_inputs(4, 32, 128, 64, 32, "bf16", seed=2)
+    ym, sm = O.siso_step(*step_args(c, st), mm_dtype=BF16)
+    y, s2 = m3.decode_step(*step_args(d, m3.SISOState(*(t.float().cuda() for t in st))))
+    assert y.dtype == BF16
+    assert_p95(y, ym, BF16_OUT_MODEL_P95, "y vs bf16 readout model")
+    assert_p95(s2.ssm, sm.ssm, FWD_F32_P95, "ssm (f32 update)")
+
+
+def test_decode_cfg4_batch_one_step(m3):
+    """cfg4 sizes: B=256, H=32, P=64, N=128; state ~ N(0, 0.1)."""
+    c, d, st = step_inputs(256, 32, 128, 64, 32, "bf16", seed=3)
+    ym, sm = O.siso_step(*step_args(c, st), mm_dtype=BF16)
+    y, s2 = m3.decode_step(*step_args(d, m3.SISOState(*(t.float().cuda() for t in st))))
+    assert_p95(y, ym, BF16_OUT_MODEL_P95, "y")
+    assert_maxrel(s2.ssm, sm.ssm, 1e-6, "ssm")
+
+
+@pytest.mark.parametrize("policy", ["f32", "bf16"])
+def test_decode_chain_equals_prefill_and_handoff(m3, policy):
+    b, h, L, n, p, nr, chunk = 1, 2, 128, 128, 64, 32, 64
+    mt = BF16 if policy == "bf16" else F32
+    x = O.make_inputs(b, h, L, n, p, nr, seed=4)
+    pre, _ = O.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"])
+    g = lambda t, dt=F32: t.to(dt).cuda()  # noqa: E731
+    q, k, v, z = g(x["q"], mt), g(x["k"], mt), g(x["v"], mt), g(x["z"], mt)
+    adt, dtt, lam = g(pre.adt), g(pre.dt), g(pre.lam)
+    qb, kb, dsk, ang = g(x["q_bias"]), g(x["k_bias"]), g(x["d_skip"]), g(x["angles"])
+    y_pre, fs, fk, fv = m3.siso_forward(q, k, v, adt, g(pre.gamma), g(pre.scale), g(pre.phi), qb,
+                                        kb, dsk, z, chunk=chunk, dtype_policy=policy)
+    st = m3.zero_state(b, h, p, n, nr, device="cuda")
+    y_dec, st = m3.decode_loop(q, k, v, adt, dtt, lam, ang, qb, kb, st, dsk, z, dtype_policy=policy)
+    tol = FWD_F32_P95 if policy == "f32" else BF16_P95   # two rounding paths in bf16
+    assert O.rel_error(cpu(y_dec), cpu(y_pre)) <= tol
+    assert O.rel_error(cpu(st.ssm), cpu(fs)) <= tol
+    assert O.rel_error(cpu(st.k), cpu(fk)) <= FWD_F32_P95
+    # prefill the first half with the layer-level segment, decode the rest
+    half = L // 2
+    out = m3.siso_segment(q[:, :half], k[:, :half], v[:, :, :half], g(x["dt_raw"][:, :half]),
+                          g(x["a_raw"][:, :half]), g(x["trap_raw"][:, :half]), ang[:, :half],
+                          g(x["dt_bias"]), qb, kb, dsk, z[:, :, :half], chunk=chunk,
+                          policy_name=policy)
+    pre2, _ = m3.preprocess(g(x["dt_raw"][:, half:]), g(x["a_raw"][:, half:]),
+                            g(x["trap_raw"][:, half:]), ang[:, half:], g(x["dt_bias"]),
+                            phi_init=out.state.phi)
+    carry = m3.SISOState(out.state.ssm.clone(), out.state.k.clone(), out.state.v.clone(),
+                         out.state.phi.clone())
+    y_b, _ = m3.decode_loop(q[:, half:], k[:, half:], v[:, :, half:], pre2.adt, pre2.dt, pre2.lam,
+                            ang[:, half:], qb, kb, carry, dsk, z[:, :, half:], dtype_policy=policy)
+    assert O.rel_error(cpu(torch.cat([out.y, y_b], dim=2)), cpu(y_pre)) <= tol
+
+
+def test_decode_reproduces_reference_torch_golden(m3):
+    """Token-by-token decode from a zero state vs upstream's step reference
+    (torch_ref.mamba3_siso_ref) for the whole golden sequence."""
+    import numpy as np
+    from pathlib import Path
+    fx = dict(np.load(Path(__file__).resolve().parent / "golden" / "torch_ref_kernel_gated.npz",
+                      allow_pickle=False))
+    t = {k_: torch.from_numpy(v_).float().cuda() for k_, v_ in fx.items() if v_.dtype != bool and v_.ndim > 0}
+    b, L, n = t["q"].shape
+    h, p, nr = t["v"].shape[2], t["v"].shape[3], t["angles"].shape[-1]
+    perm = O.deinterleave_perm(n).cuda()
+    st = m3.zero_state(b, h, p, n, nr, device="cuda")
+    lam = torch.sigmoid(t["trap"])
+    ys = []
+    for tt in range(L):
+        y, st = m3.decode_step(t["q"][:, tt][..., perm], t["k"][:, tt][..., perm], t["v"][:, tt],
+                               t["adt"][:, :, tt], t["dt"][:, :, tt], lam[:, :, tt], t["angles"][:, tt],
+                               t["q_bias"][:, perm], t["k_bias"][:, perm], st, t["d"], t["z"][:, tt],
+                               dtype_policy="f32")
+        ys.append(y)
+    want = torch.from_numpy(fx["out"]).double()
+    assert O.max_rel(cpu(torch.stack(ys, 1)), want) <= 2e-5
+    assert O.max_rel(cpu(st.ssm), torch.from_numpy(fx["ssm_state"]).double()[..., perm.cpu()]) <= 2e-5
+    assert O.rel_error(cpu(st.phi), torch.from_numpy(fx["angle_state"]).double(), angle=True) <= 1e-5

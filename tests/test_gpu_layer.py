@@ -1,0 +1,132 @@
+"""The layer on the GPU: BASELINE config 1 end to end (forward, final state, every
+gradient), the reference's torch layer via convert, segmented prefill, bf16 layer
+parity and the layer-level decode step -- all against the CPU oracle."""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16, BF16_MAXREL, GRAD_F32_P95, assert_maxrel, assert_p95, cpu
+from oracle import siso_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def params_dict(params, dtype=torch.float64):
+    return {f: getattr(params, f).detach().cpu().to(dtype) for f in params._fields}
+
+
+def cfg1(m3):
+    return m3.SISOConfig(d_model=64, d_state=16, headdim=16, expand=1, chunk=64, policy_name="f32")
+
+
+def test_cfg1_forward_state_and_all_gradients(m3):
+    """B=1, L=512, d_model=64, H=4, P=16, N=16, chunk 64, fp32;
+    params from init_params(seed=0); u ~ N(0,1) (seed 0); loss sum(y * g), g ~ N(0,1)
+    (seed 1). Checks y, the final state and the gradients of u and all 8 params."""
+    cfg = cfg1(m3)
+    p_cpu = m3.init_params(cfg, 0)
+    u = torch.randn(1, 512, 64, generator=torch.Generator().manual_seed(0))
+    gy = torch.randn(1, 512, 64, generator=torch.Generator().manual_seed(1))
+    # device run
+    params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+    ud = u.cuda().requires_grad_(True)
+    y, st = m3.mamba3_siso_layer(params, ud, cfg)
+    (y * gy.cuda()).sum().backward()
+    # oracle run (float64, autograd)
+    pd = {k_: v_.requires_grad_(True) for k_, v_ in params_dict(p_cpu).items()}
+    uo = u.double().requires_grad_(True)
+    yr, sr = O.layer_forward(pd, uo, d_state=16, headdim=16, expand=1, chunk=64)
+    (yr * gy.double()).sum().backward()
+    assert_p95(y, yr.detach(), 2e-5, "y")
+    assert_p95(st.ssm, sr.ssm.detach(), 2e-5, "final ssm")
+    assert_p95(st.k, sr.k.detach(), 2e-5, "final k")
+    assert O.rel_error(cpu(st.phi), sr.phi.detach(), angle=True) <= 1e-5
+    assert_p95(ud.grad, uo.grad, GRAD_F32_P95, "du")
+    for f in p_cpu._fields:
+        assert_p95(getattr(params, f).grad, pd[f].grad, GRAD_F32_P95, f"d{f}")
+
+
+@pytest.mark.parametrize("name", ["torch_ref_layer_half", "torch_ref_layer_full"])
+def test_reference_torch_layer_via_convert_on_gpu(m3, name):
+    fx = dict(np.load(GOLDEN / f"{name}.npz", allow_pickle=False))
+    sd = {k[4:].replace("__", "."): torch.from_numpy(v) for k, v in fx.items() if k.startswith("sd__")}
+    d_model, n, p, expand = (int(v) for v in fx["cfg"])
+    if not m3.kernels._lib.supported(0, 0, 32, n, p):
+        pytest.skip(f"no f32 kernel for N={n} P={p}")
+    cfg = m3.convert.config_from_state_dict(sd, headdim=p, chunk=32, policy_name="f32",
+                                            rope_fraction=float(fx["rope_fraction"]))
+    params = m3.convert.torch_to_jax(sd, cfg, device="cuda")
+    y, _ = m3.mamba3_siso_layer(params, torch.from_numpy(fx["u"]).cuda(), cfg)
+    assert O.max_rel(cpu(y), torch.from_numpy(fx["y"]).double()) <= 1e-4
+
+
+def test_segmented_prefill_equals_one_call_with_gradients(m3):
+    """tests.py:653-726 at layer level: two chained segments == one call, grads too."""
+    cfg = m3.SISOConfig(d_model=64, d_state=16, headdim=16, expand=1, chunk=32, policy_name="f32")
+    params = m3.SISOParams(*(t.cuda() for t in m3.init_params(cfg, 3)))
+    g = torch.Generator().manual_seed(4)
+    u = torch.randn(2, 256, 64, generator=g).cuda()
+    gy = torch.randn(2, 256, 64, generator=g).cuda()
+    u1 = u.clone().requires_grad_(True)
+    y_full, st_full = m3.mamba3_siso_layer(params, u1, cfg)
+    (y_full * gy).sum().backward()
+    u2 = u.clone().requires_grad_(True)
+    ya, sa = m3.mamba3_siso_layer(params, u2[:, :128], cfg)
+    yb, sb = m3.mamba3_siso_layer(params, u2[:, 128:], cfg, state=sa)
+    (torch.cat([ya, yb], 1) * gy).sum().backward()
+    assert O.rel_error(cpu(torch.cat([ya, yb], 1)), cpu(y_full)) <= 2e-5
+    assert O.rel_error(cpu(sb.ssm), cpu(st_full.ssm)) <= 2e-5
+    assert O.rel_error(cpu(sb.phi), cpu(st_full.phi), angle=True) <= 1e-4
+    assert O.rel_error(cpu(u2.grad), cpu(u1.grad)) <= GRAD_F32_P95
+
+
+def test_layer_bf16_forward_and_grads(m3):
+    cfg = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=128)
+    p_cpu = m3.init_params(cfg, 5)
+    g = torch.Generator().manual_seed(6)
+    u = torch.randn(2, 512, 256, generator=g).to(BF16)
+    gy = torch.randn(2, 512, 256, generator=g).to(BF16)
+    params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+    ud = u.cuda().requires_grad_(True)
+    y, st = m3.mamba3_siso_layer(params, ud, cfg)
+    (y.float() * gy.cuda().float()).sum().backward()
+    pd = {k_: v_.requires_grad_(True) for k_, v_ in params_dict(p_cpu).items()}
+    uo = u.double().requires_grad_(True)
+    yr, sr = O.layer_forward(pd, uo, d_state=128, headdim=64, expand=2, chunk=128)
+    (yr * gy.double()).sum().backward()
+    # bf16 GEMMs on both sides of the scan make small outputs cancellation-prone, so the
+    # layer-level bf16 check is max-normalised only
+    assert_maxrel(y, yr.detach(), BF16_MAXREL, "y")
+    assert_maxrel(st.ssm, sr.ssm.detach(), BF16_MAXREL, "ssm")
+    assert_maxrel(ud.grad, uo.grad, 3 * BF16_MAXREL, "du")
+    for f in ("in_proj", "out_proj", "dt_bias", "b_bias", "c_bias", "d_skip"):
+        assert_maxrel(getattr(params, f).grad, pd[f].grad, 3 * BF16_MAXREL, f"d{f}")
+
+
+@pytest.mark.parametrize("policy", ["f32", "bf16"])
+def test_layer_decode_step_matches_oracle(m3, policy):
+    cfg = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=128, policy_name=policy)
+    p_cpu = m3.init_params(cfg, 7)
+    params = m3.SISOParams(*(t.cuda() for t in p_cpu))
+    g = torch.Generator().manual_seed(8)
+    B, H, P, N, Nr = 3, cfg.nheads, 64, 128, cfg.n_angles
+    st = O.SISOState(torch.randn(B, H, P, N, generator=g, dtype=torch.float64).float().double() * 0.1,
+                     torch.randn(B, H, N, generator=g, dtype=torch.float64).float().double(),
+                     torch.randn(B, H, P, generator=g, dtype=torch.float64).float().double(),
+                     (torch.rand(B, H, Nr, generator=g, dtype=torch.float64) * 6).float().double())
+    mt = BF16 if policy == "bf16" else torch.float32
+    u = torch.randn(B, 256, generator=g).to(mt)
+    y, s2 = m3.mamba3_siso_decode_step(params, u.cuda(), cfg,
+                                       m3.SISOState(*(t.float().cuda() for t in st)))
+    yr, sr = O.layer_decode_step(params_dict(p_cpu), u.double(), st, d_state=N, headdim=P,
+                                 mm_dtype=BF16 if policy == "bf16" else None)
+    if policy == "f32":
+        assert_p95(y, yr, 1e-4, "y")
+        assert_p95(s2.ssm, sr.ssm, 2e-5, "ssm")
+    else:
+        assert_maxrel(y, yr, BF16_MAXREL, "y")
+        assert_maxrel(s2.ssm, sr.ssm, BF16_MAXREL, "ssm")

@@ -317,7 +317,7 @@ def test_step_matches_reference_torch_golden_first_tokens():
     """One decode step from a zero state is the first token of upstream's recurrence."""
     fx = _load("torch_ref_kernel_gated")
     x, t, perm = _golden_kernel_inputs(fx)
-    b, h, p, n = 2, 3, 8, 16
+    b, h, p, n = 2, 3, 16, 16
     st = O.zero_state(b, h, p, n, 4)
     angles = t["angles"]
     for tt in range(3):
