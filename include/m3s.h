@@ -77,7 +77,8 @@ typedef struct m3s_fwd_args {
 
 /* Reverse-scan backward. Replaces `kernel_bwd.siso_backward_kernel`
  * (kernel_bwd.py:358-511) plus the dfinal_v injection of `siso_backward`
- * (kernel_bwd.py:632-637). dq/dk are summed over heads (zeroed by this call). */
+ * (kernel_bwd.py:632-637). The per-head dq/dk rows go to `workspace` and a second
+ * launch sums them over heads into dq/dk (deterministic; no atomics). */
 typedef struct m3s_bwd_args {
   int32_t struct_size; /* sizeof(m3s_bwd_args) */
   int32_t batch, seqlen, nheads, headdim, state_dim, n_angles, chunk;
@@ -112,6 +113,7 @@ typedef struct m3s_bwd_args {
   float* dk_bias;              /* out (B, H, N)                                        */
   float* k_final;              /* out (B, H, N) rotated k at the last position         */
   float* dseed_ssm;            /* out (B, H, P, N) adjoint of the seeded state         */
+  void* workspace;             /* scratch, m3s_bwd_workspace_bytes() bytes, 16-aligned */
 } m3s_bwd_args;
 
 /* Single-token decode, in place. Replaces `kernel_decode.siso_decode_folded` /
@@ -149,6 +151,12 @@ const char* m3s_last_error(void);
  * chunk = 0. `which` is 0 = forward, 1 = backward, 2 = decode. */
 int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, int32_t state_dim,
                       int32_t headdim);
+
+/* Bytes of m3s_bwd_args.workspace: the per-head dq/dk rows, 2*B*H*L*N elements of
+ * the dtype. No counterpart in the reference (its head sum is an in-kernel
+ * accumulation over an H-innermost grid, kernel_bwd.py:324-333). */
+int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen, int32_t nheads,
+                                int32_t state_dim);
 
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);

@@ -56,6 +56,7 @@ class BwdArgs(C.Structure):
         ("dq", vp), ("dk", vp), ("dv", Bhlp), ("dz", Bhlp),
         ("dadt", vp), ("dqk_diag", vp), ("dscale", vp), ("uw", vp), ("dphi", vp),
         ("dq_bias", vp), ("dk_bias", vp), ("k_final", vp), ("dseed_ssm", vp),
+        ("workspace", vp),
     ]
 
 
@@ -75,8 +76,8 @@ class DecodeArgs(C.Structure):
 
 
 #: Every symbol ``include/m3s.h`` declares.
-EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_fwd", "m3s_bwd",
-           "m3s_decode")
+EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
+           "m3s_fwd", "m3s_bwd", "m3s_decode")
 
 _lib = None
 
@@ -97,6 +98,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_last_error.restype = C.c_char_p
     lib.m3s_supported.restype = i32
     lib.m3s_supported.argtypes = [i32, i32, i32, i32, i32]
+    lib.m3s_bwd_workspace_bytes.restype = i64
+    lib.m3s_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.m3s_fwd.restype = i32
     lib.m3s_fwd.argtypes = [C.POINTER(FwdArgs), vp]
     lib.m3s_bwd.restype = i32

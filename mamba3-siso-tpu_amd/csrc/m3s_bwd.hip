@@ -64,6 +64,7 @@ struct BwdParams {
   float* dkb;
   float* kfin;
   float* dseed;
+  void* part;   // (2, B, H, L, N) per-head du / dw rows, MT
 };
 
 template <typename MT> struct BV16;
@@ -189,8 +190,8 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   const float* sclg = p.scale + bh * L;
   const float* phig = p.phi + bh * (int64_t)L * Nr;
   const MT* csg = static_cast<const MT*>(p.cstates) + bh * (int64_t)nc * N * P;
-  float* dqg = p.dq + (int64_t)b * L * N;
-  float* dkg = p.dk + (int64_t)b * L * N;
+  MT* dug = static_cast<MT*>(p.part) + bh * (int64_t)L * N;                 // du rows of (b, h)
+  MT* dwg = static_cast<MT*>(p.part) + ((int64_t)p.B * p.H + bh) * L * N;   // dw rows of (b, h)
   const bool phi_vec = (Nr % 4) == 0;
 
   // ---- adjoint G (registers, MFMA layout [p][n]) -----------------------------------
@@ -439,6 +440,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
     }
     __syncthreads();
 
+    if (c > 0) prefetch(c - 1);   // in flight during the products of this chunk
     // ============ phase P1: register score tiles, inter-chunk terms ===================
     const int w = wave;
     const bool strip = w < CB;
@@ -686,6 +688,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
           const float sc = sScl[t];
           const float cd = sDqk[t] * sGam[t];
           const float* pr = phig + tg * Nr;
+          vec du0, du1, dw0, dw1;
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             const int j = j0 + i;
@@ -713,15 +716,20 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
               p.kfin[bh * N + j] = klo;
               p.kfin[bh * N + H2 + j] = khi;
             }
-            unsafeAtomicAdd(dqg + tg * N + j, dulo);
-            unsafeAtomicAdd(dqg + tg * N + H2 + j, duhi);
-            unsafeAtomicAdd(dkg + tg * N + j, dwlo);
-            unsafeAtomicAdd(dkg + tg * N + H2 + j, dwhi);
+            du0[i] = dulo;
+            du1[i] = duhi;
+            dw0[i] = dwlo;
+            dw1[i] = dwhi;
             bq[0][i] += dulo;
             bq[1][i] += duhi;
             bk[0][i] += dwlo;
             bk[1][i] += dwhi;
           }
+          // this head's du / dw row pieces; the head sum happens in headsum_kernel
+          *reinterpret_cast<vec*>(dug + tg * N + j0) = du0;
+          *reinterpret_cast<vec*>(dug + tg * N + H2 + j0) = du1;
+          *reinterpret_cast<vec*>(dwg + tg * N + j0) = dw0;
+          *reinterpret_cast<vec*>(dwg + tg * N + H2 + j0) = dw1;
         }
       }
       dA[0] = group_sum<F::QKG>(dA[0]);
@@ -757,7 +765,6 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
     __syncthreads();
 
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
-    if (c > 0) prefetch(c - 1);
     if (wave == 0) {
       const float extra = sRed[0];
       float a[F::E];
@@ -805,24 +812,37 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   }
 }
 
-__global__ void zero_kernel(float4* a, float4* b, int64_t n4) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n4) {
-    a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    b[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+// dq[b, t, :] = sum_h du[b, h, t, :] (and dk from dw): one thread per 4 consecutive
+// elements of a (b, t) row, summing over heads in f32. Bandwidth-bound.
+template <typename MT>
+__global__ void __launch_bounds__(256) headsum_kernel(const MT* __restrict__ part,
+                                                      float* __restrict__ dq,
+                                                      float* __restrict__ dk, int B, int H,
+                                                      int64_t LN) {
+  const int64_t i4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int which = blockIdx.y;           // 0: dq from du, 1: dk from dw
+  const int b = blockIdx.z;
+  if (i4 >= LN) return;
+  const MT* src = part + ((int64_t)which * B + b) * H * LN + i4;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < H; ++h) {
+    const sub_t<MT> v = *reinterpret_cast<const sub_t<MT>*>(src + h * LN);
+    acc += sub_to_f32<MT>(v);
   }
+  *reinterpret_cast<f32x4*>((which ? dk : dq) + (int64_t)b * LN + i4) = acc;
 }
 
 template <typename MT, int C, int N, int P>
 static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
-  const int64_t n4 = (int64_t)prm.B * prm.L * N / 4;
-  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
-                     reinterpret_cast<float4*>(prm.dq), reinterpret_cast<float4*>(prm.dk), n4);
-  int32_t rc = launch_status("m3s_bwd (zero dq/dk)");
-  if (rc != M3S_OK) return rc;
   hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
-  return launch_status("m3s_bwd");
+  int32_t rc = launch_status("m3s_bwd");
+  if (rc != M3S_OK) return rc;
+  const int64_t LN = (int64_t)prm.L * N;
+  const dim3 hgrid((unsigned)((LN / 4 + 255) / 256), 2, prm.B);
+  hipLaunchKernelGGL((headsum_kernel<MT>), hgrid, dim3(256), 0, stream,
+                     static_cast<const MT*>(prm.part), prm.dq, prm.dk, prm.B, prm.H, LN);
+  return launch_status("m3s_bwd (head sum)");
 }
 
 #define M3S_BWD_CONFIGS(X) \
@@ -854,6 +874,12 @@ int32_t bwd_supported(int dtype, int chunk, int n, int pdim) {
 }
 
 }  // namespace m3s
+
+extern "C" int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen,
+                                           int32_t nheads, int32_t state_dim) {
+  const int64_t el = dtype == M3S_DTYPE_BF16 ? 2 : 4;
+  return 2 * (int64_t)batch * nheads * seqlen * state_dim * el;
+}
 
 extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
   using namespace m3s;
@@ -889,8 +915,8 @@ extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
   M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_bwd: has_d but d_skip is NULL");
   M3S_REQUIRE(a->dq && a->dk && aligned16(a->dq) && aligned16(a->dk) && a->dadt && a->dqk_diag &&
                   a->dscale && a->uw && a->dq_bias && a->dk_bias && a->k_final && a->dseed_ssm &&
-                  (Nr == 0 || a->dphi),
-              "m3s_bwd: an output pointer is NULL or misaligned");
+                  (Nr == 0 || a->dphi) && a->workspace && aligned16(a->workspace),
+              "m3s_bwd: an output or workspace pointer is NULL or misaligned");
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_bwd: B*H too large");
 
   BwdParams prm{};
@@ -912,6 +938,7 @@ extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
   prm.dadt = a->dadt; prm.dqk = a->dqk_diag; prm.dscale = a->dscale; prm.uw = a->uw;
   prm.dphi = a->dphi; prm.dqb = a->dq_bias; prm.dkb = a->dk_bias; prm.kfin = a->k_final;
   prm.dseed = a->dseed_ssm;
+  prm.part = a->workspace;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int grid = B * H;
 #define X(MT, CC, NN, PP)                                              \

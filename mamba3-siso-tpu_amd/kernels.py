@@ -363,6 +363,8 @@ def siso_backward_kernel(
     dkb = torch.empty(batch, nheads, state_dim, **f32)
     kfin = torch.empty(batch, nheads, state_dim, **f32)
     dseed = torch.empty(batch, nheads, headdim, state_dim, **f32)
+    ws_bytes = _lib.load().m3s_bwd_workspace_bytes(dcode, batch, seqlen, nheads, state_dim)
+    workspace = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
 
     a = _lib.BwdArgs()
     a.struct_size = ctypes.sizeof(_lib.BwdArgs)
@@ -379,6 +381,7 @@ def siso_backward_kernel(
     a.dadt, a.dqk_diag, a.dscale, a.uw = (t.data_ptr() for t in (dadt, dqk, dscale, uw))
     a.dphi, a.dq_bias, a.dk_bias = dphi.data_ptr(), dqb.data_ptr(), dkb.data_ptr()
     a.k_final, a.dseed_ssm = kfin.data_ptr(), dseed.data_ptr()
+    a.workspace = workspace.data_ptr()
     with torch.cuda.device(dev):
         _lib.check(_lib.load().m3s_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_bwd")
     return KernelGrads(dq=dq, dk=dk, dv=dv, dadt=dadt, dqk_diag=dqk, dscale=dscale, dphi=dphi,

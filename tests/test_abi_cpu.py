@@ -23,7 +23,7 @@ def lib(m3):
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int32_t|const char\*)\s+(m3s_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char\*)\s+(m3s_\w+)\s*\(", text, re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol(lib):
@@ -95,6 +95,12 @@ def test_unsupported_shapes_and_bad_dims_are_reported(lib):
     a.n_angles = 32   # now only the pointers are missing
     assert h.m3s_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
     assert b"q/k" in h.m3s_last_error()
+
+
+def test_workspace_size(lib):
+    h = lib.load()
+    assert h.m3s_bwd_workspace_bytes(lib.DTYPE_BF16, 8, 8192, 32, 128) == 2 * 8 * 32 * 8192 * 128 * 2
+    assert h.m3s_bwd_workspace_bytes(lib.DTYPE_F32, 1, 64, 2, 16) == 2 * 2 * 64 * 16 * 4
 
 
 def test_capability_table(lib):
