@@ -36,6 +36,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=512)
+    ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy"), default="all",
+                    help="run one leg alone (for rocprofv3 counter passes): 'scan' = the forward "
+                         "scan kernel at the kernel boundary, 'bwd' = the backward scan kernel, "
+                         "'decode' = the decode kernel, 'copy' = a plain 1 GiB device copy that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -53,6 +58,21 @@ def gpu_time_ms(fn, iters, torch):
     return start.elapsed_time(end) / iters
 
 
+def scan_inputs(m3, params16, cfg, u, torch):
+    """Kernel-boundary operands of the configs[1] layer: the projections of ``u`` through
+    split_in_proj, BCNorm and preprocess, exactly as the layer hands them to the scan."""
+    with torch.no_grad():
+        proj = u @ params16.in_proj
+        z, x, bb, cc, dt_raw, a_raw, trap_raw, angles = m3.split_in_proj(proj, cfg)
+        kq = m3.rms_norm(cc, params16.c_norm_weight, cfg.norm_eps)
+        kk = m3.rms_norm(bb, params16.b_norm_weight, cfg.norm_eps)
+        pre, _ = m3.preprocess(dt_raw, a_raw, trap_raw, angles, params16.dt_bias)
+        kv, kz = x.permute(0, 2, 1, 3), z.permute(0, 2, 1, 3)
+    return dict(q=kq, k=kk, v=kv, adt=pre.adt, gamma=pre.gamma, scale=pre.scale, phi=pre.phi,
+                q_bias=params16.c_bias.float(), k_bias=params16.b_bias.float(),
+                d_skip=params16.d_skip.float(), z=kz)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -68,6 +88,19 @@ def main():
     from mamba3_siso_tpu_amd import kernels as K
 
     dev = torch.device("cuda:0")
+    if args.leg == "copy":
+        # 1 GiB read + 1 GiB written by one plain copy kernel: the FETCH_SIZE / WRITE_SIZE
+        # calibration for the traffic figures.
+        src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        ms = gpu_time_ms(lambda: dst.copy_(src), 10, torch)
+        print(json.dumps({"leg": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30,
+                          "ms": round(ms, 4), "gbs": round(2 * (1 << 30) / (ms * 1e-3) / 1e9, 1)}))
+        return
+
     B, L, H, P, N, DM = 8, 8192, 32, 64, 128, 1024
     cfg = m3.SISOConfig(d_model=DM, d_state=N, headdim=P, expand=2, chunk=128, policy_name="bf16")
     assert cfg.nheads == H
@@ -79,43 +112,94 @@ def main():
     gen = torch.Generator(device=dev)
     u = torch.randn(B, L, DM, generator=gen.manual_seed(0), device=dev).to(torch.bfloat16)
     tokens = B * L
+    line = {}
 
-    # ---------------- headline: layer forward ---------------------------
-    def fwd_step():
-        with torch.no_grad():
-            return m3.mamba3_siso_layer(params16, u, cfg)
-
-    for _ in range(args.warmup):
-        fwd_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        fwd_step()
-    torch.cuda.synchronize()
-    fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    # ---------------- the scan kernel alone, kernel boundary -------------------------
-    with torch.no_grad():
-        proj = u @ params16.in_proj
-        z, x, bb, cc, dt_raw, a_raw, trap_raw, angles = m3.split_in_proj(proj, cfg)
-        kq = m3.rms_norm(cc, params16.c_norm_weight, cfg.norm_eps)
-        kk = m3.rms_norm(bb, params16.b_norm_weight, cfg.norm_eps)
-        pre, _ = m3.preprocess(dt_raw, a_raw, trap_raw, angles, params16.dt_bias)
-        kv, kz = x.permute(0, 2, 1, 3), z.permute(0, 2, 1, 3)
-        kargs = (kq, kk, kv, pre.adt, pre.gamma, pre.scale, pre.phi, params16.c_bias.float(),
-                 params16.b_bias.float(), params16.d_skip.float(), kz)
-        scan = lambda: K.siso_forward(*kargs, chunk=128)  # noqa: E731
-        for _ in range(3):
-            scan()
-        scan_ms = gpu_time_ms(scan, 20, torch)
-        del proj
-    # algorithmic bytes of one launch: q, k once (head-shared), v, z, y bf16;
+    # ---------------- the scan kernels alone, kernel boundary -------------------------
+    # algorithmic bytes of one forward launch: q, k once (head-shared), v, z, y bf16;
     # adt/gamma/scale f32; phi f32; final ssm f32 (+ k, v rows)
     scan_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * H * L * 4
                   + B * H * L * Nr * 4 + B * H * P * N * 4 + B * H * (N + P) * 4)
     scan_flops = B * H * L * 2 * (2 * N * P + cfg.chunk * N + cfg.chunk * P)
-    scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
-    scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
+    if args.leg in ("all", "scan", "bwd"):
+        ka = scan_inputs(m3, params16, cfg, u, torch)
+        if args.leg in ("all", "scan"):
+            scan = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
+            for _ in range(args.warmup):
+                scan()
+            scan_ms = gpu_time_ms(scan, args.steps, torch)
+            scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
+            scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
+            line.update(scan_kernel_ms=round(scan_ms, 4),
+                        scan_kernel_tok_s=round(tokens / (scan_ms * 1e-3), 1),
+                        scan_kernel_gbs=round(scan_gbs, 1),
+                        scan_kernel_tflops=round(scan_tflops, 2),
+                        scan_kernel_mfma_frac=round(scan_tflops / BF16_PEAK_TFLOPS, 5))
+            line["roofline"] = {
+                "kernel": "fwd_kernel<bf16,128,128,64> (m3s_fwd, kernel boundary)",
+                "bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
+                "traffic": traffic_figure("fwd_kernel"), "algorithmic_bytes": scan_bytes}
+        if args.leg in ("all", "bwd"):
+            with torch.no_grad():
+                y, fs, fk, fv, res = K.siso_forward(**ka, chunk=128, save_residuals=True)
+                dyk = torch.randn(y.shape, generator=gen.manual_seed(2), device=dev
+                                  ).to(torch.bfloat16)
+                bw = lambda: K.siso_backward_kernel(  # noqa: E731
+                    dyk, res.ybar, ka["z"], ka["q"], ka["k"], ka["v"], ka["adt"], ka["gamma"],
+                    ka["scale"], ka["phi"], ka["q_bias"], ka["k_bias"], res.chunk_states,
+                    d_skip=ka["d_skip"], chunk=128)
+                for _ in range(max(1, args.warmup)):
+                    bw()
+                bwd_ms = gpu_time_ms(bw, max(3, args.steps // 2), torch)
+            bwd_flops = B * H * L * (2 * cfg.chunk * (3 * N + 2 * P) + 8 * P * N)
+            line.update(bwd_kernel_ms=round(bwd_ms, 4),
+                        bwd_kernel_tflops=round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2))
+            del y, res, dyk
+        del ka
+        torch.cuda.empty_cache()
+        if args.leg != "all":
+            print(json.dumps({"leg": args.leg, **line}))
+            return
+
+    # ---------------- decode (configs[3]) ---------------------------------------------
+    BD, T = 256, args.decode_tokens
+
+    def rnd(shape, seed, scale=1.0):
+        return torch.randn(*shape, generator=gen.manual_seed(seed), device=dev) * scale
+
+    state = m3.SISOState(rnd((BD, H, P, N), 3, 0.1), rnd((BD, H, N), 4), rnd((BD, H, P), 5),
+                         torch.rand(BD, H, Nr, generator=gen.manual_seed(6), device=dev) * 2 * math.pi)
+    with torch.no_grad():
+        q1 = torch.randn(BD, N, device=dev).to(torch.bfloat16)
+        v1 = torch.randn(BD, H, P, device=dev).to(torch.bfloat16)
+        s1 = torch.full((BD, H), 0.01, device=dev)
+        ang1 = torch.randn(BD, Nr, device=dev)
+        dstep = lambda: K.decode_step(q1, q1, v1, -s1, s1, s1 * 50, ang1,  # noqa: E731
+                                      params16.c_bias.float(), params16.b_bias.float(), state,
+                                      params16.d_skip.float(), v1)
+        for _ in range(args.warmup):
+            dstep()
+        dec_kernel_ms = gpu_time_ms(dstep, 50, torch)
+    dec_bytes = (2 * BD * H * P * N * 4 + 2 * BD * H * (N + P + Nr) * 4
+                 + BD * N * 2 * 2 + 3 * BD * H * P * 2 + 3 * BD * H * 4 + BD * Nr * 4)
+    dec_gbs = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
+    line.update(decode_kernel_ms=round(dec_kernel_ms, 4), decode_kernel_gbs=round(dec_gbs, 1),
+                decode_kernel_hbm_frac=round(dec_gbs / HBM_PEAK_GBS, 4))
+    if args.leg == "decode":
+        print(json.dumps({"leg": "decode", **line}))
+        return
+    toks = [rnd((BD, DM), 1000 + t).to(torch.bfloat16) for t in range(T)]
+    with torch.no_grad():
+        for t in range(4):
+            _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(T):
+            _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
+        torch.cuda.synchronize()
+        dec_ms = (time.perf_counter() - t0) * 1e3 / T
+    del toks, state
+    torch.cuda.empty_cache()
 
     # ---------------- forward + backward ---------------------------------
     pg = m3.SISOParams(*(t.detach().clone().requires_grad_(True) for t in params32))
@@ -138,45 +222,26 @@ def main():
     del pg, ug, dy
     torch.cuda.empty_cache()
 
-    # ---------------- decode (configs[3]) ---------------------------------------------
-    BD, T = 256, args.decode_tokens
+    # ---------------- headline: layer forward, the K timed steps ----------
+    def fwd_step():
+        with torch.no_grad():
+            return m3.mamba3_siso_layer(params16, u, cfg)
 
-    def rnd(shape, seed, scale=1.0):
-        return torch.randn(*shape, generator=gen.manual_seed(seed), device=dev) * scale
-
-    state = m3.SISOState(rnd((BD, H, P, N), 3, 0.1), rnd((BD, H, N), 4), rnd((BD, H, P), 5),
-                         torch.rand(BD, H, Nr, generator=gen.manual_seed(6), device=dev) * 2 * math.pi)
-    toks = [rnd((BD, DM), 1000 + t).to(torch.bfloat16) for t in range(T)]
-    with torch.no_grad():
-        for t in range(4):
-            _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for t in range(T):
-            _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
-        torch.cuda.synchronize()
-        dec_ms = (time.perf_counter() - t0) * 1e3 / T
-        # the decode kernel alone
-        q1 = torch.randn(BD, N, device=dev).to(torch.bfloat16)
-        v1 = torch.randn(BD, H, P, device=dev).to(torch.bfloat16)
-        s1 = torch.full((BD, H), 0.01, device=dev)
-        ang1 = torch.randn(BD, Nr, device=dev)
-        dstep = lambda: K.decode_step(q1, q1, v1, -s1, s1, s1 * 50, ang1,  # noqa: E731
-                                      params16.c_bias.float(), params16.b_bias.float(), state,
-                                      params16.d_skip.float(), v1)
-        dec_kernel_ms = gpu_time_ms(dstep, 50, torch)
-    dec_bytes = (2 * BD * H * P * N * 4 + 2 * BD * H * (N + P + Nr) * 4
-                 + BD * N * 2 * 2 + 3 * BD * H * P * 2 + 3 * BD * H * 4 + BD * Nr * 4)
-    dec_gbs = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
-    del toks, state
-    torch.cuda.empty_cache()
+    for _ in range(args.warmup):
+        fwd_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fwd_step()
+    torch.cuda.synchronize()
+    fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # ---------------- CPU baseline: the oracle on a bounded sample --------------------
     cpu_base = None
     if not args.no_cpu_baseline:
         cpu_base = cpu_baseline(m3, params32, cfg, torch)
 
-    line = {
+    out = {
         "metric": METRIC,
         "value": round(tokens / (fwd_ms * 1e-3), 1),
         "unit": "tok/s",
@@ -196,22 +261,27 @@ def main():
         "fwd_bwd_ms": round(fb_ms, 3),
         "fwd_bwd_tok_s": round(tokens / (fb_ms * 1e-3), 1),
         "decode_ms_per_token": round(dec_ms, 4),
-        "decode_kernel_ms": round(dec_kernel_ms, 4),
-        "decode_kernel_gbs": round(dec_gbs, 1),
-        "decode_kernel_hbm_frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-        "scan_kernel_ms": round(scan_ms, 4),
-        "scan_kernel_tok_s": round(tokens / (scan_ms * 1e-3), 1),
-        "scan_kernel_tflops": round(scan_tflops, 2),
-        "scan_kernel_mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5),
+        **{k: v for k, v in line.items() if k != "roofline"},
         "reference_tpu_v5e": {"fwd_kernel_ms_chunk128_pinned": 21.66, "fwd_bwd_ms": 80.1,
                               "decode_ms_per_token_b256": 1.4},
-        "roofline": {"kernel": "m3s_fwd (bf16, chunk 128, kernel boundary)", "bound": "hbm",
-                     "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(scan_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes": scan_bytes},
+        "roofline": line["roofline"],
         "cpu_baseline": cpu_base,
     }
-    print(json.dumps(line))
+    print(json.dumps(out))
+
+
+def traffic_figure(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the
+    ratio the same counter shows for a plain 1 GiB copy), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("traffic_bytes")
 
 
 def cpu_baseline(m3, params32, cfg, torch):

@@ -20,8 +20,10 @@
 // already an operand fragment with its row index as K (see m3s_common.h). Operands
 // whose K is their row index (q~, khat, g over time) are served from transposed LDS
 // copies, built in place by one transpose pass between the two product phases. The
-// elementwise pullback runs row-major on f32 dq~/dkhat staged through LDS, so the
-// head-sum of dq/dk is a coalesced f32 atomic add per row.
+// elementwise pullback runs row-major on f32 dq~/dkhat staged through LDS and writes
+// each head's du/dw rows to the workspace with coalesced 16-byte stores; a second,
+// HBM-bound launch (headsum_kernel) sums them over heads into dq/dk, so the result
+// does not depend on the order in which workgroups finish.
 #include "m3s_common.h"
 #include "m3s_internal.h"
 
