@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 1
+#define M3S_ABI_VERSION 2
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -43,6 +43,13 @@ typedef struct m3s_bhlp {
   void* ptr;
   int64_t stride_b, stride_h, stride_t; /* elements */
 } m3s_bhlp;
+
+/* A (B, L, X) operand: base pointer plus b and t element strides; X is contiguous.
+ * The layer passes the raw slices of its fused projection (B, L, d_in_proj) this way. */
+typedef struct m3s_blx {
+  void* ptr;
+  int64_t stride_b, stride_t; /* elements */
+} m3s_blx;
 
 /* Chunked forward. Replaces `kernel_fwd.siso_forward` (kernel_fwd.py:204-388),
  * i.e. the `pl.pallas_call(_fwd_kernel, grid=(B, nc, H))` at kernel_fwd.py:367-380. */
@@ -143,6 +150,58 @@ typedef struct m3s_decode_args {
   void* y;                /* out (B, H, P)                 */
 } m3s_decode_args;
 
+/* Per-token preprocessing. Replaces `reference.preprocess` (reference.py:160-199) with
+ * `heavy_tail` (202-209), `trapezoid_coeffs` (104-131) and `cumulative_angles`
+ * (134-157): dt = softplus(dt_raw + dt_bias), lam = sigmoid(trap_raw),
+ * a = min(-heavy_tail(a_raw), -a_floor), adt = a dt, gamma = dt lam,
+ * scale_t = gamma_t + dt_{t+1}(1 - lam_{t+1}), phi = wrap(phi_init + cumsum tanh(angles) pi dt). */
+typedef struct m3s_prep_fwd_args {
+  int32_t struct_size; /* sizeof(m3s_prep_fwd_args) */
+  int32_t batch, seqlen, nheads, n_angles;
+  int32_t dtype;       /* M3S_DTYPE_* of dt_raw, a_raw, trap_raw and angles */
+  int32_t has_phi_init;
+  float a_floor;
+  m3s_blx dt_raw;      /* (B, L, H)                       */
+  m3s_blx a_raw;       /* (B, L, H)                       */
+  m3s_blx trap_raw;    /* (B, L, H)                       */
+  m3s_blx angles;      /* (B, L, Nr), shared by the heads */
+  const float* dt_bias;  /* (H)                           */
+  const float* phi_init; /* (B, H, Nr), if has_phi_init   */
+  float* adt;          /* out (B, H, L)                   */
+  float* gamma;        /* out (B, H, L)                   */
+  float* scale;        /* out (B, H, L)                   */
+  float* lam;          /* out (B, H, L)                   */
+  float* dt;           /* out (B, H, L)                   */
+  float* phi;          /* out (B, H, L, Nr)               */
+  float* phi_final;    /* out (B, H, Nr) = phi[:, :, L-1] */
+} m3s_prep_fwd_args;
+
+/* Backward of m3s_prep_fwd: the reference obtains it from jax.grad of `preprocess`
+ * (siso.py:1-11). Every cotangent input may be NULL (= zero). The dangles output is
+ * summed over heads (angles are shared); ddt_bias is summed over batch and time. */
+typedef struct m3s_prep_bwd_args {
+  int32_t struct_size; /* sizeof(m3s_prep_bwd_args) */
+  int32_t batch, seqlen, nheads, n_angles;
+  int32_t dtype;       /* dtype of the raw inputs and of the raw cotangents */
+  float a_floor;
+  m3s_blx dt_raw, a_raw, trap_raw, angles; /* the forward's inputs           */
+  const float* dt_bias;                    /* (H)                            */
+  const float* dadt;                       /* (B, H, L) or NULL              */
+  const float* dgamma;                     /* (B, H, L) or NULL              */
+  const float* dscale;                     /* (B, H, L) or NULL              */
+  const float* dlam;                       /* (B, H, L) or NULL              */
+  const float* ddt;                        /* (B, H, L) or NULL              */
+  const float* dphi;                       /* (B, H, L, Nr) or NULL          */
+  const float* dphi_final;                 /* (B, H, Nr) or NULL             */
+  m3s_blx ddt_raw;                         /* out (B, L, H)                  */
+  m3s_blx da_raw;                          /* out (B, L, H)                  */
+  m3s_blx dtrap_raw;                       /* out (B, L, H)                  */
+  m3s_blx dangles;                         /* out (B, L, Nr)                 */
+  float* ddt_bias;                         /* out (H)                        */
+  float* dphi_init;                        /* out (B, H, Nr) or NULL         */
+  void* workspace; /* scratch, m3s_prep_bwd_workspace_bytes() bytes, 16-aligned */
+} m3s_prep_bwd_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -158,9 +217,17 @@ int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, int32_t state
 int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen, int32_t nheads,
                                 int32_t state_dim);
 
+/* Bytes of m3s_prep_bwd_args.workspace: the suffix-summed phi cotangent (B, H, L, Nr)
+ * f32 and the per-block dt_bias partials. No counterpart in the reference. -1 on bad
+ * dimensions. */
+int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
+                                     int32_t n_angles);
+
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
 int32_t m3s_decode(const m3s_decode_args* args, void* stream);
+int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
+int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
 
 #ifdef __cplusplus
 }

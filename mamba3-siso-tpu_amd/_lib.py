@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -24,6 +24,10 @@ i32, i64, vp = C.c_int32, C.c_int64, C.c_void_p
 
 class Bhlp(C.Structure):
     _fields_ = [("ptr", vp), ("stride_b", i64), ("stride_h", i64), ("stride_t", i64)]
+
+
+class Blx(C.Structure):
+    _fields_ = [("ptr", vp), ("stride_b", i64), ("stride_t", i64)]
 
 
 class FwdArgs(C.Structure):
@@ -75,9 +79,37 @@ class DecodeArgs(C.Structure):
     ]
 
 
+class PrepFwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("nheads", i32), ("n_angles", i32),
+        ("dtype", i32), ("has_phi_init", i32), ("a_floor", C.c_float),
+        ("dt_raw", Blx), ("a_raw", Blx), ("trap_raw", Blx), ("angles", Blx),
+        ("dt_bias", vp), ("phi_init", vp),
+        ("adt", vp), ("gamma", vp), ("scale", vp), ("lam", vp), ("dt", vp),
+        ("phi", vp), ("phi_final", vp),
+    ]
+
+
+class PrepBwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("nheads", i32), ("n_angles", i32),
+        ("dtype", i32), ("a_floor", C.c_float),
+        ("dt_raw", Blx), ("a_raw", Blx), ("trap_raw", Blx), ("angles", Blx),
+        ("dt_bias", vp),
+        ("dadt", vp), ("dgamma", vp), ("dscale", vp), ("dlam", vp), ("ddt", vp),
+        ("dphi", vp), ("dphi_final", vp),
+        ("ddt_raw", Blx), ("da_raw", Blx), ("dtrap_raw", Blx), ("dangles", Blx),
+        ("ddt_bias", vp), ("dphi_init", vp),
+        ("workspace", vp),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
-           "m3s_fwd", "m3s_bwd", "m3s_decode")
+           "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
+           "m3s_prep_fwd", "m3s_prep_bwd")
 
 _lib = None
 
@@ -106,6 +138,12 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_bwd.argtypes = [C.POINTER(BwdArgs), vp]
     lib.m3s_decode.restype = i32
     lib.m3s_decode.argtypes = [C.POINTER(DecodeArgs), vp]
+    lib.m3s_prep_bwd_workspace_bytes.restype = i64
+    lib.m3s_prep_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    lib.m3s_prep_fwd.restype = i32
+    lib.m3s_prep_fwd.argtypes = [C.POINTER(PrepFwdArgs), vp]
+    lib.m3s_prep_bwd.restype = i32
+    lib.m3s_prep_bwd.argtypes = [C.POINTER(PrepBwdArgs), vp]
     ver = lib.m3s_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
@@ -146,6 +184,15 @@ def bhlp(t) -> Bhlp:
     if t.stride(3) != 1:
         raise ValueError("(B, H, L, P) operand must be contiguous along P")
     return Bhlp(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def blx(t) -> Blx:
+    """A (B, L, X) tensor with unit stride on X."""
+    if t is None:
+        return Blx(None, 0, 0)
+    if t.stride(2) != 1 and t.shape[2] > 1:
+        raise ValueError("(B, L, X) operand must be contiguous along its last axis")
+    return Blx(t.data_ptr(), t.stride(0), t.stride(1))
 
 
 def stream_handle(device) -> int:

@@ -1,21 +1,28 @@
 """The carried state and the per-token preprocessing (``reference.py`` product half).
 
 ``SISOState`` / ``zero_state`` / ``preprocess`` and its helpers keep the reference's
-names and semantics (``reference.py:46-209``). The preprocessing is cheap elementwise
-algebra plus one cumulative sum over time; it runs as torch ops on the device and
-its autograd supplies the cotangents of ``dt``/``lambda``/``angles`` from the kernel's
-``dgamma``/``dscale``/``dphi``, exactly as the reference leaves it to ``jax.grad``
-(``siso.py:1-11``).
+names and semantics (``reference.py:46-209``).
+
+`preprocess` -- elementwise algebra plus the cumulative angle sum over time -- runs as
+one HIP launch (``m3s_prep_fwd``), and its backward (``m3s_prep_bwd``: the suffix sum
+of ``dphi``, the head sum of the angle cotangent, the raw-slice cotangents) is wired
+in as a `torch.autograd.Function`, where the reference leaves it to ``jax.grad``
+(``siso.py:1-11``). The small helpers `heavy_tail`, `trapezoid_coeffs`, `wrap_angle`
+and `cumulative_angles` stay plain torch functions for callers that use them
+directly; the layer does not.
 """
 
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 import math
 from typing import NamedTuple, Optional
 
 import torch
 import torch.nn.functional as F
+
+from . import _lib
 
 TWO_PI = 2.0 * math.pi
 Tensor = torch.Tensor
@@ -89,17 +96,139 @@ def cumulative_angles(angles: Tensor, dt: Tensor, phi_init: Optional[Tensor] = N
     return phi, phi[:, :, -1, :]
 
 
+def _raw_dtype(*ts) -> torch.dtype:
+    dts = {t.dtype for t in ts}
+    if len(dts) == 1 and dts <= {torch.bfloat16, torch.float32}:
+        return dts.pop()
+    return torch.float32
+
+
+def _raw_operand(t: Tensor, dt: torch.dtype) -> Tensor:
+    """A (B, L, X) operand the kernel reads in place: unit stride on X."""
+    if t.dtype != dt:
+        t = t.to(dt)
+    return t if (t.stride(2) == 1 or t.shape[2] <= 1) else t.contiguous()
+
+
+def _check_device(*ts) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(
+                "preprocess runs on the ROCm device only; got a CPU tensor "
+                "(move inputs to 'cuda' -- there is no CPU fallback)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _f32c(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.to(torch.float32).contiguous()
+
+
+class _PrepFn(torch.autograd.Function):
+    """``reference.preprocess`` with its backward (``jax.grad`` in the reference) as
+    two HIP launches. Outputs: adt, gamma, scale, phi, lam, dt, phi_final."""
+
+    @staticmethod
+    def forward(ctx, dt_raw, a_raw, trap_raw, angles, dt_bias, phi_init, a_floor):
+        dev = _check_device(dt_raw, a_raw, trap_raw, angles, dt_bias, phi_init)
+        batch, seqlen, nheads = dt_raw.shape
+        n_angles = angles.shape[-1]
+        for name, t in (("a_raw", a_raw), ("trap_raw", trap_raw)):
+            if tuple(t.shape) != (batch, seqlen, nheads):
+                raise ValueError(f"{name} must be (B, L, H) = {(batch, seqlen, nheads)}, "
+                                 f"got {tuple(t.shape)}")
+        if tuple(angles.shape[:2]) != (batch, seqlen) or angles.dim() != 3:
+            raise ValueError(f"angles must be (B, L, Nr), got {tuple(angles.shape)}")
+        if tuple(dt_bias.shape) != (nheads,):
+            raise ValueError(f"dt_bias must be (H,) = ({nheads},), got {tuple(dt_bias.shape)}")
+        if phi_init is not None and tuple(phi_init.shape) != (batch, nheads, n_angles):
+            raise ValueError(f"phi_init must be (B, H, Nr) = {(batch, nheads, n_angles)}, "
+                             f"got {tuple(phi_init.shape)}")
+        rdt = _raw_dtype(dt_raw, a_raw, trap_raw, angles)
+        r_dt, r_a, r_tr, r_ang = (_raw_operand(t, rdt) for t in (dt_raw, a_raw, trap_raw, angles))
+        bias = _f32c(dt_bias)
+        init = _f32c(phi_init)
+        f32 = dict(device=dev, dtype=torch.float32)
+        adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
+        phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
+        phi_final = torch.empty(batch, nheads, n_angles, **f32)
+        a = _lib.PrepFwdArgs()
+        a.struct_size = ctypes.sizeof(_lib.PrepFwdArgs)
+        a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
+        a.dtype = _lib.dtype_code(rdt)
+        a.has_phi_init = int(init is not None)
+        a.a_floor = float(a_floor)
+        a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
+        a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
+        a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
+        a.phi, a.phi_final = phi.data_ptr(), phi_final.data_ptr()
+        with torch.cuda.device(dev):
+            _lib.check(_lib.load().m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)),
+                       "m3s_prep_fwd")
+        ctx.save_for_backward(r_dt, r_a, r_tr, r_ang, bias)
+        ctx.a_floor = float(a_floor)
+        ctx.in_dtypes = (dt_raw.dtype, a_raw.dtype, trap_raw.dtype, angles.dtype, dt_bias.dtype,
+                         None if phi_init is None else phi_init.dtype)
+        ctx.set_materialize_grads(False)
+        return adt, gamma, scale, phi, lam, dt, phi_final
+
+    @staticmethod
+    def backward(ctx, dadt, dgamma, dscale, dphi, dlam, ddt, dphi_final):
+        r_dt, r_a, r_tr, r_ang, bias = ctx.saved_tensors
+        batch, seqlen, nheads = r_dt.shape
+        n_angles = r_ang.shape[-1]
+        dev = r_dt.device
+        rdt = r_dt.dtype
+        ins = [_f32c(t) for t in (dadt, dgamma, dscale, dlam, ddt, dphi, dphi_final)]
+        d_dt = torch.empty(batch, seqlen, nheads, device=dev, dtype=rdt)
+        d_a = torch.empty_like(d_dt)
+        d_tr = torch.empty_like(d_dt)
+        d_ang = torch.empty(batch, seqlen, n_angles, device=dev, dtype=rdt)
+        d_bias = torch.empty(nheads, device=dev, dtype=torch.float32)
+        want_init = ctx.in_dtypes[5] is not None and ctx.needs_input_grad[5]
+        d_init = (torch.empty(batch, nheads, n_angles, device=dev, dtype=torch.float32)
+                  if want_init else None)
+        lib = _lib.load()
+        ws = torch.empty(lib.m3s_prep_bwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+                         device=dev, dtype=torch.uint8)
+        a = _lib.PrepBwdArgs()
+        a.struct_size = ctypes.sizeof(_lib.PrepBwdArgs)
+        a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
+        a.dtype = _lib.dtype_code(rdt)
+        a.a_floor = ctx.a_floor
+        a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
+        a.dt_bias = bias.data_ptr()
+        (a.dadt, a.dgamma, a.dscale, a.dlam, a.ddt, a.dphi,
+         a.dphi_final) = (_lib.ptr(t) for t in ins)
+        a.ddt_raw, a.da_raw, a.dtrap_raw, a.dangles = (_lib.blx(t) for t in (d_dt, d_a, d_tr, d_ang))
+        a.ddt_bias, a.dphi_init = d_bias.data_ptr(), _lib.ptr(d_init)
+        a.workspace = ws.data_ptr()
+        with torch.cuda.device(dev):
+            _lib.check(lib.m3s_prep_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_bwd")
+        dts = ctx.in_dtypes
+
+        def cast(t, d):
+            return None if (t is None or d is None) else t.to(d)
+
+        return (cast(d_dt, dts[0]), cast(d_a, dts[1]), cast(d_tr, dts[2]), cast(d_ang, dts[3]),
+                cast(d_bias, dts[4]), cast(d_init, dts[5]), None)
+
+
 def preprocess(dt_raw: Tensor, a_raw: Tensor, trap_raw: Tensor, angles: Tensor,
                dt_bias: Tensor, a_floor: float = 1e-4, phi_init: Optional[Tensor] = None):
-    """``reference.py:160-199``. Raw slices ``(B, L, H)``, angles ``(B, L, Nr)``.
+    """``reference.py:160-199``. Raw slices ``(B, L, H)``, angles ``(B, L, Nr)`` (any
+    strides with a unit last stride -- e.g. slices of the fused projection); all on the
+    ROCm device.
 
-    Returns ``(Preprocessed, phi_final)``; every output is f32.
+    Returns ``(Preprocessed, phi_final)``; every output is f32 and differentiable
+    w.r.t. the raw slices, ``dt_bias`` and ``phi_init``.
     """
-    dt = F.softplus(dt_raw.float() + dt_bias.float()).transpose(1, 2)
-    a = -heavy_tail(a_raw.float()).transpose(1, 2)
-    a = torch.clamp(a, max=-a_floor)  # negate first, then clamp (torch_ref.py:212-217)
-    lam = torch.sigmoid(trap_raw.float()).transpose(1, 2)
-    gamma, scale = trapezoid_coeffs(dt, lam)
-    phi, phi_final = cumulative_angles(angles[:, None], dt, phi_init)
-    return Preprocessed(adt=(a * dt).contiguous(), gamma=gamma.contiguous(),
-                        scale=scale.contiguous(), phi=phi.contiguous(), lam=lam, dt=dt), phi_final
+    adt, gamma, scale, phi, lam, dt, phi_final = _PrepFn.apply(
+        dt_raw, a_raw, trap_raw, angles, dt_bias, phi_init, a_floor)
+    return Preprocessed(adt=adt, gamma=gamma, scale=scale, phi=phi, lam=lam, dt=dt), phi_final

@@ -2,9 +2,9 @@
 
 The differentiable boundary sits where the reference puts it (``siso.py:39-151``):
 at ``(q, k, v, adt, gamma, scale, phi, q_bias, k_bias, d_skip, z, seed_ssm, seed_kv,
-seed_coef)``. `preprocess` runs as ordinary torch ops in front of it, so autograd
-carries ``dgamma``/``dscale``/``dphi`` back to ``dt``/``lambda``/``angles`` exactly as
-``jax.grad`` does for the reference.
+seed_coef)``. `preprocess` runs in front of it as its own differentiable HIP step
+(``scan_prep._PrepFn``), which carries ``dgamma``/``dscale``/``dphi`` back to
+``dt``/``lambda``/``angles`` where the reference relies on ``jax.grad``.
 """
 
 from __future__ import annotations
@@ -101,8 +101,8 @@ def siso_segment(q, k, v, dt_raw, a_raw, trap_raw, angles, dt_bias, q_bias, k_bi
     """``siso.py:154-216``: preprocess this segment's own raw inputs (``phi_init`` from
     the carry -- never slice a whole-sequence ``scale``), seed from the carried state,
     run the scan, return the carry."""
-    pre, _ = preprocess(dt_raw, a_raw, trap_raw, angles, dt_bias, a_floor=a_floor,
-                        phi_init=None if state is None else state.phi)
+    pre, phi_final = preprocess(dt_raw, a_raw, trap_raw, angles, dt_bias, a_floor=a_floor,
+                                phi_init=None if state is None else state.phi)
     if state is None:
         seed_ssm = seed_kv = seed_coef = None
     else:
@@ -111,4 +111,4 @@ def siso_segment(q, k, v, dt_raw, a_raw, trap_raw, angles, dt_bias, q_bias, k_bi
         seed_coef = pre.dt[:, :, 0] * (1.0 - pre.lam[:, :, 0])
     y, fs, fk, fv = siso(q, k, v, pre.adt, pre.gamma, pre.scale, pre.phi, q_bias, k_bias,
                          d_skip, z, seed_ssm, seed_kv, seed_coef, chunk, policy_name)
-    return SISOOutput(y=y, state=SISOState(ssm=fs, k=fk, v=fv, phi=pre.phi[:, :, -1, :]))
+    return SISOOutput(y=y, state=SISOState(ssm=fs, k=fk, v=fv, phi=phi_final))

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 1
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 2
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -47,6 +47,9 @@ int main(void) {
          sizeof(m3s_bwd_args), sizeof(m3s_decode_args));
   printf("%zu %zu %zu\n", offsetof(m3s_fwd_args, final_v), offsetof(m3s_bwd_args, dseed_ssm),
          offsetof(m3s_decode_args, y));
+  printf("%zu %zu %zu\n", sizeof(m3s_blx), sizeof(m3s_prep_fwd_args), sizeof(m3s_prep_bwd_args));
+  printf("%zu %zu %zu\n", offsetof(m3s_prep_fwd_args, dt_raw), offsetof(m3s_prep_bwd_args, ddt_raw),
+         offsetof(m3s_prep_bwd_args, workspace));
   return 0;
 }
 """
@@ -59,8 +62,12 @@ int main(void) {
     sizes = [int(x) for x in out]
     assert sizes[:4] == [ctypes.sizeof(lib.Bhlp), ctypes.sizeof(lib.FwdArgs),
                          ctypes.sizeof(lib.BwdArgs), ctypes.sizeof(lib.DecodeArgs)]
-    assert sizes[4:] == [lib.FwdArgs.final_v.offset, lib.BwdArgs.dseed_ssm.offset,
-                         lib.DecodeArgs.y.offset]
+    assert sizes[4:7] == [lib.FwdArgs.final_v.offset, lib.BwdArgs.dseed_ssm.offset,
+                          lib.DecodeArgs.y.offset]
+    assert sizes[7:10] == [ctypes.sizeof(lib.Blx), ctypes.sizeof(lib.PrepFwdArgs),
+                           ctypes.sizeof(lib.PrepBwdArgs)]
+    assert sizes[10:] == [lib.PrepFwdArgs.dt_raw.offset, lib.PrepBwdArgs.ddt_raw.offset,
+                          lib.PrepBwdArgs.workspace.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -101,6 +108,25 @@ def test_workspace_size(lib):
     h = lib.load()
     assert h.m3s_bwd_workspace_bytes(lib.DTYPE_BF16, 8, 8192, 32, 128) == 2 * 8 * 32 * 8192 * 128 * 2
     assert h.m3s_bwd_workspace_bytes(lib.DTYPE_F32, 1, 64, 2, 16) == 2 * 2 * 64 * 16 * 4
+
+
+def test_prep_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_prep_fwd(None, None) == lib.ERR_INVALID
+    a = lib.PrepFwdArgs()
+    a.struct_size = ctypes.sizeof(lib.PrepFwdArgs)
+    a.batch, a.seqlen, a.nheads, a.n_angles = 1, 16, 2, 4
+    a.dtype = 7
+    assert h.m3s_prep_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"bad dtype" in h.m3s_last_error()
+    a.dtype = lib.DTYPE_F32
+    assert h.m3s_prep_fwd(ctypes.byref(a), None) == lib.ERR_INVALID   # null pointers
+    b = lib.PrepBwdArgs()
+    b.struct_size = ctypes.sizeof(lib.PrepBwdArgs) - 8
+    assert h.m3s_prep_bwd(ctypes.byref(b), None) == lib.ERR_INVALID
+    assert b"ABI mismatch" in h.m3s_last_error()
+    assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 32 * 8192 * 32 * 4 + 8 * 128 * 32 * 4
+    assert h.m3s_prep_bwd_workspace_bytes(0, 8, 1, 1) == -1
 
 
 def test_capability_table(lib):

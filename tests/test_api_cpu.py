@@ -69,17 +69,12 @@ def test_rms_norm_matches_oracle(m3):
     torch.testing.assert_close(m3.rms_norm(x, w, 1e-5), O.rms_norm(x, w, 1e-5), rtol=0, atol=0)
 
 
-def test_preprocess_matches_oracle(m3):
+def test_preprocess_fails_loudly_on_cpu_tensors(m3):
+    """preprocess is a HIP launch (m3s_prep_fwd); its parity with the oracle is
+    tests/test_gpu_prep.py. On CPU tensors it raises instead of computing."""
     x = O.make_inputs(2, 3, 40, 16, 8, 4, seed=2, dtype=torch.float32)
-    st_phi = torch.rand(2, 3, 4) * 6
-    pre, fin = m3.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"],
-                             phi_init=st_phi)
-    ref, rfin = O.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"],
-                             phi_init=st_phi)
-    for name in ("adt", "gamma", "scale", "lam", "dt"):
-        torch.testing.assert_close(getattr(pre, name), getattr(ref, name), rtol=1e-6, atol=1e-7)
-    assert O.rel_error(pre.phi, ref.phi, angle=True) < 1e-5
-    assert O.rel_error(fin, rfin, angle=True) < 1e-5
+    with pytest.raises(ValueError, match="ROCm device"):
+        m3.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"])
 
 
 def _golden_sd(name):
