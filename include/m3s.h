@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 2
+#define M3S_ABI_VERSION 3
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -174,6 +174,7 @@ typedef struct m3s_prep_fwd_args {
   float* dt;           /* out (B, H, L)                   */
   float* phi;          /* out (B, H, L, Nr)               */
   float* phi_final;    /* out (B, H, Nr) = phi[:, :, L-1] */
+  void* workspace;     /* scratch, m3s_prep_fwd_workspace_bytes() bytes, 16-aligned */
 } m3s_prep_fwd_args;
 
 /* Backward of m3s_prep_fwd: the reference obtains it from jax.grad of `preprocess`
@@ -217,9 +218,14 @@ int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, int32_t state
 int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen, int32_t nheads,
                                 int32_t state_dim);
 
-/* Bytes of m3s_prep_bwd_args.workspace: the suffix-summed phi cotangent (B, H, L, Nr)
- * f32 and the per-block dt_bias partials. No counterpart in the reference. -1 on bad
- * dimensions. */
+/* Bytes of m3s_prep_fwd_args.workspace: the tanh(angles) pi table (B, L, Nr) and the
+ * per-block theta totals (B, ceil(L/64), H, Nr), f32. No counterpart in the reference.
+ * -1 on bad dimensions. */
+int64_t m3s_prep_fwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
+                                     int32_t n_angles);
+/* Bytes of m3s_prep_bwd_args.workspace: the per-block dphi carries (B, ceil(L/64), H,
+ * Nr) and dt_bias partials (B, ceil(L/64), H), f32. No counterpart in the reference.
+ * -1 on bad dimensions. */
 int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                      int32_t n_angles);
 

@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -87,7 +87,7 @@ class PrepFwdArgs(C.Structure):
         ("dt_raw", Blx), ("a_raw", Blx), ("trap_raw", Blx), ("angles", Blx),
         ("dt_bias", vp), ("phi_init", vp),
         ("adt", vp), ("gamma", vp), ("scale", vp), ("lam", vp), ("dt", vp),
-        ("phi", vp), ("phi_final", vp),
+        ("phi", vp), ("phi_final", vp), ("workspace", vp),
     ]
 
 
@@ -108,7 +108,7 @@ class PrepBwdArgs(C.Structure):
 
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
-           "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
+           "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd")
 
 _lib = None
@@ -138,6 +138,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_bwd.argtypes = [C.POINTER(BwdArgs), vp]
     lib.m3s_decode.restype = i32
     lib.m3s_decode.argtypes = [C.POINTER(DecodeArgs), vp]
+    lib.m3s_prep_fwd_workspace_bytes.restype = i64
+    lib.m3s_prep_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.m3s_prep_bwd_workspace_bytes.restype = i64
     lib.m3s_prep_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.m3s_prep_fwd.restype = i32

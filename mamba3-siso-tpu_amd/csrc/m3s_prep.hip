@@ -10,17 +10,19 @@
 //   adt   = a dt,  gamma = dt lam,  scale_t = gamma_t + dt_{t+1} (1 - lam_{t+1})  (0 past L-1)
 //   theta = tanh(angles) pi dt (angles shared by the heads),  phi = wrap(phi_init + cumsum_t theta)
 //
-// Kernels (all HBM-bound):
-//  * prep_fwd_kernel, one workgroup per (b, h): the (B, H, L) scalars with consecutive
-//    threads on consecutive t, then the phi prefix sum as a two-level scan -- each
-//    thread owns a column quad and a contiguous time range, the range totals are
-//    scanned in LDS, and a second pass writes phi as 16-byte rows.
-//  * prep_dphi_suffix_kernel, one workgroup per (b, h): dtheta_t = dphi_final +
-//    sum_{s>=t} dphi_s (the adjoint of the cumulative sum), same two-level scheme.
-//  * prep_bwd_kernel, one workgroup per (b, block of 64 tokens) holding every head:
-//    sums the per-head angle cotangents over heads in registers (angles are shared
-//    across heads), and writes the raw-slice cotangents as contiguous (t, h) rows.
-//  * prep_bias_kernel: the deterministic sum of the per-block dt_bias partials.
+// Every kernel works on one (batch element, block of 64 tokens) with all heads, so a
+// launch has B * L / 64 workgroups and each reads its raw (t, h) rows once. The time
+// recurrence (the phi prefix sum, and its adjoint, a suffix sum) is split in three
+// HBM-bound launches: per-block totals, a carry scan over the blocks of each
+// (b, h, angle), and the block pass that adds the carry to an in-block scan.
+//  * forward: prep_scalars_kernel (adt, gamma, scale, lam, dt as (b, h) rows; the
+//    tanh(angles) pi table, shared by the heads; theta totals), prep_carry_kernel,
+//    prep_phi_kernel (phi as 16-byte rows).
+//  * backward: prep_dphi_totals_kernel, prep_carry_kernel (suffix direction, seeded
+//    with dphi_final; its total is dphi_init), prep_bwd_kernel (walks its block in
+//    reverse: dtheta, the head sum of the angle cotangent by shuffles within a wave
+//    and LDS adds across waves, the raw-slice cotangents as (t, h) rows, dt_bias
+//    partials), prep_bias_kernel (a fixed-order tree sum of the partials).
 // Gradient conventions follow torch autograd of the same ops (clamp masks inclusive,
 // softplus threshold 20), which is what the oracle's autograd produces.
 #include "m3s_common.h"
@@ -42,25 +44,12 @@ __device__ __forceinline__ float softplus_(float x) {
 __device__ __forceinline__ float heavy_tail_(float x) {
   return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
 }
+__device__ __forceinline__ float sigmoid_(float x) { return 1.f / (1.f + expf(-x)); }
 __device__ __forceinline__ float wrap_(float x) {
   return x - kTwoPiF * floorf(x / kTwoPiF);
 }
 
-struct PrepFwdParams {
-  int B, L, H, Nr;
-  float a_floor;
-  const void* dtr; int64_t dtr_sb, dtr_st;
-  const void* ar;  int64_t ar_sb, ar_st;
-  const void* tr;  int64_t tr_sb, tr_st;
-  const void* ang; int64_t ang_sb, ang_st;
-  const float* dt_bias;
-  const float* phi_init;
-  float* adt; float* gamma; float* scale; float* lam; float* dt;
-  float* phi;
-  float* phi_final;
-};
-
-// Column quad jg of row `row` of a (rows, Nr) f32 array, zero past Nr.
+// Column quad [j0, j0 + 4) of a row of Nr f32 values, zero past Nr.
 __device__ __forceinline__ f32x4 ld_quad(const float* row, int j0, int Nr) {
   if (j0 + 4 <= Nr && (Nr & 3) == 0) return *reinterpret_cast<const f32x4*>(row + j0);
   f32x4 r;
@@ -77,164 +66,196 @@ __device__ __forceinline__ void st_quad(float* row, int j0, int Nr, f32x4 v) {
   for (int i = 0; i < 4; ++i)
     if (j0 + i < Nr) row[j0 + i] = v[i];
 }
-template <typename RT>
-__device__ __forceinline__ f32x4 ld_quad_raw(const RT* row, int j0, int Nr) {
-  f32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = (j0 + i < Nr) ? (float)row[j0 + i] : 0.f;
-  return r;
+
+struct PrepIn {
+  const void* p;
+  int64_t sb, st;
+};
+struct PrepOut {
+  void* p;
+  int64_t sb, st;
+};
+
+struct PrepFwdParams {
+  int B, L, H, Nr, nblk;
+  float a_floor;
+  PrepIn dtr, ar, tr, ang;
+  const float* dt_bias;
+  const float* phi_init;
+  float* adt; float* gamma; float* scale; float* lam; float* dt;
+  float* phi;
+  float* phi_final;
+  float* tpi;  // (B, L, Nr) tanh(angles) * pi
+  float* tot;  // (B, nblk, H, Nr) block totals of theta, then exclusive carries
+};
+
+__host__ __device__ inline int prep_fwd_lds_floats(int H, int Nr) {
+  return 3 * (kPrepTB + 1) * H + kPrepTB * Nr;
 }
 
 template <typename RT>
-__global__ void __launch_bounds__(kPrepThreads) prep_fwd_kernel(const PrepFwdParams p) {
-  __shared__ f32x4 sPart[kPrepThreads];
-  const int tid = threadIdx.x;
-  const int bh = xcd_remap(blockIdx.x, gridDim.x);
-  const int b = bh / p.H, h = bh % p.H;
-  const int L = p.L, Nr = p.Nr;
-  const RT* dtr = static_cast<const RT*>(p.dtr) + b * p.dtr_sb + h;
-  const RT* ar = static_cast<const RT*>(p.ar) + b * p.ar_sb + h;
-  const RT* tr = static_cast<const RT*>(p.tr) + b * p.tr_sb + h;
-  const float bias = p.dt_bias[h];
-  const int64_t o = (int64_t)bh * L;
+__global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFwdParams p) {
+  extern __shared__ float lds[];
+  const int H = p.H, Nr = p.Nr, L = p.L;
+  const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
+  const int t0 = blk * kPrepTB;
+  const int nt = min(kPrepTB, L - t0), nt1 = min(kPrepTB + 1, L - t0);
+  float* sDt = lds;                          // [TB + 1][H]
+  float* sLam = sDt + (kPrepTB + 1) * H;     // [TB + 1][H]
+  float* sA = sLam + (kPrepTB + 1) * H;      // [TB + 1][H]
+  float* sT = sA + (kPrepTB + 1) * H;        // [TB][Nr]  tanh(angles) * pi
+  const RT* dtr = static_cast<const RT*>(p.dtr.p) + b * p.dtr.sb;
+  const RT* ar = static_cast<const RT*>(p.ar.p) + b * p.ar.sb;
+  const RT* tr = static_cast<const RT*>(p.tr.p) + b * p.tr.sb;
+  const RT* ang = static_cast<const RT*>(p.ang.p) + b * p.ang.sb;
 
-  // ---- (B, H, L) scalars -------------------------------------------------------
-  for (int t = tid; t < L; t += kPrepThreads) {
-    const float dt = softplus_(ldr(dtr, t * p.dtr_st) + bias);
-    const float lam = 1.f / (1.f + expf(-ldr(tr, t * p.tr_st)));
-    const float a = fminf(-heavy_tail_(ldr(ar, t * p.ar_st)), -p.a_floor);
-    float nxt = 0.f;
-    if (t + 1 < L) {
-      const float dtn = softplus_(ldr(dtr, (t + 1) * p.dtr_st) + bias);
-      const float lamn = 1.f / (1.f + expf(-ldr(tr, (t + 1) * p.tr_st)));
-      nxt = dtn * (1.f - lamn);
-    }
+  for (int i = tid; i < nt1 * H; i += kPrepThreads) {
+    const int t = i / H, h = i % H;
+    const int64_t tg = t0 + t;
+    sDt[i] = softplus_(ldr(dtr, tg * p.dtr.st + h) + p.dt_bias[h]);
+    sLam[i] = sigmoid_(ldr(tr, tg * p.tr.st + h));
+    sA[i] = fminf(-heavy_tail_(ldr(ar, tg * p.ar.st + h)), -p.a_floor);
+  }
+  for (int i = tid; i < nt * Nr; i += kPrepThreads) {
+    const int t = i / Nr, j = i % Nr;
+    const float tp = tanhf(ldr(ang, (int64_t)(t0 + t) * p.ang.st + j)) * kPiF;
+    sT[i] = tp;
+    p.tpi[((int64_t)b * L + t0) * Nr + i] = tp;
+  }
+  __syncthreads();
+  for (int i = tid; i < H * nt; i += kPrepThreads) {  // (h, t) order: (b, h) rows
+    const int h = i / nt, t = i % nt;
+    const int k = t * H + h;
+    const float dt = sDt[k], lam = sLam[k];
+    const float nxt = (t0 + t + 1 < L) ? sDt[k + H] * (1.f - sLam[k + H]) : 0.f;
     const float gam = dt * lam;
-    p.adt[o + t] = a * dt;
-    p.gamma[o + t] = gam;
-    p.scale[o + t] = gam + nxt;
-    p.lam[o + t] = lam;
-    p.dt[o + t] = dt;
+    const int64_t o = ((int64_t)b * H + h) * L + t0 + t;
+    p.adt[o] = sA[k] * dt;
+    p.gamma[o] = gam;
+    p.scale[o] = gam + nxt;
+    p.lam[o] = lam;
+    p.dt[o] = dt;
   }
   if (Nr == 0) return;
-  __syncthreads();  // dt above is read back below by other threads of this block
-
-  // ---- phi: two-level prefix sum over t, one column quad per thread -------------
   const int J4 = (Nr + 3) / 4;
-  const int G = kPrepThreads / J4;
-  const int jg = tid % J4, g = tid / J4;
-  const bool act = g < G;
-  const int TS = (L + G - 1) / G;
-  const int tb = act ? min(L, g * TS) : L, te = act ? min(L, tb + TS) : L;
-  const RT* ang = static_cast<const RT*>(p.ang) + b * p.ang_sb;
-  const int j0 = 4 * jg;
-  auto theta = [&](int t) {
-    const float dt = p.dt[o + t];
-    f32x4 a = ld_quad_raw(ang + t * p.ang_st, j0, Nr);
-    f32x4 th;
+  for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
+    const int h = pr / J4, j0 = 4 * (pr % J4);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < nt; ++t) {
+      const float dt = sDt[t * H + h];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) th[i] = tanhf(a[i]) * kPiF * dt;
-    return th;
-  };
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int t = tb; t < te; ++t) {
-    const f32x4 th = theta(t);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] += th[i];
-  }
-  sPart[tid] = s;
-  __syncthreads();
-  if (!act) return;
-  f32x4 run = {0.f, 0.f, 0.f, 0.f};
-  for (int gg = 0; gg < g; ++gg) {
-    const f32x4 q = sPart[gg * J4 + jg];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) run[i] += q[i];
-  }
-  f32x4 init = {0.f, 0.f, 0.f, 0.f};
-  if (p.phi_init) init = ld_quad(p.phi_init + (int64_t)bh * Nr, j0, Nr);
-#pragma unroll 4
-  for (int t = tb; t < te; ++t) {
-    const f32x4 th = theta(t);
-    f32x4 out;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      run[i] += th[i];
-      out[i] = wrap_(run[i] + init[i]);
+      for (int i = 0; i < 4; ++i)
+        if (j0 + i < Nr) s[i] += sT[t * Nr + j0 + i] * dt;
     }
-    st_quad(p.phi + (o + t) * Nr, j0, Nr, out);
-    if (t == L - 1) st_quad(p.phi_final + (int64_t)bh * Nr, j0, Nr, out);
+    st_quad(p.tot + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr, s);
   }
 }
 
-// dtheta_t = dphi_final + sum_{s >= t} dphi_s, written to `dth` (B, H, L, Nr).
+// Over the blocks of one (b, h, angle): replace each block total by the exclusive
+// running sum -- in time order (reverse = 0), or from the end, seeded with `init`,
+// with the full sum written to `total` (reverse = 1).
 __global__ void __launch_bounds__(kPrepThreads)
-prep_dphi_suffix_kernel(const float* __restrict__ dphi, const float* __restrict__ dphi_final,
-                        float* __restrict__ dth, float* __restrict__ dphi_init, int L, int Nr) {
-  __shared__ f32x4 sPart[kPrepThreads];
-  const int tid = threadIdx.x;
-  const int64_t bh = blockIdx.x;
+prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
+                  float* __restrict__ total, int B, int HN, int nblk, int reverse) {
+  const int64_t idx = (int64_t)blockIdx.x * kPrepThreads + threadIdx.x;
+  if (idx >= (int64_t)B * HN) return;
+  const int64_t b = idx / HN, r = idx % HN;
+  float* base = tot + b * nblk * HN + r;
+  if (!reverse) {
+    float run = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < nblk; ++k) {
+      const float q = base[(int64_t)k * HN];
+      base[(int64_t)k * HN] = run;
+      run += q;
+    }
+  } else {
+    float run = init ? init[idx] : 0.f;
+#pragma unroll 8
+    for (int k = nblk - 1; k >= 0; --k) {
+      const float q = base[(int64_t)k * HN];
+      base[(int64_t)k * HN] = run;
+      run += q;
+    }
+    if (total) total[idx] = run;
+  }
+}
+
+__global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdParams p) {
+  const int H = p.H, Nr = p.Nr, L = p.L;
+  const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
+  const int t0 = blk * kPrepTB;
+  const int nt = min(kPrepTB, L - t0);
   const int J4 = (Nr + 3) / 4;
-  const int G = kPrepThreads / J4;
-  const int jg = tid % J4, g = tid / J4;
-  const bool act = g < G;
-  const int TS = (L + G - 1) / G;
-  const int tb = act ? min(L, g * TS) : L, te = act ? min(L, tb + TS) : L;
-  const int j0 = 4 * jg;
-  const float* src = dphi ? dphi + bh * L * Nr : nullptr;
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  if (src) {
-    for (int t = tb; t < te; ++t) {
-      const f32x4 d = ld_quad(src + (int64_t)t * Nr, j0, Nr);
+  for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
+    const int h = pr / J4, j0 = 4 * (pr % J4);
+    const int64_t bh = (int64_t)b * H + h;
+    f32x4 run = ld_quad(p.tot + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
+    f32x4 init = {0.f, 0.f, 0.f, 0.f};
+    if (p.phi_init) init = ld_quad(p.phi_init + bh * Nr, j0, Nr);
+    const float* dtrow = p.dt + bh * L + t0;
+    const float* trow = p.tpi + ((int64_t)b * L + t0) * Nr;
+    float* prow = p.phi + (bh * L + t0) * Nr;
+#pragma unroll 4
+    for (int t = 0; t < nt; ++t) {
+      const float dt = dtrow[t];
+      const f32x4 tp = ld_quad(trow + t * Nr, j0, Nr);
+      f32x4 out;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        run[i] += tp[i] * dt;
+        out[i] = wrap_(run[i] + init[i]);
+      }
+      st_quad(prow + t * Nr, j0, Nr, out);
+      if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kPrepThreads)
+prep_fill_zero_kernel(float* __restrict__ x, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kPrepThreads + threadIdx.x;
+  if (i < n) x[i] = 0.f;
+}
+
+__global__ void __launch_bounds__(kPrepThreads)
+prep_dphi_totals_kernel(const float* __restrict__ dphi, float* __restrict__ tot, int L, int H,
+                        int Nr, int nblk) {
+  const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
+  const int t0 = blk * kPrepTB;
+  const int nt = min(kPrepTB, L - t0);
+  const int J4 = (Nr + 3) / 4;
+  for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
+    const int h = pr / J4, j0 = 4 * (pr % J4);
+    const float* src = dphi + (((int64_t)b * H + h) * L + t0) * Nr;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int t = 0; t < nt; ++t) {
+      const f32x4 d = ld_quad(src + t * Nr, j0, Nr);
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[i] += d[i];
     }
+    st_quad(tot + (((int64_t)b * nblk + blk) * H + h) * Nr, j0, Nr, s);
   }
-  sPart[tid] = s;
-  __syncthreads();
-  if (!act) return;
-  f32x4 run = {0.f, 0.f, 0.f, 0.f};
-  if (dphi_final) run = ld_quad(dphi_final + bh * Nr, j0, Nr);
-  for (int gg = G - 1; gg > g; --gg) {
-    const f32x4 q = sPart[gg * J4 + jg];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) run[i] += q[i];
-  }
-  float* dst = dth + bh * L * Nr;
-  for (int t = te - 1; t >= tb; --t) {
-    if (src) {
-      const f32x4 d = ld_quad(src + (int64_t)t * Nr, j0, Nr);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) run[i] += d[i];
-    }
-    st_quad(dst + (int64_t)t * Nr, j0, Nr, run);
-  }
-  if (tb == 0 && dphi_init) st_quad(dphi_init + bh * Nr, j0, Nr, run);
 }
 
 struct PrepBwdParams {
   int B, L, H, Nr, nblk;
   float a_floor;
-  const void* dtr; int64_t dtr_sb, dtr_st;
-  const void* ar;  int64_t ar_sb, ar_st;
-  const void* tr;  int64_t tr_sb, tr_st;
-  const void* ang; int64_t ang_sb, ang_st;
+  PrepIn dtr, ar, tr, ang;
   const float* dt_bias;
   const float* dadt; const float* dgamma; const float* dscale;
   const float* dlam; const float* ddt;
-  const float* dth;      // (B, H, L, Nr) suffix-summed dphi, or NULL
-  void* ddtr; int64_t ddtr_sb, ddtr_st;
-  void* dar;  int64_t dar_sb, dar_st;
-  void* dtrr; int64_t dtrr_sb, dtrr_st;
-  void* dang; int64_t dang_sb, dang_st;
-  float* bias_part;      // (B * nblk, H)
+  const float* dphi;   // (B, H, L, Nr) or NULL
+  const float* carry;  // (B, nblk, H, Nr) suffix carries of dphi incl. dphi_final, or NULL
+  PrepOut ddtr, dar, dtrr, dang;
+  float* bias_part;    // (B * nblk, H)
 };
 
-// LDS layout of prep_bwd_kernel (floats): per (t, h) tables of TB x H, the TB x Nr
-// tanh table, and the dscale value just before the block for each head.
+// LDS of prep_bwd_kernel (floats): six TB x H tables, the TB x Nr tanh table and
+// angle-cotangent accumulator, and dscale just before the block for each head.
 __host__ __device__ inline int prep_bwd_lds_floats(int H, int Nr) {
-  return 6 * kPrepTB * H + kPrepTB * Nr + H;
+  return 6 * kPrepTB * H + 2 * kPrepTB * Nr + H;
 }
 
 template <typename RT>
@@ -250,22 +271,23 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   float* sBias = sDadt;                // [TB][H] d dt_raw for the dt_bias partial; each
                                        // thread overwrites only entries it has read
   float* sT = sPhi + kPrepTB * H;      // [TB][Nr] tanh(angles)
-  float* sDsPrev = sT + kPrepTB * Nr;  // [H] dscale at t0 - 1
+  float* sAng = sT + kPrepTB * Nr;     // [TB][Nr] sum_h dtheta dt
+  float* sDsPrev = sAng + kPrepTB * Nr;  // [H] dscale at t0 - 1
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * kPrepTB;
   const int nt = min(kPrepTB, L - t0);
-  const RT* dtr = static_cast<const RT*>(p.dtr) + b * p.dtr_sb;
-  const RT* ar = static_cast<const RT*>(p.ar) + b * p.ar_sb;
-  const RT* tr = static_cast<const RT*>(p.tr) + b * p.tr_sb;
-  const RT* ang = static_cast<const RT*>(p.ang) + b * p.ang_sb;
+  const RT* dtr = static_cast<const RT*>(p.dtr.p) + b * p.dtr.sb;
+  const RT* ar = static_cast<const RT*>(p.ar.p) + b * p.ar.sb;
+  const RT* tr = static_cast<const RT*>(p.tr.p) + b * p.tr.sb;
+  const RT* ang = static_cast<const RT*>(p.ang.p) + b * p.ang.sb;
 
   // ---- stage: recomputed dt / lambda, incoming cotangents, tanh table -------------
   for (int i = tid; i < nt * H; i += kPrepThreads) {
     const int t = i / H, h = i % H;
-    sDt[i] = softplus_(ldr(dtr, (int64_t)(t0 + t) * p.dtr_st + h) + p.dt_bias[h]);
-    sLam[i] = 1.f / (1.f + expf(-ldr(tr, (int64_t)(t0 + t) * p.tr_st + h)));
+    sDt[i] = softplus_(ldr(dtr, (int64_t)(t0 + t) * p.dtr.st + h) + p.dt_bias[h]);
+    sLam[i] = sigmoid_(ldr(tr, (int64_t)(t0 + t) * p.tr.st + h));
     sPhi[i] = 0.f;
   }
   for (int i = tid; i < nt * H; i += kPrepThreads) {  // (h, t) order: coalesced reads
@@ -279,69 +301,84 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     sDsPrev[h] = (p.dscale && t0 > 0) ? p.dscale[((int64_t)b * H + h) * L + t0 - 1] : 0.f;
   for (int i = tid; i < nt * Nr; i += kPrepThreads) {
     const int t = i / Nr, j = i % Nr;
-    sT[i] = tanhf(ldr(ang, (int64_t)(t0 + t) * p.ang_st + j));
+    sT[i] = tanhf(ldr(ang, (int64_t)(t0 + t) * p.ang.st + j));
+    sAng[i] = 0.f;
   }
   __syncthreads();
 
-  // ---- angles: d angles = pi (1 - tanh^2) sum_h dtheta_h dt_h; and per (t, h)
-  //      the dt term sum_j dtheta tanh pi --------------------------------------------
-  if (Nr > 0) {
+  // ---- dtheta_t = carry + sum_{s >= t in block} dphi_s, walked in reverse; per t:
+  //      sPhi[t][h] = sum_j dtheta tanh pi and sAng[t][j] = sum_h dtheta dt -----------
+  if (Nr > 0 && p.carry) {
     const int J4 = (Nr + 3) / 4;
-    const bool pow2 = (J4 & (J4 - 1)) == 0;
-    RT* dang = static_cast<RT*>(p.dang) + b * p.dang_sb;
-    const int npair = nt * J4;
-    // every lane of a wave runs the same number of iterations (the shuffles need it)
+    const bool pow2 = (J4 & (J4 - 1)) == 0 && J4 <= 64;
+    const int npair = H * J4;
+    // every lane of a wave runs the same iterations (the shuffles need all lanes)
     const int iters = (npair + kPrepThreads - 1) / kPrepThreads;
     for (int it = 0; it < iters; ++it) {
       const int pr = tid + it * kPrepThreads;
       const bool valid = pr < npair;
-      const int tt = valid ? pr / J4 : 0, jg = valid ? pr % J4 : 0, j0 = 4 * jg;
-      f32x4 tq = {0.f, 0.f, 0.f, 0.f};
-      if (valid) {
+      const int h = valid ? pr / J4 : 0, jg = valid ? pr % J4 : 0, j0 = 4 * jg;
+      const int64_t bh = (int64_t)b * H + h;
+      f32x4 run = {0.f, 0.f, 0.f, 0.f};
+      if (valid) run = ld_quad(p.carry + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
+      const float* src = p.dphi ? p.dphi + (bh * L + t0) * Nr : nullptr;
+      for (int t = nt - 1; t >= 0; --t) {
+        if (valid && src) {
+          const f32x4 d = ld_quad(src + t * Nr, j0, Nr);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tq[i] = (j0 + i < Nr) ? sT[tt * Nr + j0 + i] : 0.f;
-      }
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int h = 0; h < H; ++h) {
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
-        if (valid && p.dth) d = ld_quad(p.dth + (((int64_t)b * H + h) * L + t0 + tt) * Nr, j0, Nr);
-        const float dth = valid ? sDt[tt * H + h] : 0.f;
+          for (int i = 0; i < 4; ++i) run[i] += d[i];
+        }
+        const float dt = valid ? sDt[t * H + h] : 0.f;
         float ph = 0.f;
+        f32x4 ag;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc[i] += d[i] * dth;
-          ph += d[i] * (tq[i] * kPiF);
+          const float tq = (valid && j0 + i < Nr) ? sT[t * Nr + j0 + i] : 0.f;
+          ph += run[i] * (tq * kPiF);
+          ag[i] = valid ? run[i] * dt : 0.f;
         }
-        if (pow2 && J4 <= 64) {
+        if (pow2) {
           for (int off = 1; off < J4; off <<= 1) ph += __shfl_xor(ph, off, 64);
-          if (valid && jg == 0) sPhi[tt * H + h] = ph;
-        } else if (valid) {
-          atomicAdd(sPhi + tt * H + h, ph);
-        }
-      }
-      if (valid) {
+          if (valid && jg == 0) sPhi[t * H + h] = ph;
+          for (int off = J4; off < 64; off <<= 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = j0 + i;
-          if (j < Nr)
-            dang[(int64_t)(t0 + tt) * p.dang_st + j] = (RT)(acc[i] * kPiF * (1.f - tq[i] * tq[i]));
+            for (int i = 0; i < 4; ++i) ag[i] += __shfl_xor(ag[i], off, 64);
+          }
+          if (lane < J4) {   // lanes jg = lane of head group 0 hold this wave's sum
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
+          }
+        } else if (valid) {
+          atomicAdd(sPhi + t * H + h, ph);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
         }
       }
     }
   }
   __syncthreads();
+  if (Nr > 0) {
+    RT* dang = static_cast<RT*>(p.dang.p) + b * p.dang.sb;
+    for (int i = tid; i < nt * Nr; i += kPrepThreads) {
+      const int t = i / Nr, j = i % Nr;
+      const float tq = sT[i];
+      dang[(int64_t)(t0 + t) * p.dang.st + j] = (RT)(sAng[i] * kPiF * (1.f - tq * tq));
+    }
+  }
 
   // ---- raw-slice cotangents, (t, h) row-major --------------------------------------
-  RT* ddtr = static_cast<RT*>(p.ddtr) + b * p.ddtr_sb;
-  RT* dar = static_cast<RT*>(p.dar) + b * p.dar_sb;
-  RT* dtrr = static_cast<RT*>(p.dtrr) + b * p.dtrr_sb;
+  RT* ddtr = static_cast<RT*>(p.ddtr.p) + b * p.ddtr.sb;
+  RT* dar = static_cast<RT*>(p.dar.p) + b * p.dar.sb;
+  RT* dtrr = static_cast<RT*>(p.dtrr.p) + b * p.dtrr.sb;
   for (int i = tid; i < nt * H; i += kPrepThreads) {
     const int t = i / H, h = i % H;
     const int tg = t0 + t;
     const int64_t g = ((int64_t)b * H + h) * L + tg;
     const float dt = sDt[i], lam = sLam[i];
-    const float x = ldr(dtr, (int64_t)tg * p.dtr_st + h) + p.dt_bias[h];
-    const float xa = ldr(ar, (int64_t)tg * p.ar_st + h);
+    const float x = ldr(dtr, (int64_t)tg * p.dtr.st + h) + p.dt_bias[h];
+    const float xa = ldr(ar, (int64_t)tg * p.ar.st + h);
     const float apre = -heavy_tail_(xa);
     const float a = fminf(apre, -p.a_floor);
     const float dadt = sDadt[i];
@@ -365,9 +402,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     const float dht = (xa >= 0.f ? 1.f : 0.f) + (xa <= 0.f ? 1.f / (wv * wv) : 0.f);
     const float dxa = -da * dht;
     const float dtrap = dlam * lam * (1.f - lam);
-    ddtr[(int64_t)tg * p.ddtr_st + h] = (RT)dx;
-    dar[(int64_t)tg * p.dar_st + h] = (RT)dxa;
-    dtrr[(int64_t)tg * p.dtrr_st + h] = (RT)dtrap;
+    ddtr[(int64_t)tg * p.ddtr.st + h] = (RT)dx;
+    dar[(int64_t)tg * p.dar.st + h] = (RT)dxa;
+    dtrr[(int64_t)tg * p.dtrr.st + h] = (RT)dtrap;
     sBias[i] = dx;
   }
   __syncthreads();
@@ -378,20 +415,52 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   }
 }
 
+// out[h] = sum_r part[r][h], one workgroup per head, fixed summation order.
 __global__ void __launch_bounds__(kPrepThreads)
 prep_bias_kernel(const float* __restrict__ part, float* __restrict__ out, int rows, int H) {
-  const int h = blockIdx.x * kPrepThreads + threadIdx.x;
-  if (h >= H) return;
+  __shared__ float red[kPrepThreads];
+  const int h = blockIdx.x, tid = threadIdx.x;
   float s = 0.f;
-  for (int r = 0; r < rows; ++r) s += part[(int64_t)r * H + h];
-  out[h] = s;
+  for (int r = tid; r < rows; r += kPrepThreads) s += part[(int64_t)r * H + h];
+  red[tid] = s;
+  __syncthreads();
+  for (int w = kPrepThreads / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (tid == 0) out[h] = red[0];
 }
 
-static bool blx_ok(const m3s_blx& t) { return t.ptr != nullptr; }
+static PrepIn prep_in(const m3s_blx& t) { return PrepIn{t.ptr, t.stride_b, t.stride_t}; }
+static PrepOut prep_out(const m3s_blx& t) { return PrepOut{t.ptr, t.stride_b, t.stride_t}; }
+
+// Launch with `lds` bytes of dynamic LDS, raising the per-kernel limit when needed.
+template <typename K, typename P>
+static int32_t launch_lds(K kern, dim3 grid, size_t lds, hipStream_t s, const P& prm,
+                          const char* what) {
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+    set_error("%s: cannot raise the dynamic LDS limit to %zu bytes", what, lds);
+    return M3S_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(kPrepThreads), lds, s, prm);
+  return launch_status(what);
+}
+
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace m3s
 
 using namespace m3s;
+
+extern "C" int64_t m3s_prep_fwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
+                                                 int32_t n_angles) {
+  if (batch <= 0 || seqlen <= 0 || nheads <= 0 || n_angles < 0) return -1;
+  const int64_t nblk = (seqlen + kPrepTB - 1) / kPrepTB;
+  return align256((int64_t)batch * seqlen * n_angles * 4) +
+         align256((int64_t)batch * nblk * nheads * n_angles * 4);
+}
 
 extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
   clear_error();
@@ -403,31 +472,43 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
   M3S_REQUIRE(B > 0 && L > 0 && H > 0 && Nr >= 0, "m3s_prep_fwd: bad dimension");
   M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
               "m3s_prep_fwd: bad dtype %d", a->dtype);
-  M3S_REQUIRE(blx_ok(a->dt_raw) && blx_ok(a->a_raw) && blx_ok(a->trap_raw) &&
-                  (Nr == 0 || blx_ok(a->angles)) && a->dt_bias,
+  M3S_REQUIRE(a->dt_raw.ptr && a->a_raw.ptr && a->trap_raw.ptr && (Nr == 0 || a->angles.ptr) &&
+                  a->dt_bias,
               "m3s_prep_fwd: a required input pointer is NULL");
   M3S_REQUIRE(!a->has_phi_init || a->phi_init, "m3s_prep_fwd: has_phi_init but phi_init is NULL");
-  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->lam && a->dt && (Nr == 0 || (a->phi && a->phi_final)),
-              "m3s_prep_fwd: an output pointer is NULL");
+  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->lam && a->dt &&
+                  (Nr == 0 || (a->phi && a->phi_final && a->workspace)),
+              "m3s_prep_fwd: an output pointer or the workspace is NULL");
+  M3S_REQUIRE(Nr == 0 || aligned16(a->workspace), "m3s_prep_fwd: workspace must be 16-byte aligned");
   M3S_REQUIRE(Nr % 4 != 0 || (aligned16(a->phi) && aligned16(a->phi_final) &&
                               (!a->has_phi_init || aligned16(a->phi_init))),
               "m3s_prep_fwd: phi buffers must be 16-byte aligned");
+  const size_t lds = (size_t)prep_fwd_lds_floats(H, Nr) * 4;
+  M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_fwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_prep_fwd: B*H too large");
+  const int nblk = (L + kPrepTB - 1) / kPrepTB;
   PrepFwdParams p{};
-  p.B = B; p.L = L; p.H = H; p.Nr = Nr; p.a_floor = a->a_floor;
-  p.dtr = a->dt_raw.ptr; p.dtr_sb = a->dt_raw.stride_b; p.dtr_st = a->dt_raw.stride_t;
-  p.ar = a->a_raw.ptr; p.ar_sb = a->a_raw.stride_b; p.ar_st = a->a_raw.stride_t;
-  p.tr = a->trap_raw.ptr; p.tr_sb = a->trap_raw.stride_b; p.tr_st = a->trap_raw.stride_t;
-  p.ang = a->angles.ptr; p.ang_sb = a->angles.stride_b; p.ang_st = a->angles.stride_t;
+  p.B = B; p.L = L; p.H = H; p.Nr = Nr; p.nblk = nblk; p.a_floor = a->a_floor;
+  p.dtr = prep_in(a->dt_raw); p.ar = prep_in(a->a_raw); p.tr = prep_in(a->trap_raw);
+  p.ang = prep_in(a->angles);
   p.dt_bias = a->dt_bias;
   p.phi_init = a->has_phi_init ? a->phi_init : nullptr;
   p.adt = a->adt; p.gamma = a->gamma; p.scale = a->scale; p.lam = a->lam; p.dt = a->dt;
   p.phi = a->phi; p.phi_final = a->phi_final;
+  p.tpi = static_cast<float*>(a->workspace);
+  p.tot = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
+                                   align256((int64_t)B * L * Nr * 4));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a->dtype == M3S_DTYPE_BF16)
-    hipLaunchKernelGGL(prep_fwd_kernel<bf16>, dim3(B * H), dim3(kPrepThreads), 0, s, p);
-  else
-    hipLaunchKernelGGL(prep_fwd_kernel<float>, dim3(B * H), dim3(kPrepThreads), 0, s, p);
+  const dim3 grid(nblk, B);
+  int32_t rc = a->dtype == M3S_DTYPE_BF16
+                   ? launch_lds(prep_scalars_kernel<bf16>, grid, lds, s, p, "m3s_prep_fwd")
+                   : launch_lds(prep_scalars_kernel<float>, grid, lds, s, p, "m3s_prep_fwd");
+  if (rc || Nr == 0) return rc;
+  const int hn = H * Nr;
+  hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
+                     dim3(kPrepThreads), 0, s, p.tot, nullptr, nullptr, B, hn, nblk, 0);
+  if ((rc = launch_status("m3s_prep_fwd"))) return rc;
+  hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads), 0, s, p);
   return launch_status("m3s_prep_fwd");
 }
 
@@ -435,9 +516,8 @@ extern "C" int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, i
                                                  int32_t n_angles) {
   if (batch <= 0 || seqlen <= 0 || nheads <= 0 || n_angles < 0) return -1;
   const int64_t nblk = (seqlen + kPrepTB - 1) / kPrepTB;
-  int64_t dth = (int64_t)batch * nheads * seqlen * n_angles * 4;
-  dth = (dth + 255) / 256 * 256;
-  return dth + (int64_t)batch * nblk * nheads * 4;
+  return align256((int64_t)batch * nblk * nheads * n_angles * 4) +
+         (int64_t)batch * nblk * nheads * 4;
 }
 
 extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
@@ -450,11 +530,11 @@ extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
   M3S_REQUIRE(B > 0 && L > 0 && H > 0 && Nr >= 0, "m3s_prep_bwd: bad dimension");
   M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
               "m3s_prep_bwd: bad dtype %d", a->dtype);
-  M3S_REQUIRE(blx_ok(a->dt_raw) && blx_ok(a->a_raw) && blx_ok(a->trap_raw) &&
-                  (Nr == 0 || blx_ok(a->angles)) && a->dt_bias,
+  M3S_REQUIRE(a->dt_raw.ptr && a->a_raw.ptr && a->trap_raw.ptr && (Nr == 0 || a->angles.ptr) &&
+                  a->dt_bias,
               "m3s_prep_bwd: a forward input pointer is NULL");
-  M3S_REQUIRE(blx_ok(a->ddt_raw) && blx_ok(a->da_raw) && blx_ok(a->dtrap_raw) &&
-                  (Nr == 0 || blx_ok(a->dangles)) && a->ddt_bias && a->workspace,
+  M3S_REQUIRE(a->ddt_raw.ptr && a->da_raw.ptr && a->dtrap_raw.ptr && (Nr == 0 || a->dangles.ptr) &&
+                  a->ddt_bias && a->workspace,
               "m3s_prep_bwd: an output pointer or the workspace is NULL");
   M3S_REQUIRE(aligned16(a->workspace), "m3s_prep_bwd: workspace must be 16-byte aligned");
   M3S_REQUIRE(Nr % 4 != 0 || ((!a->dphi || aligned16(a->dphi)) &&
@@ -465,46 +545,44 @@ extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
   M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_bwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_prep_bwd: B*H too large");
   const int nblk = (L + kPrepTB - 1) / kPrepTB;
-  int64_t dth_bytes = (int64_t)B * H * L * Nr * 4;
-  dth_bytes = (dth_bytes + 255) / 256 * 256;
-  float* dth = static_cast<float*>(a->workspace);
-  float* part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + dth_bytes);
+  float* carry = static_cast<float*>(a->workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
+                                         align256((int64_t)B * nblk * H * Nr * 4));
   const bool any_dphi = a->dphi || a->dphi_final;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(nblk, B);
+  int32_t rc;
+  const int hn = H * Nr;
   if (Nr > 0 && (any_dphi || a->dphi_init)) {
-    hipLaunchKernelGGL(prep_dphi_suffix_kernel, dim3(B * H), dim3(kPrepThreads), 0, s,
-                       a->dphi, a->dphi_final, dth, a->dphi_init, L, Nr);
-    int32_t rc = launch_status("m3s_prep_bwd");
-    if (rc) return rc;
+    if (a->dphi) {
+      hipLaunchKernelGGL(prep_dphi_totals_kernel, grid, dim3(kPrepThreads), 0, s, a->dphi, carry,
+                         L, H, Nr, nblk);
+    } else {
+      hipLaunchKernelGGL(prep_fill_zero_kernel, dim3((B * nblk * hn + kPrepThreads - 1) / kPrepThreads),
+                         dim3(kPrepThreads), 0, s, carry, (int64_t)B * nblk * hn);
+    }
+    if ((rc = launch_status("m3s_prep_bwd"))) return rc;
+    hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
+                       dim3(kPrepThreads), 0, s, carry, a->dphi_final, a->dphi_init, B, hn, nblk, 1);
+    if ((rc = launch_status("m3s_prep_bwd"))) return rc;
   }
   PrepBwdParams p{};
   p.B = B; p.L = L; p.H = H; p.Nr = Nr; p.nblk = nblk; p.a_floor = a->a_floor;
-  p.dtr = a->dt_raw.ptr; p.dtr_sb = a->dt_raw.stride_b; p.dtr_st = a->dt_raw.stride_t;
-  p.ar = a->a_raw.ptr; p.ar_sb = a->a_raw.stride_b; p.ar_st = a->a_raw.stride_t;
-  p.tr = a->trap_raw.ptr; p.tr_sb = a->trap_raw.stride_b; p.tr_st = a->trap_raw.stride_t;
-  p.ang = a->angles.ptr; p.ang_sb = a->angles.stride_b; p.ang_st = a->angles.stride_t;
+  p.dtr = prep_in(a->dt_raw); p.ar = prep_in(a->a_raw); p.tr = prep_in(a->trap_raw);
+  p.ang = prep_in(a->angles);
   p.dt_bias = a->dt_bias;
   p.dadt = a->dadt; p.dgamma = a->dgamma; p.dscale = a->dscale;
   p.dlam = a->dlam; p.ddt = a->ddt;
-  p.dth = (Nr > 0 && any_dphi) ? dth : nullptr;
-  p.ddtr = a->ddt_raw.ptr; p.ddtr_sb = a->ddt_raw.stride_b; p.ddtr_st = a->ddt_raw.stride_t;
-  p.dar = a->da_raw.ptr; p.dar_sb = a->da_raw.stride_b; p.dar_st = a->da_raw.stride_t;
-  p.dtrr = a->dtrap_raw.ptr; p.dtrr_sb = a->dtrap_raw.stride_b; p.dtrr_st = a->dtrap_raw.stride_t;
-  p.dang = a->dangles.ptr; p.dang_sb = a->dangles.stride_b; p.dang_st = a->dangles.stride_t;
+  p.dphi = a->dphi;
+  p.carry = (Nr > 0 && any_dphi) ? carry : nullptr;
+  p.ddtr = prep_out(a->ddt_raw); p.dar = prep_out(a->da_raw); p.dtrr = prep_out(a->dtrap_raw);
+  p.dang = prep_out(a->dangles);
   p.bias_part = part;
-  auto launch = [&](auto kern) {
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-      set_error("m3s_prep_bwd: cannot raise the dynamic LDS limit to %zu bytes", lds);
-      return M3S_ERR_LAUNCH;
-    }
-    hipLaunchKernelGGL(kern, dim3(nblk, B), dim3(kPrepThreads), lds, s, p);
-    return launch_status("m3s_prep_bwd");
-  };
-  int32_t rc = a->dtype == M3S_DTYPE_BF16 ? launch(prep_bwd_kernel<bf16>) : launch(prep_bwd_kernel<float>);
+  rc = a->dtype == M3S_DTYPE_BF16
+           ? launch_lds(prep_bwd_kernel<bf16>, grid, lds, s, p, "m3s_prep_bwd")
+           : launch_lds(prep_bwd_kernel<float>, grid, lds, s, p, "m3s_prep_bwd");
   if (rc) return rc;
-  hipLaunchKernelGGL(prep_bias_kernel, dim3((H + kPrepThreads - 1) / kPrepThreads),
-                     dim3(kPrepThreads), 0, s, part, a->ddt_bias, B * nblk, H);
+  hipLaunchKernelGGL(prep_bias_kernel, dim3(H), dim3(kPrepThreads), 0, s, part, a->ddt_bias,
+                     B * nblk, H);
   return launch_status("m3s_prep_bwd");
 }

@@ -3,8 +3,8 @@
 ``SISOState`` / ``zero_state`` / ``preprocess`` and its helpers keep the reference's
 names and semantics (``reference.py:46-209``).
 
-`preprocess` -- elementwise algebra plus the cumulative angle sum over time -- runs as
-one HIP launch (``m3s_prep_fwd``), and its backward (``m3s_prep_bwd``: the suffix sum
+`preprocess` -- elementwise algebra plus the cumulative angle sum over time -- runs on
+the device through ``m3s_prep_fwd``, and its backward (``m3s_prep_bwd``: the suffix sum
 of ``dphi``, the head sum of the angle cotangent, the raw-slice cotangents) is wired
 in as a `torch.autograd.Function`, where the reference leaves it to ``jax.grad``
 (``siso.py:1-11``). The small helpers `heavy_tail`, `trapezoid_coeffs`, `wrap_angle`
@@ -158,6 +158,9 @@ class _PrepFn(torch.autograd.Function):
         adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
         phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
         phi_final = torch.empty(batch, nheads, n_angles, **f32)
+        lib = _lib.load()
+        ws = torch.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+                         device=dev, dtype=torch.uint8)
         a = _lib.PrepFwdArgs()
         a.struct_size = ctypes.sizeof(_lib.PrepFwdArgs)
         a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
@@ -168,9 +171,9 @@ class _PrepFn(torch.autograd.Function):
         a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
         a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
         a.phi, a.phi_final = phi.data_ptr(), phi_final.data_ptr()
+        a.workspace = ws.data_ptr()
         with torch.cuda.device(dev):
-            _lib.check(_lib.load().m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)),
-                       "m3s_prep_fwd")
+            _lib.check(lib.m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_fwd")
         ctx.save_for_backward(r_dt, r_a, r_tr, r_ang, bias)
         ctx.a_floor = float(a_floor)
         ctx.in_dtypes = (dt_raw.dtype, a_raw.dtype, trap_raw.dtype, angles.dtype, dt_bias.dtype,

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 2
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 3
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -125,8 +125,10 @@ def test_prep_arguments_are_checked_without_a_launch(lib):
     b.struct_size = ctypes.sizeof(lib.PrepBwdArgs) - 8
     assert h.m3s_prep_bwd(ctypes.byref(b), None) == lib.ERR_INVALID
     assert b"ABI mismatch" in h.m3s_last_error()
-    assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 32 * 8192 * 32 * 4 + 8 * 128 * 32 * 4
+    assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 128 * 32 * 32 * 4 + 8 * 128 * 32 * 4
     assert h.m3s_prep_bwd_workspace_bytes(0, 8, 1, 1) == -1
+    assert h.m3s_prep_fwd_workspace_bytes(8, 8192, 32, 32) == 8 * 8192 * 32 * 4 + 8 * 128 * 32 * 32 * 4
+    assert h.m3s_prep_fwd_workspace_bytes(1, 8, 1, -1) == -1
 
 
 def test_capability_table(lib):

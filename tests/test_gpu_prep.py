@@ -99,6 +99,7 @@ def test_prep_forward_full_length(m3, dev):
 @pytest.mark.parametrize("b,l,h,nr,a_floor,init,raw_dtype", [
     (2, 40, 3, 4, 1e-4, True, torch.float32),
     (1, 200, 4, 6, 1e-4, False, torch.float32),
+    (1, 150, 5, 12, 1e-4, True, torch.float32),    # 3 angle quads: the LDS-atomic reductions
     (2, 130, 8, 32, 0.5, True, torch.float32),
     (2, 256, 4, 16, 1e-4, True, torch.bfloat16),
 ])
@@ -151,4 +152,24 @@ def test_prep_backward_with_partial_cotangents(m3, dev):
     got = torch.autograd.grad((pre.phi.sin()).sum() + pre.scale.sum(), d_in + [d_bias])
     for gv, wv in zip(got, want):
         assert O.rel_error(gv, wv) < 1e-4
+        assert O.max_abs(gv, wv) <= 1e-4 * max(1.0, float(wv.abs().max()))
+
+
+def test_prep_backward_final_phi_only(m3, dev):
+    """A loss on the carried phi and on adt only: dphi arrives as None, dphi_final not."""
+    b, l, h, nr = 2, 100, 3, 8
+    dtr, ar, tr, ang, bias = raw_inputs(b, l, h, nr, seed=31)
+    g = torch.Generator().manual_seed(4)
+    phi0 = torch.rand(b, h, nr, generator=g, dtype=F64) * 6.0
+    leaves = [t.clone().requires_grad_(True) for t in (dtr, ar, tr, ang, bias)]
+    p0 = phi0.clone().requires_grad_(True)
+    ref, rfin = O.preprocess(*leaves, phi_init=p0)
+    want = torch.autograd.grad(rfin.cos().sum() + ref.adt.sum(), leaves + [p0], allow_unused=True)
+    want = [torch.zeros_like(x) if w is None else w for w, x in zip(want, leaves + [p0])]
+    d_in = [t.detach().requires_grad_(True) for t in as_proj(dev, torch.float32, dtr, ar, tr, ang)]
+    d_bias = bias.float().to(dev).requires_grad_(True)
+    d_p0 = phi0.float().to(dev).requires_grad_(True)
+    pre, fin = m3.preprocess(*d_in, d_bias, phi_init=d_p0)
+    got = torch.autograd.grad(fin.cos().sum() + pre.adt.sum(), d_in + [d_bias, d_p0])
+    for gv, wv in zip(got, want):
         assert O.max_abs(gv, wv) <= 1e-4 * max(1.0, float(wv.abs().max()))
