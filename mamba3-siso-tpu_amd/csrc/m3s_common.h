@@ -109,6 +109,67 @@ __device__ __forceinline__ void gemm_nt(f32x4& acc, const MT* A, int lda, int rA
   }
 }
 
+// ---- bf16 operands for a 32-wide K block in the hardware's own slot order ----------
+// v_mfma_f32_16x16x32_bf16 gives lane l the K slots 8*(l >> 4) + s, s < 8. When both
+// operands come from LDS (neither is an accumulator tile) that contiguous order is
+// used: one 16-byte read per lane.
+__device__ __forceinline__ void mma32x(f32x4& acc, bf16x8 a, bf16x8 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+// Row-contiguous storage, rows r0 + (l & 15), K = k0 + 8 (l >> 4) + s. The lane index
+// is an argument so a kernel can pass one it re-derived inside its loop (which keeps
+// the compiler from hoisting every per-lane LDS address out of the loop).
+__device__ __forceinline__ bf16x8 ld_nat8(const bf16* buf, int ld, int r0, int k0, int l) {
+  return *reinterpret_cast<const bf16x8*>(buf + (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
+}
+
+// ---- transposed bf16 reads (ds_read_b64_tr_b16) ------------------------------------
+// For storage T[k][m] (element (k, m) at buf[k * ld + m]), every lane of a 16-lane
+// group receives 4 consecutive k of one column:
+//   ld_tr4(buf, ld, kb, m0) = { T[kb + s][m0 + (l & 15)] : s < 4 }
+// where kb may differ between lane groups. The instruction returns, to lane 4r + c of
+// a group, element c of the 8-byte pieces addressed by lanes r, r + 4, r + 8, r + 12
+// of that group; lane j therefore addresses row kb + j / 4, columns m0 + 4 (j % 4).
+// ld must keep every row 8-byte aligned (ld % 4 == 0). l is the lane index.
+__device__ __forceinline__ bf16x4 ld_tr4(const bf16* buf, int ld, int kb, int m0, int l) {
+  const int j = l & 15;
+  const bf16* p = buf + (kb + (j >> 2)) * ld + m0 + 4 * (j & 3);
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(bf16x4, r);
+}
+
+// ---- buffer (SGPR-descriptor) global memory access ---------------------------------
+// A descriptor covers [base, base + bytes) of one workgroup's stream; each access adds a
+// 32-bit per-lane byte offset (one VGPR, instead of a 64-bit address pair) and a
+// uniform one (an SGPR, e.g. the chunk's start). Offsets past `bytes` read as zero and
+// are dropped on store. 0x00020000 is the gfx9-family descriptor word 3 for raw dword
+// access (as composable_kernel uses).
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <typename T> __device__ __forceinline__ T buf_load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s);
+template <> __device__ __forceinline__ bf16x8 buf_load<bf16x8>(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0));
+}
+template <> __device__ __forceinline__ f32x4 buf_load<f32x4>(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0));
+}
+template <> __device__ __forceinline__ float buf_load<float>(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));
+}
+__device__ __forceinline__ void buf_store(bf16x8 x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, v, s, 0);
+}
+__device__ __forceinline__ void buf_store(f32x4 x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, v, s, 0);
+}
+__device__ __forceinline__ void buf_store(bf16x4 x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, v, s, 0);
+}
+
 // ---- wave reductions ------------------------------------------------------------
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {

@@ -22,6 +22,8 @@
 //    gate, stores) runs on contiguous rows with 16-byte global accesses.
 //  * XCD-aware block numbering keeps the H heads of one batch element (which share
 //    q/k) on one XCD's L2.
+#include <type_traits>
+
 #include "m3s_common.h"
 #include "m3s_internal.h"
 
@@ -524,12 +526,502 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   }
 }
 
+// ===================================================================================
+// fwd_bf16_kernel: the bf16 forward for state_dim % 64 == 0 (the configs[1] shape).
+//
+// Same maths and rounding points as fwd_kernel; the data flow is rebuilt around three
+// gfx950 facts measured on fwd_kernel (LDS bandwidth and bank conflicts, not MFMA or
+// HBM, bounded it, and four barriers per chunk serialised its phases):
+//  * The wave that owns query strip w loads, biases and rotates the q/k rows of that
+//    strip itself, in the MFMA operand order (lane: row l & 15, K slots 8 (l >> 4) + s).
+//    q~ never goes to LDS: it stays in registers as the B operand of the score and
+//    inter-chunk products. khat goes to LDS once, row-major.
+//  * Operands whose contraction axis is time (v^T for P = W^T-weighted sums, v^T and
+//    khat^T for the state update) are read with ds_read_b64_tr_b16 from the same
+//    row-major tiles, so no transposed copy is ever written.
+//  * The chunk loop is software-pipelined with two barriers per chunk: phase A stages
+//    chunk c-1's output and chunk c's state into LDS and builds chunk c's tiles; phase
+//    B runs chunk c-1's epilogue (gate, stores) alongside chunk c's products, so the
+//    store-heavy epilogue of one wave overlaps the MFMA work of another.
+// ===================================================================================
+
+template <int C, int N, int P>
+struct Fwd2Cfg {
+  static constexpr int NW = C / 16;        // one query strip per wave
+  static constexpr int NT = NW * 64;
+  static constexpr int NBK = N / 32;       // 32-wide K blocks over N
+  static constexpr int LOB = N / 64;       // blocks in the rotated half; partner = +LOB
+  static constexpr int LDK = N + 8;        // sK, sS row stride (bf16)
+  static constexpr int LDV = P + 8;        // sV row stride (bf16)
+  static constexpr int LDO = P + 4;        // sOut row stride (f32)
+  static constexpr int PB = P / 16, NB = N / 16, CB = C / 16;
+  static constexpr int SPW = PB * NB / NW; // state tiles per wave
+  static constexpr int NSTEP = NW / PB;    // nb stride between a wave's state tiles
+  static constexpr int VG = P / 8;         // v / z column groups of 16 bytes
+  static constexpr int VT = (C / 2) * VG;  // v / z tasks: (row pair, column group)
+  // The v / z traffic and the epilogue go to the first half of the waves: their query
+  // strips are the short end of the causal triangle, so they would idle at the barrier.
+  static constexpr int VTH = NT / 2;       // threads that own v / z tasks
+  static constexpr int VR = (VT + VTH - 1) / VTH;
+  static constexpr int E = C / 64;         // A-scan values per lane of wave 0
+  static constexpr int SZ_K = C * LDK * 2;
+  static constexpr int SZ_V = C * LDV * 2;
+  static constexpr int SZ_S = P * LDK * 2;
+  static constexpr int SZ_O = C * LDO * 4;
+  static constexpr int SZ_SC = (4 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb
+  static constexpr int LDS_BYTES = SZ_K + SZ_V + SZ_S + SZ_O + SZ_SC;
+  static_assert(N % 64 == 0 && P % 16 == 0 && C % 64 == 0, "tile shape");
+  static_assert(NW % PB == 0 && (PB * NB) % NW == 0, "state tiles split evenly over waves");
+  static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
+};
+
+template <int C, int N, int P>
+__global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p) {
+  using F = Fwd2Cfg<C, N, P>;
+  constexpr int NW = F::NW, NT = F::NT, LDK = F::LDK, LDV = F::LDV, LDO = F::LDO;
+  constexpr int H2 = N / 2, PB = F::PB, SPW = F::SPW, NSTEP = F::NSTEP;
+
+  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
+  auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
+  bf16* sK = reinterpret_cast<bf16*>(smem);
+  bf16* sV = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));
+  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + F::SZ_V));
+  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + F::SZ_V + F::SZ_S));
+  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + F::SZ_V + F::SZ_S + F::SZ_O));
+  float* sExpA = sA + C;   // 2^{A_t}
+  float* sFac = sExpA + C; // 2^{A_last - A_t}
+  float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
+  float* sQb = sCoef + C;
+  float* sKb = sQb + N;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = wid / p.H, h = wid % p.H;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int L = p.L, Nr = p.Nr, nc = p.nc;
+
+  for (int i = tid; i < N; i += NT) {
+    sQb[i] = p.qb[h * N + i];
+    sKb[i] = p.kb[h * N + i];
+  }
+  const float dsk = p.has_d ? p.dsk[h] : 0.f;
+
+  const bf16* qg = static_cast<const bf16*>(p.q) + (int64_t)b * L * N;
+  const bf16* kg = static_cast<const bf16*>(p.k) + (int64_t)b * L * N;
+  const bf16* vg = static_cast<const bf16*>(p.v) + b * p.v_sb + h * p.v_sh;
+  const bf16* zg = p.has_z ? static_cast<const bf16*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
+  bf16* yg = static_cast<bf16*>(p.y) + b * p.y_sb + h * p.y_sh;
+  const float* adtg = p.adt + bh * L;
+  const float* gamg = p.gamma + bh * L;
+  const float* sclg = p.scale + bh * L;
+  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  bf16* csg = p.save ? static_cast<bf16*>(p.cstates) + bh * (int64_t)nc * N * P : nullptr;
+  // buffer descriptors of this (b, h)'s streams (the host checked every extent < 2^31)
+  const auto rQ = make_rsrc(qg, (uint32_t)L * N * 2);
+  const auto rK = make_rsrc(kg, (uint32_t)L * N * 2);
+  const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
+  const auto rScl = make_rsrc(sclg, (uint32_t)L * 4);
+  const auto rGam = make_rsrc(gamg, (uint32_t)L * 4);
+  const auto rAdt = make_rsrc(adtg, (uint32_t)L * 4);
+  const auto rV = make_rsrc(vg, (uint32_t)(((int64_t)(L - 1) * p.v_st + P) * 2));
+  const auto rZ = make_rsrc(zg, zg ? (uint32_t)(((int64_t)(L - 1) * p.z_st + P) * 2) : 0u);
+  const auto rY = make_rsrc(yg, (uint32_t)(((int64_t)(L - 1) * p.y_st + P) * 2));
+  const auto rYb = make_rsrc(p.save ? p.ybar + bh * L * (int64_t)P : nullptr, p.save ? (uint32_t)L * P * 4 : 0u);
+  const auto rCs = make_rsrc(csg, p.save ? (uint32_t)nc * N * P * 2 : 0u);
+
+  // ---- carried state: registers; wave owns tiles (pb_w, nb0 + NSTEP m) ------------
+  const int pb_w = wave % PB, nb0 = wave / PB;
+  f32x4 Sacc[SPW];
+#pragma unroll
+  for (int m = 0; m < SPW; ++m) {
+    Sacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (p.has_seed) {
+      const int ncol = (nb0 + NSTEP * m) * 16 + (lane & 15);
+      const float coef = p.seed_coef[bh];
+      const float kp = p.seed_k[bh * N + ncol];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int prow = pb_w * 16 + 4 * (lane >> 4) + i;
+        Sacc[m][i] = p.seed_ssm[(bh * P + prow) * N + ncol] + coef * p.seed_v[bh * P + prow] * kp;
+      }
+    }
+  }
+  auto publish_state = [&](int cidx) {
+    // S (registers) -> sS in bf16, and the chunk_states residual (N-major)
+#pragma unroll
+    for (int m = 0; m < SPW; ++m) {
+      const int ncol = (nb0 + NSTEP * m) * 16 + (lane & 15);
+      const int prow0 = pb_w * 16 + 4 * (lane >> 4);
+      const bf16x4 sv = sub_from_f32<bf16>(Sacc[m]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sS[(prow0 + i) * LDK + ncol] = sv[i];
+      if (csg && cidx < nc)
+        buf_store(sv, rCs, (uint32_t)(ncol * P + prow0) * 2, (uint32_t)cidx * N * P * 2);
+    }
+  };
+
+  // ---- raw inputs of one chunk, prefetched into registers one chunk ahead ----------
+  // Strip layout for q, k, phi, scale, gamma: lane row 16 wave + (lane & 15), K group
+  // 8 (lane >> 4). Task layout for v (and z, loaded for the epilogue one phase ahead):
+  // (row pair, 16-byte column group).
+  bf16x8 rq[F::NBK], rk[F::NBK];
+  f32x4 rphi[F::LOB][2];
+  float rscale, rgam;
+  bf16x8 rv[F::VR][2], rz[F::VR][2];
+  float radt[F::E];
+  const bool phi_vec = (Nr % 4) == 0;
+
+  auto prefetch_qk = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63;
+    const int trow = 16 * wave + (lane & 15);   // row within the chunk
+    const int g8 = 8 * (lane >> 4);
+    const uint32_t oqk = (uint32_t)(trow * N + g8) * 2;
+#pragma unroll
+    for (int blk = 0; blk < F::NBK; ++blk) {
+      rq[blk] = buf_load<bf16x8>(rQ, oqk + 64 * blk, (uint32_t)c * C * N * 2);
+      rk[blk] = buf_load<bf16x8>(rK, oqk + 64 * blk, (uint32_t)c * C * N * 2);
+    }
+  };
+  // the rest of chunk c's inputs; issued from the middle of the products, so that the
+  // wait for free memory-request slots overlaps MFMA work instead of stalling a phase
+  auto prefetch_rest = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63, tid = ln;
+    const int trow = 16 * wave + (lane & 15);
+    const int g8 = 8 * (lane >> 4);
+    const uint32_t sphi = (uint32_t)c * C * Nr * 4;
+#pragma unroll
+    for (int lb = 0; lb < F::LOB; ++lb) {
+#pragma unroll
+      for (int qd = 0; qd < 2; ++qd) {
+        const int j = 32 * lb + g8 + 4 * qd;
+        const uint32_t o = (uint32_t)(trow * Nr + j) * 4;
+        if (phi_vec && j + 4 <= Nr) {
+          rphi[lb][qd] = buf_load<f32x4>(rPhi, o, sphi);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            rphi[lb][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, o + 4 * i, sphi) : 0.f;
+        }
+      }
+    }
+    rscale = buf_load<float>(rScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+    rgam = buf_load<float>(rGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * F::VTH;
+      if (tid < F::VTH && task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          rv[r][e] = buf_load<bf16x8>(rV, (uint32_t)((2 * tp + e) * p.v_st + p0) * 2,
+                                      (uint32_t)(c * C * p.v_st * 2));
+      }
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e)
+        radt[e] = buf_load<float>(rAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+    }
+  };
+
+  auto load_z = [&](int c) {  // the gate of chunk c, for its epilogue
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int tid = ln;
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * F::VTH;
+      if (tid < F::VTH && task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          rz[r][e] = buf_load<bf16x8>(rZ, (uint32_t)((2 * tp + e) * p.z_st + p0) * 2,
+                                      (uint32_t)(c * C * p.z_st * 2));
+      }
+    }
+  };
+
+  bf16x8 qf[F::NBK];                        // q~ of this wave's strip (MFMA B operand)
+  f32x4 out[PB];                            // out^T tiles of this wave's strip
+
+  // ---- phase L: chunk c's raw registers -> q~ (registers), khat / v (LDS), scalars --
+  auto stage = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63, tid = ln;
+    const bool last = (c == nc - 1);
+    if (wave == 0) {  // inclusive prefix sum of adt * log2(e)
+      float a[F::E];
+      float run = 0.f;
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        run += radt[e] * kLog2e;
+        a[e] = run;
+      }
+      float incl = run;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+      }
+      const float excl = incl - run;
+      const float a_last = __shfl(incl, 63, 64);
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        const float A = excl + a[e];
+        sA[tt] = A;
+        sExpA[tt] = exp2f(A);
+        sFac[tt] = exp2f(a_last - A);
+      }
+    }
+    const int trow = 16 * wave + (lane & 15);
+    const int g8 = 8 * (lane >> 4);
+    float uw = 0.f;
+#pragma unroll
+    for (int lb = 0; lb < F::LOB; ++lb) {
+      const int hb = lb + F::LOB;
+      bf16x8 kl8, kh8;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int n = 32 * lb + g8 + s;
+        float ql = (float)rq[lb][s] + sQb[n];
+        float qh = (float)rq[hb][s] + sQb[n + H2];
+        float kl = (float)rk[lb][s] + sKb[n];
+        float kh = (float)rk[hb][s] + sKb[n + H2];
+        uw += ql * kl + qh * kh;
+        if (n < Nr) {
+          // phi is wrapped to [0, 2 pi): the hardware sin / cos (argument in turns)
+          // are accurate far below the bf16 rounding of the operands they feed
+          const float turns = rphi[lb][s >> 2][s & 3] * 0.15915494309189535f;
+          const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
+          const float q0 = ql * cs - qh * sn, q1 = qh * cs + ql * sn;
+          const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
+          ql = q0; qh = q1; kl = k0; kh = k1;
+        }
+        qf[lb][s] = (bf16)ql;
+        qf[hb][s] = (bf16)qh;
+        kl8[s] = (bf16)(kl * rscale);
+        kh8[s] = (bf16)(kh * rscale);
+        if (last && trow == C - 1) {
+          p.fk[bh * N + n] = kl;
+          p.fk[bh * N + n + H2] = kh;
+        }
+      }
+      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * lb + g8) = kl8;
+      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * hb + g8) = kh8;
+    }
+    uw += __shfl_xor(uw, 16, 64);
+    uw += __shfl_xor(uw, 32, 64);
+    if ((lane >> 4) == 0) sCoef[trow] = rgam * uw + dsk;
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * F::VTH;
+      if (tid < F::VTH && task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          *reinterpret_cast<bf16x8*>(sV + (2 * tp + e) * LDV + p0) = rv[r][e];
+        if (last && 2 * tp + 1 == C - 1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) p.fv[bh * P + p0 + i] = (float)rv[r][1][i];
+        }
+      }
+    }
+  };
+
+  // ---- phase G: scores, intra + inter + diagonal output, state update -------------
+  auto products = [&](int cnext) {
+    // lane index re-derived opaquely: the per-lane LDS addresses below are recomputed
+    // each chunk instead of being hoisted out of the chunk loop (and spilled)
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63;
+    const int tb = wave;
+    const int tcol = tb * 16 + (lane & 15);
+    const int g4 = 4 * (lane >> 4);
+    const float At = sA[tcol];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // masked, decayed score tile s^T[j][t] for key strip jb (rows j) and this wave's
+    // query strip (columns t), as a sub-fragment with K = j
+    auto score = [&](int jb) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk)
+        mma32x(acc, ld_nat8(sK, LDK, jb * 16, 32 * blk, lane), qf[blk]);
+      f32x4 sv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = jb * 16 + g4 + i;
+        sv[i] = (tcol > j) ? acc[i] * __builtin_amdgcn_exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+      }
+      return sub_from_f32<bf16>(sv);
+    };
+    // intra-chunk: out^T[p][t] += sum_j v^T[p][j] s^T[j][t]   (v^T by transposed reads),
+    // one pair of key strips at a time so only two score tiles are live
+    for (int jb = 0; jb <= tb; jb += 2) {
+      const bf16x4 s0 = score(jb);
+      if (jb + 1 <= tb) {
+        const bf16x4 s1 = score(jb + 1);
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb)
+          mma32(out[pb], ld_tr4(sV, LDV, jb * 16 + g4, pb * 16, lane),
+                ld_tr4(sV, LDV, jb * 16 + 16 + g4, pb * 16, lane), s0, s1);
+      } else {
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb)
+          mma16(out[pb], ld_tr4(sV, LDV, jb * 16 + g4, pb * 16, lane), s0);
+      }
+    }
+    if (cnext >= 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch_rest(cnext);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
+    const float eA = sExpA[tcol];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      f32x4 it = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk)
+        mma32x(it, ld_nat8(sS, LDK, pb * 16, 32 * blk, lane), qf[blk]);
+      // diagonal and skip: (D + gamma_t u_t . w_t) v_t
+      const bf16x4 vd = *reinterpret_cast<const bf16x4*>(sV + tcol * LDV + pb * 16 + g4);
+      const float coef = sCoef[tcol];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[pb][i] = (out[pb][i] + eA * it[i]) + coef * (float)vd[i];
+    }
+    // state: S <- 2^{A_last} S + sum_t (v_t 2^{A_last - A_t}) khat_t^T   (K = time)
+    const float eAl = sExpA[C - 1];
+#pragma unroll
+    for (int m = 0; m < SPW; ++m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Sacc[m][i] *= eAl;
+    }
+    const int g8 = 8 * (lane >> 4);
+#pragma unroll 1
+    for (int k0 = 0; k0 < C; k0 += 32) {
+      const int kb = k0 + g8;
+      bf16x4 a0 = ld_tr4(sV, LDV, kb, pb_w * 16, lane);
+      bf16x4 a1 = ld_tr4(sV, LDV, kb + 4, pb_w * 16, lane);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        a0[s] = (bf16)((float)a0[s] * sFac[kb + s]);
+        a1[s] = (bf16)((float)a1[s] * sFac[kb + 4 + s]);
+      }
+#pragma unroll
+      for (int m = 0; m < SPW; ++m) {
+        const int nb = nb0 + NSTEP * m;
+        mma32(Sacc[m], a0, a1, ld_tr4(sK, LDK, kb, nb * 16, lane), ld_tr4(sK, LDK, kb + 4, nb * 16, lane));
+      }
+    }
+  };
+
+  // ---- phase E: gate, 16-byte row stores ------------------------------------------
+  auto epilogue = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int tid = ln;
+    const int t0 = c * C;
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * F::VTH;
+      if (tid < F::VTH && task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          float yb[8];
+#pragma unroll
+          for (int i = 0; i < 8; i += 4) {
+            const f32x4 o = *reinterpret_cast<const f32x4*>(sOut + t * LDO + p0 + i);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) yb[i + u] = o[u];
+          }
+          if (p.save) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 4)
+              buf_store(f32x4{yb[i], yb[i + 1], yb[i + 2], yb[i + 3]}, rYb,
+                        (uint32_t)(t * P + p0 + i) * 4, (uint32_t)t0 * P * 4);
+          }
+          bf16x8 yo;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float g = zg ? silu((float)rz[r][e][i]) : 1.f;
+            yo[i] = (bf16)(yb[i] * g);
+          }
+          buf_store(yo, rY, (uint32_t)(t * p.y_st + p0) * 2, (uint32_t)(t0 * p.y_st * 2));
+        }
+      }
+    }
+  };
+
+  prefetch_qk(0);
+  prefetch_rest(0);
+  __syncthreads();  // sQb / sKb
+  for (int c = 0; c <= nc; ++c) {
+    // ---------------- phase A: stage out(c-1) and S(c); build chunk c -------------
+    if (c > 0) {
+      if (zg && wave < NW / 2) load_z(c - 1);  // in flight during this phase, for the epilogue
+      const int tcol = wave * 16 + (lane & 15);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb)
+        *reinterpret_cast<f32x4*>(sOut + tcol * LDO + pb * 16 + 4 * (lane >> 4)) = out[pb];
+    }
+    publish_state(c);
+    if (c < nc) stage(c);
+    __syncthreads();
+    // ---------------- phase B: epilogue of c-1 alongside the products of c --------
+    if (c + 1 < nc) prefetch_qk(c + 1);
+    if (c > 0 && wave < NW / 2) epilogue(c - 1);
+    if (c < nc) products(c + 1 < nc ? c + 1 : -1);
+    __syncthreads();
+  }
+
+  // final state
+#pragma unroll
+  for (int m = 0; m < SPW; ++m) {
+    const int ncol = (nb0 + NSTEP * m) * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int prow = pb_w * 16 + 4 * (lane >> 4) + i;
+      p.fssm[(bh * P + prow) * N + ncol] = Sacc[m][i];
+    }
+  }
+}
+
 // ---- dispatch ---------------------------------------------------------------------
+
+// Every per-(b, h) stream of fwd_bf16_kernel must be addressable with 31-bit byte
+// offsets from its buffer descriptor.
+static bool fits_rsrc(const FwdParams& p, int N, int P) {
+  const int64_t lim = (int64_t(1) << 31) - 1;
+  const int64_t L = p.L;
+  auto span = [&](int64_t st) { return ((L - 1) * st + P) * 2; };
+  return L * N * 2 <= lim && L * p.Nr * 4 <= lim && span(p.v_st) <= lim &&
+         (!p.has_z || span(p.z_st) <= lim) && span(p.y_st) <= lim && L * P * 4 <= lim &&
+         (int64_t)p.nc * N * P * 2 <= lim;
+}
 
 template <typename MT, int C, int N, int P>
 static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
-  constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
-  hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
+    if (fits_rsrc(prm, N, P)) {
+      hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      return launch_status("m3s_fwd");
+    }
+  }
+  {
+    constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
+    hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  }
   return launch_status("m3s_fwd");
 }
 
