@@ -170,6 +170,18 @@ __device__ __forceinline__ void buf_store(bf16x4 x, __amdgpu_buffer_rsrc_t r, ui
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, v, s, 0);
 }
 
+// Asynchronous 16-byte-per-lane load straight into LDS (no VGPR round trip): lane l's
+// 16 bytes from rsrc + voffset + soffset land at lds_block + 16 l, so one instruction
+// fills a contiguous 1 KiB LDS block. lds_block must be wave-uniform. Completion is
+// tracked by vmcnt: wait with vm_wait_all() before a barrier that publishes the data.
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds_block,
+                                               uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_block,
+                                           16, v, s, 0, 0);
+}
+// s_waitcnt vmcnt(0), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ---- wave reductions ------------------------------------------------------------
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
@@ -181,6 +193,11 @@ __device__ __forceinline__ float group_sum(float v) {
 // ---- elementwise maths ----------------------------------------------------------
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
+// silu from the hardware exp2 / reciprocal (~2 ulp): for gates whose product is rounded
+// to bf16 right after.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
 __device__ __forceinline__ float wrap_2pi(float phi) {
   return phi - kTwoPi * floorf(phi / kTwoPi);
 }

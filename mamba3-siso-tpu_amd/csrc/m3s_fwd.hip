@@ -552,42 +552,62 @@ struct Fwd2Cfg {
   static constexpr int NBK = N / 32;       // 32-wide K blocks over N
   static constexpr int LOB = N / 64;       // blocks in the rotated half; partner = +LOB
   static constexpr int LDK = N + 8;        // sK, sS row stride (bf16)
-  static constexpr int LDV = P + 8;        // sV row stride (bf16)
   static constexpr int LDO = P + 4;        // sOut row stride (f32)
   static constexpr int PB = P / 16, NB = N / 16, CB = C / 16;
   static constexpr int SPW = PB * NB / NW; // state tiles per wave
   static constexpr int NSTEP = NW / PB;    // nb stride between a wave's state tiles
-  static constexpr int VG = P / 8;         // v / z column groups of 16 bytes
-  static constexpr int VT = (C / 2) * VG;  // v / z tasks: (row pair, column group)
-  // The v / z traffic and the epilogue go to the first half of the waves: their query
-  // strips are the short end of the causal triangle, so they would idle at the barrier.
-  static constexpr int VTH = NT / 2;       // threads that own v / z tasks
+  // v / z tiles: C rows of P bf16 (128 bytes), unpadded, the 16-byte pieces of row r
+  // stored at slot piece ^ (r & 7) so transposed and row reads hit distinct banks.
+  // They arrive by direct global->LDS loads (1 KiB = 8 rows per instruction) issued by
+  // the first half of the waves -- whose query strips are the short end of the causal
+  // triangle -- and those waves also run the epilogue.
+  static constexpr int VBLK = C * P * 2 / 1024;   // 1 KiB blocks per v (or z) tile
+  static constexpr int NWL = NW / 2;              // light waves
+  static constexpr int VBW = VBLK / NWL;          // blocks per light wave
+  static constexpr int VG = P / 8;                // epilogue column groups (16 bytes)
+  static constexpr int VT = (C / 2) * VG;         // epilogue tasks: (row pair, group)
+  static constexpr int VTH = NWL * 64;            // epilogue threads
   static constexpr int VR = (VT + VTH - 1) / VTH;
-  static constexpr int E = C / 64;         // A-scan values per lane of wave 0
+  static constexpr int E = C / 64;                // A-scan values per lane of wave 0
   static constexpr int SZ_K = C * LDK * 2;
-  static constexpr int SZ_V = C * LDV * 2;
+  static constexpr int SZ_V = C * P * 2;          // one v or z tile
   static constexpr int SZ_S = P * LDK * 2;
   static constexpr int SZ_O = C * LDO * 4;
   static constexpr int SZ_SC = (4 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb
-  static constexpr int LDS_BYTES = SZ_K + SZ_V + SZ_S + SZ_O + SZ_SC;
-  static_assert(N % 64 == 0 && P % 16 == 0 && C % 64 == 0, "tile shape");
+  static constexpr int LDS_BYTES = SZ_K + 4 * SZ_V + SZ_S + SZ_O + SZ_SC;
+  static_assert(N % 64 == 0 && P == 64 && C % 64 == 0, "tile shape");
   static_assert(NW % PB == 0 && (PB * NB) % NW == 0, "state tiles split evenly over waves");
+  static_assert(VBLK % NWL == 0, "v / z blocks split evenly over the light waves");
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
 };
+
+// Element offset of (row r, column col) in a swizzled 64-column bf16 tile.
+__device__ __forceinline__ int vz_off(int r, int col) {
+  return r * 64 + ((((col >> 3) ^ r) & 7) << 3) + (col & 7);
+}
+// ld_tr4 on a swizzled 64-column tile: { T[kb + s][m0 + (l & 15)] : s < 4 }.
+__device__ __forceinline__ bf16x4 ld_tr4_vz(const bf16* buf, int kb, int m0, int l) {
+  const int j = l & 15;
+  const bf16* ptr = buf + vz_off(kb + (j >> 2), m0 + 4 * (j & 3));
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(ptr));
+  return __builtin_bit_cast(bf16x4, r);
+}
 
 template <int C, int N, int P>
 __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p) {
   using F = Fwd2Cfg<C, N, P>;
-  constexpr int NW = F::NW, NT = F::NT, LDK = F::LDK, LDV = F::LDV, LDO = F::LDO;
+  constexpr int NT = F::NT, LDK = F::LDK, LDO = F::LDO;
   constexpr int H2 = N / 2, PB = F::PB, SPW = F::SPW, NSTEP = F::NSTEP;
 
   __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
   auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
   bf16* sK = reinterpret_cast<bf16*>(smem);
-  bf16* sV = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));
-  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + F::SZ_V));
-  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + F::SZ_V + F::SZ_S));
-  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + F::SZ_V + F::SZ_S + F::SZ_O));
+  bf16* sVb = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));                 // [2] v tiles
+  bf16* sZb = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 2 * F::SZ_V));   // [2] z tiles
+  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 4 * F::SZ_V));
+  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + 4 * F::SZ_V + F::SZ_S));
+  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + 4 * F::SZ_V + F::SZ_S + F::SZ_O));
   float* sExpA = sA + C;   // 2^{A_t}
   float* sFac = sExpA + C; // 2^{A_last - A_t}
   float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
@@ -596,6 +616,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool light = wave < F::NWL;
   const int wid = xcd_remap(blockIdx.x, gridDim.x);
   const int b = wid / p.H, h = wid % p.H;
   const int64_t bh = (int64_t)b * p.H + h;
@@ -661,14 +682,26 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
-  // ---- raw inputs of one chunk, prefetched into registers one chunk ahead ----------
-  // Strip layout for q, k, phi, scale, gamma: lane row 16 wave + (lane & 15), K group
-  // 8 (lane >> 4). Task layout for v (and z, loaded for the epilogue one phase ahead):
-  // (row pair, 16-byte column group).
+  // ---- v / z tiles of chunk c: direct global->LDS loads by the light waves ----------
+  auto issue_vz = [&](const __amdgpu_buffer_rsrc_t& r, int64_t st, bf16* tile, int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63;
+#pragma unroll
+    for (int i = 0; i < F::VBW; ++i) {
+      const int blk = wave * F::VBW + i;           // 1 KiB block = rows 8 blk .. 8 blk + 7
+      const int row = 8 * blk + (lane >> 3);
+      const int piece = (lane & 7) ^ (row & 7);    // LDS slot lane & 7 holds this piece
+      buf_load_lds16(r, tile + blk * 512, (uint32_t)(row * st + 8 * piece) * 2,
+                     (uint32_t)(c * C * st * 2));
+    }
+  };
+
+  // ---- raw q, k, phi, scale, gamma of one chunk, prefetched into registers ---------
+  // Strip layout: lane row 16 wave + (lane & 15), K group 8 (lane >> 4).
   bf16x8 rq[F::NBK], rk[F::NBK];
   f32x4 rphi[F::LOB][2];
   float rscale, rgam;
-  bf16x8 rv[F::VR][2], rz[F::VR][2];
   float radt[F::E];
   const bool phi_vec = (Nr % 4) == 0;
 
@@ -690,7 +723,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   auto prefetch_rest = [&](int c) {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
-    const int lane = ln & 63, tid = ln;
+    const int lane = ln & 63;
     const int trow = 16 * wave + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     const uint32_t sphi = (uint32_t)c * C * Nr * 4;
@@ -711,17 +744,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
     rscale = buf_load<float>(rScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
     rgam = buf_load<float>(rGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
-#pragma unroll
-    for (int r = 0; r < F::VR; ++r) {
-      const int task = tid + r * F::VTH;
-      if (tid < F::VTH && task < F::VT) {
-        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          rv[r][e] = buf_load<bf16x8>(rV, (uint32_t)((2 * tp + e) * p.v_st + p0) * 2,
-                                      (uint32_t)(c * C * p.v_st * 2));
-      }
-    }
     if (wave == 0) {
 #pragma unroll
       for (int e = 0; e < F::E; ++e)
@@ -729,31 +751,14 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
-  auto load_z = [&](int c) {  // the gate of chunk c, for its epilogue
-    int ln = threadIdx.x;
-    asm volatile("" : "+v"(ln));
-    const int tid = ln;
-#pragma unroll
-    for (int r = 0; r < F::VR; ++r) {
-      const int task = tid + r * F::VTH;
-      if (tid < F::VTH && task < F::VT) {
-        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          rz[r][e] = buf_load<bf16x8>(rZ, (uint32_t)((2 * tp + e) * p.z_st + p0) * 2,
-                                      (uint32_t)(c * C * p.z_st * 2));
-      }
-    }
-  };
-
   bf16x8 qf[F::NBK];                        // q~ of this wave's strip (MFMA B operand)
   f32x4 out[PB];                            // out^T tiles of this wave's strip
 
-  // ---- phase L: chunk c's raw registers -> q~ (registers), khat / v (LDS), scalars --
+  // ---- phase L: chunk c's raw registers -> q~ (registers), khat (LDS), scalars -----
   auto stage = [&](int c) {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
-    const int lane = ln & 63, tid = ln;
+    const int lane = ln & 63;
     const bool last = (c == nc - 1);
     if (wave == 0) {  // inclusive prefix sum of adt * log2(e)
       float a[F::E];
@@ -819,24 +824,10 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     uw += __shfl_xor(uw, 16, 64);
     uw += __shfl_xor(uw, 32, 64);
     if ((lane >> 4) == 0) sCoef[trow] = rgam * uw + dsk;
-#pragma unroll
-    for (int r = 0; r < F::VR; ++r) {
-      const int task = tid + r * F::VTH;
-      if (tid < F::VTH && task < F::VT) {
-        const int tp = task / F::VG, p0 = (task % F::VG) * 8;
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          *reinterpret_cast<bf16x8*>(sV + (2 * tp + e) * LDV + p0) = rv[r][e];
-        if (last && 2 * tp + 1 == C - 1) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) p.fv[bh * P + p0 + i] = (float)rv[r][1][i];
-        }
-      }
-    }
   };
 
   // ---- phase G: scores, intra + inter + diagonal output, state update -------------
-  auto products = [&](int cnext) {
+  auto products = [&](int c) {
     // lane index re-derived opaquely: the per-lane LDS addresses below are recomputed
     // each chunk instead of being hoisted out of the chunk loop (and spilled)
     int ln = threadIdx.x;
@@ -845,6 +836,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int tb = wave;
     const int tcol = tb * 16 + (lane & 15);
     const int g4 = 4 * (lane >> 4);
+    const bf16* sV = sVb + (c & 1) * (C * P);
     const float At = sA[tcol];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -864,24 +856,32 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       return sub_from_f32<bf16>(sv);
     };
     // intra-chunk: out^T[p][t] += sum_j v^T[p][j] s^T[j][t]   (v^T by transposed reads),
-    // one pair of key strips at a time so only two score tiles are live
+    // one pair of key strips per step (two steps in flight) so few score tiles are live
+#pragma unroll 2
     for (int jb = 0; jb <= tb; jb += 2) {
       const bf16x4 s0 = score(jb);
       if (jb + 1 <= tb) {
         const bf16x4 s1 = score(jb + 1);
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb)
-          mma32(out[pb], ld_tr4(sV, LDV, jb * 16 + g4, pb * 16, lane),
-                ld_tr4(sV, LDV, jb * 16 + 16 + g4, pb * 16, lane), s0, s1);
+          mma32(out[pb], ld_tr4_vz(sV, jb * 16 + g4, pb * 16, lane),
+                ld_tr4_vz(sV, jb * 16 + 16 + g4, pb * 16, lane), s0, s1);
       } else {
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb)
-          mma16(out[pb], ld_tr4(sV, LDV, jb * 16 + g4, pb * 16, lane), s0);
+          mma16(out[pb], ld_tr4_vz(sV, jb * 16 + g4, pb * 16, lane), s0);
       }
     }
-    if (cnext >= 0) {
+    // next chunk's inputs: issued here so the memory-issue waits overlap MFMA work
+    if (c + 1 < nc) {
       __builtin_amdgcn_sched_barrier(0);
-      prefetch_rest(cnext);
+      prefetch_rest(c + 1);
+      if (light) issue_vz(rV, p.v_st, sVb + ((c + 1) & 1) * (C * P), c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (zg && light) {  // this chunk's gate, for its epilogue one phase later
+      __builtin_amdgcn_sched_barrier(0);
+      issue_vz(rZ, p.z_st, sZb + (c & 1) * (C * P), c);
       __builtin_amdgcn_sched_barrier(0);
     }
     // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
@@ -893,7 +893,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       for (int blk = 0; blk < F::NBK; ++blk)
         mma32x(it, ld_nat8(sS, LDK, pb * 16, 32 * blk, lane), qf[blk]);
       // diagonal and skip: (D + gamma_t u_t . w_t) v_t
-      const bf16x4 vd = *reinterpret_cast<const bf16x4*>(sV + tcol * LDV + pb * 16 + g4);
+      const bf16x4 vd = *reinterpret_cast<const bf16x4*>(sV + vz_off(tcol, pb * 16 + g4));
       const float coef = sCoef[tcol];
 #pragma unroll
       for (int i = 0; i < 4; ++i) out[pb][i] = (out[pb][i] + eA * it[i]) + coef * (float)vd[i];
@@ -909,8 +909,8 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 #pragma unroll 1
     for (int k0 = 0; k0 < C; k0 += 32) {
       const int kb = k0 + g8;
-      bf16x4 a0 = ld_tr4(sV, LDV, kb, pb_w * 16, lane);
-      bf16x4 a1 = ld_tr4(sV, LDV, kb + 4, pb_w * 16, lane);
+      bf16x4 a0 = ld_tr4_vz(sV, kb, pb_w * 16, lane);
+      bf16x4 a1 = ld_tr4_vz(sV, kb + 4, pb_w * 16, lane);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         a0[s] = (bf16)((float)a0[s] * sFac[kb + s]);
@@ -924,16 +924,17 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
-  // ---- phase E: gate, 16-byte row stores ------------------------------------------
+  // ---- phase E (light waves): gate, 16-byte row stores -----------------------------
   auto epilogue = [&](int c) {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int tid = ln;
     const int t0 = c * C;
+    const bf16* sZ = sZb + (c & 1) * (C * P);
 #pragma unroll
     for (int r = 0; r < F::VR; ++r) {
       const int task = tid + r * F::VTH;
-      if (tid < F::VTH && task < F::VT) {
+      if (task < F::VT) {
         const int tp = task / F::VG, p0 = (task % F::VG) * 8;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -951,10 +952,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
               buf_store(f32x4{yb[i], yb[i + 1], yb[i + 2], yb[i + 3]}, rYb,
                         (uint32_t)(t * P + p0 + i) * 4, (uint32_t)t0 * P * 4);
           }
+          bf16x8 zz;
+          if (zg) zz = *reinterpret_cast<const bf16x8*>(sZ + vz_off(t, p0));
           bf16x8 yo;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const float g = zg ? silu((float)rz[r][e][i]) : 1.f;
+            const float g = zg ? silu_fast((float)zz[i]) : 1.f;
             yo[i] = (bf16)(yb[i] * g);
           }
           buf_store(yo, rY, (uint32_t)(t * p.y_st + p0) * 2, (uint32_t)(t0 * p.y_st * 2));
@@ -963,13 +966,14 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
+  if (light) issue_vz(rV, p.v_st, sVb, 0);
   prefetch_qk(0);
   prefetch_rest(0);
-  __syncthreads();  // sQb / sKb
+  vm_wait_all();
+  __syncthreads();  // sQb / sKb, v tile of chunk 0
   for (int c = 0; c <= nc; ++c) {
     // ---------------- phase A: stage out(c-1) and S(c); build chunk c -------------
     if (c > 0) {
-      if (zg && wave < NW / 2) load_z(c - 1);  // in flight during this phase, for the epilogue
       const int tcol = wave * 16 + (lane & 15);
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb)
@@ -977,15 +981,16 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
     publish_state(c);
     if (c < nc) stage(c);
+    vm_wait_all();  // this wave's direct-to-LDS loads (v of c, z of c-1) have landed
     __syncthreads();
     // ---------------- phase B: epilogue of c-1 alongside the products of c --------
     if (c + 1 < nc) prefetch_qk(c + 1);
-    if (c > 0 && wave < NW / 2) epilogue(c - 1);
-    if (c < nc) products(c + 1 < nc ? c + 1 : -1);
+    if (c > 0 && light) epilogue(c - 1);
+    if (c < nc) products(c);
     __syncthreads();
   }
 
-  // final state
+  // final state, and the last v row (still in its LDS tile)
 #pragma unroll
   for (int m = 0; m < SPW; ++m) {
     const int ncol = (nb0 + NSTEP * m) * 16 + (lane & 15);
@@ -995,9 +1000,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       p.fssm[(bh * P + prow) * N + ncol] = Sacc[m][i];
     }
   }
+  const bf16* sVl = sVb + ((nc - 1) & 1) * (C * P);
+  for (int i = tid; i < P; i += NT) p.fv[bh * P + i] = (float)sVl[vz_off(C - 1, i)];
 }
-
-// ---- dispatch ---------------------------------------------------------------------
 
 // Every per-(b, h) stream of fwd_bf16_kernel must be addressable with 31-bit byte
 // offsets from its buffer descriptor.
