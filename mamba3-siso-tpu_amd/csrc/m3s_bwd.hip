@@ -24,6 +24,8 @@
 // each head's du/dw rows to the workspace with coalesced 16-byte stores; a second,
 // HBM-bound launch (headsum_kernel) sums them over heads into dq/dk, so the result
 // does not depend on the order in which workgroups finish.
+#include <type_traits>
+
 #include "m3s_common.h"
 #include "m3s_internal.h"
 
@@ -814,6 +816,740 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   }
 }
 
+// ===================================================================================
+// bwd_bf16_kernel: the bf16 backward for state_dim % 64 == 0 (the configs[2] shape).
+//
+// Same maths and rounding points as bwd_kernel. Rebuilt like fwd_bf16_kernel:
+//  * No transpose pass. Operands whose contraction axis is time or the state index
+//    (g^T, q~^T, khat^T, G^T read by columns) come from ds_read_b64_tr_b16 on the
+//    row-major tiles, so the three in-place transposes and their barriers are gone.
+//  * Each score-like tile pair (W, dM for the wave's key strip; dM^T for its query
+//    strip) is consumed by its products as soon as it is built: only two tiles live.
+//  * Global traffic through per-(b, h) buffer descriptors (32-bit offsets), and the
+//    lane index re-derived per phase, so nothing spills.
+//  * v, dy, z, ybar and the chunk state of the previous chunk are prefetched after the
+//    pullback (their registers never coexist with the product accumulators or the
+//    pullback's); q, k, phi are loaded at the start of the chunk that uses them.
+// ===================================================================================
+
+template <int C, int N, int P>
+struct Bwd2Cfg {
+  static constexpr int NW = C / 16;
+  static constexpr int NT = NW * 64;
+  static constexpr int VEC = 8;
+  static constexpr int H2 = N / 2;
+  static constexpr int LDQ = N + 8;     // sQ, sK rows (positions)
+  static constexpr int LDP = P + 8;     // sG, sV rows (positions); sST, sGaT rows (n)
+  static constexpr int LDF = N + 4;     // f32 staging rows of dq~ / dkhat
+  static constexpr int PB = P / 16, NB = N / 16, CB = C / 16;
+  static constexpr int T4 = PB * NB;
+  static constexpr int SPW = T4 / NW;
+  static constexpr int E = C / 64;
+  static constexpr int QKG = H2 / VEC;
+  static constexpr int QKT = (C / 2) * QKG;
+  static constexpr int QKR = (QKT + NT - 1) / NT;
+  static constexpr int VG = P / VEC;
+  static constexpr int VT = (C / 2) * VG;
+  static constexpr int VR = (VT + NT - 1) / NT;
+  static constexpr int SV = N * P / VEC;           // 16-byte pieces of a chunk state
+  static constexpr int SR = (SV + NT - 1) / NT;
+  static constexpr int SZ_Q = C * LDQ * 2;
+  static constexpr int SZ_G = C * LDP * 2;
+  static constexpr int SZ_ST = N * LDP * 2;
+  static constexpr int SZ_X = 2 * SZ_Q + 2 * SZ_G + SZ_ST;     // sQ sK sG sV sST
+  static constexpr int SZ_STAGE = 2 * C * LDF * 4;            // dq~, dkhat f32
+  static constexpr int SZ_R = cmax(SZ_X, SZ_STAGE);
+  static constexpr int SZ_GAT = N * LDP * 2;                  // G^T [n][p]
+  static constexpr int SZ_SC = (8 * C + 4 * N + 16) * 4;
+  static constexpr int LDS_BYTES = SZ_R + SZ_GAT + SZ_SC;
+  static_assert(N % 64 == 0 && P % 16 == 0 && C % 64 == 0, "tile shape");
+  static_assert(T4 % NW == 0 && NW % PB == 0, "adjoint tiles split evenly, one pb per wave");
+  static_assert(QKG <= 64 && VG <= 64, "row groups must fit a wave");
+  static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
+};
+
+template <int C, int N, int P>
+__global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p) {
+  using F = Bwd2Cfg<C, N, P>;
+  using vec = bf16x8;
+  constexpr int NW = F::NW, NT = F::NT, VEC = F::VEC, H2 = F::H2;
+  constexpr int LDQ = F::LDQ, LDP = F::LDP, LDF = F::LDF;
+  constexpr int PB = F::PB, NB = F::NB, CB = F::CB, SPW = F::SPW;
+
+  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
+  auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
+  bf16* sQ = reinterpret_cast<bf16*>(smem);                                        // q~ [t][n]
+  bf16* sK = reinterpret_cast<bf16*>(smem + opq(F::SZ_Q));                         // khat [j][n]
+  bf16* sG = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_Q));                     // g [t][p]
+  bf16* sV = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_Q + F::SZ_G));           // v [t][p]
+  bf16* sST = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_Q + 2 * F::SZ_G));      // S^T [n][p]
+  float* sDQ = reinterpret_cast<float*>(smem);                 // staging, after the products
+  float* sDK = reinterpret_cast<float*>(smem + opq(C * LDF * 4));
+  bf16* sGaT = reinterpret_cast<bf16*>(smem + opq(F::SZ_R));                       // G^T [n][p]
+  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_R + F::SZ_GAT));
+  float* sExpA = sA + C;
+  float* sFac = sExpA + C;
+  float* sGam = sFac + C;
+  float* sScl = sGam + C;
+  float* sDqk = sScl + C;
+  float* sCoef = sDqk + C;
+  float* sDA = sCoef + C;
+  float* sQb = sDA + C;
+  float* sKb = sQb + N;
+  float* sDqb = sKb + N;
+  float* sDkb = sDqb + N;
+  float* sRed = sDkb + N;  // [0]: 2^{A_last}<G,S> + <v, dv_inter> for the current chunk
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = xcd_remap(blockIdx.x, gridDim.x);
+  const int b = wid / p.H, h = wid % p.H;
+  const int64_t bh = (int64_t)b * p.H + h;
+  const int L = p.L, Nr = p.Nr, nc = p.nc;
+
+  for (int i = tid; i < N; i += NT) {
+    sQb[i] = p.qb[h * N + i];
+    sKb[i] = p.kb[h * N + i];
+    sDqb[i] = 0.f;
+    sDkb[i] = 0.f;
+  }
+  if (tid == 0) sRed[0] = 0.f;
+  const float dsk = p.has_d ? p.dsk[h] : 0.f;
+
+  const bf16* qg = static_cast<const bf16*>(p.q) + (int64_t)b * L * N;
+  const bf16* kg = static_cast<const bf16*>(p.k) + (int64_t)b * L * N;
+  const bf16* vg = static_cast<const bf16*>(p.v) + b * p.v_sb + h * p.v_sh;
+  const bf16* dyg = static_cast<const bf16*>(p.dy) + b * p.dy_sb + h * p.dy_sh;
+  const bf16* zg = p.has_z ? static_cast<const bf16*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
+  bf16* dzg = p.has_z ? static_cast<bf16*>(p.dz) + b * p.dz_sb + h * p.dz_sh : nullptr;
+  bf16* dvg = static_cast<bf16*>(p.dv) + b * p.dv_sb + h * p.dv_sh;
+  const float* ybg = p.ybar + bh * (int64_t)L * P;
+  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  const bf16* csg = static_cast<const bf16*>(p.cstates) + bh * (int64_t)nc * N * P;
+  bf16* dug = static_cast<bf16*>(p.part) + bh * (int64_t)L * N;                 // du rows of (b, h)
+  bf16* dwg = static_cast<bf16*>(p.part) + ((int64_t)p.B * p.H + bh) * L * N;   // dw rows of (b, h)
+  const bool phi_vec = (Nr % 4) == 0;
+  auto span = [&](int64_t st) { return (uint32_t)(((int64_t)(L - 1) * st + P) * 2); };
+  const auto rQ = make_rsrc(qg, (uint32_t)L * N * 2);
+  const auto rK = make_rsrc(kg, (uint32_t)L * N * 2);
+  const auto rV = make_rsrc(vg, span(p.v_st));
+  const auto rDy = make_rsrc(dyg, span(p.dy_st));
+  const auto rZ = make_rsrc(zg, zg ? span(p.z_st) : 0u);
+  const auto rDz = make_rsrc(dzg, dzg ? span(p.dz_st) : 0u);
+  const auto rDv = make_rsrc(dvg, span(p.dv_st));
+  const auto rYb = make_rsrc(ybg, (uint32_t)L * P * 4);
+  const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
+  const auto rCs = make_rsrc(csg, (uint32_t)nc * N * P * 2);
+  const auto rAdt = make_rsrc(p.adt + bh * L, (uint32_t)L * 4);
+  const auto rGam = make_rsrc(p.gamma + bh * L, (uint32_t)L * 4);
+  const auto rScl = make_rsrc(p.scale + bh * L, (uint32_t)L * 4);
+  const auto rUw = make_rsrc(p.uw + bh * L, (uint32_t)L * 4);
+  const auto rDqk = make_rsrc(p.dqk + bh * L, (uint32_t)L * 4);
+  const auto rDsc = make_rsrc(p.dscale + bh * L, (uint32_t)L * 4);
+  const auto rDadt = make_rsrc(p.dadt + bh * L, (uint32_t)L * 4);
+  const auto rDphi = make_rsrc(p.dphi ? p.dphi + bh * (int64_t)L * Nr : nullptr,
+                               p.dphi ? (uint32_t)L * Nr * 4 : 0u);
+  const auto rDu = make_rsrc(dug, (uint32_t)L * N * 2);
+  const auto rDw = make_rsrc(dwg, (uint32_t)L * N * 2);
+
+  // ---- adjoint G (registers, MFMA layout [p][n]); wave owns (pb_w, nb0 + NSTEP m) --
+  constexpr int NSTEP = NW / PB;
+  const int pb_w = wave % PB, nb0 = wave / PB;
+  f32x4 Gacc[SPW];
+#pragma unroll
+  for (int m = 0; m < SPW; ++m) {
+    Gacc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (p.dfs) {
+      const int nb = nb0 + NSTEP * m;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        Gacc[m][i] = p.dfs[(bh * P + pb_w * 16 + 4 * (lane >> 4) + i) * N + nb * 16 + (lane & 15)];
+    }
+  }
+  auto publish_adjoint = [&]() {
+#pragma unroll
+    for (int m = 0; m < SPW; ++m) {
+      const int nb = nb0 + NSTEP * m;
+      *reinterpret_cast<bf16x4*>(sGaT + (nb * 16 + (lane & 15)) * LDP + pb_w * 16 + 4 * (lane >> 4)) =
+          sub_from_f32<bf16>(Gacc[m]);
+    }
+  };
+  publish_adjoint();
+
+  // ---- register prefetch of one chunk's raw inputs, in two parts -------------------
+  vec rq[F::QKR][2][2], rk[F::QKR][2][2];
+  f32x4 rphi[F::QKR][2][VEC / 4];
+  float rscale[F::QKR][2];
+  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2];
+  f32x4 ryb[F::VR][2][VEC / 4];
+  vec rs[F::SR];
+  float radt[F::E], rgam_s, rscl_s;
+
+  auto prefetch_qk = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int tid = ln;
+    const uint32_t sqk = (uint32_t)c * C * N * 2, sphi = (uint32_t)c * C * Nr * 4;
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::QKT) {
+        const int tp = task / F::QKG, j0 = (task % F::QKG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          const uint32_t o = (uint32_t)(t * N + j0) * 2;
+          rq[r][e][0] = buf_load<vec>(rQ, o, sqk);
+          rq[r][e][1] = buf_load<vec>(rQ, o + 2 * H2, sqk);
+          rk[r][e][0] = buf_load<vec>(rK, o, sqk);
+          rk[r][e][1] = buf_load<vec>(rK, o + 2 * H2, sqk);
+#pragma unroll
+          for (int qd = 0; qd < VEC / 4; ++qd) {
+            const int j = j0 + 4 * qd;
+            const uint32_t op = (uint32_t)(t * Nr + j) * 4;
+            if (phi_vec && j + 4 <= Nr) {
+              rphi[r][e][qd] = buf_load<f32x4>(rPhi, op, sphi);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                rphi[r][e][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, op + 4 * i, sphi) : 0.f;
+            }
+          }
+          rscale[r][e] = buf_load<float>(rScl, (uint32_t)t * 4, (uint32_t)c * C * 4);
+        }
+      }
+    }
+  };
+  auto prefetch_rest = [&](int c) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int tid = ln, lane = ln & 63;
+#pragma unroll
+    for (int r = 0; r < F::VR; ++r) {
+      const int task = tid + r * NT;
+      if (task < F::VT) {
+        const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          rv[r][e] = buf_load<vec>(rV, (uint32_t)(t * p.v_st + p0) * 2, (uint32_t)(c * C * p.v_st * 2));
+          rdy[r][e] = buf_load<vec>(rDy, (uint32_t)(t * p.dy_st + p0) * 2, (uint32_t)(c * C * p.dy_st * 2));
+          if (zg) {
+            rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
+#pragma unroll
+            for (int i = 0; i < VEC; i += 4)
+              ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < F::SR; ++r) {
+      const int f = tid + r * NT;
+      if (f < F::SV) rs[r] = buf_load<vec>(rCs, (uint32_t)f * VEC * 2, (uint32_t)c * N * P * 2);
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e)
+        radt[e] = buf_load<float>(rAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+    }
+    if (tid < C) {
+      rgam_s = buf_load<float>(rGam, (uint32_t)tid * 4, (uint32_t)c * C * 4);
+      rscl_s = buf_load<float>(rScl, (uint32_t)tid * 4, (uint32_t)c * C * 4);
+    }
+  };
+
+  prefetch_rest(nc - 1);
+  __syncthreads();
+
+  for (int c = nc - 1; c >= 0; --c) {
+    const int t0 = c * C;
+    // ============ phase L: raw -> LDS (q~, khat, g, v, S^T), dz, dqk, uw ==============
+    prefetch_qk(c);   // q, k, phi, scale of this chunk; the A-scan below covers part of the wait
+    {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int tid = ln, lane = ln & 63;
+      if (wave == 0) {
+        float a[F::E];
+        float run = 0.f;
+#pragma unroll
+        for (int e = 0; e < F::E; ++e) {
+          run += radt[e] * kLog2e;
+          a[e] = run;
+        }
+        float incl = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const float o = __shfl_up(incl, off, 64);
+          if (lane >= off) incl += o;
+        }
+        const float excl = incl - run;
+        const float a_last = __shfl(incl, 63, 64);
+#pragma unroll
+        for (int e = 0; e < F::E; ++e) {
+          const int tt = lane * F::E + e;
+          const float A = excl + a[e];
+          sA[tt] = A;
+          sExpA[tt] = exp2f(A);
+          sFac[tt] = exp2f(a_last - A);
+        }
+      }
+      if (tid < C) {
+        sGam[tid] = rgam_s;
+        sScl[tid] = rscl_s;
+      }
+#pragma unroll
+      for (int r = 0; r < F::QKR; ++r) {
+        const int task = tid + r * NT;
+        const bool valid = task < F::QKT;
+        const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
+        float uw[2] = {0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          if (valid) {
+            vec oq0, oq1, ok0, ok1;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              const int j = j0 + i;
+              const float ulo = (float)rq[r][e][0][i] + sQb[j];
+              const float uhi = (float)rq[r][e][1][i] + sQb[H2 + j];
+              const float wlo = (float)rk[r][e][0][i] + sKb[j];
+              const float whi = (float)rk[r][e][1][i] + sKb[H2 + j];
+              uw[e] += ulo * wlo + uhi * whi;
+              float sn = 0.f, cs = 1.f;
+              if (j < Nr) {  // phi in [0, 2 pi): hardware sin / cos, argument in turns
+                const float turns = rphi[r][e][i / 4][i % 4] * 0.15915494309189535f;
+                sn = __builtin_amdgcn_sinf(turns);
+                cs = __builtin_amdgcn_cosf(turns);
+              }
+              const float sc = rscale[r][e];
+              oq0[i] = (bf16)(ulo * cs - uhi * sn);
+              oq1[i] = (bf16)(uhi * cs + ulo * sn);
+              ok0[i] = (bf16)((wlo * cs - whi * sn) * sc);
+              ok1[i] = (bf16)((whi * cs + wlo * sn) * sc);
+            }
+            *reinterpret_cast<vec*>(sQ + t * LDQ + j0) = oq0;
+            *reinterpret_cast<vec*>(sQ + t * LDQ + H2 + j0) = oq1;
+            *reinterpret_cast<vec*>(sK + t * LDQ + j0) = ok0;
+            *reinterpret_cast<vec*>(sK + t * LDQ + H2 + j0) = ok1;
+          }
+        }
+        uw[0] = group_sum<F::QKG>(uw[0]);
+        uw[1] = group_sum<F::QKG>(uw[1]);
+        if (valid && j0 == 0) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int t = 2 * tp + e;
+            buf_store_f32(uw[e], rUw, (uint32_t)t * 4, (uint32_t)t0 * 4);
+            sCoef[t] = buf_load<float>(rGam, (uint32_t)t * 4, (uint32_t)t0 * 4) * uw[e] + dsk;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < F::VR; ++r) {
+        const int task = tid + r * NT;
+        const bool valid = task < F::VT;
+        const int tp = valid ? task / F::VG : 0, p0 = valid ? (task % F::VG) * VEC : 0;
+        float dqk[2] = {0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          if (valid) {
+            vec og, odz;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              const float dy = (float)rdy[r][e][i];
+              float gv = dy;
+              if (zg) {
+                const float zf = (float)rz[r][e][i];
+                const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zf * kLog2e));
+                gv = dy * (zf * sg);
+                odz[i] = (bf16)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
+              }
+              dqk[e] += gv * (float)rv[r][e][i];
+              og[i] = (bf16)gv;
+            }
+            *reinterpret_cast<vec*>(sG + t * LDP + p0) = og;
+            *reinterpret_cast<vec*>(sV + t * LDP + p0) = rv[r][e];
+            if (dzg) buf_store(odz, rDz, (uint32_t)(t * p.dz_st + p0) * 2, (uint32_t)(t0 * p.dz_st * 2));
+          }
+        }
+        dqk[0] = group_sum<F::VG>(dqk[0]);
+        dqk[1] = group_sum<F::VG>(dqk[1]);
+        if (valid && p0 == 0) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int t = 2 * tp + e;
+            sDqk[t] = dqk[e];
+            buf_store_f32(dqk[e], rDqk, (uint32_t)t * 4, (uint32_t)t0 * 4);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < F::SR; ++r) {
+        const int f = tid + r * NT;
+        if (f < F::SV) {
+          const int n = (f * VEC) / P, pp = (f * VEC) % P;
+          *reinterpret_cast<vec*>(sST + n * LDP + pp) = rs[r];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ products: score tiles consumed as they are built ===================
+    f32x4 dQ[NB], dKh[NB], dV[PB];
+    {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63, g4 = lane >> 4, l16 = lane & 15;
+      const int w = wave;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        dQ[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dKh[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int i = 0; i < PB; ++i) dV[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      float red = 0.f;
+      const int jcol = w * 16 + l16;     // this lane's key position (cols of W, dM)
+      const float Aj = sA[jcol];
+      // W[t][j] and dM[t][j] for query strip tb (rows t) and key strip w (cols j)
+      auto wdm = [&](int tb, bf16x4& wt, bf16x4& mt) {
+        if (tb < w) {
+          wt = sub_from_f32<bf16>(f32x4{0.f, 0.f, 0.f, 0.f});
+          mt = wt;
+          return;
+        }
+        f32x4 aw = {0.f, 0.f, 0.f, 0.f}, am = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += 32)
+          mma32x(aw, ld_nat8(sQ, LDQ, tb * 16, k0, lane), ld_nat8(sK, LDQ, w * 16, k0, lane));
+#pragma unroll
+        for (int k0 = 0; k0 < P; k0 += 32)
+          mma32x(am, ld_nat8(sG, LDP, tb * 16, k0, lane), ld_nat8(sV, LDP, w * 16, k0, lane));
+        f32x4 vw, vm;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = tb * 16 + 4 * g4 + i;
+          const float dec = (t > jcol) ? __builtin_amdgcn_exp2f(fminf(sA[t] - Aj, 0.f)) : 0.f;
+          vw[i] = aw[i] * dec;
+          vm[i] = am[i] * dec;
+        }
+        wt = sub_from_f32<bf16>(vw);
+        mt = sub_from_f32<bf16>(vm);
+      };
+      // dv[j][p] += sum_t W[t][j] g[t][p];  dkhat[j][n] += sum_t dM[t][j] q~[t][n]
+      for (int tb = w & ~1; tb < CB; tb += 2) {
+        bf16x4 w0, m0, w1, m1;
+        wdm(tb, w0, m0);
+        wdm(tb + 1, w1, m1);
+        const int kb = tb * 16 + 4 * g4;
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb)
+          mma32(dV[pb], w0, w1, ld_tr4(sG, LDP, kb, pb * 16, lane), ld_tr4(sG, LDP, kb + 16, pb * 16, lane));
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          mma32(dKh[nb], m0, m1, ld_tr4(sQ, LDQ, kb, nb * 16, lane), ld_tr4(sQ, LDQ, kb + 16, nb * 16, lane));
+      }
+      // dq~[t][n] += sum_j dM^T[j][t] khat[j][n]   (query strip w, key strips jb <= w)
+      const int tcol = w * 16 + l16;
+      const float At = sA[tcol];
+      auto dmt = [&](int jb) {
+        if (jb > w) return sub_from_f32<bf16>(f32x4{0.f, 0.f, 0.f, 0.f});
+        f32x4 am = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < P; k0 += 32)
+          mma32x(am, ld_nat8(sV, LDP, jb * 16, k0, lane), ld_nat8(sG, LDP, w * 16, k0, lane));
+        f32x4 vm;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = jb * 16 + 4 * g4 + i;
+          vm[i] = (tcol > j) ? am[i] * __builtin_amdgcn_exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+        }
+        return sub_from_f32<bf16>(vm);
+      };
+      for (int jb = 0; jb <= w; jb += 2) {
+        const bf16x4 d0 = dmt(jb), d1 = dmt(jb + 1);
+        const int kb = jb * 16 + 4 * g4;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          mma32(dQ[nb], d0, d1, ld_tr4(sK, LDQ, kb, nb * 16, lane), ld_tr4(sK, LDQ, kb + 16, nb * 16, lane));
+      }
+      // dq~ inter: 2^{A_t} sum_p g[t][p] S[p][n];  dkhat inter: 2^{A_last-A_j} sum_p v[j][p] G[p][n]
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 iq = {0.f, 0.f, 0.f, 0.f}, ik = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < P; k0 += 32) {
+          mma32x(iq, ld_nat8(sG, LDP, w * 16, k0, lane), ld_nat8(sST, LDP, nb * 16, k0, lane));
+          mma32x(ik, ld_nat8(sV, LDP, w * 16, k0, lane), ld_nat8(sGaT, LDP, nb * 16, k0, lane));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = w * 16 + 4 * g4 + i;
+          dQ[nb][i] += iq[i] * sExpA[r];
+          dKh[nb][i] += ik[i] * sFac[r];
+        }
+      }
+      // dv inter: 2^{A_last-A_j} sum_n khat[j][n] G[p][n]   (G^T read by columns)
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        f32x4 iv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < N; k0 += 32) {
+          const int kb = k0 + 4 * g4;
+          mma32(iv, ld_sub<bf16>(sK, LDQ, w * 16, k0), ld_sub<bf16>(sK, LDQ, w * 16, k0 + 16),
+                ld_tr4(sGaT, LDP, kb, pb * 16, lane), ld_tr4(sGaT, LDP, kb + 16, pb * 16, lane));
+        }
+        const bf16x4 vj = ld_tr4(sV, LDP, w * 16 + 4 * g4, pb * 16, lane);   // v[j][p]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = w * 16 + 4 * g4 + i;
+          iv[i] *= sFac[j];
+          dV[pb][i] += iv[i];
+          // <v, dv_inter> == <khat, dk_inter>: the A_last share of the state update
+          red += (float)vj[i] * iv[i];
+        }
+      }
+      // 2^{A_last} <G, S> from this wave's adjoint tiles (before the G update)
+      {
+        float gs = 0.f;
+#pragma unroll
+        for (int m = 0; m < SPW; ++m) {
+          const int nb = nb0 + NSTEP * m;
+          const f32x4 sv = sub_to_f32<bf16>(
+              *reinterpret_cast<const bf16x4*>(sST + (nb * 16 + l16) * LDP + pb_w * 16 + 4 * g4));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) gs += Gacc[m][i] * sv[i];
+        }
+        red += sExpA[C - 1] * gs;
+      }
+      red = group_sum<64>(red);
+      if (lane == 0) atomicAdd(sRed, red);
+      // G <- 2^{A_last} G + sum_t (2^{A_t} g[t][p]) q~[t][n]   (K = time, both by columns)
+      const float eAl = sExpA[C - 1];
+#pragma unroll
+      for (int m = 0; m < SPW; ++m) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Gacc[m][i] *= eAl;
+      }
+#pragma unroll 1
+      for (int k0 = 0; k0 < C; k0 += 32) {
+        const int kb = k0 + 4 * g4;
+        bf16x4 a0 = ld_tr4(sG, LDP, kb, pb_w * 16, lane);
+        bf16x4 a1 = ld_tr4(sG, LDP, kb + 16, pb_w * 16, lane);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          a0[s] = (bf16)((float)a0[s] * sExpA[kb + s]);
+          a1[s] = (bf16)((float)a1[s] * sExpA[kb + 16 + s]);
+        }
+#pragma unroll
+        for (int m = 0; m < SPW; ++m) {
+          const int nb = nb0 + NSTEP * m;
+          mma32(Gacc[m], a0, a1, ld_tr4(sQ, LDQ, kb, nb * 16, lane), ld_tr4(sQ, LDQ, kb + 16, nb * 16, lane));
+        }
+      }
+      // dv epilogue: + (D + gamma u.w) g, + dfinal_v on the sequence's last row; store
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        const int pcol = pb * 16 + l16;
+        const f32x4 gv = sub_to_f32<bf16>(ld_tr4(sG, LDP, w * 16 + 4 * g4, pb * 16, lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = w * 16 + 4 * g4 + i;
+          float d = dV[pb][i] + sCoef[j] * gv[i];
+          if (p.dfv && t0 + j == L - 1) d += p.dfv[bh * P + pcol];
+          buf_store_bf16(d, rDv, (uint32_t)(j * p.dv_st + pcol) * 2, (uint32_t)(t0 * p.dv_st * 2));
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ stage dq~ [t][n] and dkhat [j][n] as f32 rows =======================
+    {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63, g4 = lane >> 4, l16 = lane & 15;
+      const int w = wave;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = w * 16 + 4 * g4 + i;
+          sDQ[r * LDF + nb * 16 + l16] = dQ[nb][i];
+          sDK[r * LDF + nb * 16 + l16] = dKh[nb][i];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ============ phase R: rotation pullback, per-row reductions, head sum ============
+    {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int tid = ln, lane = ln & 63;
+      const uint32_t sqk = (uint32_t)t0 * N * 2, sphi = (uint32_t)t0 * Nr * 4;
+#pragma unroll
+      for (int r = 0; r < F::QKR; ++r) {
+        const int task = tid + r * NT;
+        const bool valid = task < F::QKT;
+        const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
+        // one row per iteration (not unrolled): halves the live temporaries
+#pragma unroll 1
+        for (int e = 0; e < 2; ++e) {
+          float dA = 0.f, dsc = 0.f;
+          if (valid) {
+            const int t = 2 * tp + e;
+            const uint32_t o = (uint32_t)(t * N + j0) * 2;
+            const vec q0 = buf_load<vec>(rQ, o, sqk), q1 = buf_load<vec>(rQ, o + 2 * H2, sqk);
+            const vec k0 = buf_load<vec>(rK, o, sqk), k1 = buf_load<vec>(rK, o + 2 * H2, sqk);
+            float ph[VEC];
+#pragma unroll
+            for (int qd = 0; qd < VEC / 4; ++qd) {
+              const int j = j0 + 4 * qd;
+              const uint32_t op = (uint32_t)(t * Nr + j) * 4;
+              f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
+              if (phi_vec && j + 4 <= Nr) {
+                v4 = buf_load<f32x4>(rPhi, op, sphi);
+              } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v4[i] = (j + i < Nr) ? buf_load<float>(rPhi, op + 4 * i, sphi) : 0.f;
+              }
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ph[4 * qd + i] = v4[i];
+            }
+            const float sc = sScl[t];
+            const float cd = sDqk[t] * sGam[t];
+            vec du0, du1, dw0, dw1;
+            float dphv[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              const int j = j0 + i;
+              const float ulo = (float)q0[i] + sQb[j];
+              const float uhi = (float)q1[i] + sQb[H2 + j];
+              const float wlo = (float)k0[i] + sKb[j];
+              const float whi = (float)k1[i] + sKb[H2 + j];
+              float sn = 0.f, cs = 1.f;
+              if (j < Nr) {
+                const float turns = ph[i] * 0.15915494309189535f;
+                sn = __builtin_amdgcn_sinf(turns);
+                cs = __builtin_amdgcn_cosf(turns);
+              }
+              const float qlo = ulo * cs - uhi * sn, qhi = uhi * cs + ulo * sn;
+              const float klo = wlo * cs - whi * sn, khi = whi * cs + wlo * sn;
+              const float dqlo = sDQ[t * LDF + j], dqhi = sDQ[t * LDF + H2 + j];
+              const float dklo = sDK[t * LDF + j], dkhi = sDK[t * LDF + H2 + j];
+              dA += qlo * dqlo + qhi * dqhi - (klo * sc) * dklo - (khi * sc) * dkhi;
+              dsc += dklo * klo + dkhi * khi;
+              const float dtlo = dklo * sc, dthi = dkhi * sc;   // d k~
+              // R^T = R(-phi): lo' = lo cos + hi sin, hi' = hi cos - lo sin
+              const float dulo = dqlo * cs + dqhi * sn + cd * wlo;
+              const float duhi = dqhi * cs - dqlo * sn + cd * whi;
+              const float dwlo = dtlo * cs + dthi * sn + cd * ulo;
+              const float dwhi = dthi * cs - dtlo * sn + cd * uhi;
+              dphv[i] = (dqhi * qlo - dqlo * qhi) + (dthi * klo - dtlo * khi);
+              if (c == nc - 1 && t == C - 1) {
+                p.kfin[bh * N + j] = klo;
+                p.kfin[bh * N + H2 + j] = khi;
+              }
+              du0[i] = dulo;
+              du1[i] = duhi;
+              dw0[i] = dwlo;
+              dw1[i] = dwhi;
+              // bias partials (f32): summed over the row pairs of the wave that share
+              // the column group, then one LDS atomic per element
+              float bqv[4] = {dulo, duhi, dwlo, dwhi};
+#pragma unroll
+              for (int m = F::QKG; m < 64; m <<= 1) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) bqv[u] += __shfl_xor(bqv[u], m, 64);
+              }
+              if (lane < F::QKG) {
+                atomicAdd(sDqb + j, bqv[0]);
+                atomicAdd(sDqb + H2 + j, bqv[1]);
+                atomicAdd(sDkb + j, bqv[2]);
+                atomicAdd(sDkb + H2 + j, bqv[3]);
+              }
+            }
+            if (p.dphi) {
+#pragma unroll
+              for (int qd = 0; qd < VEC / 4; ++qd) {
+                const int j = j0 + 4 * qd;
+                const uint32_t op = (uint32_t)(t * Nr + j) * 4;
+                if (phi_vec && j + 4 <= Nr) {
+                  buf_store(f32x4{dphv[4 * qd], dphv[4 * qd + 1], dphv[4 * qd + 2], dphv[4 * qd + 3]},
+                            rDphi, op, sphi);
+                } else {
+#pragma unroll
+                  for (int i = 0; i < 4; ++i)
+                    if (j + i < Nr) buf_store_f32(dphv[4 * qd + i], rDphi, op + 4 * i, sphi);
+                }
+              }
+            }
+            // this head's du / dw row pieces; the head sum happens in headsum_kernel
+            buf_store(du0, rDu, o, sqk);
+            buf_store(du1, rDu, o + 2 * H2, sqk);
+            buf_store(dw0, rDw, o, sqk);
+            buf_store(dw1, rDw, o + 2 * H2, sqk);
+          }
+          dA = group_sum<F::QKG>(dA);
+          dsc = group_sum<F::QKG>(dsc);
+          if (valid && j0 == 0) {
+            sDA[2 * tp + e] = dA;
+            buf_store_f32(dsc, rDsc, (uint32_t)(2 * tp + e) * 4, (uint32_t)t0 * 4);
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    if (c > 0) prefetch_rest(c - 1);   // the previous chunk's v, dy, z, ybar, state
+    // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
+    if (wave == 0) {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63;
+      const float extra = sRed[0];
+      float a[F::E];
+      float run = 0.f;
+#pragma unroll
+      for (int e = F::E - 1; e >= 0; --e) {
+        run += sDA[lane * F::E + e];
+        a[e] = run;
+      }
+      float incl = run;   // suffix scan across lanes: inclusive sum over lanes >= this one
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_down(incl, off, 64);
+        if (lane + off < 64) incl += o;
+      }
+      const float excl = incl - run;
+#pragma unroll
+      for (int e = 0; e < F::E; ++e)
+        buf_store_f32(excl + a[e] + extra, rDadt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)t0 * 4);
+    }
+    publish_adjoint();
+    __syncthreads();
+    if (tid == 0) sRed[0] = 0.f;
+  }
+
+  // ---- per-(b, h) outputs ------------------------------------------------------------
+#pragma unroll
+  for (int m = 0; m < SPW; ++m) {
+    const int nb = nb0 + NSTEP * m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      p.dseed[(bh * P + pb_w * 16 + 4 * (lane >> 4) + i) * N + nb * 16 + (lane & 15)] = Gacc[m][i];
+  }
+  __syncthreads();
+  for (int i = tid; i < N; i += NT) {
+    p.dqb[bh * N + i] = sDqb[i];
+    p.dkb[bh * N + i] = sDkb[i];
+  }
+}
+
 // dq[b, t, :] = sum_h du[b, h, t, :] (and dk from dw): one thread per 4 consecutive
 // elements of a (b, t) row, summing over heads in f32. Bandwidth-bound.
 template <typename MT>
@@ -834,10 +1570,31 @@ __global__ void __launch_bounds__(256) headsum_kernel(const MT* __restrict__ par
   *reinterpret_cast<f32x4*>((which ? dk : dq) + (int64_t)b * LN + i4) = acc;
 }
 
+// Every per-(b, h) stream of bwd_bf16_kernel must be addressable with 31-bit byte
+// offsets from its buffer descriptor.
+static bool bwd_fits_rsrc(const BwdParams& p, int N, int P) {
+  const int64_t lim = (int64_t(1) << 31) - 1;
+  const int64_t L = p.L;
+  auto span = [&](int64_t st) { return ((L - 1) * st + P) * 2; };
+  return L * N * 2 <= lim && L * p.Nr * 4 <= lim && L * P * 4 <= lim && span(p.v_st) <= lim &&
+         span(p.dy_st) <= lim && span(p.dv_st) <= lim &&
+         (!p.has_z || (span(p.z_st) <= lim && span(p.dz_st) <= lim)) &&
+         (int64_t)p.nc * N * P * 2 <= lim;
+}
+
 template <typename MT, int C, int N, int P>
 static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
-  constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
-  hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  bool done = false;
+  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
+    if (bwd_fits_rsrc(prm, N, P)) {
+      hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      done = true;
+    }
+  }
+  if (!done) {
+    constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
+    hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+  }
   int32_t rc = launch_status("m3s_bwd");
   if (rc != M3S_OK) return rc;
   const int64_t LN = (int64_t)prm.L * N;

@@ -169,6 +169,12 @@ __device__ __forceinline__ void buf_store(f32x4 x, __amdgpu_buffer_rsrc_t r, uin
 __device__ __forceinline__ void buf_store(bf16x4 x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i32x2, x), r, v, s, 0);
 }
+__device__ __forceinline__ void buf_store_f32(float x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, x), r, v, s, 0);
+}
+__device__ __forceinline__ void buf_store_bf16(float x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (bf16)x), r, v, s, 0);
+}
 
 // Asynchronous 16-byte-per-lane load straight into LDS (no VGPR round trip): lane l's
 // 16 bytes from rsrc + voffset + soffset land at lds_block + 16 l, so one instruction
