@@ -940,13 +940,15 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   const auto rYb = make_rsrc(ybg, (uint32_t)L * P * 4);
   const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
   const auto rCs = make_rsrc(csg, (uint32_t)nc * N * P * 2);
-  const auto rAdt = make_rsrc(p.adt + bh * L, (uint32_t)L * 4);
-  const auto rGam = make_rsrc(p.gamma + bh * L, (uint32_t)L * 4);
-  const auto rScl = make_rsrc(p.scale + bh * L, (uint32_t)L * 4);
-  const auto rUw = make_rsrc(p.uw + bh * L, (uint32_t)L * 4);
-  const auto rDqk = make_rsrc(p.dqk + bh * L, (uint32_t)L * 4);
-  const auto rDsc = make_rsrc(p.dscale + bh * L, (uint32_t)L * 4);
-  const auto rDadt = make_rsrc(p.dadt + bh * L, (uint32_t)L * 4);
+  // the (B, H, L) scalar streams: a uniform row base plus a 32-bit offset (SGPR-base
+  // global access), which keeps them out of the descriptor set
+  const float* adt_r = p.adt + bh * L;
+  const float* gam_r = p.gamma + bh * L;
+  const float* scl_r = p.scale + bh * L;
+  float* uw_r = p.uw + bh * L;
+  float* dqk_r = p.dqk + bh * L;
+  float* dsc_r = p.dscale + bh * L;
+  float* dadt_r = p.dadt + bh * L;
   const auto rDphi = make_rsrc(p.dphi ? p.dphi + bh * (int64_t)L * Nr : nullptr,
                                p.dphi ? (uint32_t)L * Nr * 4 : 0u);
   const auto rDu = make_rsrc(dug, (uint32_t)L * N * 2);
@@ -1015,7 +1017,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
                 rphi[r][e][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, op + 4 * i, sphi) : 0.f;
             }
           }
-          rscale[r][e] = buf_load<float>(rScl, (uint32_t)t * 4, (uint32_t)c * C * 4);
+          rscale[r][e] = scl_r[(uint32_t)(c * C + t)];
         }
       }
     }
@@ -1051,11 +1053,11 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     if (wave == 0) {
 #pragma unroll
       for (int e = 0; e < F::E; ++e)
-        radt[e] = buf_load<float>(rAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+        radt[e] = adt_r[(uint32_t)(c * C + lane * F::E + e)];
     }
     if (tid < C) {
-      rgam_s = buf_load<float>(rGam, (uint32_t)tid * 4, (uint32_t)c * C * 4);
-      rscl_s = buf_load<float>(rScl, (uint32_t)tid * 4, (uint32_t)c * C * 4);
+      rgam_s = gam_r[(uint32_t)(c * C + tid)];
+      rscl_s = scl_r[(uint32_t)(c * C + tid)];
     }
   };
 
@@ -1108,6 +1110,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int t = 2 * tp + e;
+          __builtin_amdgcn_sched_barrier(0);   // rows one after the other: fewer live values
           if (valid) {
             vec oq0, oq1, ok0, ok1;
 #pragma unroll
@@ -1142,8 +1145,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
             const int t = 2 * tp + e;
-            buf_store_f32(uw[e], rUw, (uint32_t)t * 4, (uint32_t)t0 * 4);
-            sCoef[t] = buf_load<float>(rGam, (uint32_t)t * 4, (uint32_t)t0 * 4) * uw[e] + dsk;
+            uw_r[(uint32_t)(t0 + t)] = uw[e];
+            sCoef[t] = gam_r[(uint32_t)(t0 + t)] * uw[e] + dsk;
           }
         }
       }
@@ -1156,6 +1159,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int t = 2 * tp + e;
+          __builtin_amdgcn_sched_barrier(0);
           if (valid) {
             vec og, odz;
 #pragma unroll
@@ -1183,7 +1187,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           for (int e = 0; e < 2; ++e) {
             const int t = 2 * tp + e;
             sDqk[t] = dqk[e];
-            buf_store_f32(dqk[e], rDqk, (uint32_t)t * 4, (uint32_t)t0 * 4);
+            dqk_r[(uint32_t)(t0 + t)] = dqk[e];
           }
         }
       }
@@ -1498,7 +1502,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           dsc = group_sum<F::QKG>(dsc);
           if (valid && j0 == 0) {
             sDA[2 * tp + e] = dA;
-            buf_store_f32(dsc, rDsc, (uint32_t)(2 * tp + e) * 4, (uint32_t)t0 * 4);
+            dsc_r[(uint32_t)(t0 + 2 * tp + e)] = dsc;
           }
         }
       }
@@ -1528,7 +1532,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
       const float excl = incl - run;
 #pragma unroll
       for (int e = 0; e < F::E; ++e)
-        buf_store_f32(excl + a[e] + extra, rDadt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)t0 * 4);
+        dadt_r[(uint32_t)(t0 + lane * F::E + e)] = excl + a[e] + extra;
     }
     publish_adjoint();
     __syncthreads();

@@ -62,6 +62,26 @@ def test_backward_bf16_matches_autograd_of_oracle(m3, chunk, seeds, dfin):
         assert_maxrel(getattr(gr, GRAD_FIELD[name]), w, BF16_MAXREL, f"d{name}")
 
 
+@pytest.mark.parametrize("n,chunk", [(64, 64), (128, 128)])
+def test_backward_bf16_state64_and_no_gate(m3, n, chunk):
+    """The bf16 backward at state_dim 64, and without the gate z and skip D."""
+    want, gr = run_case(m3, 2, 2, 256, n, 64, n // 4, chunk, "bf16", True, True)
+    for name, w in want.items():
+        assert_maxrel(getattr(gr, GRAD_FIELD[name]), w, BF16_MAXREL, f"d{name}")
+    c, d = boundary_inputs(1, 3, 256, 128, 64, 32, "bf16", seed=5)
+    for t in (c, d):
+        t.pop("d_skip"), t.pop("z")
+    want = O.boundary_grads({k_: c[k_] for k_ in NAMES if k_ in c}, c["dy"], None, None, None,
+                            chunk=chunk)
+    out = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy="bf16", save_residuals=True)
+    gr = m3.siso_backward(d["dy"], d["q"], d["k"], d["v"], d["adt"], d["gamma"], d["scale"],
+                          d["phi"], d["q_bias"], d["k_bias"], out[4].ybar, out[4].chunk_states,
+                          chunk=chunk, dtype_policy="bf16")
+    assert gr.dz is None and gr.dd_skip is None
+    for name, w in want.items():
+        assert_maxrel(getattr(gr, GRAD_FIELD[name]), w, BF16_MAXREL, f"d{name} (no gate)")
+
+
 def test_backward_matches_finite_differences_of_the_kernel_forward(m3):
     """Central differences of the HIP forward itself (f32, tiny): the VJP is checked
     against the function it differentiates, as tests.py:614-645 does."""

@@ -5,8 +5,8 @@ import math
 import pytest
 import torch
 
-from helpers import (BF16, BF16_MAXREL, BF16_MODEL_P95, BF16_P95, F32, FWD_F32_P95,
-                     assert_maxrel, assert_p95, boundary_inputs, cpu, fwd_args)
+from helpers import (BF16, BF16_MAXREL, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_P95, F32,
+                     FWD_F32_P95, assert_maxrel, assert_p95, boundary_inputs, cpu, fwd_args)
 from oracle import siso_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -58,6 +58,37 @@ def test_forward_bf16_matches_rounding_model_and_maths(m3, chunk):
     assert_maxrel(y, yr, BF16_MAXREL, "y")
     assert_maxrel(fs, sr.ssm, BF16_MAXREL, "final ssm")
     assert_p95(fk, sr.k, FWD_F32_P95, "final k (computed in f32)")
+
+
+@pytest.mark.parametrize("n,chunk,gate", [(64, 64, True), (128, 128, False), (128, 64, False)])
+def test_forward_bf16_other_shapes_and_no_gate(m3, n, chunk, gate):
+    """The bf16 kernel's other compiled shapes (state_dim 64) and its path without the
+    gate z and the skip D, against the rounding model and the float64 maths."""
+    c, d = boundary_inputs(2, 3, 256, n, 64, n // 4, "bf16", seed=11)
+    if not gate:
+        c.pop("d_skip"), c.pop("z"), d.pop("d_skip"), d.pop("z")
+    yr, sr, _ = oracle_fwd(c, chunk)
+    ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
+    y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy="bf16",
+                                         save_residuals=True)
+    assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+    assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
+    # chunk states are stored in bf16: one more rounding of up to 2^-8 relative
+    assert_p95(res.chunk_states, dbgm["chunk_states"], BF16_OUT_MODEL_P95, "chunk states vs bf16 model")
+    assert_maxrel(y, yr, BF16_MAXREL, "y")
+    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+    assert_p95(fv, sr.v, FWD_F32_P95, "final v")
+
+
+def test_forward_bf16_with_carried_state(m3):
+    c, d = boundary_inputs(2, 2, 256, 128, 64, 32, "bf16", seed=13, seeds=True)
+    yr, sr, _ = oracle_fwd(c, 128, with_seed=True)
+    ym, sm, dbgm = oracle_fwd(c, 128, with_seed=True, mm=BF16)
+    y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=128, dtype_policy="bf16",
+                                         save_residuals=True)
+    assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model (seeded)")
+    assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model (seeded)")
+    assert_maxrel(y, yr, BF16_MAXREL, "y (seeded)")
 
 
 def test_forward_with_carried_state(m3):
