@@ -135,10 +135,10 @@ def main():
                         scan_kernel_tflops=round(scan_tflops, 2),
                         scan_kernel_mfma_frac=round(scan_tflops / BF16_PEAK_TFLOPS, 5))
             line["roofline"] = {
-                "kernel": "fwd_kernel<bf16,128,128,64> (m3s_fwd, kernel boundary)",
+                "kernel": "fwd_bf16_kernel<128,128,64> (m3s_fwd, kernel boundary)",
                 "bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic_figure("fwd_kernel"), "algorithmic_bytes": scan_bytes}
+                "traffic": traffic_figure("fwd_bf16_kernel"), "algorithmic_bytes": scan_bytes}
         if args.leg in ("all", "bwd"):
             with torch.no_grad():
                 y, fs, fk, fv, res = K.siso_forward(**ka, chunk=128, save_residuals=True)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 3
+#define M3S_ABI_VERSION 4
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -203,6 +203,42 @@ typedef struct m3s_prep_bwd_args {
   void* workspace; /* scratch, m3s_prep_bwd_workspace_bytes() bytes, 16-aligned */
 } m3s_prep_bwd_args;
 
+/* The layer's BCNorm. Replaces `layer.rms_norm` (layer.py:190-198) as applied to the B
+ * and C slices of the projection (layer.py:235-236): rstd = rsqrt(mean(x^2) + eps),
+ * y = (x rstd w) cast to x's dtype, computed in f32. `count` norms (1 or 2) run in one
+ * launch. */
+typedef struct m3s_norm_fwd_args {
+  int32_t struct_size;   /* sizeof(m3s_norm_fwd_args) */
+  int32_t batch, seqlen, width; /* width: the normalised axis (state_dim); a multiple of
+                                   16 bytes, at most 64 * 16 bytes */
+  int32_t dtype;         /* M3S_DTYPE_* of x and y */
+  int32_t count;         /* 1 or 2 */
+  float eps;
+  m3s_blx x[2];          /* (B, L, width), 16-byte aligned rows */
+  const float* weight[2];/* (width) gains */
+  void* y[2];            /* out (B, L, width), dense, 16-byte aligned */
+  float* rstd[2];        /* out (B, L) for the backward, or NULL */
+} m3s_norm_fwd_args;
+
+/* Backward of m3s_norm_fwd (autograd of layer.py:190-198). dy arrives in f32 and is
+ * first cast to the dtype, as the scan's q/k cotangents are cast to the primal dtype
+ * (siso.py:140-148); dx is written through strides (the layer writes it into the B and
+ * C slices of the projection's gradient); dweight is summed over batch and time in a
+ * fixed order. */
+typedef struct m3s_norm_bwd_args {
+  int32_t struct_size;   /* sizeof(m3s_norm_bwd_args) */
+  int32_t batch, seqlen, width;
+  int32_t dtype;         /* M3S_DTYPE_* of x and dx */
+  int32_t count;         /* 1 or 2 */
+  m3s_blx x[2];          /* the forward's inputs */
+  const float* weight[2];/* (width) */
+  const float* rstd[2];  /* (B, L), from m3s_norm_fwd */
+  const float* dy[2];    /* (B, L, width) f32, dense, 16-byte aligned */
+  m3s_blx dx[2];         /* out (B, L, width), 16-byte aligned rows */
+  float* dweight[2];     /* out (width) */
+  void* workspace;       /* scratch, m3s_norm_bwd_workspace_bytes() bytes, 16-aligned */
+} m3s_norm_bwd_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -229,11 +265,17 @@ int64_t m3s_prep_fwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nhea
 int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                      int32_t n_angles);
 
+/* Bytes of m3s_norm_bwd_args.workspace: per-block gain partials (1024, 2, width) f32.
+ * No counterpart in the reference. -1 on a bad width. */
+int64_t m3s_norm_bwd_workspace_bytes(int32_t width);
+
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
 int32_t m3s_decode(const m3s_decode_args* args, void* stream);
 int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
 int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
+int32_t m3s_norm_fwd(const m3s_norm_fwd_args* args, void* stream);
+int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
 
 #ifdef __cplusplus
 }

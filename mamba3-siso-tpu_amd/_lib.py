@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -106,10 +106,31 @@ class PrepBwdArgs(C.Structure):
     ]
 
 
+class NormFwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("width", i32),
+        ("dtype", i32), ("count", i32), ("eps", C.c_float),
+        ("x", Blx * 2), ("weight", vp * 2), ("y", vp * 2), ("rstd", vp * 2),
+    ]
+
+
+class NormBwdArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("seqlen", i32), ("width", i32),
+        ("dtype", i32), ("count", i32),
+        ("x", Blx * 2), ("weight", vp * 2), ("rstd", vp * 2), ("dy", vp * 2),
+        ("dx", Blx * 2), ("dweight", vp * 2),
+        ("workspace", vp),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
-           "m3s_prep_fwd", "m3s_prep_bwd")
+           "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
+           "m3s_norm_bwd")
 
 _lib = None
 
@@ -146,6 +167,12 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_prep_fwd.argtypes = [C.POINTER(PrepFwdArgs), vp]
     lib.m3s_prep_bwd.restype = i32
     lib.m3s_prep_bwd.argtypes = [C.POINTER(PrepBwdArgs), vp]
+    lib.m3s_norm_bwd_workspace_bytes.restype = i64
+    lib.m3s_norm_bwd_workspace_bytes.argtypes = [i32]
+    lib.m3s_norm_fwd.restype = i32
+    lib.m3s_norm_fwd.argtypes = [C.POINTER(NormFwdArgs), vp]
+    lib.m3s_norm_bwd.restype = i32
+    lib.m3s_norm_bwd.argtypes = [C.POINTER(NormBwdArgs), vp]
     ver = lib.m3s_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")

@@ -1,0 +1,282 @@
+// The layer's BCNorm on gfx950: RMSNorm over the state axis of the projection's B and
+// C slices, forward and backward, both norms in one launch.
+//
+// Replaces `layer.rms_norm` (layer.py:190-198) as applied to B and C at
+// layer.py:235-236, and its autograd:
+//
+//   forward:   rstd = rsqrt(mean_n x^2 + eps),   y = (x rstd w) cast to x's dtype   (f32 math)
+//   backward:  g = dy cast to x's dtype (the layer hands its q/k cotangent back in the
+//              primal dtype, siso.py:140-148), then in f32
+//              dx = rstd g w - (rstd^3 / N) x sum_n(g w x),   dw = sum_rows g x rstd
+//
+// A row of N values is owned by a group of G lanes (16 bytes each, G a power of two,
+// lanes past N idle); the row statistic is a shuffle reduction inside the group. Rows
+// are read in place through (b, t) strides, so the slices of the fused projection need
+// no copy, and dx lands directly in the slices of the projection's gradient. The gain
+// gradient is summed per block in a fixed order, then over blocks by a second launch,
+// so it does not depend on the order in which blocks finish. HBM-bound.
+#include <algorithm>
+
+#include "m3s_common.h"
+#include "m3s_internal.h"
+
+namespace m3s {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormBwdBlocks = 1024;   // fixed grid of the backward: bounded partials
+
+struct NormRows {
+  const void* x[2];
+  int64_t xsb[2], xst[2];
+  const float* w[2];
+};
+
+struct NormFwdParams {
+  NormRows in;
+  int B, L, N, G;
+  float eps;
+  void* y[2];
+  float* rstd[2];
+};
+
+struct NormBwdParams {
+  NormRows in;
+  int B, L, N, G;
+  const float* rstd[2];
+  const float* dy[2];
+  void* dx[2];
+  int64_t dxsb[2], dxst[2];
+  float* part;   // (gridDim.x, 2, N) gain partials
+};
+
+template <typename T> struct NVec;
+template <> struct NVec<bf16> { static constexpr int n = 8; typedef bf16x8 type; };
+template <> struct NVec<float> { static constexpr int n = 4; typedef f32x4 type; };
+
+template <typename T>
+__device__ __forceinline__ void load_row(const T* p, float (&v)[NVec<T>::n]) {
+  const auto r = *reinterpret_cast<const typename NVec<T>::type*>(p);
+#pragma unroll
+  for (int i = 0; i < NVec<T>::n; ++i) v[i] = (float)r[i];
+}
+
+template <typename T>
+__device__ __forceinline__ void store_row(T* p, const float (&v)[NVec<T>::n]) {
+  typename NVec<T>::type r;
+#pragma unroll
+  for (int i = 0; i < NVec<T>::n; ++i) r[i] = (T)v[i];
+  *reinterpret_cast<typename NVec<T>::type*>(p) = r;
+}
+
+__device__ __forceinline__ float group_sum_dyn(float v, int G) {
+  for (int m = 1; m < G; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kNormThreads) norm_fwd_kernel(const NormFwdParams p) {
+  constexpr int VEC = NVec<T>::n;
+  const int which = blockIdx.y;
+  const int G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
+  const int rows_per_block = kNormThreads / G;
+  const int64_t M = (int64_t)p.B * p.L;
+  const int64_t r = (int64_t)blockIdx.x * rows_per_block + gid;
+  if (r >= M) return;   // whole groups leave together: the shuffles below stay in-group
+  const int b = (int)(r / p.L), t = (int)(r % p.L);
+  const int n0 = gl * VEC;
+  const bool act = n0 < p.N;
+  const T* xrow = static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] + t * p.in.xst[which];
+  float x[VEC];
+  float ss = 0.f;
+  if (act) {
+    load_row<T>(xrow + n0, x);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) ss += x[i] * x[i];
+  }
+  ss = group_sum_dyn(ss, G);
+  const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
+  if (act) {
+    const float* w = p.in.w[which] + n0;
+    float y[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) y[i] = x[i] * rstd * w[i];
+    store_row<T>(static_cast<T*>(p.y[which]) + r * p.N + n0, y);
+  }
+  if (gl == 0 && p.rstd[which]) p.rstd[which][r] = rstd;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kNormThreads) norm_bwd_kernel(const NormBwdParams p) {
+  constexpr int VEC = NVec<T>::n;
+  __shared__ float sAcc[kNormThreads * VEC];
+  const int which = blockIdx.y;
+  const int G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
+  const int rows_per_pass = kNormThreads / G;
+  const int64_t M = (int64_t)p.B * p.L;
+  const int n0 = gl * VEC;
+  const bool act = n0 < p.N;
+  const float* w = p.in.w[which] + (act ? n0 : 0);
+  float wv[VEC], acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    wv[i] = act ? w[i] : 0.f;
+    acc[i] = 0.f;
+  }
+  const float inv_n = 1.f / (float)p.N;
+  for (int64_t r = (int64_t)blockIdx.x * rows_per_pass + gid; r < M;
+       r += (int64_t)gridDim.x * rows_per_pass) {
+    const int b = (int)(r / p.L), t = (int)(r % p.L);
+    const float rstd = p.rstd[which][r];
+    float x[VEC], g[VEC];
+    float s = 0.f;
+    if (act) {
+      load_row<T>(static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] + t * p.in.xst[which] + n0, x);
+      const float* dyr = p.dy[which] + r * p.N + n0;
+#pragma unroll
+      for (int i = 0; i < VEC; i += 4) {
+        const f32x4 d = *reinterpret_cast<const f32x4*>(dyr + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g[i + k] = (float)(T)d[k];   // the primal-dtype cast
+      }
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        s += g[i] * wv[i] * x[i];
+        acc[i] += g[i] * x[i] * rstd;
+      }
+    }
+    s = group_sum_dyn(s, G);
+    if (act) {
+      const float c = rstd * rstd * rstd * inv_n * s;
+      float dx[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) dx[i] = rstd * g[i] * wv[i] - c * x[i];
+      store_row<T>(static_cast<T*>(p.dx[which]) + b * p.dxsb[which] + t * p.dxst[which] + n0, dx);
+    }
+  }
+  // gain partials: sum the groups of this block in a fixed order
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) sAcc[threadIdx.x * VEC + i] = acc[i];
+  __syncthreads();
+  for (int n = threadIdx.x; n < p.N; n += kNormThreads) {
+    const int l = n / VEC, i = n % VEC;
+    float tot = 0.f;
+    for (int q = 0; q < rows_per_pass; ++q) tot += sAcc[(q * G + l) * VEC + i];
+    p.part[((int64_t)blockIdx.x * 2 + which) * p.N + n] = tot;
+  }
+}
+
+// dw[which][n] = sum over blocks of the partials, in block order (one thread per column,
+// four independent accumulators).
+__global__ void __launch_bounds__(kNormThreads) norm_gain_kernel(const float* __restrict__ part,
+                                                                 float* dw0, float* dw1,
+                                                                 int nblk, int N) {
+  const int which = blockIdx.y;
+  const int n = blockIdx.x * kNormThreads + threadIdx.x;
+  if (n >= N) return;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (; k + 4 <= nblk; k += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] += part[((int64_t)(k + u) * 2 + which) * N + n];
+  }
+  for (; k < nblk; ++k) a[0] += part[((int64_t)k * 2 + which) * N + n];
+  (which ? dw1 : dw0)[n] = (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+static int norm_group(int N, int vec) {
+  int lanes = N / vec, G = 1;
+  while (G < lanes) G <<= 1;
+  return G;
+}
+
+static bool blx_ok(const m3s_blx& t, int vec) {
+  return t.ptr != nullptr && aligned16(t.ptr) && t.stride_b % vec == 0 && t.stride_t % vec == 0;
+}
+
+}  // namespace m3s
+
+using namespace m3s;
+
+extern "C" int64_t m3s_norm_bwd_workspace_bytes(int32_t width) {
+  if (width <= 0) return -1;
+  return (int64_t)kNormBwdBlocks * 2 * width * 4;
+}
+
+extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
+  clear_error();
+  M3S_REQUIRE(a != nullptr, "m3s_norm_fwd: args is NULL");
+  M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_norm_fwd_args),
+              "m3s_norm_fwd: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              (int)sizeof(m3s_norm_fwd_args));
+  const int B = a->batch, L = a->seqlen, N = a->width, cnt = a->count;
+  M3S_REQUIRE(B > 0 && L > 0 && N > 0 && (cnt == 1 || cnt == 2), "m3s_norm_fwd: bad dimension");
+  M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
+              "m3s_norm_fwd: bad dtype %d", a->dtype);
+  const int vec = a->dtype == M3S_DTYPE_BF16 ? 8 : 4;
+  M3S_REQUIRE(N % vec == 0 && N / vec <= 64,
+              "m3s_norm_fwd: width %d must be a multiple of %d and at most %d", N, vec, 64 * vec);
+  M3S_REQUIRE((int64_t)B * L < (1ll << 31), "m3s_norm_fwd: B*L too large");
+  NormFwdParams p{};
+  for (int i = 0; i < cnt; ++i) {
+    M3S_REQUIRE(blx_ok(a->x[i], vec), "m3s_norm_fwd: x[%d] must be 16-byte aligned rows", i);
+    M3S_REQUIRE(a->weight[i] && a->y[i] && aligned16(a->y[i]),
+                "m3s_norm_fwd: weight[%d] NULL or y[%d] NULL / misaligned", i, i);
+    p.in.x[i] = a->x[i].ptr; p.in.xsb[i] = a->x[i].stride_b; p.in.xst[i] = a->x[i].stride_t;
+    p.in.w[i] = a->weight[i];
+    p.y[i] = a->y[i];
+    p.rstd[i] = a->rstd[i];
+  }
+  p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec); p.eps = a->eps;
+  const int64_t rows_per_block = kNormThreads / p.G;
+  const dim3 grid((unsigned)(((int64_t)B * L + rows_per_block - 1) / rows_per_block), cnt);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->dtype == M3S_DTYPE_BF16)
+    hipLaunchKernelGGL(norm_fwd_kernel<bf16>, grid, dim3(kNormThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(norm_fwd_kernel<float>, grid, dim3(kNormThreads), 0, s, p);
+  return launch_status("m3s_norm_fwd");
+}
+
+extern "C" int32_t m3s_norm_bwd(const m3s_norm_bwd_args* a, void* stream) {
+  clear_error();
+  M3S_REQUIRE(a != nullptr, "m3s_norm_bwd: args is NULL");
+  M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_norm_bwd_args),
+              "m3s_norm_bwd: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              (int)sizeof(m3s_norm_bwd_args));
+  const int B = a->batch, L = a->seqlen, N = a->width, cnt = a->count;
+  M3S_REQUIRE(B > 0 && L > 0 && N > 0 && (cnt == 1 || cnt == 2), "m3s_norm_bwd: bad dimension");
+  M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
+              "m3s_norm_bwd: bad dtype %d", a->dtype);
+  const int vec = a->dtype == M3S_DTYPE_BF16 ? 8 : 4;
+  M3S_REQUIRE(N % vec == 0 && N / vec <= 64,
+              "m3s_norm_bwd: width %d must be a multiple of %d and at most %d", N, vec, 64 * vec);
+  M3S_REQUIRE((int64_t)B * L < (1ll << 31), "m3s_norm_bwd: B*L too large");
+  M3S_REQUIRE(a->workspace && aligned16(a->workspace), "m3s_norm_bwd: workspace NULL or misaligned");
+  NormBwdParams p{};
+  for (int i = 0; i < cnt; ++i) {
+    M3S_REQUIRE(blx_ok(a->x[i], vec), "m3s_norm_bwd: x[%d] must be 16-byte aligned rows", i);
+    M3S_REQUIRE(blx_ok(a->dx[i], vec), "m3s_norm_bwd: dx[%d] must be 16-byte aligned rows", i);
+    M3S_REQUIRE(a->weight[i] && a->rstd[i] && a->dy[i] && aligned16(a->dy[i]) && a->dweight[i],
+                "m3s_norm_bwd: weight/rstd/dy/dweight[%d] NULL or dy misaligned", i);
+    p.in.x[i] = a->x[i].ptr; p.in.xsb[i] = a->x[i].stride_b; p.in.xst[i] = a->x[i].stride_t;
+    p.in.w[i] = a->weight[i];
+    p.rstd[i] = a->rstd[i];
+    p.dy[i] = a->dy[i];
+    p.dx[i] = a->dx[i].ptr; p.dxsb[i] = a->dx[i].stride_b; p.dxst[i] = a->dx[i].stride_t;
+  }
+  p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec);
+  p.part = static_cast<float*>(a->workspace);
+  const int64_t rows_per_pass = kNormThreads / p.G;
+  const int nblk = (int)std::min<int64_t>(kNormBwdBlocks, ((int64_t)B * L + rows_per_pass - 1) / rows_per_pass);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->dtype == M3S_DTYPE_BF16)
+    hipLaunchKernelGGL(norm_bwd_kernel<bf16>, dim3(nblk, cnt), dim3(kNormThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL(norm_bwd_kernel<float>, dim3(nblk, cnt), dim3(kNormThreads), 0, s, p);
+  int32_t rc = launch_status("m3s_norm_bwd");
+  if (rc) return rc;
+  hipLaunchKernelGGL(norm_gain_kernel, dim3((N + kNormThreads - 1) / kNormThreads, cnt),
+                     dim3(kNormThreads), 0, s, p.part, a->dweight[0], cnt > 1 ? a->dweight[1] : nullptr,
+                     nblk, N);
+  return launch_status("m3s_norm_bwd");
+}

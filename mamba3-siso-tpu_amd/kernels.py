@@ -302,6 +302,20 @@ class KernelGrads(NamedTuple):
     dseed_ssm: Tensor
 
 
+def _out_buffer(out: Optional[Tensor], like: Tensor, mt: torch.dtype, name: str) -> Tensor:
+    """``out`` checked as a (B, H, L, P) destination the kernel writes in place, or a new
+    tensor laid out like ``like``."""
+    if out is None:
+        return _empty_like_layout(like, mt)
+    vec = 16 // out.element_size()
+    if (tuple(out.shape) != tuple(like.shape) or out.dtype != mt or out.device != like.device
+            or out.stride(3) != 1 or out.data_ptr() % 16
+            or any(out.stride(i) % vec for i in range(3))):
+        raise ValueError(f"{name} must be a {tuple(like.shape)} {mt} tensor on {like.device} "
+                         "with 16-byte aligned rows and a unit last stride")
+    return out
+
+
 def _nmajor_states(chunk_states: Tensor, mt: torch.dtype) -> Tensor:
     """The kernel reads chunk states N-major, ``(B, H, nc, N, P)`` contiguous. The
     forward's residual is a transposed view of exactly that; anything else is copied."""
@@ -318,10 +332,14 @@ def siso_backward_kernel(
     dfinal_ssm: Optional[Tensor] = None, chunk: int = 128,
     dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
     device_kind: str | None = None, *, dfinal_v: Optional[Tensor] = None,
+    dv_out: Optional[Tensor] = None, dz_out: Optional[Tensor] = None,
 ) -> KernelGrads:
     """Reverse chunk scan (``kernel_bwd.py:358-395``). ``dfinal_v`` (keyword-only) is
     added to ``dv``'s last row inside the kernel, before the cast to the operand type
-    (the reference does it in its epilogue, ``kernel_bwd.py:632-637``)."""
+    (the reference does it in its epilogue, ``kernel_bwd.py:632-637``). ``dv_out`` /
+    ``dz_out`` (keyword-only) are ``(B, H, L, P)`` buffers of the operand type, any
+    strides with a unit P stride (e.g. slices of the projection's gradient), that
+    receive ``dv`` / ``dz`` in place of fresh tensors."""
     pol = LY.policy(dtype_policy)
     LY.validate_chunk(chunk)
     batch, seqlen, state_dim = q.shape
@@ -352,8 +370,8 @@ def siso_backward_kernel(
     f32 = dict(device=dev, dtype=torch.float32)
     dq = torch.empty(batch, seqlen, state_dim, **f32)
     dk = torch.empty(batch, seqlen, state_dim, **f32)
-    dv = _empty_like_layout(vc, mt)
-    dz = _empty_like_layout(zc, mt) if zc is not None else None
+    dv = _out_buffer(dv_out, vc, mt, "dv_out")
+    dz = _out_buffer(dz_out, zc, mt, "dz_out") if zc is not None else None
     dadt = torch.empty(batch, nheads, seqlen, **f32)
     dqk = torch.empty(batch, nheads, seqlen, **f32)
     dscale = torch.empty(batch, nheads, seqlen, **f32)
@@ -418,7 +436,8 @@ def siso_backward(
     dfinal_ssm: Optional[Tensor] = None, dfinal_k: Optional[Tensor] = None,
     dfinal_v: Optional[Tensor] = None, chunk: int = 128,
     dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
-    device_kind: str | None = None,
+    device_kind: str | None = None, *, dv_out: Optional[Tensor] = None,
+    dz_out: Optional[Tensor] = None,
 ) -> SISOGrads:
     """The HIP reverse scan plus the small epilogue of ``kernel_bwd.py:534-669``
     (dgamma, dD, the dfinal_k rotation pullback, seed gradients), in device torch ops
@@ -428,7 +447,8 @@ def siso_backward(
     n_angles = phi.shape[-1]
     kg = siso_backward_kernel(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias,
                               chunk_states, d_skip=d_skip, dfinal_ssm=dfinal_ssm, chunk=chunk,
-                              dtype_policy=dtype_policy, dfinal_v=dfinal_v)
+                              dtype_policy=dtype_policy, dfinal_v=dfinal_v,
+                              dv_out=dv_out, dz_out=dz_out)
     dq, dk, dphi = kg.dq, kg.dk, kg.dphi
     dq_bias, dk_bias = kg.dq_bias, kg.dk_bias
     dgamma = kg.dqk_diag * kg.uw
@@ -454,3 +474,80 @@ def siso_backward(
                      dphi=dphi, dq_bias=dq_bias, dk_bias=dk_bias, dd_skip=dd_skip, dz=kg.dz,
                      dseed_ssm=dseed_ssm, dseed_k=dseed_k, dseed_v=dseed_v,
                      dseed_coef=dseed_coef)
+
+
+# ======================================================================================
+# BCNorm (layer.py:190-198 applied to B and C, layer.py:235-236)
+# ======================================================================================
+
+
+def _norm_rows_ok(t: Tensor) -> bool:
+    vec = 16 // t.element_size()
+    return (t.dim() == 3 and t.stride(2) == 1 and t.data_ptr() % 16 == 0
+            and t.stride(0) % vec == 0 and t.stride(1) % vec == 0)
+
+
+def bcnorm_supported(x: Tensor) -> bool:
+    """True if `bcnorm_forward` / `bcnorm_backward` take ``x`` (a (B, L, N) view) in place:
+    bf16 or f32, 16-byte aligned rows, N a multiple of 16 bytes and at most 64 of them."""
+    if x.dtype not in (torch.bfloat16, torch.float32) or not x.is_cuda:
+        return False
+    vec = 16 // x.element_size()
+    n = x.shape[-1]
+    return n % vec == 0 and n // vec <= 64 and _norm_rows_ok(x)
+
+
+def bcnorm_forward(xs, weights, eps: float):
+    """RMSNorm of each (B, L, N) view in ``xs`` (one or two, same shape and dtype) with its
+    gain; one ``m3s_norm_fwd`` launch. Returns ``(ys, rstds)``: dense (B, L, N) outputs in
+    the input dtype and the (B, L) f32 reciprocal RMS values the backward reuses."""
+    x0 = xs[0]
+    dev = _device_of(*xs, *weights)
+    batch, seqlen, width = x0.shape
+    for x in xs:
+        if tuple(x.shape) != tuple(x0.shape) or x.dtype != x0.dtype or not _norm_rows_ok(x):
+            raise ValueError("bcnorm inputs must share shape and dtype, with 16-byte aligned rows")
+    ys = [torch.empty(batch, seqlen, width, device=dev, dtype=x0.dtype) for _ in xs]
+    rstds = [torch.empty(batch, seqlen, device=dev, dtype=torch.float32) for _ in xs]
+    ws = [_f32c(w) for w in weights]
+    a = _lib.NormFwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.NormFwdArgs)
+    a.batch, a.seqlen, a.width = batch, seqlen, width
+    a.dtype, a.count, a.eps = _lib.dtype_code(x0.dtype), len(xs), float(eps)
+    for i, x in enumerate(xs):
+        a.x[i] = _lib.blx(x)
+        a.weight[i], a.y[i], a.rstd[i] = ws[i].data_ptr(), ys[i].data_ptr(), rstds[i].data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_norm_fwd(ctypes.byref(a), _lib.stream_handle(dev)),
+                   "m3s_norm_fwd")
+    return ys, rstds
+
+
+def bcnorm_backward(xs, weights, rstds, dys, dxs):
+    """Backward of `bcnorm_forward`: ``dys`` are f32 (B, L, N) cotangents (cast to the
+    input dtype first, as the scan's q/k gradients are, ``siso.py:140-148``); the input
+    gradients are written into ``dxs`` ((B, L, N) views of the input dtype, e.g. slices
+    of the projection's gradient). Returns the f32 gain gradients."""
+    x0 = xs[0]
+    dev = _device_of(*xs, *weights, *rstds, *dys, *dxs)
+    batch, seqlen, width = x0.shape
+    for dx in dxs:
+        if tuple(dx.shape) != tuple(x0.shape) or dx.dtype != x0.dtype or not _norm_rows_ok(dx):
+            raise ValueError("bcnorm gradient buffers must match the inputs, with 16-byte aligned rows")
+    ws = [_f32c(w) for w in weights]
+    dyc = [_f32c(d) for d in dys]
+    dws = [torch.empty(width, device=dev, dtype=torch.float32) for _ in xs]
+    lib = _lib.load()
+    work = torch.empty(lib.m3s_norm_bwd_workspace_bytes(width), device=dev, dtype=torch.uint8)
+    a = _lib.NormBwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.NormBwdArgs)
+    a.batch, a.seqlen, a.width = batch, seqlen, width
+    a.dtype, a.count = _lib.dtype_code(x0.dtype), len(xs)
+    for i, x in enumerate(xs):
+        a.x[i], a.dx[i] = _lib.blx(x), _lib.blx(dxs[i])
+        a.weight[i], a.rstd[i] = ws[i].data_ptr(), rstds[i].data_ptr()
+        a.dy[i], a.dweight[i] = dyc[i].data_ptr(), dws[i].data_ptr()
+    a.workspace = work.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(lib.m3s_norm_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_norm_bwd")
+    return dws

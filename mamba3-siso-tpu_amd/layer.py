@@ -13,6 +13,18 @@ Layout: the scan reads ``x`` and ``z`` in place from the fused projection
 ``(B, L, d_in_proj)`` (strided ``(B, H, L, P)`` views) and writes ``y`` as a
 ``(B, L, H, P)`` buffer, so no transpose is ever materialised (the reference pays three,
 ``layer.py:240,249,258``).
+
+Two execution paths, same results:
+
+* `_LayerFn` (no carried state): the whole layer as one autograd node. The projection
+  is computed ``(B, L, D_pad)`` wide, D_pad = d_in_proj rounded up to 256 columns, from
+  a transposed, zero-padded copy of ``in_proj`` (the layout hipBLASLt runs fastest at
+  these shapes; the padding columns are never read). BCNorm is one HIP launch
+  (``m3s_norm_fwd``). In the backward every kernel writes its slice of one projection
+  gradient buffer in place -- dz, dx from the scan, dB, dC from ``m3s_norm_bwd``, the
+  raw-scalar and angle slices from ``m3s_prep_bwd`` -- so no concatenation is needed.
+* the composed path (a carried ``state``, or shapes the in-place kernels cannot
+  address): torch autograd over `rms_norm`, the differentiable `preprocess` and `siso`.
 """
 
 from __future__ import annotations
@@ -26,6 +38,7 @@ import torch.nn.functional as F
 
 from . import kernels as K
 from . import layout as LY
+from . import scan_prep as SP
 from .scan_prep import SISOState, heavy_tail
 from .siso import siso_segment
 
@@ -148,12 +161,128 @@ def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
     return (xf * rstd * weight.float()).to(x.dtype)
 
 
+_PROJ_PAD = 256
+
+
+def _padded_width(d: int) -> int:
+    return (d + _PROJ_PAD - 1) // _PROJ_PAD * _PROJ_PAD
+
+
+def _fused_ok(u: Tensor, cfg: SISOConfig, state) -> bool:
+    """Whether `_LayerFn` can run this call: no carried state, the policy's operand dtype
+    equals ``u``'s, and every slice of the padded projection the kernels address in place
+    starts on a 16-byte boundary (z, x, B, C; the scalar slices are read elementwise)."""
+    if state is not None or not u.is_cuda or u.dim() != 3:
+        return False
+    if u.dtype not in (torch.bfloat16, torch.float32) or LY.policy(cfg.policy_name).matmul != u.dtype:
+        return False
+    vec = 16 // u.element_size()
+    n = cfg.d_state
+    return (cfg.d_inner % vec == 0 and cfg.headdim % vec == 0 and n % vec == 0
+            and n // vec <= 64)
+
+
+class _LayerFn(torch.autograd.Function):
+    """``layer.py:201-262`` with state=None as one autograd node (see the module notes).
+    Outputs: out (B, L, d_model), final ssm, final k, final v, final phi."""
+
+    @staticmethod
+    def forward(ctx, u, in_proj, out_proj, dt_bias, b_norm_weight, c_norm_weight, b_bias,
+                c_bias, d_skip, cfg):
+        dt = u.dtype
+        batch, seqlen, dm = u.shape
+        m = batch * seqlen
+        d, dp = cfg.d_in_proj, _padded_width(cfg.d_in_proj)
+        if tuple(in_proj.shape) != (dm, d) or tuple(out_proj.shape) != (cfg.d_inner, dm):
+            raise ValueError(f"in_proj must be {(dm, d)} and out_proj {(cfg.d_inner, dm)}")
+        # the reference casts the weights per call (layer.py:233, 256); this lays them out too
+        w_t = torch.empty(dp, dm, device=u.device, dtype=dt)
+        w_t[:d].copy_(in_proj.t())
+        w_t[d:].zero_()
+        u2 = u.reshape(m, dm)
+        proj = (u2 @ w_t.t()).view(batch, seqlen, dp)
+        z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
+        (k, q), (rk, rq) = K.bcnorm_forward([b, c], [b_norm_weight, c_norm_weight], cfg.norm_eps)
+        bias = dt_bias.float().contiguous()
+        adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
+            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor)
+        need = any(ctx.needs_input_grad[:9])   # all False under no_grad
+        outs = K.siso_forward(q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias,
+                              b_bias, d_skip=d_skip, z=z.permute(0, 2, 1, 3), chunk=cfg.chunk,
+                              dtype_policy=cfg.policy_name, save_residuals=need)
+        y, fs, fk, fv = outs[:4]
+        y2 = y.permute(0, 2, 1, 3).reshape(m, cfg.d_inner)
+        wo_t = out_proj.t().to(dt).contiguous()
+        out = (y2 @ wo_t.t()).view(batch, seqlen, dm)
+        if need:
+            res = outs[4]
+            ctx.save_for_backward(u, proj, q, k, rk, rq, adt, gamma, scale, phi, y, res.ybar,
+                                  res.chunk_states, in_proj, out_proj, bias, b_norm_weight,
+                                  c_norm_weight, b_bias, c_bias, d_skip)
+        ctx.cfg = cfg
+        ctx.set_materialize_grads(False)
+        return out, fs, fk, fv, phi_final
+
+    @staticmethod
+    def backward(ctx, dout, dfs, dfk, dfv, dphi_final):
+        (u, proj, q, k, rk, rq, adt, gamma, scale, phi, y, ybar, cstates, in_proj, out_proj,
+         bias, wb, wc, b_bias, c_bias, d_skip) = ctx.saved_tensors
+        cfg = ctx.cfg
+        dt = u.dtype
+        batch, seqlen, dm = u.shape
+        m = batch * seqlen
+        d, dp = cfg.d_in_proj, _padded_width(cfg.d_in_proj)
+        H, P = cfg.nheads, cfg.headdim
+        needs = ctx.needs_input_grad
+        z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
+        y2 = y.permute(0, 2, 1, 3).reshape(m, cfg.d_inner)
+        d_out_proj = None
+        if dout is not None:
+            dout2 = dout.reshape(m, dm).to(dt)
+            dy2 = dout2 @ out_proj.to(dt).t()
+            if needs[2]:
+                d_out_proj = (y2.t() @ dout2).to(out_proj.dtype)
+            dys = dy2.view(batch, seqlen, H, P).permute(0, 2, 1, 3)
+        else:
+            dys = torch.zeros_like(y)
+        # every slice of the projection gradient is written by exactly one kernel below
+        dproj = torch.empty(batch, seqlen, dp, device=u.device, dtype=dt)
+        dz_v, dx_v, db_v, dc_v, ddt_v, da_v, dtr_v, dang_v = split_in_proj(dproj[..., :d], cfg)
+        g = K.siso_backward(
+            dys, q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias, b_bias, ybar,
+            cstates, d_skip=d_skip, z=z.permute(0, 2, 1, 3), dfinal_ssm=dfs, dfinal_k=dfk,
+            dfinal_v=dfv, chunk=cfg.chunk, dtype_policy=cfg.policy_name,
+            dv_out=dx_v.permute(0, 2, 1, 3), dz_out=dz_v.permute(0, 2, 1, 3))
+        dwb, dwc = K.bcnorm_backward([b, c], [wb, wc], [rk, rq], [g.dk, g.dq], [db_v, dc_v])
+        d_bias = torch.empty(H, device=u.device, dtype=torch.float32)
+        SP.prep_backward_launch(dt_raw, a_raw, trap_raw, angles, bias, cfg.a_floor,
+                                (g.dadt, g.dgamma, g.dscale, None, None, g.dphi, dphi_final),
+                                ddt_v, da_v, dtr_v, dang_v, d_bias, None)
+        dp2 = dproj.view(m, dp)[:, :d]
+        du = d_in_proj = None
+        if needs[0]:
+            du = (dp2 @ in_proj.to(dt).t()).view(batch, seqlen, dm)
+        if needs[1]:
+            d_in_proj = (dp2.t() @ u.reshape(m, dm)).t().to(in_proj.dtype)
+
+        def like(t, p_):
+            return None if (t is None or p_ is None) else t.to(p_.dtype)
+
+        return (du, d_in_proj, d_out_proj, like(d_bias, bias), like(dwb, wb), like(dwc, wc),
+                like(g.dk_bias, b_bias), like(g.dq_bias, c_bias), like(g.dd_skip, d_skip), None)
+
+
 def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
                       state: Optional[SISOState] = None, interpret: Any = False,
                       device_kind: str | None = None):
     """Forward of one layer (``layer.py:201-262``). ``u`` is ``(B, L, d_model)`` on the
     ROCm device; returns ``(out (B, L, d_model), SISOState)``. Differentiable w.r.t.
     ``u`` and every `SISOParams` field through torch autograd."""
+    if _fused_ok(u, cfg, state):
+        out, fs, fk, fv, phi_final = _LayerFn.apply(
+            u, params.in_proj, params.out_proj, params.dt_bias, params.b_norm_weight,
+            params.c_norm_weight, params.b_bias, params.c_bias, params.d_skip, cfg)
+        return out, SISOState(ssm=fs, k=fk, v=fv, phi=phi_final)
     batch, seqlen, _ = u.shape
     proj = u @ params.in_proj.to(u.dtype)
     z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj, cfg)

@@ -130,6 +130,67 @@ def _f32c(t: Optional[Tensor]) -> Optional[Tensor]:
     return None if t is None else t.to(torch.float32).contiguous()
 
 
+def prep_forward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
+                        bias: Tensor, init: Optional[Tensor], a_floor: float):
+    """One ``m3s_prep_fwd`` call on raw ``(B, L, X)`` operands with a unit last stride and
+    one dtype (bf16 or f32); ``bias`` and ``init`` f32 contiguous. Returns fresh
+    ``(adt, gamma, scale, lam, dt, phi, phi_final)``."""
+    batch, seqlen, nheads = r_dt.shape
+    n_angles = r_ang.shape[-1]
+    dev = r_dt.device
+    f32 = dict(device=dev, dtype=torch.float32)
+    adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
+    phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
+    phi_final = torch.empty(batch, nheads, n_angles, **f32)
+    lib = _lib.load()
+    ws = torch.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+                     device=dev, dtype=torch.uint8)
+    a = _lib.PrepFwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.PrepFwdArgs)
+    a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
+    a.dtype = _lib.dtype_code(r_dt.dtype)
+    a.has_phi_init = int(init is not None)
+    a.a_floor = float(a_floor)
+    a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
+    a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
+    a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
+    a.phi, a.phi_final = phi.data_ptr(), phi_final.data_ptr()
+    a.workspace = ws.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(lib.m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_fwd")
+    return adt, gamma, scale, lam, dt, phi, phi_final
+
+
+def prep_backward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor, bias: Tensor,
+                         a_floor: float, cots, d_dt: Tensor, d_a: Tensor, d_tr: Tensor,
+                         d_ang: Tensor, d_bias: Tensor, d_init: Optional[Tensor]) -> None:
+    """One ``m3s_prep_bwd`` call. ``cots`` = (dadt, dgamma, dscale, dlam, ddt, dphi,
+    dphi_final), each a tensor or None. The raw cotangents are written into ``d_dt``,
+    ``d_a``, ``d_tr``, ``d_ang`` (any ``(B, L, X)`` strides with a unit last stride, in
+    the raw operands' dtype -- e.g. slices of the projection's gradient)."""
+    batch, seqlen, nheads = r_dt.shape
+    n_angles = r_ang.shape[-1]
+    dev = r_dt.device
+    ins = [_f32c(t) for t in cots]
+    lib = _lib.load()
+    ws = torch.empty(lib.m3s_prep_bwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+                     device=dev, dtype=torch.uint8)
+    a = _lib.PrepBwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.PrepBwdArgs)
+    a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
+    a.dtype = _lib.dtype_code(r_dt.dtype)
+    a.a_floor = float(a_floor)
+    a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
+    a.dt_bias = bias.data_ptr()
+    (a.dadt, a.dgamma, a.dscale, a.dlam, a.ddt, a.dphi,
+     a.dphi_final) = (_lib.ptr(t) for t in ins)
+    a.ddt_raw, a.da_raw, a.dtrap_raw, a.dangles = (_lib.blx(t) for t in (d_dt, d_a, d_tr, d_ang))
+    a.ddt_bias, a.dphi_init = d_bias.data_ptr(), _lib.ptr(d_init)
+    a.workspace = ws.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(lib.m3s_prep_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_bwd")
+
+
 class _PrepFn(torch.autograd.Function):
     """``reference.preprocess`` with its backward (``jax.grad`` in the reference) as
     two HIP launches. Outputs: adt, gamma, scale, phi, lam, dt, phi_final."""
@@ -153,27 +214,8 @@ class _PrepFn(torch.autograd.Function):
         rdt = _raw_dtype(dt_raw, a_raw, trap_raw, angles)
         r_dt, r_a, r_tr, r_ang = (_raw_operand(t, rdt) for t in (dt_raw, a_raw, trap_raw, angles))
         bias = _f32c(dt_bias)
-        init = _f32c(phi_init)
-        f32 = dict(device=dev, dtype=torch.float32)
-        adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
-        phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
-        phi_final = torch.empty(batch, nheads, n_angles, **f32)
-        lib = _lib.load()
-        ws = torch.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
-                         device=dev, dtype=torch.uint8)
-        a = _lib.PrepFwdArgs()
-        a.struct_size = ctypes.sizeof(_lib.PrepFwdArgs)
-        a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
-        a.dtype = _lib.dtype_code(rdt)
-        a.has_phi_init = int(init is not None)
-        a.a_floor = float(a_floor)
-        a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
-        a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
-        a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
-        a.phi, a.phi_final = phi.data_ptr(), phi_final.data_ptr()
-        a.workspace = ws.data_ptr()
-        with torch.cuda.device(dev):
-            _lib.check(lib.m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_fwd")
+        adt, gamma, scale, lam, dt, phi, phi_final = prep_forward_launch(
+            r_dt, r_a, r_tr, r_ang, bias, _f32c(phi_init), a_floor)
         ctx.save_for_backward(r_dt, r_a, r_tr, r_ang, bias)
         ctx.a_floor = float(a_floor)
         ctx.in_dtypes = (dt_raw.dtype, a_raw.dtype, trap_raw.dtype, angles.dtype, dt_bias.dtype,
@@ -188,7 +230,6 @@ class _PrepFn(torch.autograd.Function):
         n_angles = r_ang.shape[-1]
         dev = r_dt.device
         rdt = r_dt.dtype
-        ins = [_f32c(t) for t in (dadt, dgamma, dscale, dlam, ddt, dphi, dphi_final)]
         d_dt = torch.empty(batch, seqlen, nheads, device=dev, dtype=rdt)
         d_a = torch.empty_like(d_dt)
         d_tr = torch.empty_like(d_dt)
@@ -197,23 +238,9 @@ class _PrepFn(torch.autograd.Function):
         want_init = ctx.in_dtypes[5] is not None and ctx.needs_input_grad[5]
         d_init = (torch.empty(batch, nheads, n_angles, device=dev, dtype=torch.float32)
                   if want_init else None)
-        lib = _lib.load()
-        ws = torch.empty(lib.m3s_prep_bwd_workspace_bytes(batch, seqlen, nheads, n_angles),
-                         device=dev, dtype=torch.uint8)
-        a = _lib.PrepBwdArgs()
-        a.struct_size = ctypes.sizeof(_lib.PrepBwdArgs)
-        a.batch, a.seqlen, a.nheads, a.n_angles = batch, seqlen, nheads, n_angles
-        a.dtype = _lib.dtype_code(rdt)
-        a.a_floor = ctx.a_floor
-        a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
-        a.dt_bias = bias.data_ptr()
-        (a.dadt, a.dgamma, a.dscale, a.dlam, a.ddt, a.dphi,
-         a.dphi_final) = (_lib.ptr(t) for t in ins)
-        a.ddt_raw, a.da_raw, a.dtrap_raw, a.dangles = (_lib.blx(t) for t in (d_dt, d_a, d_tr, d_ang))
-        a.ddt_bias, a.dphi_init = d_bias.data_ptr(), _lib.ptr(d_init)
-        a.workspace = ws.data_ptr()
-        with torch.cuda.device(dev):
-            _lib.check(lib.m3s_prep_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_bwd")
+        prep_backward_launch(r_dt, r_a, r_tr, r_ang, bias, ctx.a_floor,
+                             (dadt, dgamma, dscale, dlam, ddt, dphi, dphi_final),
+                             d_dt, d_a, d_tr, d_ang, d_bias, d_init)
         dts = ctx.in_dtypes
 
         def cast(t, d):

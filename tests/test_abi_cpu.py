@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 3
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 4
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -50,6 +50,9 @@ int main(void) {
   printf("%zu %zu %zu\n", sizeof(m3s_blx), sizeof(m3s_prep_fwd_args), sizeof(m3s_prep_bwd_args));
   printf("%zu %zu %zu\n", offsetof(m3s_prep_fwd_args, dt_raw), offsetof(m3s_prep_bwd_args, ddt_raw),
          offsetof(m3s_prep_bwd_args, workspace));
+  printf("%zu %zu %zu %zu %zu %zu\n", sizeof(m3s_norm_fwd_args), sizeof(m3s_norm_bwd_args),
+         offsetof(m3s_norm_fwd_args, x), offsetof(m3s_norm_fwd_args, rstd),
+         offsetof(m3s_norm_bwd_args, dx), offsetof(m3s_norm_bwd_args, workspace));
   return 0;
 }
 """
@@ -66,8 +69,11 @@ int main(void) {
                           lib.DecodeArgs.y.offset]
     assert sizes[7:10] == [ctypes.sizeof(lib.Blx), ctypes.sizeof(lib.PrepFwdArgs),
                            ctypes.sizeof(lib.PrepBwdArgs)]
-    assert sizes[10:] == [lib.PrepFwdArgs.dt_raw.offset, lib.PrepBwdArgs.ddt_raw.offset,
-                          lib.PrepBwdArgs.workspace.offset]
+    assert sizes[10:13] == [lib.PrepFwdArgs.dt_raw.offset, lib.PrepBwdArgs.ddt_raw.offset,
+                            lib.PrepBwdArgs.workspace.offset]
+    assert sizes[13:] == [ctypes.sizeof(lib.NormFwdArgs), ctypes.sizeof(lib.NormBwdArgs),
+                          lib.NormFwdArgs.x.offset, lib.NormFwdArgs.rstd.offset,
+                          lib.NormBwdArgs.dx.offset, lib.NormBwdArgs.workspace.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -144,3 +150,26 @@ def test_capability_table(lib):
                     if lib.supported(1, dt, c, n, p):
                         assert lib.supported(0, dt, c, n, p)
     assert not lib.supported(0, lib.DTYPE_F32, 128, 128, 64)   # does not fit in LDS
+
+
+def test_norm_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_norm_bwd_workspace_bytes(128) == 1024 * 2 * 128 * 4
+    assert h.m3s_norm_bwd_workspace_bytes(0) == -1
+    a = lib.NormFwdArgs()
+    a.struct_size = ctypes.sizeof(lib.NormFwdArgs)
+    a.batch, a.seqlen, a.width, a.dtype, a.count, a.eps = 2, 8, 128, lib.DTYPE_BF16, 3, 1e-5
+    assert h.m3s_norm_fwd(ctypes.byref(a), None) == lib.ERR_INVALID      # count must be 1 or 2
+    a.count = 1
+    a.width = 100                                                        # not a multiple of 8
+    assert h.m3s_norm_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"multiple of 8" in h.m3s_last_error()
+    a.width = 128
+    a.x[0] = lib.Blx(0x1008, 4480, 8 * 4480)                            # 8-byte aligned base
+    assert h.m3s_norm_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"aligned" in h.m3s_last_error()
+    b = lib.NormBwdArgs()
+    b.struct_size = ctypes.sizeof(lib.NormBwdArgs)
+    b.batch, b.seqlen, b.width, b.dtype, b.count = 2, 8, 128, lib.DTYPE_BF16, 2
+    assert h.m3s_norm_bwd(ctypes.byref(b), None) == lib.ERR_INVALID      # no workspace
+    assert b"workspace" in h.m3s_last_error()
