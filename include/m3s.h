@@ -150,6 +150,32 @@ typedef struct m3s_decode_args {
   void* y;                /* out (B, H, P)                 */
 } m3s_decode_args;
 
+/* The layer's per-token decode step (model.py:266-289 without the block norm, residual
+ * and MLP; the layer step that BASELINE configs[3] times) from the in_proj output rows:
+ * BCNorm of the B and C slices (layer.py:190-198), dt = softplus(dt_raw + dt_bias),
+ * lam = sigmoid(trap_raw), adt = min(-heavy_tail(a_raw), -a_floor) dt, then the step of
+ * m3s_decode on x, z and the raw angles, all in one launch. The state is updated in place
+ * as in m3s_decode. */
+typedef struct m3s_decode_layer_args {
+  int32_t struct_size;  /* sizeof(m3s_decode_layer_args) */
+  int32_t batch, nheads, headdim, state_dim, n_angles;
+  int32_t dtype;        /* M3S_DTYPE_* of proj and y */
+  float a_floor, norm_eps;
+  const void* proj;     /* (B, >= d_in_proj) rows: [z, x, B, C, dt_raw, a_raw, trap_raw, angles] */
+  int64_t proj_stride;  /* elements between rows */
+  const float* b_norm_weight; /* (N)    */
+  const float* c_norm_weight; /* (N)    */
+  const float* dt_bias; /* (H)          */
+  const float* q_bias;  /* (H, N): the layer's c_bias */
+  const float* k_bias;  /* (H, N): the layer's b_bias */
+  const float* d_skip;  /* (H) or NULL  */
+  float* ssm;           /* in/out (B, H, P, N) */
+  float* k_state;       /* in/out (B, H, N)    */
+  float* v_state;       /* in/out (B, H, P)    */
+  float* phi_state;     /* in/out (B, H, Nr)   */
+  void* y;              /* out (B, H, P) = (B, d_inner), gated */
+} m3s_decode_layer_args;
+
 /* Per-token preprocessing. Replaces `reference.preprocess` (reference.py:160-199) with
  * `heavy_tail` (202-209), `trapezoid_coeffs` (104-131) and `cumulative_angles`
  * (134-157): dt = softplus(dt_raw + dt_bias), lam = sigmoid(trap_raw),
@@ -272,6 +298,7 @@ int64_t m3s_norm_bwd_workspace_bytes(int32_t width);
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
 int32_t m3s_decode(const m3s_decode_args* args, void* stream);
+int32_t m3s_decode_layer(const m3s_decode_layer_args* args, void* stream);
 int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
 int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
 int32_t m3s_norm_fwd(const m3s_norm_fwd_args* args, void* stream);

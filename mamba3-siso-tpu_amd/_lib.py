@@ -79,6 +79,20 @@ class DecodeArgs(C.Structure):
     ]
 
 
+class DecodeLayerArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("nheads", i32), ("headdim", i32), ("state_dim", i32),
+        ("n_angles", i32),
+        ("dtype", i32), ("a_floor", C.c_float), ("norm_eps", C.c_float),
+        ("proj", vp), ("proj_stride", i64),
+        ("b_norm_weight", vp), ("c_norm_weight", vp), ("dt_bias", vp),
+        ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
+        ("ssm", vp), ("k_state", vp), ("v_state", vp), ("phi_state", vp),
+        ("y", vp),
+    ]
+
+
 class PrepFwdArgs(C.Structure):
     _fields_ = [
         ("struct_size", i32),
@@ -130,7 +144,7 @@ class NormBwdArgs(C.Structure):
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
-           "m3s_norm_bwd")
+           "m3s_norm_bwd", "m3s_decode_layer")
 
 _lib = None
 
@@ -167,6 +181,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_prep_fwd.argtypes = [C.POINTER(PrepFwdArgs), vp]
     lib.m3s_prep_bwd.restype = i32
     lib.m3s_prep_bwd.argtypes = [C.POINTER(PrepBwdArgs), vp]
+    lib.m3s_decode_layer.restype = i32
+    lib.m3s_decode_layer.argtypes = [C.POINTER(DecodeLayerArgs), vp]
     lib.m3s_norm_bwd_workspace_bytes.restype = i64
     lib.m3s_norm_bwd_workspace_bytes.argtypes = [i32]
     lib.m3s_norm_fwd.restype = i32

@@ -13,6 +13,14 @@
 // state as 16-byte vectors with consecutive threads on consecutive addresses, so each
 // load/store instruction of the workgroup moves one contiguous 4 KiB span. All loads
 // are issued before any arithmetic so every thread keeps its whole share in flight.
+//
+// Two entry points share the kernel. `m3s_decode` takes the step's inputs as the
+// reference's decode kernel does. `m3s_decode_layer` takes the in_proj output row of
+// each batch element instead and does the layer's per-token glue in the same launch
+// (model.py:266-289 without the block norm): BCNorm of the B and C slices (one wave
+// reduction per row; the normalised rows are rounded to the operand type as
+// `rms_norm` returns them), dt = softplus(dt_raw + dt_bias), lam = sigmoid(trap_raw),
+// adt = min(-heavy_tail(a_raw), -a_floor) dt, and x, z, angles read in place.
 #include "m3s_common.h"
 #include "m3s_internal.h"
 
@@ -37,11 +45,23 @@ struct DecParams {
   float* vst;
   float* phist;
   void* y;
+  // layer mode: the projection rows and the layer's parameters
+  const void* proj;
+  int64_t proj_st;
+  const float* wb;
+  const float* wc;
+  const float* dt_bias;
+  float a_floor, eps;
 };
 
 constexpr int kDecThreads = 256;
 
-template <typename MT, int N, int P>
+__device__ __forceinline__ float dec_softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float dec_heavy_tail(float x) {
+  return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
+}
+
+template <typename MT, int N, int P, bool LAYER>
 __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) {
   constexpr int NT = kDecThreads;
   constexpr int H2 = N / 2;
@@ -71,19 +91,57 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
     if (f < NV) st[it] = __builtin_nontemporal_load(sg + f);
   }
 
-  const float adt = p.adt[bh], dt = p.dt[bh], lam = p.lam[bh];
-  // ---- angle advance + rotation (one thread per rotary pair) --------------------
-  if (tid < H2) {
+  // projection row of this batch element (layer mode): [z, x, B, C, dt, a, trap, angles]
+  const int HP = p.H * P;
+  const MT* prow = LAYER ? static_cast<const MT*>(p.proj) + (int64_t)b * p.proj_st : nullptr;
+  float adt, dt, lam;
+  if constexpr (LAYER) {
+    const MT* sc = prow + 2 * HP + 2 * N;
+    dt = dec_softplus((float)sc[h] + p.dt_bias[h]);
+    lam = 1.f / (1.f + expf(-(float)sc[2 * p.H + h]));
+    adt = fminf(-dec_heavy_tail((float)sc[p.H + h]), -p.a_floor) * dt;
+  } else {
+    adt = p.adt[bh];
+    dt = p.dt[bh];
+    lam = p.lam[bh];
+  }
+  // ---- angle advance + rotation (one thread per rotary pair; wave 0) ------------
+  if (tid < 64) {
     const int j = tid;
-    const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * N;
-    const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * N;
-    const float ulo = (float)qg[j] + p.qb[h * N + j];
-    const float uhi = (float)qg[H2 + j] + p.qb[h * N + H2 + j];
-    const float wlo = (float)kg[j] + p.kb[h * N + j];
-    const float whi = (float)kg[H2 + j] + p.kb[h * N + H2 + j];
+    const bool act = j < H2;
+    float qlo = 0.f, qhi = 0.f, klo = 0.f, khi = 0.f;
+    if constexpr (LAYER) {
+      // BCNorm of the C (query) and B (key) rows, f32, output rounded to MT
+      const MT* crow = prow + 2 * HP + N;
+      const MT* brow = prow + 2 * HP;
+      float cl = 0.f, ch = 0.f, bl = 0.f, bh_ = 0.f;
+      if (act) {
+        cl = (float)crow[j]; ch = (float)crow[H2 + j];
+        bl = (float)brow[j]; bh_ = (float)brow[H2 + j];
+      }
+      const float sq = group_sum<64>(cl * cl + ch * ch), sk = group_sum<64>(bl * bl + bh_ * bh_);
+      const float rq = 1.f / sqrtf(sq / (float)N + p.eps), rk = 1.f / sqrtf(sk / (float)N + p.eps);
+      if (act) {
+        qlo = (float)(MT)(cl * rq * p.wc[j]);
+        qhi = (float)(MT)(ch * rq * p.wc[H2 + j]);
+        klo = (float)(MT)(bl * rk * p.wb[j]);
+        khi = (float)(MT)(bh_ * rk * p.wb[H2 + j]);
+      }
+    } else if (act) {
+      const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * N;
+      const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * N;
+      qlo = (float)qg[j]; qhi = (float)qg[H2 + j];
+      klo = (float)kg[j]; khi = (float)kg[H2 + j];
+    }
+    if (act) {
+    const float ulo = qlo + p.qb[h * N + j];
+    const float uhi = qhi + p.qb[h * N + H2 + j];
+    const float wlo = klo + p.kb[h * N + j];
+    const float whi = khi + p.kb[h * N + H2 + j];
     float sn = 0.f, cs = 1.f;
     if (j < p.Nr) {
-      const float th = tanhf(p.angles[(int64_t)b * p.Nr + j]) * kPi * dt;
+      const float ang = LAYER ? (float)prow[2 * HP + 2 * N + 3 * p.H + j] : p.angles[(int64_t)b * p.Nr + j];
+      const float th = tanhf(ang) * kPi * dt;
       const float phi = wrap_2pi(p.phist[bh * p.Nr + j] + th);
       p.phist[bh * p.Nr + j] = phi;
       sincosf(phi, &sn, &cs);
@@ -92,11 +150,13 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
     sQt[H2 + j] = (float)(MT)(uhi * cs + ulo * sn);
     sKt[j] = wlo * cs - whi * sn;
     sKt[H2 + j] = whi * cs + wlo * sn;
+    }
   }
+  const MT* vrow = LAYER ? prow + HP + h * P : static_cast<const MT*>(p.v) + bh * P;
   for (int i = tid; i < N; i += NT) sKp[i] = p.kst[bh * N + i];
   for (int i = tid; i < P; i += NT) {
     sVp[i] = p.vst[bh * P + i];
-    sV[i] = (float)static_cast<const MT*>(p.v)[bh * P + i];
+    sV[i] = (float)vrow[i];
   }
   __syncthreads();
   // the carried (k, v) pair is now in LDS: overwrite it with this token's
@@ -113,7 +173,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
   const f32x4 kt = *reinterpret_cast<const f32x4*>(sKt + n0);
   const f32x4 qt = *reinterpret_cast<const f32x4*>(sQt + n0);
   MT* yg = static_cast<MT*>(p.y) + bh * P;
-  const MT* zg = p.has_z ? static_cast<const MT*>(p.z) + bh * P : nullptr;
+  const MT* zg = LAYER ? prow + h * P : (p.has_z ? static_cast<const MT*>(p.z) + bh * P : nullptr);
   const float dsk = p.has_d ? p.dsk[h] : 0.f;
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
@@ -139,10 +199,10 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
   }
 }
 
-template <typename MT, int N, int P>
+template <typename MT, int N, int P, bool LAYER>
 static int32_t launch_dec(const DecParams& prm, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_kernel<MT, N, P>), dim3(grid), dim3(kDecThreads), 0, stream, prm);
-  return launch_status("m3s_decode");
+  hipLaunchKernelGGL((decode_kernel<MT, N, P, LAYER>), dim3(grid), dim3(kDecThreads), 0, stream, prm);
+  return launch_status(LAYER ? "m3s_decode_layer" : "m3s_decode");
 }
 
 #define M3S_DEC_CONFIGS(X) \
@@ -200,9 +260,51 @@ extern "C" int32_t m3s_decode(const m3s_decode_args* a, void* stream) {
   prm.y = a->y;
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define X(MT, NN, PP) \
-  if (a->dtype == dcode<MT>() && N == NN && P == PP) return launch_dec<MT, NN, PP>(prm, B * H, s);
+  if (a->dtype == dcode<MT>() && N == NN && P == PP) return launch_dec<MT, NN, PP, false>(prm, B * H, s);
   M3S_DEC_CONFIGS(X)
 #undef X
   set_error("m3s_decode: unreachable dispatch");
+  return M3S_ERR_UNSUPPORTED;
+}
+
+extern "C" int32_t m3s_decode_layer(const m3s_decode_layer_args* a, void* stream) {
+  using namespace m3s;
+  clear_error();
+  M3S_REQUIRE(a != nullptr, "m3s_decode_layer: args is NULL");
+  M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_decode_layer_args),
+              "m3s_decode_layer: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              (int)sizeof(m3s_decode_layer_args));
+  const int B = a->batch, H = a->nheads, P = a->headdim, N = a->state_dim, Nr = a->n_angles;
+  M3S_REQUIRE(B > 0 && H > 0 && P > 0 && N > 0, "m3s_decode_layer: non-positive dimension");
+  M3S_REQUIRE(Nr >= 0 && 2 * Nr <= N, "m3s_decode_layer: n_angles %d exceeds state_dim/2", Nr);
+  M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
+              "m3s_decode_layer: bad dtype %d", a->dtype);
+  if (!decode_supported(a->dtype, N, P)) {
+    set_error("m3s_decode_layer: no kernel for dtype=%s state_dim=%d headdim=%d",
+              a->dtype == M3S_DTYPE_BF16 ? "bf16" : "f32", N, P);
+    return M3S_ERR_UNSUPPORTED;
+  }
+  const int64_t width = 2LL * H * P + 2LL * N + 3LL * H + Nr;
+  M3S_REQUIRE(a->proj && a->proj_stride >= width, "m3s_decode_layer: proj NULL or row stride %lld < %lld",
+              (long long)a->proj_stride, (long long)width);
+  M3S_REQUIRE(a->b_norm_weight && a->c_norm_weight && a->dt_bias && a->q_bias && a->k_bias,
+              "m3s_decode_layer: a parameter pointer is NULL");
+  M3S_REQUIRE(a->ssm && aligned16(a->ssm) && a->k_state && a->v_state && a->phi_state && a->y,
+              "m3s_decode_layer: state/output pointers NULL or ssm misaligned");
+  M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_decode_layer: B*H too large");
+  DecParams prm{};
+  prm.B = B; prm.H = H; prm.Nr = Nr; prm.has_d = a->d_skip != nullptr; prm.has_z = 1;
+  prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
+  prm.ssm = a->ssm; prm.kst = a->k_state; prm.vst = a->v_state; prm.phist = a->phi_state;
+  prm.y = a->y;
+  prm.proj = a->proj; prm.proj_st = a->proj_stride;
+  prm.wb = a->b_norm_weight; prm.wc = a->c_norm_weight; prm.dt_bias = a->dt_bias;
+  prm.a_floor = a->a_floor; prm.eps = a->norm_eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define X(MT, NN, PP) \
+  if (a->dtype == dcode<MT>() && N == NN && P == PP) return launch_dec<MT, NN, PP, true>(prm, B * H, s);
+  M3S_DEC_CONFIGS(X)
+#undef X
+  set_error("m3s_decode_layer: unreachable dispatch");
   return M3S_ERR_UNSUPPORTED;
 }

@@ -240,6 +240,47 @@ def siso_decode(q: Tensor, k: Tensor, v: Tensor, adt: Tensor, dt: Tensor, lam: T
     return y, SISOState(ssm=ssm, k=kst, v=vst, phi=phist)
 
 
+def decode_layer_step(proj: Tensor, state, *, nheads: int, headdim: int, state_dim: int,
+                      n_angles: int, b_norm_weight: Tensor, c_norm_weight: Tensor,
+                      dt_bias: Tensor, q_bias: Tensor, k_bias: Tensor,
+                      d_skip: Optional[Tensor], a_floor: float, norm_eps: float):
+    """The layer's decode step from its in_proj output (``model.py:266-289`` without the
+    block norm): ``proj`` is ``(B, >= d_in_proj)`` with a unit last stride, in bf16 or
+    f32; BCNorm, dt / lambda / a, and the state update + readout of `siso_decode` run in
+    one ``m3s_decode_layer`` launch. ``q_bias`` / ``k_bias`` are the layer's c_bias /
+    b_bias. Returns ``(y (B, H, P), next_state)``; the state is updated in place."""
+    from .scan_prep import SISOState
+
+    batch = proj.shape[0]
+    dev = _device_of(proj, b_norm_weight, c_norm_weight, dt_bias, q_bias, k_bias, d_skip, *state)
+    mt = proj.dtype
+    dcode = _lib.dtype_code(mt)
+    if proj.dim() != 2 or proj.stride(1) != 1:
+        raise ValueError("proj must be (B, d_in_proj) with a unit last stride")
+    if not _lib.supported(2, dcode, 0, state_dim, headdim):
+        raise ValueError(f"no decode kernel for {mt} d_state={state_dim} headdim={headdim}")
+    ssm = _state_buf(state.ssm, (batch, nheads, headdim, state_dim), dev)
+    kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
+    vst = _state_buf(state.v, (batch, nheads, headdim), dev)
+    phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
+    wb, wc, bias = _f32c(b_norm_weight), _f32c(c_norm_weight), _f32c(dt_bias)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    y = torch.empty(batch, nheads, headdim, device=dev, dtype=mt)
+    a = _lib.DecodeLayerArgs()
+    a.struct_size = ctypes.sizeof(_lib.DecodeLayerArgs)
+    a.batch, a.nheads, a.headdim, a.state_dim, a.n_angles = batch, nheads, headdim, state_dim, n_angles
+    a.dtype, a.a_floor, a.norm_eps = dcode, float(a_floor), float(norm_eps)
+    a.proj, a.proj_stride = proj.data_ptr(), proj.stride(0)
+    a.b_norm_weight, a.c_norm_weight, a.dt_bias = wb.data_ptr(), wc.data_ptr(), bias.data_ptr()
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.ssm, a.k_state, a.v_state, a.phi_state = (t.data_ptr() for t in (ssm, kst, vst, phist))
+    a.y = y.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_decode_layer(ctypes.byref(a), _lib.stream_handle(dev)),
+                   "m3s_decode_layer")
+    return y, SISOState(ssm=ssm, k=kst, v=vst, phi=phist)
+
+
 def siso_decode_folded(*args, **kw):
     """``kernel_decode.py:363-464``. Same kernel as `siso_decode`: on MI355X one
     workgroup per (b, h) state serves both of the reference's grids."""

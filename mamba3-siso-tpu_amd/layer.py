@@ -297,21 +297,36 @@ def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
     return y.to(u.dtype) @ params.out_proj.to(u.dtype), out.state
 
 
+def _decode_fused_ok(u: Tensor, cfg: SISOConfig) -> bool:
+    """Whether the decode step runs as one ``m3s_decode_layer`` launch: ``u`` on the
+    device in the policy's operand dtype (otherwise the composed step casts as needed)."""
+    return u.is_cuda and u.dtype == LY.policy(cfg.policy_name).matmul
+
+
 def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,
                             state: SISOState):
     """One token through the layer (``model.py:266-289`` without block norm/residual):
     ``u`` ``(B, d_model)`` -> ``(out (B, d_model), next_state)``. The state is updated in
-    place by the decode kernel (the reference donates it)."""
+    place by the decode kernel (the reference donates it). When ``u`` is in the policy's
+    operand dtype, everything between the two projections (BCNorm, dt / lambda / a, the
+    state update and readout) is one ``m3s_decode_layer`` launch on the projection rows."""
     proj = u @ params.in_proj.to(u.dtype)
-    z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[:, None, :], cfg)
-    b = rms_norm(b, params.b_norm_weight, cfg.norm_eps)[:, 0]
-    c = rms_norm(c, params.c_norm_weight, cfg.norm_eps)[:, 0]
-    dt = F.softplus(dt_raw[:, 0].float() + params.dt_bias.float())
-    a = torch.clamp(-heavy_tail(a_raw[:, 0].float()), max=-cfg.a_floor)
-    lam = torch.sigmoid(trap_raw[:, 0].float())
-    y, st = K.decode_step(c, b, x[:, 0], a * dt, dt, lam, angles[:, 0], params.c_bias,
-                          params.b_bias, state, d_skip=params.d_skip, z=z[:, 0],
-                          dtype_policy=cfg.policy_name)
+    if _decode_fused_ok(u, cfg):
+        y, st = K.decode_layer_step(
+            proj, state, nheads=cfg.nheads, headdim=cfg.headdim, state_dim=cfg.d_state,
+            n_angles=cfg.n_angles, b_norm_weight=params.b_norm_weight,
+            c_norm_weight=params.c_norm_weight, dt_bias=params.dt_bias, q_bias=params.c_bias,
+            k_bias=params.b_bias, d_skip=params.d_skip, a_floor=cfg.a_floor,
+            norm_eps=cfg.norm_eps)
+    else:
+        z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[:, None, :], cfg)
+        b = rms_norm(b, params.b_norm_weight, cfg.norm_eps)[:, 0]
+        c = rms_norm(c, params.c_norm_weight, cfg.norm_eps)[:, 0]
+        dt = F.softplus(dt_raw[:, 0].float() + params.dt_bias.float())
+        a = torch.clamp(-heavy_tail(a_raw[:, 0].float()), max=-cfg.a_floor)
+        lam = torch.sigmoid(trap_raw[:, 0].float())
+        y, st = K.decode_step(c, b, x[:, 0], a * dt, dt, lam, angles[:, 0], params.c_bias,
+                              params.b_bias, state, d_skip=params.d_skip, z=z[:, 0],
+                              dtype_policy=cfg.policy_name)
     out = y.reshape(u.shape[0], cfg.d_inner).to(u.dtype) @ params.out_proj.to(u.dtype)
     return out, st
-

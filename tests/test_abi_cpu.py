@@ -53,6 +53,8 @@ int main(void) {
   printf("%zu %zu %zu %zu %zu %zu\n", sizeof(m3s_norm_fwd_args), sizeof(m3s_norm_bwd_args),
          offsetof(m3s_norm_fwd_args, x), offsetof(m3s_norm_fwd_args, rstd),
          offsetof(m3s_norm_bwd_args, dx), offsetof(m3s_norm_bwd_args, workspace));
+  printf("%zu %zu %zu\n", sizeof(m3s_decode_layer_args), offsetof(m3s_decode_layer_args, proj_stride),
+         offsetof(m3s_decode_layer_args, y));
   return 0;
 }
 """
@@ -71,9 +73,11 @@ int main(void) {
                            ctypes.sizeof(lib.PrepBwdArgs)]
     assert sizes[10:13] == [lib.PrepFwdArgs.dt_raw.offset, lib.PrepBwdArgs.ddt_raw.offset,
                             lib.PrepBwdArgs.workspace.offset]
-    assert sizes[13:] == [ctypes.sizeof(lib.NormFwdArgs), ctypes.sizeof(lib.NormBwdArgs),
-                          lib.NormFwdArgs.x.offset, lib.NormFwdArgs.rstd.offset,
-                          lib.NormBwdArgs.dx.offset, lib.NormBwdArgs.workspace.offset]
+    assert sizes[13:19] == [ctypes.sizeof(lib.NormFwdArgs), ctypes.sizeof(lib.NormBwdArgs),
+                            lib.NormFwdArgs.x.offset, lib.NormFwdArgs.rstd.offset,
+                            lib.NormBwdArgs.dx.offset, lib.NormBwdArgs.workspace.offset]
+    assert sizes[19:] == [ctypes.sizeof(lib.DecodeLayerArgs), lib.DecodeLayerArgs.proj_stride.offset,
+                          lib.DecodeLayerArgs.y.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -173,3 +177,16 @@ def test_norm_arguments_are_checked_without_a_launch(lib):
     b.batch, b.seqlen, b.width, b.dtype, b.count = 2, 8, 128, lib.DTYPE_BF16, 2
     assert h.m3s_norm_bwd(ctypes.byref(b), None) == lib.ERR_INVALID      # no workspace
     assert b"workspace" in h.m3s_last_error()
+
+
+def test_decode_layer_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    a = lib.DecodeLayerArgs()
+    a.struct_size = ctypes.sizeof(lib.DecodeLayerArgs)
+    a.batch, a.nheads, a.headdim, a.state_dim, a.n_angles = 4, 32, 64, 128, 32
+    a.dtype = lib.DTYPE_BF16
+    a.proj, a.proj_stride = 0x1000, 4000          # narrower than d_in_proj = 4480
+    assert h.m3s_decode_layer(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"row stride" in h.m3s_last_error()
+    a.state_dim = 96
+    assert h.m3s_decode_layer(ctypes.byref(a), None) == lib.ERR_UNSUPPORTED

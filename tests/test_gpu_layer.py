@@ -130,3 +130,40 @@ def test_layer_decode_step_matches_oracle(m3, policy):
     else:
         assert_maxrel(y, yr, BF16_MAXREL, "y")
         assert_maxrel(s2.ssm, sr.ssm, BF16_MAXREL, "ssm")
+
+
+@pytest.mark.parametrize("policy", ["bf16", "f32"])
+def test_layer_decode_fused_matches_composed_over_steps(m3, policy, monkeypatch):
+    """The one-launch layer step (m3s_decode_layer) against the composed step (torch
+    BCNorm / dt / lambda ops + m3s_decode) over 6 chained tokens, with non-unit norm
+    gains, scaled inputs and a batch that is not a multiple of 8."""
+    cfg = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=128,
+                        policy_name=policy)
+    p_cpu = m3.init_params(cfg, 9)
+    g = torch.Generator().manual_seed(10)
+    p_cpu = p_cpu._replace(b_norm_weight=torch.rand(128, generator=g) + 0.5,
+                           c_norm_weight=torch.rand(128, generator=g) + 0.5)
+    params = m3.SISOParams(*(t.cuda() for t in p_cpu))
+    mt = BF16 if policy == "bf16" else torch.float32
+    B, H, Nr = 5, cfg.nheads, cfg.n_angles
+
+    def fresh_state():
+        gs = torch.Generator().manual_seed(11)
+        return m3.SISOState(torch.randn(B, H, 64, 128, generator=gs).cuda() * 0.1,
+                            torch.randn(B, H, 128, generator=gs).cuda(),
+                            torch.randn(B, H, 64, generator=gs).cuda(),
+                            (torch.rand(B, H, Nr, generator=gs) * 6).cuda())
+
+    toks = [(torch.randn(B, 256, generator=g) * 3).to(mt).cuda() for _ in range(6)]
+    s1, s0 = fresh_state(), fresh_state()
+    tol = BF16_MAXREL if policy == "bf16" else 2e-5
+    for t in toks:
+        assert m3.layer._decode_fused_ok(t, cfg)
+        y1, s1 = m3.mamba3_siso_decode_step(params, t, cfg, s1)
+        with monkeypatch.context() as mp:
+            mp.setattr(m3.layer, "_decode_fused_ok", lambda *a: False)
+            y0, s0 = m3.mamba3_siso_decode_step(params, t, cfg, s0)
+        assert_maxrel(y1, cpu(y0), tol, "y")
+    for name in ("ssm", "k", "v"):
+        assert_maxrel(getattr(s1, name), cpu(getattr(s0, name)), tol, name)
+    assert O.rel_error(cpu(s1.phi), cpu(s0.phi), angle=True) <= 1e-5
