@@ -1030,7 +1030,6 @@ static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   return launch_status("m3s_fwd");
 }
 
-// The (dtype, chunk, N, P) instantiations compiled into the library.
 // The (dtype, chunk, N, P) instantiations compiled into the library. Every backward
 // configuration (m3s_bwd.hip) is also a forward one.
 #define M3S_FWD_CONFIGS(X)  \
