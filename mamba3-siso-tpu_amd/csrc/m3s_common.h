@@ -187,6 +187,13 @@ __device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* l
 }
 // s_waitcnt vmcnt(0), leaving expcnt / lgkmcnt unconstrained (gfx9 encoding).
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(n), n < 16: every vector memory operation but the n most recent has
+// completed (they complete in issue order for the purpose of this count).
+template <int n>
+__device__ __forceinline__ void vm_wait_keep() {
+  static_assert(n >= 0 && n < 16, "vmcnt field of the gfx9 encoding");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | n);
+}
 
 // ---- wave reductions ------------------------------------------------------------
 template <int W>

@@ -792,13 +792,23 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     for (int lb = 0; lb < F::LOB; ++lb) {
       const int hb = lb + F::LOB;
       bf16x8 kl8, kh8;
+      // this lane's 8 bias columns of each half, as 16-byte LDS reads
+      const int nb8 = 32 * lb + g8;
+      f32x4 bql[2], bqh[2], bkl[2], bkh[2];
+#pragma unroll
+      for (int h4 = 0; h4 < 2; ++h4) {
+        bql[h4] = *reinterpret_cast<const f32x4*>(sQb + nb8 + 4 * h4);
+        bqh[h4] = *reinterpret_cast<const f32x4*>(sQb + nb8 + H2 + 4 * h4);
+        bkl[h4] = *reinterpret_cast<const f32x4*>(sKb + nb8 + 4 * h4);
+        bkh[h4] = *reinterpret_cast<const f32x4*>(sKb + nb8 + H2 + 4 * h4);
+      }
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const int n = 32 * lb + g8 + s;
-        float ql = (float)rq[lb][s] + sQb[n];
-        float qh = (float)rq[hb][s] + sQb[n + H2];
-        float kl = (float)rk[lb][s] + sKb[n];
-        float kh = (float)rk[hb][s] + sKb[n + H2];
+        const int n = nb8 + s;
+        float ql = (float)rq[lb][s] + bql[s >> 2][s & 3];
+        float qh = (float)rq[hb][s] + bqh[s >> 2][s & 3];
+        float kl = (float)rk[lb][s] + bkl[s >> 2][s & 3];
+        float kh = (float)rk[hb][s] + bkh[s >> 2][s & 3];
         uw += ql * kl + qh * kh;
         if (n < Nr) {
           // phi is wrapped to [0, 2 pi): the hardware sin / cos (argument in turns)
@@ -981,10 +991,18 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
     publish_state(c);
     if (c < nc) stage(c);
-    vm_wait_all();  // this wave's direct-to-LDS loads (v of c, z of c-1) have landed
+    if (c + 1 < nc) {
+      // chunk c+1's q / k rows: issued before the barrier, where the vector-memory
+      // pipe is idle (after it, the light waves' epilogue stores compete for it)
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch_qk(c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      vm_wait_keep<2 * F::NBK>();   // all but those loads: v of c, z of c-1 have landed
+    } else {
+      vm_wait_all();
+    }
     __syncthreads();
     // ---------------- phase B: epilogue of c-1 alongside the products of c --------
-    if (c + 1 < nc) prefetch_qk(c + 1);
     if (c > 0 && light) epilogue(c - 1);
     if (c < nc) products(c);
     __syncthreads();
