@@ -759,7 +759,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
-    const bool last = (c == nc - 1);
     if (wave == 0) {  // inclusive prefix sum of adt * log2(e)
       float a[F::E];
       float run = 0.f;
@@ -788,13 +787,28 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int trow = 16 * wave + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     float uw = 0.f;
-#pragma unroll
-    for (int lb = 0; lb < F::LOB; ++lb) {
+    // u = q + qb, w = k + kb for one pair (n, n + N/2) of this lane's block lb, s < 8
+    auto pair = [&](int lb, int s, const f32x4 (&bql)[2], const f32x4 (&bqh)[2],
+                    const f32x4 (&bkl)[2], const f32x4 (&bkh)[2], float& ql, float& qh,
+                    float& kl, float& kh) {
       const int hb = lb + F::LOB;
-      bf16x8 kl8, kh8;
-      // this lane's 8 bias columns of each half, as 16-byte LDS reads
-      const int nb8 = 32 * lb + g8;
-      f32x4 bql[2], bqh[2], bkl[2], bkh[2];
+      ql = (float)rq[lb][s] + bql[s >> 2][s & 3];
+      qh = (float)rq[hb][s] + bqh[s >> 2][s & 3];
+      kl = (float)rk[lb][s] + bkl[s >> 2][s & 3];
+      kh = (float)rk[hb][s] + bkh[s >> 2][s & 3];
+    };
+    // rotate (lo, hi) by phi: the hardware sin / cos with the argument in turns (phi is
+    // wrapped to [0, 2 pi)); accurate far below the bf16 rounding of what they feed
+    auto rotate = [](float phi, float& ql, float& qh, float& kl, float& kh) {
+      const float turns = phi * 0.15915494309189535f;
+      const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
+      const float q0 = ql * cs - qh * sn, q1 = qh * cs + ql * sn;
+      const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
+      ql = q0; qh = q1; kl = k0; kh = k1;
+    };
+    auto load_bias = [&](int lb, f32x4 (&bql)[2], f32x4 (&bqh)[2], f32x4 (&bkl)[2],
+                         f32x4 (&bkh)[2]) {
+      const int nb8 = 32 * lb + g8;   // this lane's 8 bias columns, as 16-byte LDS reads
 #pragma unroll
       for (int h4 = 0; h4 < 2; ++h4) {
         bql[h4] = *reinterpret_cast<const f32x4*>(sQb + nb8 + 4 * h4);
@@ -802,31 +816,27 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         bkl[h4] = *reinterpret_cast<const f32x4*>(sKb + nb8 + 4 * h4);
         bkh[h4] = *reinterpret_cast<const f32x4*>(sKb + nb8 + H2 + 4 * h4);
       }
+    };
+#pragma unroll
+    for (int lb = 0; lb < F::LOB; ++lb) {
+      const int hb = lb + F::LOB;
+      f32x4 bql[2], bqh[2], bkl[2], bkh[2];
+      load_bias(lb, bql, bqh, bkl, bkh);
+      // which of the block's 32 pairs are rotary (n < Nr) is uniform over the wave except
+      // for a block that Nr cuts; only that case tests per pair
+      const bool all_rot = 32 * lb + 32 <= Nr, none_rot = 32 * lb >= Nr;
+      bf16x8 kl8, kh8;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const int n = nb8 + s;
-        float ql = (float)rq[lb][s] + bql[s >> 2][s & 3];
-        float qh = (float)rq[hb][s] + bqh[s >> 2][s & 3];
-        float kl = (float)rk[lb][s] + bkl[s >> 2][s & 3];
-        float kh = (float)rk[hb][s] + bkh[s >> 2][s & 3];
+        const int n = 32 * lb + g8 + s;
+        float ql, qh, kl, kh;
+        pair(lb, s, bql, bqh, bkl, bkh, ql, qh, kl, kh);
         uw += ql * kl + qh * kh;
-        if (n < Nr) {
-          // phi is wrapped to [0, 2 pi): the hardware sin / cos (argument in turns)
-          // are accurate far below the bf16 rounding of the operands they feed
-          const float turns = rphi[lb][s >> 2][s & 3] * 0.15915494309189535f;
-          const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
-          const float q0 = ql * cs - qh * sn, q1 = qh * cs + ql * sn;
-          const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
-          ql = q0; qh = q1; kl = k0; kh = k1;
-        }
+        if (all_rot || (!none_rot && n < Nr)) rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
         qf[lb][s] = (bf16)ql;
         qf[hb][s] = (bf16)qh;
         kl8[s] = (bf16)(kl * rscale);
         kh8[s] = (bf16)(kh * rscale);
-        if (last && trow == C - 1) {
-          p.fk[bh * N + n] = kl;
-          p.fk[bh * N + n + H2] = kh;
-        }
       }
       *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * lb + g8) = kl8;
       *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * hb + g8) = kh8;
@@ -1020,6 +1030,22 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   }
   const bf16* sVl = sVb + ((nc - 1) & 1) * (C * P);
   for (int i = tid; i < P; i += NT) p.fv[bh * P + i] = (float)sVl[vz_off(C - 1, i)];
+  // final_k: the sequence's last key row, rotated and unscaled (the same arithmetic as
+  // the stage), one rotary pair per lane of wave 0
+  if (wave == 0 && lane < H2) {
+    const int j = lane;
+    const int64_t row = (int64_t)(L - 1) * N;
+    float kl = (float)kg[row + j] + sKb[j], kh = (float)kg[row + H2 + j] + sKb[H2 + j];
+    if (j < Nr) {
+      const float turns = phig[(int64_t)(L - 1) * Nr + j] * 0.15915494309189535f;
+      const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
+      const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
+      kl = k0;
+      kh = k1;
+    }
+    p.fk[bh * N + j] = kl;
+    p.fk[bh * N + H2 + j] = kh;
+  }
 }
 
 // Every per-(b, h) stream of fwd_bf16_kernel must be addressable with 31-bit byte
