@@ -862,16 +862,22 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     for (int pb = 0; pb < PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // masked, decayed score tile s^T[j][t] for key strip jb (rows j) and this wave's
     // query strip (columns t), as a sub-fragment with K = j
+    // (all K fragments are read before the first MFMA, and the mask is a select: the
+    // decay 2^{min(A_t - A_j, 0)} is finite for every entry, masked or not)
     auto score = [&](int jb) {
+      bf16x8 kfr[F::NBK];
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk) kfr[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
+      const f32x4 aj = *reinterpret_cast<const f32x4*>(sA + jb * 16 + g4);
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk)
-        mma32x(acc, ld_nat8(sK, LDK, jb * 16, 32 * blk, lane), qf[blk]);
+      for (int blk = 0; blk < F::NBK; ++blk) mma32x(acc, kfr[blk], qf[blk]);
       f32x4 sv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = jb * 16 + g4 + i;
-        sv[i] = (tcol > j) ? acc[i] * __builtin_amdgcn_exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+        const float dec = __builtin_amdgcn_exp2f(fminf(At - aj[i], 0.f));
+        sv[i] = (tcol > j) ? acc[i] * dec : 0.f;
       }
       return sub_from_f32<bf16>(sv);
     };
@@ -931,10 +937,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       const int kb = k0 + g8;
       bf16x4 a0 = ld_tr4_vz(sV, kb, pb_w * 16, lane);
       bf16x4 a1 = ld_tr4_vz(sV, kb + 4, pb_w * 16, lane);
+      const f32x4 f0 = *reinterpret_cast<const f32x4*>(sFac + kb);
+      const f32x4 f1 = *reinterpret_cast<const f32x4*>(sFac + kb + 4);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        a0[s] = (bf16)((float)a0[s] * sFac[kb + s]);
-        a1[s] = (bf16)((float)a1[s] * sFac[kb + 4 + s]);
+        a0[s] = (bf16)((float)a0[s] * f0[s]);
+        a1[s] = (bf16)((float)a1[s] * f1[s]);
       }
 #pragma unroll
       for (int m = 0; m < SPW; ++m) {
