@@ -1233,11 +1233,14 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int k0 = 0; k0 < P; k0 += 32)
           mma32x(am, ld_nat8(sG, LDP, tb * 16, k0, lane), ld_nat8(sV, LDP, w * 16, k0, lane));
+        // branch-free mask: 2^{min(A_t - A_j, 0)} is finite for every entry
+        const f32x4 at = *reinterpret_cast<const f32x4*>(sA + tb * 16 + 4 * g4);
         f32x4 vw, vm;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = tb * 16 + 4 * g4 + i;
-          const float dec = (t > jcol) ? __builtin_amdgcn_exp2f(fminf(sA[t] - Aj, 0.f)) : 0.f;
+          const float e = __builtin_amdgcn_exp2f(fminf(at[i] - Aj, 0.f));
+          const float dec = (t > jcol) ? e : 0.f;
           vw[i] = aw[i] * dec;
           vm[i] = am[i] * dec;
         }
@@ -1266,11 +1269,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int k0 = 0; k0 < P; k0 += 32)
           mma32x(am, ld_nat8(sV, LDP, jb * 16, k0, lane), ld_nat8(sG, LDP, w * 16, k0, lane));
+        const f32x4 aj = *reinterpret_cast<const f32x4*>(sA + jb * 16 + 4 * g4);
         f32x4 vm;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = jb * 16 + 4 * g4 + i;
-          vm[i] = (tcol > j) ? am[i] * __builtin_amdgcn_exp2f(fminf(At - sA[j], 0.f)) : 0.f;
+          const float e = __builtin_amdgcn_exp2f(fminf(At - aj[i], 0.f));
+          vm[i] = (tcol > j) ? am[i] * e : 0.f;
         }
         return sub_from_f32<bf16>(vm);
       };
@@ -1344,10 +1349,12 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         const int kb = k0 + 4 * g4;
         bf16x4 a0 = ld_tr4(sG, LDP, kb, pb_w * 16, lane);
         bf16x4 a1 = ld_tr4(sG, LDP, kb + 16, pb_w * 16, lane);
+        const f32x4 e0 = *reinterpret_cast<const f32x4*>(sExpA + kb);
+        const f32x4 e1 = *reinterpret_cast<const f32x4*>(sExpA + kb + 16);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          a0[s] = (bf16)((float)a0[s] * sExpA[kb + s]);
-          a1[s] = (bf16)((float)a1[s] * sExpA[kb + 16 + s]);
+          a0[s] = (bf16)((float)a0[s] * e0[s]);
+          a1[s] = (bf16)((float)a1[s] * e1[s]);
         }
 #pragma unroll
         for (int m = 0; m < SPW; ++m) {
