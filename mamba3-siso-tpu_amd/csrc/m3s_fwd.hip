@@ -914,10 +914,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const float eA = sExpA[tcol];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
+      bf16x8 sfr[F::NBK];   // all K fragments of this row block first, then the chain
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk) sfr[blk] = ld_nat8(sS, LDK, pb * 16, 32 * blk, lane);
       f32x4 it = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk)
-        mma32x(it, ld_nat8(sS, LDK, pb * 16, 32 * blk, lane), qf[blk]);
+      for (int blk = 0; blk < F::NBK; ++blk) mma32x(it, sfr[blk], qf[blk]);
       // diagonal and skip: (D + gamma_t u_t . w_t) v_t
       const bf16x4 vd = *reinterpret_cast<const bf16x4*>(sV + vz_off(tcol, pb * 16 + g4));
       const float coef = sCoef[tcol];
@@ -939,16 +941,20 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       bf16x4 a1 = ld_tr4_vz(sV, kb + 4, pb_w * 16, lane);
       const f32x4 f0 = *reinterpret_cast<const f32x4*>(sFac + kb);
       const f32x4 f1 = *reinterpret_cast<const f32x4*>(sFac + kb + 4);
+      bf16x4 kb0[SPW], kb1[SPW];   // every tile's K fragments first: independent MFMAs
+#pragma unroll
+      for (int m = 0; m < SPW; ++m) {
+        const int nb = nb0 + NSTEP * m;
+        kb0[m] = ld_tr4(sK, LDK, kb, nb * 16, lane);
+        kb1[m] = ld_tr4(sK, LDK, kb + 4, nb * 16, lane);
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         a0[s] = (bf16)((float)a0[s] * f0[s]);
         a1[s] = (bf16)((float)a1[s] * f1[s]);
       }
 #pragma unroll
-      for (int m = 0; m < SPW; ++m) {
-        const int nb = nb0 + NSTEP * m;
-        mma32(Sacc[m], a0, a1, ld_tr4(sK, LDK, kb, nb * 16, lane), ld_tr4(sK, LDK, kb + 4, nb * 16, lane));
-      }
+      for (int m = 0; m < SPW; ++m) mma32(Sacc[m], a0, a1, kb0[m], kb1[m]);
     }
   };
 
