@@ -265,6 +265,20 @@ typedef struct m3s_norm_bwd_args {
   void* workspace;       /* scratch, m3s_norm_bwd_workspace_bytes() bytes, 16-aligned */
 } m3s_norm_bwd_args;
 
+/* Weight layout for the layer's projection GEMMs: out = transpose(in), cast to
+ * out_dtype, with zero rows appended up to out_rows. No counterpart in the reference,
+ * which casts its weights per call (`params.in_proj.astype(u.dtype)`, layer.py:233, 256);
+ * the layer computes its GEMMs against this transposed, padded copy instead. */
+typedef struct m3s_transpose_args {
+  int32_t struct_size;  /* sizeof(m3s_transpose_args) */
+  int32_t rows, cols;   /* in is (rows, cols) */
+  int32_t out_rows;     /* >= cols; out is (out_rows, rows), dense; rows >= cols are zero */
+  int32_t in_dtype, out_dtype; /* M3S_DTYPE_* */
+  const void* in;
+  int64_t in_stride;    /* elements between rows of in */
+  void* out;
+} m3s_transpose_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -303,6 +317,7 @@ int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
 int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
 int32_t m3s_norm_fwd(const m3s_norm_fwd_args* args, void* stream);
 int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
+int32_t m3s_transpose(const m3s_transpose_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -140,11 +140,19 @@ class NormBwdArgs(C.Structure):
     ]
 
 
+class TransposeArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32), ("rows", i32), ("cols", i32), ("out_rows", i32),
+        ("in_dtype", i32), ("out_dtype", i32),
+        ("inp", vp), ("in_stride", i64), ("out", vp),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
-           "m3s_norm_bwd", "m3s_decode_layer")
+           "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose")
 
 _lib = None
 
@@ -181,6 +189,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_prep_fwd.argtypes = [C.POINTER(PrepFwdArgs), vp]
     lib.m3s_prep_bwd.restype = i32
     lib.m3s_prep_bwd.argtypes = [C.POINTER(PrepBwdArgs), vp]
+    lib.m3s_transpose.restype = i32
+    lib.m3s_transpose.argtypes = [C.POINTER(TransposeArgs), vp]
     lib.m3s_decode_layer.restype = i32
     lib.m3s_decode_layer.argtypes = [C.POINTER(DecodeLayerArgs), vp]
     lib.m3s_norm_bwd_workspace_bytes.restype = i64

@@ -592,3 +592,23 @@ def bcnorm_backward(xs, weights, rstds, dys, dxs):
     with torch.cuda.device(dev):
         _lib.check(lib.m3s_norm_bwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_norm_bwd")
     return dws
+
+
+def transpose_pad(w: Tensor, dtype: torch.dtype, out_rows: int) -> Tensor:
+    """``w`` (R, C) -> a dense (out_rows, R) tensor of ``dtype`` holding ``w.T`` in its
+    first C rows and zeros below (one ``m3s_transpose`` launch): the projection weights'
+    GEMM layout."""
+    dev = _device_of(w)
+    if w.dim() != 2 or w.stride(1) != 1:
+        w = w.contiguous()
+    rows, cols = w.shape
+    out = torch.empty(out_rows, rows, device=dev, dtype=dtype)
+    a = _lib.TransposeArgs()
+    a.struct_size = ctypes.sizeof(_lib.TransposeArgs)
+    a.rows, a.cols, a.out_rows = rows, cols, out_rows
+    a.in_dtype, a.out_dtype = _lib.dtype_code(w.dtype), _lib.dtype_code(dtype)
+    a.inp, a.in_stride, a.out = w.data_ptr(), w.stride(0), out.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_transpose(ctypes.byref(a), _lib.stream_handle(dev)),
+                   "m3s_transpose")
+    return out

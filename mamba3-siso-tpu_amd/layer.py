@@ -196,9 +196,7 @@ class _LayerFn(torch.autograd.Function):
         if tuple(in_proj.shape) != (dm, d) or tuple(out_proj.shape) != (cfg.d_inner, dm):
             raise ValueError(f"in_proj must be {(dm, d)} and out_proj {(cfg.d_inner, dm)}")
         # the reference casts the weights per call (layer.py:233, 256); this lays them out too
-        w_t = torch.empty(dp, dm, device=u.device, dtype=dt)
-        w_t[:d].copy_(in_proj.t())
-        w_t[d:].zero_()
+        w_t = K.transpose_pad(in_proj, dt, dp)
         u2 = u.reshape(m, dm)
         proj = (u2 @ w_t.t()).view(batch, seqlen, dp)
         z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
@@ -212,7 +210,7 @@ class _LayerFn(torch.autograd.Function):
                               dtype_policy=cfg.policy_name, save_residuals=need)
         y, fs, fk, fv = outs[:4]
         y2 = y.permute(0, 2, 1, 3).reshape(m, cfg.d_inner)
-        wo_t = out_proj.t().to(dt).contiguous()
+        wo_t = K.transpose_pad(out_proj, dt, dm)
         out = (y2 @ wo_t.t()).view(batch, seqlen, dm)
         if need:
             res = outs[4]

@@ -55,6 +55,8 @@ int main(void) {
          offsetof(m3s_norm_bwd_args, dx), offsetof(m3s_norm_bwd_args, workspace));
   printf("%zu %zu %zu\n", sizeof(m3s_decode_layer_args), offsetof(m3s_decode_layer_args, proj_stride),
          offsetof(m3s_decode_layer_args, y));
+  printf("%zu %zu %zu\n", sizeof(m3s_transpose_args), offsetof(m3s_transpose_args, in_stride),
+         offsetof(m3s_transpose_args, out));
   return 0;
 }
 """
@@ -76,8 +78,10 @@ int main(void) {
     assert sizes[13:19] == [ctypes.sizeof(lib.NormFwdArgs), ctypes.sizeof(lib.NormBwdArgs),
                             lib.NormFwdArgs.x.offset, lib.NormFwdArgs.rstd.offset,
                             lib.NormBwdArgs.dx.offset, lib.NormBwdArgs.workspace.offset]
-    assert sizes[19:] == [ctypes.sizeof(lib.DecodeLayerArgs), lib.DecodeLayerArgs.proj_stride.offset,
-                          lib.DecodeLayerArgs.y.offset]
+    assert sizes[19:22] == [ctypes.sizeof(lib.DecodeLayerArgs), lib.DecodeLayerArgs.proj_stride.offset,
+                            lib.DecodeLayerArgs.y.offset]
+    assert sizes[22:] == [ctypes.sizeof(lib.TransposeArgs), lib.TransposeArgs.in_stride.offset,
+                          lib.TransposeArgs.out.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -190,3 +194,17 @@ def test_decode_layer_arguments_are_checked_without_a_launch(lib):
     assert b"row stride" in h.m3s_last_error()
     a.state_dim = 96
     assert h.m3s_decode_layer(ctypes.byref(a), None) == lib.ERR_UNSUPPORTED
+
+
+def test_transpose_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    a = lib.TransposeArgs()
+    a.struct_size = ctypes.sizeof(lib.TransposeArgs)
+    a.rows, a.cols, a.out_rows = 64, 100, 96                 # out_rows < cols
+    a.in_dtype = a.out_dtype = lib.DTYPE_BF16
+    a.inp, a.in_stride, a.out = 0x1000, 100, 0x2000
+    assert h.m3s_transpose(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"out_rows" in h.m3s_last_error()
+    a.out_rows, a.in_stride = 128, 50                        # row stride shorter than a row
+    assert h.m3s_transpose(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"in_stride" in h.m3s_last_error()

@@ -1,5 +1,6 @@
 """GPU parity of the BCNorm kernels (m3s_norm_fwd / m3s_norm_bwd) against the oracle's
-``rms_norm`` (``layer.py:190-198``) and its float64 autograd, and of the fused layer path
+``rms_norm`` (``layer.py:190-198``) and its float64 autograd, of the weight-layout kernel
+(m3s_transpose, exact against torch's transpose + cast), and of the fused layer path
 (`_LayerFn`) against the composed one.
 
 Tolerances: the forward output is stored in the input dtype, so it must sit within one
@@ -136,3 +137,20 @@ def test_fused_layer_without_grad_saves_nothing(m3, dev):
         y, st = m3.mamba3_siso_layer(params, u, cfg)
     assert y.shape == (1, 256, 256) and y.dtype == BF16 and not y.requires_grad
     assert st.ssm.shape == (1, cfg.nheads, 64, 128)
+
+
+@pytest.mark.parametrize("src,dst,rows,cols,out_rows,stride_pad", [
+    (BF16, BF16, 1024, 4480, 4608, 0),     # the configs[1] in_proj layout
+    (F32, BF16, 200, 133, 256, 5),         # ragged tiles, strided input, f32 parameters
+    (F32, F32, 64, 64, 64, 0),
+    (BF16, F32, 70, 1, 8, 3),
+])
+def test_transpose_pad_matches_torch_exactly(m3, dev, src, dst, rows, cols, out_rows, stride_pad):
+    g = torch.Generator().manual_seed(rows + cols)
+    base = torch.randn(rows, cols + stride_pad, generator=g).to(src).to(dev)
+    w = base[:, :cols]
+    got = m3.kernels.transpose_pad(w, dst, out_rows)
+    want = torch.zeros(out_rows, rows, dtype=dst, device=dev)
+    want[:cols] = w.t().to(dst)
+    assert got.shape == (out_rows, rows) and got.dtype == dst and got.is_contiguous()
+    assert torch.equal(got, want)
