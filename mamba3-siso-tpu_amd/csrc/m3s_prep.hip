@@ -45,8 +45,15 @@ __device__ __forceinline__ float heavy_tail_(float x) {
   return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
 }
 __device__ __forceinline__ float sigmoid_(float x) { return 1.f / (1.f + expf(-x)); }
+// x mod 2 pi in [0, 2 pi): the quotient from a multiply by 1 / (2 pi), the remainder by
+// one fma, then one correction step. Where x / (2 pi) lies within an ulp of an integer the
+// quotient can differ by one from floor(x / (2 pi)); the correction keeps the result in
+// range and it is the same angle.
 __device__ __forceinline__ float wrap_(float x) {
-  return x - kTwoPiF * floorf(x / kTwoPiF);
+  constexpr float kInvTwoPiF = 0.15915494309189535f;
+  float r = fmaf(-kTwoPiF, floorf(x * kInvTwoPiF), x);
+  r = r < 0.f ? r + kTwoPiF : r;
+  return r >= kTwoPiF ? r - kTwoPiF : r;
 }
 
 // Column quad [j0, j0 + 4) of a row of Nr f32 values, zero past Nr.
@@ -181,30 +188,66 @@ prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
   }
 }
 
+// phi for one (batch element, block of 64 tokens): each wave takes one head at a time,
+// so a store instruction covers whole rows of one head's contiguous (t, Nr) slab. Lane
+// (row group rg, column quad q) owns RPL consecutive rows of that quad: a first pass
+// sums them, a shuffle scan over the row groups of the column gives each lane's
+// exclusive prefix, a second pass writes the running sum wrapped to [0, 2 pi). The
+// block's tanh(angles) pi rows, shared by the heads, are staged in LDS once.
 __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdParams p) {
+  extern __shared__ float sT[];   // [kPrepTB][Nr]
   const int H = p.H, Nr = p.Nr, L = p.L;
   const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * kPrepTB;
   const int nt = min(kPrepTB, L - t0);
+  const float* trow = p.tpi + ((int64_t)b * L + t0) * Nr;
+  for (int i = tid; i < nt * Nr; i += kPrepThreads) sT[i] = trow[i];
+  __syncthreads();
   const int J4 = (Nr + 3) / 4;
-  for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
-    const int h = pr / J4, j0 = 4 * (pr % J4);
+  const int RG = 64 / J4;                      // row groups per wave (J4 <= 64)
+  const int RPL = (kPrepTB + RG - 1) / RG;     // consecutive rows per lane
+  const int lane = tid & 63, wave = tid >> 6;
+  const bool act = lane < RG * J4;
+  const int rg = act ? lane / J4 : 0, j0 = act ? 4 * (lane % J4) : 0;
+  const int r0 = rg * RPL;
+  for (int h = wave; h < H; h += kPrepThreads / 64) {
     const int64_t bh = (int64_t)b * H + h;
+    const float* dtrow = p.dt + bh * L + t0;
+    f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < RPL; ++i) {
+      const int t = r0 + i;
+      if (act && t < nt) {
+        const float dt = dtrow[t];
+        const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) tot[c] += tp[c] * dt;
+      }
+    }
+    f32x4 incl = tot;
+    for (int off = 1; off < RG; off <<= 1) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float o = __shfl_up(incl[c], off * J4, 64);
+        if (rg >= off) incl[c] += o;
+      }
+    }
+    if (!act) continue;
     f32x4 run = ld_quad(p.tot + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
     f32x4 init = {0.f, 0.f, 0.f, 0.f};
     if (p.phi_init) init = ld_quad(p.phi_init + bh * Nr, j0, Nr);
-    const float* dtrow = p.dt + bh * L + t0;
-    const float* trow = p.tpi + ((int64_t)b * L + t0) * Nr;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) run[c] += incl[c] - tot[c];
     float* prow = p.phi + (bh * L + t0) * Nr;
-#pragma unroll 4
-    for (int t = 0; t < nt; ++t) {
+    for (int i = 0; i < RPL; ++i) {
+      const int t = r0 + i;
+      if (t >= nt) break;
       const float dt = dtrow[t];
-      const f32x4 tp = ld_quad(trow + t * Nr, j0, Nr);
+      const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
       f32x4 out;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        run[i] += tp[i] * dt;
-        out[i] = wrap_(run[i] + init[i]);
+      for (int c = 0; c < 4; ++c) {
+        run[c] += tp[c] * dt;
+        out[c] = wrap_(run[c] + init[c]);
       }
       st_quad(prow + t * Nr, j0, Nr, out);
       if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
@@ -485,6 +528,7 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
               "m3s_prep_fwd: phi buffers must be 16-byte aligned");
   const size_t lds = (size_t)prep_fwd_lds_floats(H, Nr) * 4;
   M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_fwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
+  M3S_REQUIRE(Nr <= 256, "m3s_prep_fwd: n_angles %d > 256 (a phi row must fit one wave)", Nr);
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_prep_fwd: B*H too large");
   const int nblk = (L + kPrepTB - 1) / kPrepTB;
   PrepFwdParams p{};
@@ -508,7 +552,7 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
   hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
                      dim3(kPrepThreads), 0, s, p.tot, nullptr, nullptr, B, hn, nblk, 0);
   if ((rc = launch_status("m3s_prep_fwd"))) return rc;
-  hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads), 0, s, p);
+  hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads), (size_t)kPrepTB * Nr * 4, s, p);
   return launch_status("m3s_prep_fwd");
 }
 
