@@ -729,13 +729,21 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const uint32_t sphi = (uint32_t)c * C * Nr * 4;
 #pragma unroll
     for (int lb = 0; lb < F::LOB; ++lb) {
+      // wave-uniform cases first: a block of 32 columns wholly past Nr needs no load, one
+      // wholly inside takes 16-byte loads; only a block that Nr cuts tests per lane (a
+      // per-lane choice between load widths makes the compiler drain the load queue)
+      if (32 * lb >= Nr) {
 #pragma unroll
-      for (int qd = 0; qd < 2; ++qd) {
-        const int j = 32 * lb + g8 + 4 * qd;
-        const uint32_t o = (uint32_t)(trow * Nr + j) * 4;
-        if (phi_vec && j + 4 <= Nr) {
-          rphi[lb][qd] = buf_load<f32x4>(rPhi, o, sphi);
-        } else {
+        for (int qd = 0; qd < 2; ++qd) rphi[lb][qd] = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else if (phi_vec && 32 * lb + 32 <= Nr) {
+#pragma unroll
+        for (int qd = 0; qd < 2; ++qd)
+          rphi[lb][qd] = buf_load<f32x4>(rPhi, (uint32_t)(trow * Nr + 32 * lb + g8 + 4 * qd) * 4, sphi);
+      } else {
+#pragma unroll
+        for (int qd = 0; qd < 2; ++qd) {
+          const int j = 32 * lb + g8 + 4 * qd;
+          const uint32_t o = (uint32_t)(trow * Nr + j) * 4;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             rphi[lb][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, o + 4 * i, sphi) : 0.f;
