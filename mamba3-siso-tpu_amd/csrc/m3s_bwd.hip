@@ -940,6 +940,23 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   const auto rYb = make_rsrc(ybg, (uint32_t)L * P * 4);
   const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
   const auto rCs = make_rsrc(csg, (uint32_t)nc * N * P * 2);
+  // phi[t][j .. j+3], zero past Nr. With Nr % 4 == 0 (wave-uniform) every lane issues one
+  // 16-byte load and lanes past Nr select zero: a per-lane choice of load width would make
+  // the compiler drain the load queue at the join.
+  auto phi_quad = [&](int t, int j, uint32_t sphi) {
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (phi_vec) {
+      const bool ok = j + 4 <= Nr;
+      const f32x4 w = buf_load<f32x4>(rPhi, ok ? (uint32_t)(t * Nr + j) * 4 : 0u, sphi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = ok ? w[i] : 0.f;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = (j + i < Nr) ? buf_load<float>(rPhi, (uint32_t)(t * Nr + j + i) * 4, sphi) : 0.f;
+    }
+    return v;
+  };
   // the (B, H, L) scalar streams: a uniform row base plus a 32-bit offset (SGPR-base
   // global access), which keeps them out of the descriptor set
   const float* adt_r = p.adt + bh * L;
@@ -1006,17 +1023,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           rk[r][e][0] = buf_load<vec>(rK, o, sqk);
           rk[r][e][1] = buf_load<vec>(rK, o + 2 * H2, sqk);
 #pragma unroll
-          for (int qd = 0; qd < VEC / 4; ++qd) {
-            const int j = j0 + 4 * qd;
-            const uint32_t op = (uint32_t)(t * Nr + j) * 4;
-            if (phi_vec && j + 4 <= Nr) {
-              rphi[r][e][qd] = buf_load<f32x4>(rPhi, op, sphi);
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                rphi[r][e][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, op + 4 * i, sphi) : 0.f;
-            }
-          }
+          for (int qd = 0; qd < VEC / 4; ++qd)
+            rphi[r][e][qd] = phi_quad(t, j0 + 4 * qd, sphi);
           rscale[r][e] = scl_r[(uint32_t)(c * C + t)];
         }
       }
@@ -1419,15 +1427,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             float ph[VEC];
 #pragma unroll
             for (int qd = 0; qd < VEC / 4; ++qd) {
-              const int j = j0 + 4 * qd;
-              const uint32_t op = (uint32_t)(t * Nr + j) * 4;
-              f32x4 v4 = {0.f, 0.f, 0.f, 0.f};
-              if (phi_vec && j + 4 <= Nr) {
-                v4 = buf_load<f32x4>(rPhi, op, sphi);
-              } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v4[i] = (j + i < Nr) ? buf_load<float>(rPhi, op + 4 * i, sphi) : 0.f;
-              }
+              const f32x4 v4 = phi_quad(t, j0 + 4 * qd, sphi);
 #pragma unroll
               for (int i = 0; i < 4; ++i) ph[4 * qd + i] = v4[i];
             }
