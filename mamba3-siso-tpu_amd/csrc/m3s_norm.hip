@@ -165,22 +165,30 @@ __global__ void __launch_bounds__(kNormThreads) norm_bwd_kernel(const NormBwdPar
   }
 }
 
-// dw[which][n] = sum over blocks of the partials, in block order (one thread per column,
-// four independent accumulators).
+// dw[which][n] = sum over blocks of the partials. A block takes 64 columns; each of its four
+// waves sums a quarter of the block partials (eight independent accumulators, fixed order),
+// and the four quarters are added in wave order.
 __global__ void __launch_bounds__(kNormThreads) norm_gain_kernel(const float* __restrict__ part,
                                                                  float* dw0, float* dw1,
                                                                  int nblk, int N) {
+  __shared__ float sq[kNormThreads];
   const int which = blockIdx.y;
-  const int n = blockIdx.x * kNormThreads + threadIdx.x;
-  if (n >= N) return;
-  float a[4] = {0.f, 0.f, 0.f, 0.f};
-  int k = 0;
-  for (; k + 4 <= nblk; k += 4) {
+  const int col = threadIdx.x % 64, slice = threadIdx.x / 64;
+  const int n = blockIdx.x * 64 + col;
+  const int per = (nblk + 3) / 4, k0 = slice * per, k1 = min(nblk, k0 + per);
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (n < N) {
+    int k = k0;
+    for (; k + 8 <= k1; k += 8) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) a[u] += part[((int64_t)(k + u) * 2 + which) * N + n];
+      for (int u = 0; u < 8; ++u) a[u] += part[((int64_t)(k + u) * 2 + which) * N + n];
+    }
+    for (; k < k1; ++k) a[0] += part[((int64_t)k * 2 + which) * N + n];
   }
-  for (; k < nblk; ++k) a[0] += part[((int64_t)k * 2 + which) * N + n];
-  (which ? dw1 : dw0)[n] = (a[0] + a[1]) + (a[2] + a[3]);
+  sq[threadIdx.x] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+  __syncthreads();
+  if (slice == 0 && n < N)
+    (which ? dw1 : dw0)[n] = (sq[col] + sq[64 + col]) + (sq[128 + col] + sq[192 + col]);
 }
 
 static int norm_group(int N, int vec) {
@@ -275,7 +283,7 @@ extern "C" int32_t m3s_norm_bwd(const m3s_norm_bwd_args* a, void* stream) {
     hipLaunchKernelGGL(norm_bwd_kernel<float>, dim3(nblk, cnt), dim3(kNormThreads), 0, s, p);
   int32_t rc = launch_status("m3s_norm_bwd");
   if (rc) return rc;
-  hipLaunchKernelGGL(norm_gain_kernel, dim3((N + kNormThreads - 1) / kNormThreads, cnt),
+  hipLaunchKernelGGL(norm_gain_kernel, dim3((N + 63) / 64, cnt),
                      dim3(kNormThreads), 0, s, p.part, a->dweight[0], cnt > 1 ? a->dweight[1] : nullptr,
                      nblk, N);
   return launch_status("m3s_norm_bwd");
