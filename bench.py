@@ -36,11 +36,13 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy"), default="all",
+    ap.add_argument("--no-lm", action="store_true", help="skip the LM-stack legs")
+    ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy", "lm"), default="all",
                     help="run one leg alone (for rocprofv3 counter passes): 'scan' = the forward "
                          "scan kernel at the kernel boundary, 'bwd' = the backward scan kernel, "
                          "'decode' = the decode kernel, 'copy' = a plain 1 GiB device copy that "
-                         "calibrates the FETCH_SIZE / WRITE_SIZE counters")
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters, 'lm' = the configs[4] "
+                         "byte-LM training step and the LM decode stack")
     return ap.parse_args()
 
 
@@ -99,6 +101,10 @@ def main():
         ms = gpu_time_ms(lambda: dst.copy_(src), 10, torch)
         print(json.dumps({"leg": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30,
                           "ms": round(ms, 4), "gbs": round(2 * (1 << 30) / (ms * 1e-3) / 1e9, 1)}))
+        return
+
+    if args.leg == "lm":
+        print(json.dumps({"leg": "lm", **lm_legs(m3, torch, dev)}))
         return
 
     B, L, H, P, N, DM = 8, 8192, 32, 64, 128, 1024
@@ -236,6 +242,8 @@ def main():
     torch.cuda.synchronize()
     fwd_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    lm = None if args.no_lm else lm_legs(m3, torch, dev)
+
     # ---------------- CPU baseline: the oracle on a bounded sample --------------------
     cpu_base = None
     if not args.no_cpu_baseline:
@@ -262,12 +270,77 @@ def main():
         "fwd_bwd_tok_s": round(tokens / (fb_ms * 1e-3), 1),
         "decode_ms_per_token": round(dec_ms, 4),
         **{k: v for k, v in line.items() if k != "roofline"},
+        "lm": lm,
         "reference_tpu_v5e": {"fwd_kernel_ms_chunk128_pinned": 21.66, "fwd_bwd_ms": 80.1,
                               "decode_ms_per_token_b256": 1.4},
         "roofline": line["roofline"],
         "cpu_baseline": cpu_base,
     }
     print(json.dumps(out))
+
+
+def lm_legs(m3, torch, dev):
+    """the 8-layer byte LM (d_model 768, headdim 64, d_state 128,
+    chunk 128, gated MLP 1536, vocab 256, tied head; 59.1M parameters) trained on B=16 x
+    L=2048 windows of i.i.d. Zipf(1.1) bytes, bf16 products, float32 master weights,
+    clip 1.0 + AdamW (wd 0.1, warmup-cosine lr). tok/s over steps 10-60 (batches staged on
+    the device beforehand). Then the decode stack on the same model: one recorded decode
+    step per token (batch 1 and batch 256), and `generate` end to end (sampling included)."""
+    T = m3.train
+    scfg = m3.SISOConfig(d_model=768, d_state=128, headdim=64, expand=2, chunk=128,
+                         policy_name="bf16")
+    cfg = m3.model.LMConfig(vocab_size=256, n_layers=8, siso=scfg, tie_head=True,
+                            d_intermediate=1536)
+    bsz, seqlen = 16, 2048
+    params = T.train_params(m3.model.init_lm(cfg, 0, device=dev))
+    data = T.zipf_bytes(8 << 20, s=1.1, seed=0)
+    stream = T.batches(data, bsz, seqlen, seed=1, device=dev)
+    staged = [next(stream) for _ in range(60)]
+    opt = T.make_optimizer(params, lr=1e-3, warmup=100, steps=2000)
+    step = T.make_step(cfg, opt)
+    losses = []
+    for i in range(10):
+        loss, params, opt = step(params, opt, *staged[i])
+        losses.append(loss)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(10, 60):
+        loss, params, opt = step(params, opt, *staged[i])
+        losses.append(loss)
+    torch.cuda.synchronize()
+    train_s = time.perf_counter() - t0
+    out = {"workload": "configs[4]: 8-layer byte LM training step (B=16, L=2048)",
+           "params": cfg.param_count(),
+           "train_tok_s": round(50 * bsz * seqlen / train_s, 1),
+           "train_ms_per_step": round(train_s * 1e3 / 50, 3),
+           "loss_step0": round(float(losses[0]), 4), "loss_step59": round(float(losses[-1]), 4),
+           "zipf_entropy_nats": round(float(_zipf_entropy(1.1)), 4)}
+    del staged, opt, stream
+    torch.cuda.empty_cache()
+
+    dp = m3.model.decode_params(params, cfg)
+    for batch in (1, 256):
+        dg = T.DecodeGraph(dp, cfg, batch=batch)
+        tok = torch.randint(0, 256, (batch,), device=dev)
+        for _ in range(5):
+            dg.step(tok)
+        ms = gpu_time_ms(lambda: dg.step(tok), 200, torch)
+        out[f"decode_graph_ms_per_token_b{batch}"] = round(ms, 4)
+        del dg
+    T.generate(dp, cfg, 0, [104, 105], n_tokens=8)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ids = T.generate(dp, cfg, 0, list(b"the "), n_tokens=256)
+    torch.cuda.synchronize()
+    out["generate_ms_per_token_b1"] = round((time.perf_counter() - t0) * 1e3 / 256, 4)
+    assert len(ids) == 4 + 256
+    return out
+
+
+def _zipf_entropy(s):
+    p = [(v + 1) ** -s for v in range(256)]
+    z = sum(p)
+    return -sum(x / z * math.log(x / z) for x in p)
 
 
 def traffic_figure(kernel):

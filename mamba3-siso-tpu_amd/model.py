@@ -1,0 +1,266 @@
+"""A stacked Mamba-3 SISO language model (``model.py`` surface).
+
+``n_layers`` SISO layers in a pre-norm residual stack with an embedding and an output
+head (``model.py:1-22``):
+
+    x = embed[tokens]
+    for each block:  x = x + siso(rms_norm(x))
+                     x = x + mlp(rms_norm2(x))        # only with d_intermediate > 0
+    logits = rms_norm(x) @ head                       # head = embed.T when tied
+
+Names, fields, defaults and initialisation follow ``model.py:39-296``. Precision: the
+residual stream stays in the embedding's dtype (float32 master weights give a float32
+stream, as in the reference), and every matrix product takes its operands in the
+layer policy's operand dtype -- under ``"bf16"`` that is the bf16 operand rounding the
+reference gets from the TPU's default matmul precision (``layout.py:243-291``). The
+SISO mixer is `layer.mamba3_siso_layer` (one fused autograd node around the HIP scan
+when no state is carried); per-token decode goes through the one-launch
+`layer.mamba3_siso_decode_step`, which updates each layer's state in place.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any, NamedTuple, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import layer as LY
+from . import layout as L
+from .scan_prep import SISOState, zero_state
+
+Tensor = torch.Tensor
+
+
+@dataclasses.dataclass(frozen=True)
+class LMConfig:
+    """Model shape (``model.py:39-92``). ``siso`` is the per-layer config shared by every
+    block; ``d_intermediate = 0`` means no MLP."""
+
+    vocab_size: int
+    n_layers: int
+    siso: LY.SISOConfig
+    tie_head: bool = True
+    d_intermediate: int = 0
+
+    @property
+    def d_model(self) -> int:
+        return self.siso.d_model
+
+    def param_count(self) -> int:
+        """Analytic parameter count (``model.py:65-92``). Exact for this build's trees:
+        `init_lm` creates exactly these tensors."""
+        c = self.siso
+        per_layer = (c.d_model * c.d_in_proj + c.d_inner * c.d_model + c.nheads * 2
+                     + c.d_state * 2 + c.nheads * c.d_state * 2 + c.d_model)
+        if self.d_intermediate:
+            per_layer += (c.d_model * 2 * self.d_intermediate
+                          + self.d_intermediate * c.d_model + c.d_model)
+        head = 0 if self.tie_head else self.d_model * self.vocab_size
+        return self.vocab_size * self.d_model + self.n_layers * per_layer + self.d_model + head
+
+
+class MLPParams(NamedTuple):
+    """Gated MLP (``model.py:95-107``): ``fc1`` ``(d_model, 2*d_intermediate)`` produces
+    the value half (first ``d_intermediate`` columns) and the gate half together."""
+
+    fc1: Tensor
+    fc2: Tensor
+
+
+class BlockParams(NamedTuple):
+    """One residual block (``model.py:110-116``)."""
+
+    norm_gain: Tensor
+    siso: LY.SISOParams
+    mlp_norm_gain: Optional[Tensor] = None
+    mlp: Optional[MLPParams] = None
+
+
+class LMParams(NamedTuple):
+    """Weights (``model.py:119-125``); ``blocks`` is a list of `BlockParams`."""
+
+    embed: Tensor
+    blocks: list
+    final_norm: Tensor
+    head: Optional[Tensor]
+
+
+def _mm_dtype(cfg: LMConfig) -> torch.dtype:
+    return L.policy(cfg.siso.policy_name).matmul
+
+
+def _mm(x: Tensor, w: Tensor, dt: torch.dtype) -> Tensor:
+    """A matrix product with both operands in the policy's operand dtype."""
+    return x.to(dt) @ w.to(dt)
+
+
+def gated_mlp(p: MLPParams, x: Tensor, mm_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """``fc2(value * silu(gate))`` (``model.py:128-141``); value is the first half of
+    ``fc1``'s output, gate the second (upstream's ``chunk(2, dim=-1)`` order). Products
+    run in ``mm_dtype`` (default: ``x``'s dtype); the result is in that dtype."""
+    dt = x.dtype if mm_dtype is None else mm_dtype
+    value, gate = _mm(x, p.fc1, dt).chunk(2, dim=-1)
+    return _mm(value * F.silu(gate), p.fc2, dt)
+
+
+def init_lm(cfg: LMConfig, key: Any = 0, dtype=torch.float32, device=None) -> LMParams:
+    """Fresh weights (``model.py:141-191``): embedding ``N(0, 0.02^2)``; each block's SISO
+    weights from `layer.init_params` with ``out_proj`` scaled by ``1/sqrt(2 n_layers)``;
+    ``fc1`` ``N(0, 1/d_model)``, ``fc2`` ``N(0, 1/d_intermediate)`` times the same residual
+    scale; norm gains ones; an untied head ``N(0, 0.02^2)``.
+
+    ``key`` is an int seed or a ``torch.Generator``; the draws happen on the CPU (JAX's
+    threefry stream is not reproduced, only the distributions), then move to ``device``.
+    """
+    gen = key if isinstance(key, torch.Generator) else torch.Generator().manual_seed(int(key))
+    d, di = cfg.d_model, cfg.d_intermediate
+    embed = torch.randn(cfg.vocab_size, d, generator=gen) * 0.02
+    resid = 1.0 / math.sqrt(2.0 * cfg.n_layers)
+    blocks = []
+    for _ in range(cfg.n_layers):
+        p = LY.init_params(cfg.siso, gen, dtype)
+        p = p._replace(out_proj=p.out_proj * resid)
+        mlp = mlp_norm = None
+        if di:
+            fc1 = torch.randn(d, 2 * di, generator=gen) / math.sqrt(d)
+            fc2 = torch.randn(di, d, generator=gen) / math.sqrt(di) * resid
+            mlp = MLPParams(fc1=fc1.to(dtype), fc2=fc2.to(dtype))
+            mlp_norm = torch.ones(d, dtype=dtype)
+        blocks.append(BlockParams(torch.ones(d, dtype=dtype), p, mlp_norm, mlp))
+    head = None if cfg.tie_head else (torch.randn(d, cfg.vocab_size, generator=gen) * 0.02).to(dtype)
+    params = LMParams(embed.to(dtype), blocks, torch.ones(d, dtype=dtype), head)
+    return params if device is None else lm_to(params, device=device)
+
+
+def lm_map(fn, params: LMParams) -> LMParams:
+    """Apply ``fn`` to every tensor of the tree, keeping its structure (``None`` stays)."""
+    f = lambda t: None if t is None else fn(t)  # noqa: E731
+    blocks = [BlockParams(f(b.norm_gain), LY.SISOParams(*(f(t) for t in b.siso)),
+                          f(b.mlp_norm_gain),
+                          None if b.mlp is None else MLPParams(f(b.mlp.fc1), f(b.mlp.fc2)))
+              for b in params.blocks]
+    return LMParams(f(params.embed), blocks, f(params.final_norm), f(params.head))
+
+
+def lm_to(params: LMParams, device=None, dtype=None) -> LMParams:
+    return lm_map(lambda t: t.to(device=device, dtype=dtype), params)
+
+
+def lm_leaves(params: LMParams) -> list:
+    """The tree's tensors in a fixed order (embed, per block: norm, the eight SISO fields,
+    MLP norm, fc1, fc2; final norm, head), ``None`` entries skipped."""
+    out = [params.embed]
+    for b in params.blocks:
+        out.append(b.norm_gain)
+        out.extend(b.siso)
+        if b.mlp is not None:
+            out.extend((b.mlp_norm_gain, b.mlp.fc1, b.mlp.fc2))
+    out.append(params.final_norm)
+    if params.head is not None:
+        out.append(params.head)
+    return out
+
+
+def decode_params(params: LMParams, cfg: LMConfig) -> LMParams:
+    """``params`` with each block's projection matrices (in_proj, out_proj, fc1, fc2) cast
+    once to the policy's operand dtype. Every product casts them to that dtype anyway, so
+    results are bit-identical; a per-token step then reads half the weight bytes and
+    launches no casts. The embedding (which sets the residual stream's dtype), the head
+    and the vectors are unchanged."""
+    dt = _mm_dtype(cfg)
+    blocks = [b._replace(siso=b.siso._replace(in_proj=b.siso.in_proj.detach().to(dt),
+                                              out_proj=b.siso.out_proj.detach().to(dt)),
+                         mlp=None if b.mlp is None else MLPParams(b.mlp.fc1.detach().to(dt),
+                                                                  b.mlp.fc2.detach().to(dt)))
+              for b in params.blocks]
+    return params._replace(blocks=blocks)
+
+
+def _head(params: LMParams, cfg: LMConfig) -> Tensor:
+    return params.embed.t() if cfg.tie_head else params.head
+
+
+def _logits(x: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
+    """``rms_norm(x) @ head`` with float32 logits. Under a bf16 policy both operands are
+    rounded to bf16 and accumulated in float32 (the head is about 0.3% of the model's
+    flops, so a float32 product of the rounded operands costs nothing measurable)."""
+    dt = _mm_dtype(cfg)
+    xn = _norm(x, params.final_norm, cfg.siso.norm_eps, dt)
+    return xn.float() @ _head(params, cfg).to(dt).float()
+
+
+def _norm(x: Tensor, gain: Tensor, eps: float, dt: torch.dtype) -> Tensor:
+    """``rms_norm(x, gain, eps)`` (``layer.py:190-198``: float32 statistics, gain after
+    scaling) returned in ``dt``, as the next product takes it. ``F.rms_norm`` on a float32
+    row is one fused kernel each way on the device, where the composed form launches about
+    seven elementwise and reduction kernels per direction."""
+    return F.rms_norm(x.float(), (x.shape[-1],), gain.float(), eps).to(dt)
+
+
+def _embed(table: Tensor, tokens: Tensor) -> Tensor:
+    """``table[tokens]``. Through ``F.embedding``, whose backward reduces duplicate ids in
+    parallel partial segments; the plain-indexing backward sums each id's rows serially,
+    which for byte data (256 ids, Zipf-skewed) costs ~5 ms per training step."""
+    return F.embedding(tokens, table)
+
+
+def lm_forward(params: LMParams, tokens: Tensor, cfg: LMConfig, interpret: Any = False,
+               device_kind: str | None = None, states: Optional[list] = None):
+    """``(B, L)`` int tokens -> ``(B, L, vocab)`` float32 logits (``model.py:194-232``).
+
+    With ``states`` (a per-layer carry-in, e.g. `zero_states`) the per-layer carry-out is
+    returned as well: ``(logits, states)`` -- the segmented prefill of generation.
+    ``interpret`` and ``device_kind`` are accepted for signature compatibility."""
+    dt = _mm_dtype(cfg)
+    x = _embed(params.embed, tokens)
+    new_states = []
+    eps = cfg.siso.norm_eps
+    for i, b in enumerate(params.blocks):
+        y, st = LY.mamba3_siso_layer(b.siso, _norm(x, b.norm_gain, eps, dt), cfg.siso,
+                                     state=None if states is None else states[i])
+        new_states.append(st)
+        x = x + y
+        if b.mlp is not None:
+            x = x + gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, eps, dt), dt)
+    logits = _logits(x, params, cfg)
+    return (logits, new_states) if states is not None else logits
+
+
+def lm_loss(params: LMParams, xs: Tensor, ys: Tensor, cfg: LMConfig) -> Tensor:
+    """Mean next-token cross-entropy of `lm_forward`'s logits against ``ys``
+    (``train.py:414-416``)."""
+    logits = lm_forward(params, xs, cfg)
+    return F.cross_entropy(logits.reshape(-1, logits.shape[-1]), ys.reshape(-1))
+
+
+def zero_states(cfg: LMConfig, batch: int, dtype=torch.float32, device=None) -> list:
+    """A fresh per-layer carry (``model.py:235-241``)."""
+    c = cfg.siso
+    out = []
+    for _ in range(cfg.n_layers):
+        s = zero_state(batch, c.nheads, c.headdim, c.d_state, c.n_angles, dtype)
+        out.append(SISOState(*(t.to(device) for t in s)) if device is not None else s)
+    return out
+
+
+def lm_decode_step(params: LMParams, token: Tensor, states: list, cfg: LMConfig,
+                   interpret: Any = False):
+    """One token through the stack (``model.py:244-296``): ``(B,)`` -> ``((B, vocab)
+    float32 logits, states)``. Each layer between its projections is one
+    ``m3s_decode_layer`` launch, which updates that layer's state in place (the
+    reference donates it); the returned list holds the same state tensors."""
+    dt = _mm_dtype(cfg)
+    c = cfg.siso
+    x = _embed(params.embed, token)
+    out_states = []
+    for i, b in enumerate(params.blocks):
+        y, st = LY.mamba3_siso_decode_step(b.siso, _norm(x, b.norm_gain, c.norm_eps, dt), c,
+                                           states[i])
+        out_states.append(st)
+        x = x + y
+        if b.mlp is not None:
+            x = x + gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, c.norm_eps, dt), dt)
+    return _logits(x, params, cfg), out_states
