@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must precede the C-ABI library load)
 
 from . import convert, kernels, layout  # noqa: F401
 from . import kernel_bwd, kernel_decode, kernel_fwd  # noqa: F401
-from . import model, train  # noqa: F401
+from . import checkpoint, model, train  # noqa: F401
 from .kernels import (  # noqa: F401
     ForwardResiduals, KernelGrads, SISOGrads, decode_loop, decode_scan, decode_step,
     siso_backward, siso_backward_kernel, siso_decode, siso_decode_folded, siso_forward,

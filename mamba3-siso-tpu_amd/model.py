@@ -135,6 +135,22 @@ def init_lm(cfg: LMConfig, key: Any = 0, dtype=torch.float32, device=None) -> LM
     return params if device is None else lm_to(params, device=device)
 
 
+def lm_template(cfg: LMConfig) -> LMParams:
+    """The tree `init_lm` builds, as storage-less ``meta`` tensors of the same shapes
+    (for loaders that only need the structure)."""
+    e = lambda *shape: torch.empty(*shape, device="meta")  # noqa: E731
+    c, d, di = cfg.siso, cfg.d_model, cfg.d_intermediate
+    blocks = []
+    for _ in range(cfg.n_layers):
+        siso = LY.SISOParams(e(d, c.d_in_proj), e(c.d_inner, d), e(c.nheads), e(c.d_state),
+                             e(c.d_state), e(c.nheads, c.d_state), e(c.nheads, c.d_state),
+                             e(c.nheads))
+        mlp = MLPParams(e(d, 2 * di), e(di, d)) if di else None
+        blocks.append(BlockParams(e(d), siso, e(d) if di else None, mlp))
+    return LMParams(e(cfg.vocab_size, d), blocks, e(d),
+                    None if cfg.tie_head else e(d, cfg.vocab_size))
+
+
 def lm_map(fn, params: LMParams) -> LMParams:
     """Apply ``fn`` to every tensor of the tree, keeping its structure (``None`` stays)."""
     f = lambda t: None if t is None else fn(t)  # noqa: E731

@@ -244,3 +244,33 @@ def test_train_step_update_matches_oracle_and_memorizes(m3, dev):
     last = float(loss)
     ratio = last / first
     assert np.isfinite(ratio) and ratio < 0.25, (first, last)
+
+
+def test_released_checkpoint_runs_and_matches_oracle(m3, dev, tmp_path):
+    """``tests.py:1058-1198`` on the device: a released-format checkpoint (config.json
+    with vocab padding, gated MLP, tied head) loaded from a local directory runs through
+    `lm_forward` to the oracle's logits, survives an npz save/load unchanged, and drives
+    `generate` with non-byte token ids."""
+    import json
+
+    from test_checkpoint_cpu import CFG_JSON, fake_released_sd
+
+    CV = m3.convert
+    cfg = CV.config_from_hf(CFG_JSON, chunk=64, policy_name="f32")
+    sd = fake_released_sd(cfg, seed=3)
+    (tmp_path / "config.json").write_text(json.dumps(CFG_JSON))
+    torch.save({k: v.clone() for k, v in sd.items()}, str(tmp_path / "pytorch_model.bin"))
+    params, cfg = CV.load_pretrained(str(tmp_path), device=dev, chunk=64, policy_name="f32")
+    toks = tokens_for(cfg, 2, 128, 21)
+    got = m3.model.lm_forward(params, toks.to(dev), cfg)
+    lay = dict(d_state=16, headdim=16, expand=2, rope_fraction=0.5, chunk=64, a_floor=2e-4,
+               norm_eps=1e-5)
+    ref = LO.lm_forward(LO.from_lm_params(params), toks, lay)
+    assert_maxrel(got, ref, 1e-4, "released checkpoint logits")
+    path = m3.checkpoint.save(str(tmp_path / "ckpt.npz"), params, cfg)
+    again, cfg2 = m3.checkpoint.load(path, device=dev)
+    assert cfg2 == cfg
+    assert torch.equal(m3.model.lm_forward(again, toks.to(dev), cfg2), got)
+    ids = [7, 11, 42]
+    out = m3.train.generate(params, cfg, 0, ids, n_tokens=4, rep_penalty=1.0)
+    assert out[:3] == ids and len(out) == 7 and all(0 <= t < cfg.vocab_size for t in out)
