@@ -86,7 +86,7 @@ def test_lm_loss_and_grads_match_oracle(m3, dev, policy, tie, di):
     tol = 1e-4 if policy == "f32" else 3e-2
     gtol = 1e-3 if policy == "f32" else 3e-2
     assert_maxrel(logits.detach(), ref_logits.detach(), tol, "logits")
-    assert abs(float(loss) - float(ref_loss)) <= tol * abs(float(ref_loss))
+    assert abs(float(loss.detach()) - float(ref_loss.detach())) <= tol * abs(float(ref_loss.detach()))
     mine = m3.model.lm_leaves(p_dev)
     theirs = [ref["embed"]]
     for b in ref["blocks"]:
