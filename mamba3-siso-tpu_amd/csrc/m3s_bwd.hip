@@ -930,16 +930,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   bf16* dwg = static_cast<bf16*>(p.part) + ((int64_t)p.B * p.H + bh) * L * N;   // dw rows of (b, h)
   const bool phi_vec = (Nr % 4) == 0;
   auto span = [&](int64_t st) { return (uint32_t)(((int64_t)(L - 1) * st + P) * 2); };
-  const auto rQ = make_rsrc(qg, (uint32_t)L * N * 2);
-  const auto rK = make_rsrc(kg, (uint32_t)L * N * 2);
-  const auto rV = make_rsrc(vg, span(p.v_st));
-  const auto rDy = make_rsrc(dyg, span(p.dy_st));
+  // q, k, v, dy, phi, states and every output go through SGPR-base global accesses
+  // (offsets stay below 2^32 bytes: the ABI's span checks); z and ybar keep buffer
+  // descriptors so that a zero-size descriptor turns their loads into zeros without z.
   const auto rZ = make_rsrc(zg, zg ? span(p.z_st) : 0u);
-  const auto rDz = make_rsrc(dzg, dzg ? span(p.dz_st) : 0u);
-  const auto rDv = make_rsrc(dvg, span(p.dv_st));
-  const auto rYb = make_rsrc(ybg, (uint32_t)L * P * 4);
-  const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
-  const auto rCs = make_rsrc(csg, (uint32_t)nc * N * P * 2);
+  // without z, ybar is not read: a zero-size descriptor makes its (unconditional) loads
+  // return zeros, as it does for z
+  const auto rYb = make_rsrc(zg ? ybg : nullptr, zg ? (uint32_t)L * P * 4 : 0u);
   // phi[t][j .. j+3], zero past Nr. With Nr % 4 == 0 (wave-uniform) every lane issues one
   // 16-byte load and lanes past Nr select zero: a per-lane choice of load width would make
   // the compiler drain the load queue at the join.
@@ -947,13 +944,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (phi_vec) {
       const bool ok = j + 4 <= Nr;
-      const f32x4 w = buf_load<f32x4>(rPhi, ok ? (uint32_t)(t * Nr + j) * 4 : 0u, sphi);
+      const f32x4 w = gld<f32x4>(phig, sphi + (ok ? (uint32_t)(t * Nr + j) * 4 : 0u));
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = ok ? w[i] : 0.f;
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        v[i] = (j + i < Nr) ? buf_load<float>(rPhi, (uint32_t)(t * Nr + j + i) * 4, sphi) : 0.f;
+        v[i] = (j + i < Nr) ? gld<float>(phig, sphi + (uint32_t)(t * Nr + j + i) * 4) : 0.f;
     }
     return v;
   };
@@ -966,10 +963,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   float* dqk_r = p.dqk + bh * L;
   float* dsc_r = p.dscale + bh * L;
   float* dadt_r = p.dadt + bh * L;
-  const auto rDphi = make_rsrc(p.dphi ? p.dphi + bh * (int64_t)L * Nr : nullptr,
-                               p.dphi ? (uint32_t)L * Nr * 4 : 0u);
-  const auto rDu = make_rsrc(dug, (uint32_t)L * N * 2);
-  const auto rDw = make_rsrc(dwg, (uint32_t)L * N * 2);
+  float* dphig = p.dphi ? p.dphi + bh * (int64_t)L * Nr : nullptr;
 
   // ---- adjoint G (registers, MFMA layout [p][n]); wave owns (pb_w, nb0 + NSTEP m) --
   constexpr int NSTEP = NW / PB;
@@ -1012,16 +1006,16 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
     for (int r = 0; r < F::QKR; ++r) {
       const int task = tid + r * NT;
-      if (task < F::QKT) {
+      if ((F::QKT % NT == 0 || task < F::QKT)) {
         const int tp = task / F::QKG, j0 = (task % F::QKG) * VEC;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int t = 2 * tp + e;
           const uint32_t o = (uint32_t)(t * N + j0) * 2;
-          rq[r][e][0] = buf_load<vec>(rQ, o, sqk);
-          rq[r][e][1] = buf_load<vec>(rQ, o + 2 * H2, sqk);
-          rk[r][e][0] = buf_load<vec>(rK, o, sqk);
-          rk[r][e][1] = buf_load<vec>(rK, o + 2 * H2, sqk);
+          rq[r][e][0] = gld<vec>(qg, sqk + o);
+          rq[r][e][1] = gld<vec>(qg, sqk + o + 2 * H2);
+          rk[r][e][0] = gld<vec>(kg, sqk + o);
+          rk[r][e][1] = gld<vec>(kg, sqk + o + 2 * H2);
 #pragma unroll
           for (int qd = 0; qd < VEC / 4; ++qd)
             rphi[r][e][qd] = phi_quad(t, j0 + 4 * qd, sphi);
@@ -1037,26 +1031,24 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
     for (int r = 0; r < F::VR; ++r) {
       const int task = tid + r * NT;
-      if (task < F::VT) {
+      if ((F::VT % NT == 0 || task < F::VT)) {
         const int tp = task / F::VG, p0 = (task % F::VG) * VEC;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int t = 2 * tp + e;
-          rv[r][e] = buf_load<vec>(rV, (uint32_t)(t * p.v_st + p0) * 2, (uint32_t)(c * C * p.v_st * 2));
-          rdy[r][e] = buf_load<vec>(rDy, (uint32_t)(t * p.dy_st + p0) * 2, (uint32_t)(c * C * p.dy_st * 2));
-          if (zg) {
-            rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
+          rv[r][e] = gld<vec>(vg, (uint32_t)(c * C * p.v_st * 2) + (uint32_t)(t * p.v_st + p0) * 2);
+          rdy[r][e] = gld<vec>(dyg, (uint32_t)(c * C * p.dy_st * 2) + (uint32_t)(t * p.dy_st + p0) * 2);
+          rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
 #pragma unroll
-            for (int i = 0; i < VEC; i += 4)
-              ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
-          }
+          for (int i = 0; i < VEC; i += 4)
+            ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
         }
       }
     }
 #pragma unroll
     for (int r = 0; r < F::SR; ++r) {
       const int f = tid + r * NT;
-      if (f < F::SV) rs[r] = buf_load<vec>(rCs, (uint32_t)f * VEC * 2, (uint32_t)c * N * P * 2);
+      if ((F::SV % NT == 0 || f < F::SV)) rs[r] = gld<vec>(csg, (uint32_t)c * N * P * 2 + (uint32_t)f * VEC * 2);
     }
     if (wave == 0) {
 #pragma unroll
@@ -1075,7 +1067,9 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   for (int c = nc - 1; c >= 0; --c) {
     const int t0 = c * C;
     // ============ phase L: raw -> LDS (q~, khat, g, v, S^T), dz, dqk, uw ==============
-    prefetch_qk(c);   // q, k, phi, scale of this chunk; the A-scan below covers part of the wait
+    // The v/dy/z/ybar/state registers (prefetched in the previous iteration's tail) are
+    // consumed first; only then are this chunk's q/k/phi/scale loaded, so the two sets
+    // are never live together.
     {
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
@@ -1110,9 +1104,61 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         sScl[tid] = rscl_s;
       }
 #pragma unroll
+      for (int r = 0; r < F::VR; ++r) {
+        const int task = tid + r * NT;
+        const bool valid = (F::VT % NT == 0 || task < F::VT);
+        const int tp = valid ? task / F::VG : 0, p0 = valid ? (task % F::VG) * VEC : 0;
+        float dqk[2] = {0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int t = 2 * tp + e;
+          __builtin_amdgcn_sched_barrier(0);
+          if (valid) {
+            vec og, odz;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              const float dy = (float)rdy[r][e][i];
+              float gv = dy;
+              if (zg) {
+                const float zf = (float)rz[r][e][i];
+                const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zf * kLog2e));
+                gv = dy * (zf * sg);
+                odz[i] = (bf16)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
+              }
+              dqk[e] += gv * (float)rv[r][e][i];
+              og[i] = (bf16)gv;
+            }
+            *reinterpret_cast<vec*>(sG + t * LDP + p0) = og;
+            *reinterpret_cast<vec*>(sV + t * LDP + p0) = rv[r][e];
+            if (dzg) gst<vec>(dzg, (uint32_t)(t0 * p.dz_st * 2) + (uint32_t)(t * p.dz_st + p0) * 2, odz);
+          }
+        }
+        dqk[0] = group_sum<F::VG>(dqk[0]);
+        dqk[1] = group_sum<F::VG>(dqk[1]);
+        if (valid && p0 == 0) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int t = 2 * tp + e;
+            sDqk[t] = dqk[e];
+            dqk_r[(uint32_t)(t0 + t)] = dqk[e];
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < F::SR; ++r) {
+        const int f = tid + r * NT;
+        if ((F::SV % NT == 0 || f < F::SV)) {
+          const int n = (f * VEC) / P, pp = (f * VEC) % P;
+          *reinterpret_cast<vec*>(sST + n * LDP + pp) = rs[r];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      prefetch_qk(c);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
       for (int r = 0; r < F::QKR; ++r) {
         const int task = tid + r * NT;
-        const bool valid = task < F::QKT;
+        const bool valid = (F::QKT % NT == 0 || task < F::QKT);
         const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
         float uw[2] = {0.f, 0.f};
 #pragma unroll
@@ -1156,55 +1202,6 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             uw_r[(uint32_t)(t0 + t)] = uw[e];
             sCoef[t] = gam_r[(uint32_t)(t0 + t)] * uw[e] + dsk;
           }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < F::VR; ++r) {
-        const int task = tid + r * NT;
-        const bool valid = task < F::VT;
-        const int tp = valid ? task / F::VG : 0, p0 = valid ? (task % F::VG) * VEC : 0;
-        float dqk[2] = {0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const int t = 2 * tp + e;
-          __builtin_amdgcn_sched_barrier(0);
-          if (valid) {
-            vec og, odz;
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-              const float dy = (float)rdy[r][e][i];
-              float gv = dy;
-              if (zg) {
-                const float zf = (float)rz[r][e][i];
-                const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zf * kLog2e));
-                gv = dy * (zf * sg);
-                odz[i] = (bf16)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
-              }
-              dqk[e] += gv * (float)rv[r][e][i];
-              og[i] = (bf16)gv;
-            }
-            *reinterpret_cast<vec*>(sG + t * LDP + p0) = og;
-            *reinterpret_cast<vec*>(sV + t * LDP + p0) = rv[r][e];
-            if (dzg) buf_store(odz, rDz, (uint32_t)(t * p.dz_st + p0) * 2, (uint32_t)(t0 * p.dz_st * 2));
-          }
-        }
-        dqk[0] = group_sum<F::VG>(dqk[0]);
-        dqk[1] = group_sum<F::VG>(dqk[1]);
-        if (valid && p0 == 0) {
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int t = 2 * tp + e;
-            sDqk[t] = dqk[e];
-            dqk_r[(uint32_t)(t0 + t)] = dqk[e];
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < F::SR; ++r) {
-        const int f = tid + r * NT;
-        if (f < F::SV) {
-          const int n = (f * VEC) / P, pp = (f * VEC) % P;
-          *reinterpret_cast<vec*>(sST + n * LDP + pp) = rs[r];
         }
       }
     }
@@ -1257,6 +1254,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
       };
       // dv[j][p] += sum_t W[t][j] g[t][p];  dkhat[j][n] += sum_t dM[t][j] q~[t][n]
       for (int tb = w & ~1; tb < CB; tb += 2) {
+        __builtin_amdgcn_sched_barrier(0);
         bf16x4 w0, m0, w1, m1;
         wdm(tb, w0, m0);
         wdm(tb + 1, w1, m1);
@@ -1288,6 +1286,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         return sub_from_f32<bf16>(vm);
       };
       for (int jb = 0; jb <= w; jb += 2) {
+        __builtin_amdgcn_sched_barrier(0);
         const bf16x4 d0 = dmt(jb), d1 = dmt(jb + 1);
         const int kb = jb * 16 + 4 * g4;
 #pragma unroll
@@ -1380,7 +1379,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           const int j = w * 16 + 4 * g4 + i;
           float d = dV[pb][i] + sCoef[j] * gv[i];
           if (p.dfv && t0 + j == L - 1) d += p.dfv[bh * P + pcol];
-          buf_store_bf16(d, rDv, (uint32_t)(j * p.dv_st + pcol) * 2, (uint32_t)(t0 * p.dv_st * 2));
+          gst<bf16>(dvg, (uint32_t)(t0 * p.dv_st * 2) + (uint32_t)(j * p.dv_st + pcol) * 2, (bf16)d);
         }
       }
     }
@@ -1413,7 +1412,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
       for (int r = 0; r < F::QKR; ++r) {
         const int task = tid + r * NT;
-        const bool valid = task < F::QKT;
+        const bool valid = (F::QKT % NT == 0 || task < F::QKT);
         const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
         // one row per iteration (not unrolled): halves the live temporaries
 #pragma unroll 1
@@ -1422,8 +1421,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           if (valid) {
             const int t = 2 * tp + e;
             const uint32_t o = (uint32_t)(t * N + j0) * 2;
-            const vec q0 = buf_load<vec>(rQ, o, sqk), q1 = buf_load<vec>(rQ, o + 2 * H2, sqk);
-            const vec k0 = buf_load<vec>(rK, o, sqk), k1 = buf_load<vec>(rK, o + 2 * H2, sqk);
+            const vec q0 = gld<vec>(qg, sqk + o), q1 = gld<vec>(qg, sqk + o + 2 * H2);
+            const vec k0 = gld<vec>(kg, sqk + o), k1 = gld<vec>(kg, sqk + o + 2 * H2);
             float ph[VEC];
 #pragma unroll
             for (int qd = 0; qd < VEC / 4; ++qd) {
@@ -1490,20 +1489,20 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
                 const int j = j0 + 4 * qd;
                 const uint32_t op = (uint32_t)(t * Nr + j) * 4;
                 if (phi_vec && j + 4 <= Nr) {
-                  buf_store(f32x4{dphv[4 * qd], dphv[4 * qd + 1], dphv[4 * qd + 2], dphv[4 * qd + 3]},
-                            rDphi, op, sphi);
+                  gst<f32x4>(dphig, sphi + op,
+                             f32x4{dphv[4 * qd], dphv[4 * qd + 1], dphv[4 * qd + 2], dphv[4 * qd + 3]});
                 } else {
 #pragma unroll
                   for (int i = 0; i < 4; ++i)
-                    if (j + i < Nr) buf_store_f32(dphv[4 * qd + i], rDphi, op + 4 * i, sphi);
+                    if (j + i < Nr) gst<float>(dphig, sphi + op + 4 * i, dphv[4 * qd + i]);
                 }
               }
             }
             // this head's du / dw row pieces; the head sum happens in headsum_kernel
-            buf_store(du0, rDu, o, sqk);
-            buf_store(du1, rDu, o + 2 * H2, sqk);
-            buf_store(dw0, rDw, o, sqk);
-            buf_store(dw1, rDw, o + 2 * H2, sqk);
+            gst<vec>(dug, sqk + o, du0);
+            gst<vec>(dug, sqk + o + 2 * H2, du1);
+            gst<vec>(dwg, sqk + o, dw0);
+            gst<vec>(dwg, sqk + o + 2 * H2, dw1);
           }
           dA = group_sum<F::QKG>(dA);
           dsc = group_sum<F::QKG>(dsc);

@@ -176,6 +176,19 @@ __device__ __forceinline__ void buf_store_bf16(float x, __amdgpu_buffer_rsrc_t r
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(short, (bf16)x), r, v, s, 0);
 }
 
+// Loads and stores at a wave-uniform base pointer plus a 32-bit unsigned byte offset: the
+// compiler emits the SGPR-base global form, two SGPRs per base where a buffer descriptor
+// holds four. Unlike a buffer access there is no range check: the caller keeps every
+// offset inside the tensor.
+template <typename T>
+__device__ __forceinline__ T gld(const void* base, uint32_t off) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + off);
+}
+template <typename T>
+__device__ __forceinline__ void gst(void* base, uint32_t off, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + off) = v;
+}
+
 // Asynchronous 16-byte-per-lane load straight into LDS (no VGPR round trip): lane l's
 // 16 bytes from rsrc + voffset + soffset land at lds_block + 16 l, so one instruction
 // fills a contiguous 1 KiB LDS block. lds_block must be wave-uniform. Completion is
