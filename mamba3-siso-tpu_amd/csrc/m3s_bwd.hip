@@ -1515,7 +1515,10 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     }
     __syncthreads();
 
-    if (c > 0) prefetch_rest(c - 1);   // the previous chunk's v, dy, z, ybar, state
+    // the previous chunk's v, dy, z, ybar, state. Issued on every iteration (chunk 0
+    // reloads itself on the last one): a conditional prefetch would keep the consumed
+    // registers alive through the whole loop body for the skipped path.
+    prefetch_rest(c > 0 ? c - 1 : 0);
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
       int ln = threadIdx.x;
