@@ -1401,6 +1401,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         }
       }
     }
+    prefetch_qk(c);   // phase R's raw q, k, phi rows: their latency overlaps the barrier
     __syncthreads();
 
     // ============ phase R: rotation pullback, per-row reductions, head sum ============
@@ -1413,22 +1414,27 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
       for (int r = 0; r < F::QKR; ++r) {
         const int task = tid + r * NT;
         const bool valid = (F::QKT % NT == 0 || task < F::QKT);
-        const int tp = valid ? task / F::QKG : 0, j0 = valid ? (task % F::QKG) * VEC : 0;
-        // one row per iteration (not unrolled): halves the live temporaries
-#pragma unroll 1
+        // j0 depends on the lane alone (NT % QKG == 0), also for idle lanes: the bias
+        // reduction below pairs lanes that share it
+        const int tp = valid ? task / F::QKG : 0, j0 = (task % F::QKG) * VEC;
+        // bias partials of this lane's two rows: [element][du lo, du hi, dw lo, dw hi]
+        float bacc[VEC * 4];
+#pragma unroll
+        for (int k = 0; k < VEC * 4; ++k) bacc[k] = 0.f;
+#pragma unroll
         for (int e = 0; e < 2; ++e) {
+          __builtin_amdgcn_sched_barrier(0);   // rows one after the other: fewer live values
           float dA = 0.f, dsc = 0.f;
           if (valid) {
             const int t = 2 * tp + e;
             const uint32_t o = (uint32_t)(t * N + j0) * 2;
-            const vec q0 = gld<vec>(qg, sqk + o), q1 = gld<vec>(qg, sqk + o + 2 * H2);
-            const vec k0 = gld<vec>(kg, sqk + o), k1 = gld<vec>(kg, sqk + o + 2 * H2);
+            const vec q0 = rq[r][e][0], q1 = rq[r][e][1];
+            const vec k0 = rk[r][e][0], k1 = rk[r][e][1];
             float ph[VEC];
 #pragma unroll
             for (int qd = 0; qd < VEC / 4; ++qd) {
-              const f32x4 v4 = phi_quad(t, j0 + 4 * qd, sphi);
 #pragma unroll
-              for (int i = 0; i < 4; ++i) ph[4 * qd + i] = v4[i];
+              for (int i = 0; i < 4; ++i) ph[4 * qd + i] = rphi[r][e][qd][i];
             }
             const float sc = sScl[t];
             const float cd = sDqk[t] * sGam[t];
@@ -1468,20 +1474,10 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               du1[i] = duhi;
               dw0[i] = dwlo;
               dw1[i] = dwhi;
-              // bias partials (f32): summed over the row pairs of the wave that share
-              // the column group, then one LDS atomic per element
-              float bqv[4] = {dulo, duhi, dwlo, dwhi};
-#pragma unroll
-              for (int m = F::QKG; m < 64; m <<= 1) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u) bqv[u] += __shfl_xor(bqv[u], m, 64);
-              }
-              if (lane < F::QKG) {
-                atomicAdd(sDqb + j, bqv[0]);
-                atomicAdd(sDqb + H2 + j, bqv[1]);
-                atomicAdd(sDkb + j, bqv[2]);
-                atomicAdd(sDkb + H2 + j, bqv[3]);
-              }
+              bacc[4 * i + 0] += dulo;
+              bacc[4 * i + 1] += duhi;
+              bacc[4 * i + 2] += dwlo;
+              bacc[4 * i + 3] += dwhi;
             }
             if (p.dphi) {
 #pragma unroll
@@ -1510,6 +1506,32 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             sDA[2 * tp + e] = dA;
             dsc_r[(uint32_t)(t0 + 2 * tp + e)] = dsc;
           }
+        }
+        // The lanes that share j0 differ in lane bits log2(QKG)..5. A transposing
+        // butterfly over those bits halves the entries a lane keeps each round (it sends
+        // the half its partner keeps), so each lane ends with the group sums of
+        // BFIN consecutive entries starting at `base`: one LDS atomic each, no idle lanes.
+        constexpr int BFIN = VEC * 4 * F::QKG / 64;
+        constexpr int ROUNDS = (F::QKG == 4) ? 4 : (F::QKG == 8) ? 3 : (F::QKG == 16) ? 2 : 1;
+        static_assert((VEC * 4) >> ROUNDS == BFIN && BFIN >= 1, "bias butterfly shape");
+        int base = 0;
+#pragma unroll
+        for (int rd = 0; rd < ROUNDS; ++rd) {
+          const int m = 32 >> rd, half = (VEC * 2) >> rd;
+          const bool up = (lane & m) != 0;
+#pragma unroll
+          for (int k = 0; k < half; ++k) {
+            const float lo = bacc[k], hi = bacc[half + k];   // values, not addresses, selected
+            const float send = up ? lo : hi;
+            const float keep = up ? hi : lo;
+            bacc[k] = keep + __shfl_xor(send, m, 64);
+          }
+          base += up ? half : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < BFIN; ++k) {
+          const int idx = base + k, u = idx & 3;
+          atomicAdd((u < 2 ? sDqb : sDkb) + (u & 1) * H2 + j0 + (idx >> 2), bacc[k]);
         }
       }
     }
