@@ -937,16 +937,16 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   // without z, ybar is not read: a zero-size descriptor makes its (unconditional) loads
   // return zeros, as it does for z
   const auto rYb = make_rsrc(zg ? ybg : nullptr, zg ? (uint32_t)L * P * 4 : 0u);
-  // phi[t][j .. j+3], zero past Nr. With Nr % 4 == 0 (wave-uniform) every lane issues one
-  // 16-byte load and lanes past Nr select zero: a per-lane choice of load width would make
-  // the compiler drain the load queue at the join.
+  // phi[t][j .. j+3] for j < Nr. With Nr % 4 == 0 (wave-uniform) every lane issues one
+  // 16-byte load: a per-lane choice of load width would make the compiler drain the load
+  // queue at the join.
   auto phi_quad = [&](int t, int j, uint32_t sphi) {
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (phi_vec) {
+      // quads past Nr load the chunk's first quad instead and are never read (every use
+      // is under j < Nr): no select here, so the load need not complete in this block
       const bool ok = j + 4 <= Nr;
-      const f32x4 w = gld<f32x4>(phig, sphi + (ok ? (uint32_t)(t * Nr + j) * 4 : 0u));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = ok ? w[i] : 0.f;
+      v = gld<f32x4>(phig, sphi + (ok ? (uint32_t)(t * Nr + j) * 4 : 0u));
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -1061,15 +1061,15 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     }
   };
 
+  prefetch_qk(nc - 1);
   prefetch_rest(nc - 1);
   __syncthreads();
 
   for (int c = nc - 1; c >= 0; --c) {
     const int t0 = c * C;
     // ============ phase L: raw -> LDS (q~, khat, g, v, S^T), dz, dqk, uw ==============
-    // The v/dy/z/ybar/state registers (prefetched in the previous iteration's tail) are
-    // consumed first; only then are this chunk's q/k/phi/scale loaded, so the two sets
-    // are never live together.
+    // Both register prefetches of this chunk (q/k/phi/scale and v/dy/z/ybar/state) were
+    // issued in the previous iteration's tail; the second set is consumed first.
     {
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
@@ -1152,8 +1152,6 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           *reinterpret_cast<vec*>(sST + n * LDP + pp) = rs[r];
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch_qk(c);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int r = 0; r < F::QKR; ++r) {
@@ -1540,6 +1538,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     // the previous chunk's v, dy, z, ybar, state. Issued on every iteration (chunk 0
     // reloads itself on the last one): a conditional prefetch would keep the consumed
     // registers alive through the whole loop body for the skipped path.
+    prefetch_qk(c > 0 ? c - 1 : 0);
     prefetch_rest(c > 0 ? c - 1 : 0);
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
