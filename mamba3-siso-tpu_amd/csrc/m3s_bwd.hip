@@ -1173,12 +1173,11 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               const float wlo = (float)rk[r][e][0][i] + sKb[j];
               const float whi = (float)rk[r][e][1][i] + sKb[H2 + j];
               uw[e] += ulo * wlo + uhi * whi;
-              float sn = 0.f, cs = 1.f;
-              if (j < Nr) {  // phi in [0, 2 pi): hardware sin / cos, argument in turns
-                const float turns = rphi[r][e][i / 4][i % 4] * 0.15915494309189535f;
-                sn = __builtin_amdgcn_sinf(turns);
-                cs = __builtin_amdgcn_cosf(turns);
-              }
+              // phi in [0, 2 pi): hardware sin / cos, argument in turns; the identity past
+              // Nr by select (no divergent branch: half of every wave's lanes rotate)
+              const float turns = rphi[r][e][i / 4][i % 4] * 0.15915494309189535f;
+              const float sn = (j < Nr) ? __builtin_amdgcn_sinf(turns) : 0.f;
+              const float cs = (j < Nr) ? __builtin_amdgcn_cosf(turns) : 1.f;
               const float sc = rscale[r][e];
               oq0[i] = (bf16)(ulo * cs - uhi * sn);
               oq1[i] = (bf16)(uhi * cs + ulo * sn);
@@ -1437,7 +1436,15 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             const float sc = sScl[t];
             const float cd = sDqk[t] * sGam[t];
             vec du0, du1, dw0, dw1;
-            float dphv[VEC];
+            float dphv[VEC], kfl[VEC], kfh[VEC];
+            f32x4 dql[VEC / 4], dqh[VEC / 4], dkl[VEC / 4], dkh[VEC / 4];   // 16-byte LDS reads
+#pragma unroll
+            for (int h4 = 0; h4 < VEC / 4; ++h4) {
+              dql[h4] = *reinterpret_cast<const f32x4*>(sDQ + t * LDF + j0 + 4 * h4);
+              dqh[h4] = *reinterpret_cast<const f32x4*>(sDQ + t * LDF + H2 + j0 + 4 * h4);
+              dkl[h4] = *reinterpret_cast<const f32x4*>(sDK + t * LDF + j0 + 4 * h4);
+              dkh[h4] = *reinterpret_cast<const f32x4*>(sDK + t * LDF + H2 + j0 + 4 * h4);
+            }
 #pragma unroll
             for (int i = 0; i < VEC; ++i) {
               const int j = j0 + i;
@@ -1445,16 +1452,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               const float uhi = (float)q1[i] + sQb[H2 + j];
               const float wlo = (float)k0[i] + sKb[j];
               const float whi = (float)k1[i] + sKb[H2 + j];
-              float sn = 0.f, cs = 1.f;
-              if (j < Nr) {
-                const float turns = ph[i] * 0.15915494309189535f;
-                sn = __builtin_amdgcn_sinf(turns);
-                cs = __builtin_amdgcn_cosf(turns);
-              }
+              const float turns = ph[i] * 0.15915494309189535f;
+              const float sn = (j < Nr) ? __builtin_amdgcn_sinf(turns) : 0.f;
+              const float cs = (j < Nr) ? __builtin_amdgcn_cosf(turns) : 1.f;
               const float qlo = ulo * cs - uhi * sn, qhi = uhi * cs + ulo * sn;
               const float klo = wlo * cs - whi * sn, khi = whi * cs + wlo * sn;
-              const float dqlo = sDQ[t * LDF + j], dqhi = sDQ[t * LDF + H2 + j];
-              const float dklo = sDK[t * LDF + j], dkhi = sDK[t * LDF + H2 + j];
+              const float dqlo = dql[i / 4][i % 4], dqhi = dqh[i / 4][i % 4];
+              const float dklo = dkl[i / 4][i % 4], dkhi = dkh[i / 4][i % 4];
               dA += qlo * dqlo + qhi * dqhi - (klo * sc) * dklo - (khi * sc) * dkhi;
               dsc += dklo * klo + dkhi * khi;
               const float dtlo = dklo * sc, dthi = dkhi * sc;   // d k~
@@ -1464,10 +1468,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               const float dwlo = dtlo * cs + dthi * sn + cd * ulo;
               const float dwhi = dthi * cs - dtlo * sn + cd * uhi;
               dphv[i] = (dqhi * qlo - dqlo * qhi) + (dthi * klo - dtlo * khi);
-              if (c == nc - 1 && t == C - 1) {
-                p.kfin[bh * N + j] = klo;
-                p.kfin[bh * N + H2 + j] = khi;
-              }
+              kfl[i] = klo;
+              kfh[i] = khi;
               du0[i] = dulo;
               du1[i] = duhi;
               dw0[i] = dwlo;
@@ -1476,6 +1478,15 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               bacc[4 * i + 1] += duhi;
               bacc[4 * i + 2] += dwlo;
               bacc[4 * i + 3] += dwhi;
+            }
+            if (c == nc - 1 && t == C - 1) {   // the sequence's last k~ row (f32)
+#pragma unroll
+              for (int h4 = 0; h4 < VEC / 4; ++h4) {
+                gst<f32x4>(p.kfin + bh * N, (uint32_t)(j0 + 4 * h4) * 4,
+                           f32x4{kfl[4 * h4], kfl[4 * h4 + 1], kfl[4 * h4 + 2], kfl[4 * h4 + 3]});
+                gst<f32x4>(p.kfin + bh * N, (uint32_t)(H2 + j0 + 4 * h4) * 4,
+                           f32x4{kfh[4 * h4], kfh[4 * h4 + 1], kfh[4 * h4 + 2], kfh[4 * h4 + 3]});
+              }
             }
             if (p.dphi) {
 #pragma unroll
