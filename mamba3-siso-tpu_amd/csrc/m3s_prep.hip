@@ -56,16 +56,19 @@ __device__ __forceinline__ float wrap_(float x) {
   return r >= kTwoPiF ? r - kTwoPiF : r;
 }
 
-// Column quad [j0, j0 + 4) of a row of Nr f32 values, zero past Nr.
+// Column quad [j0, j0 + 4) of a row of Nr f32 values (j0 a multiple of 4 below Nr), zero
+// past Nr. With Nr % 4 == 0 every quad is whole: the test is wave-uniform, so the loads
+// of an unrolled run are not split by a per-lane choice of width (which would make the
+// compiler wait for each one at the join).
 __device__ __forceinline__ f32x4 ld_quad(const float* row, int j0, int Nr) {
-  if (j0 + 4 <= Nr && (Nr & 3) == 0) return *reinterpret_cast<const f32x4*>(row + j0);
+  if ((Nr & 3) == 0) return *reinterpret_cast<const f32x4*>(row + j0);
   f32x4 r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) r[i] = (j0 + i < Nr) ? row[j0 + i] : 0.f;
   return r;
 }
 __device__ __forceinline__ void st_quad(float* row, int j0, int Nr, f32x4 v) {
-  if (j0 + 4 <= Nr && (Nr & 3) == 0) {
+  if ((Nr & 3) == 0) {
     *reinterpret_cast<f32x4*>(row + j0) = v;
     return;
   }
@@ -365,38 +368,51 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
       f32x4 run = {0.f, 0.f, 0.f, 0.f};
       if (valid) run = ld_quad(p.carry + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
       const float* src = p.dphi ? p.dphi + (bh * L + t0) * Nr : nullptr;
-      for (int t = nt - 1; t >= 0; --t) {
-        if (valid && src) {
-          const f32x4 d = ld_quad(src + t * Nr, j0, Nr);
+      // rows in runs of kRun, all of a run's loads issued before its first use (idle lanes
+      // load head 0's row and drop it: the loads stay unconditional per lane)
+      constexpr int kRun = 8;
+      for (int tr = nt - 1; tr >= 0; tr -= kRun) {
+        f32x4 dq[kRun];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) run[i] += d[i];
+        for (int u = 0; u < kRun; ++u) {
+          dq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (src && tr - u >= 0) dq[u] = ld_quad(src + (tr - u) * Nr, j0, Nr);
         }
-        const float dt = valid ? sDt[t * H + h] : 0.f;
-        float ph = 0.f;
-        f32x4 ag;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float tq = (valid && j0 + i < Nr) ? sT[t * Nr + j0 + i] : 0.f;
-          ph += run[i] * (tq * kPiF);
-          ag[i] = valid ? run[i] * dt : 0.f;
-        }
-        if (pow2) {
-          for (int off = 1; off < J4; off <<= 1) ph += __shfl_xor(ph, off, 64);
-          if (valid && jg == 0) sPhi[t * H + h] = ph;
-          for (int off = J4; off < 64; off <<= 1) {
+        for (int u = 0; u < kRun; ++u) {
+          const int t = tr - u;
+          if (t < 0) break;
+          if (valid) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ag[i] += __shfl_xor(ag[i], off, 64);
+            for (int i = 0; i < 4; ++i) run[i] += dq[u][i];
           }
-          if (lane < J4) {   // lanes jg = lane of head group 0 hold this wave's sum
+          const float dt = valid ? sDt[t * H + h] : 0.f;
+          float ph = 0.f;
+          f32x4 ag;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float tq = (valid && j0 + i < Nr) ? sT[t * Nr + j0 + i] : 0.f;
+            ph += run[i] * (tq * kPiF);
+            ag[i] = valid ? run[i] * dt : 0.f;
+          }
+          if (pow2) {
+            for (int off = 1; off < J4; off <<= 1) ph += __shfl_xor(ph, off, 64);
+            if (valid && jg == 0) sPhi[t * H + h] = ph;
+            for (int off = J4; off < 64; off <<= 1) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) ag[i] += __shfl_xor(ag[i], off, 64);
+            }
+            if (lane < J4) {   // lanes jg = lane of head group 0 hold this wave's sum
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
+            }
+          } else if (valid) {
+            atomicAdd(sPhi + t * H + h, ph);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
           }
-        } else if (valid) {
-          atomicAdd(sPhi + t * H + h, ph);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
         }
       }
     }
