@@ -763,7 +763,35 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   f32x4 out[PB];                            // out^T tiles of this wave's strip
 
   // ---- phase L: chunk c's raw registers -> q~ (registers), khat (LDS), scalars -----
-  auto stage = [&](int c) {
+  // Chunk c's q~ fragments (qf), k-hat rows and row coefficients are computed into
+  // registers at the end of chunk c-1's product phase (stage_regs), while other waves
+  // still run their products, and written to LDS after the barrier (stage_write).
+  bf16x8 kst[2 * F::LOB];        // this lane's k-hat row pieces of the next chunk
+  float coefv = 0.f;             // D + gamma_t (u_t . w_t) of this lane's row
+  float sAv[F::E], sEv[F::E], sFv[F::E];   // wave 0: A_t, 2^{A_t}, 2^{A_last - A_t}
+  auto stage_write = [&]() {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63;
+    const int trow = 16 * wave + (lane & 15);
+    const int g8 = 8 * (lane >> 4);
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < F::E; ++e) {
+        const int tt = lane * F::E + e;
+        sA[tt] = sAv[e];
+        sExpA[tt] = sEv[e];
+        sFac[tt] = sFv[e];
+      }
+    }
+#pragma unroll
+    for (int lb = 0; lb < F::LOB; ++lb) {
+      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * lb + g8) = kst[lb];
+      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * (lb + F::LOB) + g8) = kst[lb + F::LOB];
+    }
+    if ((lane >> 4) == 0) sCoef[trow] = coefv;
+  };
+  auto stage_regs = [&]() {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
@@ -785,14 +813,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       const float a_last = __shfl(incl, 63, 64);
 #pragma unroll
       for (int e = 0; e < F::E; ++e) {
-        const int tt = lane * F::E + e;
         const float A = excl + a[e];
-        sA[tt] = A;
-        sExpA[tt] = exp2f(A);
-        sFac[tt] = exp2f(a_last - A);
+        sAv[e] = A;
+        sEv[e] = exp2f(A);
+        sFv[e] = exp2f(a_last - A);
       }
     }
-    const int trow = 16 * wave + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     float uw = 0.f;
     // u = q + qb, w = k + kb for one pair (n, n + N/2) of this lane's block lb, s < 8
@@ -846,12 +872,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         kl8[s] = (bf16)(kl * rscale);
         kh8[s] = (bf16)(kh * rscale);
       }
-      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * lb + g8) = kl8;
-      *reinterpret_cast<bf16x8*>(sK + trow * LDK + 32 * hb + g8) = kh8;
+      kst[lb] = kl8;
+      kst[hb] = kh8;
     }
     uw += __shfl_xor(uw, 16, 64);
     uw += __shfl_xor(uw, 32, 64);
-    if ((lane >> 4) == 0) sCoef[trow] = rgam * uw + dsk;
+    coefv = rgam * uw + dsk;
   };
 
   // ---- phase G: scores, intra + inter + diagonal output, state update -------------
@@ -1013,8 +1039,10 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   prefetch_rest(0);
   vm_wait_all();
   __syncthreads();  // sQb / sKb, v tile of chunk 0
+  stage_regs();     // chunk 0
+  if (nc > 1) prefetch_qk(1);
   for (int c = 0; c <= nc; ++c) {
-    // ---------------- phase A: stage out(c-1) and S(c); build chunk c -------------
+    // ---------------- phase A: stage out(c-1), S(c) and chunk c's k-hat / scalars ----
     if (c > 0) {
       const int tcol = wave * 16 + (lane & 15);
 #pragma unroll
@@ -1022,21 +1050,26 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         *reinterpret_cast<f32x4*>(sOut + tcol * LDO + pb * 16 + 4 * (lane >> 4)) = out[pb];
     }
     publish_state(c);
-    if (c < nc) stage(c);
+    if (c < nc) stage_write();
     if (c + 1 < nc) {
-      // chunk c+1's q / k rows: issued before the barrier, where the vector-memory
-      // pipe is idle (after it, the light waves' epilogue stores compete for it)
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch_qk(c + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      vm_wait_keep<2 * F::NBK>();   // all but those loads: v of c, z of c-1 have landed
+      vm_wait_keep<2 * F::NBK>();   // all but chunk c+1's q / k rows: v of c, z of c-1
     } else {
       vm_wait_all();
     }
     __syncthreads();
-    // ---------------- phase B: epilogue of c-1 alongside the products of c --------
+    // ---------------- phase B: epilogue of c-1, products of c, then chunk c+1's rotation
+    // into registers (a wave whose products end early rotates while others still run
+    // theirs: the VALU work overlaps the partner wave's MFMA work on the same SIMD)
     if (c > 0 && light) epilogue(c - 1);
     if (c < nc) products(c);
+    if (c + 1 < nc) {
+      stage_regs();
+      if (c + 2 < nc) {
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch_qk(c + 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     __syncthreads();
   }
 
