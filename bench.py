@@ -130,9 +130,11 @@ def main():
         ka = scan_inputs(m3, params16, cfg, u, torch)
         if args.leg in ("all", "scan"):
             scan = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
-            for _ in range(args.warmup):
+            # a kernel-boundary micro-measurement: enough launches that the clocks have
+            # settled (a few ms of warmup), whatever --steps says for the headline
+            for _ in range(max(args.warmup, 10)):
                 scan()
-            scan_ms = gpu_time_ms(scan, args.steps, torch)
+            scan_ms = gpu_time_ms(scan, max(args.steps, 50), torch)
             scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
             scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
             line.update(scan_kernel_ms=round(scan_ms, 4),
@@ -154,9 +156,9 @@ def main():
                     dyk, res.ybar, ka["z"], ka["q"], ka["k"], ka["v"], ka["adt"], ka["gamma"],
                     ka["scale"], ka["phi"], ka["q_bias"], ka["k_bias"], res.chunk_states,
                     d_skip=ka["d_skip"], chunk=128)
-                for _ in range(max(1, args.warmup)):
+                for _ in range(max(3, args.warmup)):
                     bw()
-                bwd_ms = gpu_time_ms(bw, max(3, args.steps // 2), torch)
+                bwd_ms = gpu_time_ms(bw, max(10, args.steps // 2), torch)
             bwd_flops = B * H * L * (2 * cfg.chunk * (3 * N + 2 * P) + 8 * P * N)
             line.update(bwd_kernel_ms=round(bwd_ms, 4),
                         bwd_kernel_tflops=round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2))
