@@ -1339,7 +1339,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         }
         red += sExpA[C - 1] * gs;
       }
-      red = group_sum<64>(red);
+      red = wave_total(red);
       if (lane == 0) atomicAdd(sRed, red);
       // G <- 2^{A_last} G + sum_t (2^{A_t} g[t][p]) q~[t][n]   (K = time, both by columns)
       const float eAl = sExpA[C - 1];

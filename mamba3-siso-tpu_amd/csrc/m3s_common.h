@@ -209,11 +209,42 @@ __device__ __forceinline__ void vm_wait_keep() {
 }
 
 // ---- wave reductions ------------------------------------------------------------
+// DPP lane moves inside a 16-lane row (no LDS round trip, unlike a lane shuffle):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror (lane i of an 8-lane half
+// reads lane 7 - i), row_mirror (lane i of a row reads lane 15 - i).
+constexpr int kDppQuadSwap1 = 0xB1, kDppQuadSwap2 = 0x4E, kDppHalfMirror = 0x141,
+              kDppRowMirror = 0x140;
+template <int ctrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64), in every lane of the
+// group: after the quad swaps each quad holds its sum, the half mirror pairs the two
+// quads of an 8-lane half, the row mirror the two halves of a row; across rows, lane
+// shuffles.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < W; m <<= 1) v += __shfl_xor(v, m, 64);
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width");
+  if constexpr (W >= 2) v += dpp_mov<kDppQuadSwap1>(v);
+  if constexpr (W >= 4) v += dpp_mov<kDppQuadSwap2>(v);
+  if constexpr (W >= 8) v += dpp_mov<kDppHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_mov<kDppRowMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
   return v;
+}
+
+// Sum over the whole wave as a wave-uniform value: row sums by DPP, then the four rows'
+// sums read from lanes 0, 16, 32 and 48.
+__device__ __forceinline__ float wave_total(float v) {
+  v = group_sum<16>(v);
+  const int i = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48)));
 }
 
 // ---- elementwise maths ----------------------------------------------------------
