@@ -866,6 +866,7 @@ struct Bwd2Cfg {
   static_assert(T4 % NW == 0 && NW % PB == 0, "adjoint tiles split evenly, one pb per wave");
   static_assert(QKG <= 64 && VG <= 64, "row groups must fit a wave");
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
+  static_assert(C <= N, "the dv rows are staged in the adjoint's N-row slot");
 };
 
 template <int C, int N, int P>
@@ -1206,6 +1207,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 
     // ============ products: score tiles consumed as they are built ===================
     f32x4 dQ[NB], dKh[NB], dV[PB];
+    bf16x4 dvo[PB];   // this wave's dv rows (MFMA layout), stored through LDS after the barrier
     {
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
@@ -1366,18 +1368,18 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           mma32(Gacc[m], a0, a1, ld_tr4(sQ, LDQ, kb, nb * 16, lane), ld_tr4(sQ, LDQ, kb + 16, nb * 16, lane));
         }
       }
-      // dv epilogue: + (D + gamma u.w) g, + dfinal_v on the sequence's last row; store
+      // dv epilogue: + (D + gamma u.w) g, + dfinal_v on the sequence's last row
+      const bool last_chunk = p.dfv && c == nc - 1;
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         const int pcol = pb * 16 + l16;
         const f32x4 gv = sub_to_f32<bf16>(ld_tr4(sG, LDP, w * 16 + 4 * g4, pb * 16, lane));
+        const f32x4 cf = *reinterpret_cast<const f32x4*>(sCoef + w * 16 + 4 * g4);
+        f32x4 d;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = w * 16 + 4 * g4 + i;
-          float d = dV[pb][i] + sCoef[j] * gv[i];
-          if (p.dfv && t0 + j == L - 1) d += p.dfv[bh * P + pcol];
-          gst<bf16>(dvg, (uint32_t)(t0 * p.dv_st * 2) + (uint32_t)(j * p.dv_st + pcol) * 2, (bf16)d);
-        }
+        for (int i = 0; i < 4; ++i) d[i] = dV[pb][i] + cf[i] * gv[i];
+        if (last_chunk && w * 16 + 4 * g4 + 3 == C - 1) d[3] += p.dfv[bh * P + pcol];
+        dvo[pb] = sub_from_f32<bf16>(d);
       }
     }
     __syncthreads();
@@ -1397,9 +1399,32 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           sDK[r * LDF + nb * 16 + l16] = dKh[nb][i];
         }
       }
+      // dv rows into the adjoint's LDS slot (free until the tail republishes G), [j][p]
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sGaT[(w * 16 + 4 * g4 + i) * LDP + pb * 16 + l16] = dvo[pb][i];
+      }
     }
     prefetch_qk(c);   // phase R's raw q, k, phi rows: their latency overlaps the barrier
     __syncthreads();
+
+    // dv: whole 16-byte row pieces from LDS, coalesced stores
+    {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int tid = ln;
+      constexpr int VGP = P / VEC, DVR = (C * VGP + NT - 1) / NT;
+#pragma unroll
+      for (int r = 0; r < DVR; ++r) {
+        const int f = tid + r * NT;
+        if ((C * VGP) % NT == 0 || f < C * VGP) {
+          const int j = f / VGP, p0 = (f % VGP) * VEC;
+          gst<vec>(dvg, (uint32_t)(t0 * p.dv_st * 2) + (uint32_t)(j * p.dv_st + p0) * 2,
+                   *reinterpret_cast<const vec*>(sGaT + j * LDP + p0));
+        }
+      }
+    }
 
     // ============ phase R: rotation pullback, per-row reductions, head sum ============
     {
