@@ -573,13 +573,16 @@ struct Fwd2Cfg {
   static constexpr int SZ_V = C * P * 2;          // one v or z tile
   static constexpr int SZ_S = P * LDK * 2;
   static constexpr int SZ_O = C * LDO * 4;
-  static constexpr int SZ_SC = (4 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb
+  static constexpr int SZ_SC = (5 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb, sDk
   static constexpr int LDS_BYTES = SZ_K + 4 * SZ_V + SZ_S + SZ_O + SZ_SC;
   static_assert(N % 64 == 0 && P == 64 && C % 64 == 0, "tile shape");
   static_assert(NW % PB == 0 && (PB * NB) % NW == 0, "state tiles split evenly over waves");
   static_assert(VBLK % NWL == 0, "v / z blocks split evenly over the light waves");
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
 };
+
+// Compile-time case selector for generic lambdas (`decltype(tag)::value`).
+template <int V> struct IntTag { static constexpr int value = V; };
 
 // Element offset of (row r, column col) in a swizzled 64-column bf16 tile.
 __device__ __forceinline__ int vz_off(int r, int col) {
@@ -589,6 +592,18 @@ __device__ __forceinline__ int vz_off(int r, int col) {
 __device__ __forceinline__ bf16x4 ld_tr4_vz(const bf16* buf, int kb, int m0, int l) {
   const int j = l & 15;
   const bf16* ptr = buf + vz_off(kb + (j >> 2), m0 + 4 * (j & 3));
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(ptr));
+  return __builtin_bit_cast(bf16x4, r);
+}
+// The swizzle of a row depends only on row & 7: a lane's ld_tr4_vz offset at rows
+// kb + 16 i (kb + 8 i) is 1024 i (512 i) elements past its offset at row kb, so
+// loops over row bands compute the offset once (vz_tr_off) and step a pointer.
+__device__ __forceinline__ int vz_tr_off(int kb, int m0, int l) {
+  const int j = l & 15;
+  return vz_off(kb + (j >> 2), m0 + 4 * (j & 3));
+}
+__device__ __forceinline__ bf16x4 ld_tr4_at(const bf16* ptr) {
   const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) s16x4*)(ptr));
   return __builtin_bit_cast(bf16x4, r);
@@ -613,10 +628,16 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
   float* sQb = sCoef + C;
   float* sKb = sQb + N;
+  float* sDk = sKb + N;    // 2^{A_{16 s + 15} - A_j}, s = j's strip: a key row's decay to its strip end
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool light = wave < F::NWL;
+  // query strip of this wave: the light waves take the short end of the causal triangle
+  // (strips 0 .. NW/2-1), the others the long end in reverse, so that waves w and
+  // w + NW/2 -- which share a SIMD -- hold strips w and NW-1-w: every SIMD gets the same
+  // number of score tiles (NW + 1) and one wave's share of the epilogue
+  const int strip = light ? wave : 3 * F::NWL - 1 - wave;
   const int wid = xcd_remap(blockIdx.x, gridDim.x);
   const int b = wid / p.H, h = wid % p.H;
   const int64_t bh = (int64_t)b * p.H + h;
@@ -698,7 +719,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   };
 
   // ---- raw q, k, phi, scale, gamma of one chunk, prefetched into registers ---------
-  // Strip layout: lane row 16 wave + (lane & 15), K group 8 (lane >> 4).
+  // Strip layout: lane row 16 strip + (lane & 15), K group 8 (lane >> 4).
   bf16x8 rq[F::NBK], rk[F::NBK];
   f32x4 rphi[F::LOB][2];
   float rscale, rgam;
@@ -709,7 +730,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
-    const int trow = 16 * wave + (lane & 15);   // row within the chunk
+    const int trow = 16 * strip + (lane & 15);   // row within the chunk
     const int g8 = 8 * (lane >> 4);
     const uint32_t oqk = (uint32_t)(trow * N + g8) * 2;
 #pragma unroll
@@ -724,7 +745,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
-    const int trow = 16 * wave + (lane & 15);
+    const int trow = 16 * strip + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     const uint32_t sphi = (uint32_t)c * C * Nr * 4;
 #pragma unroll
@@ -768,12 +789,13 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // still run their products, and written to LDS after the barrier (stage_write).
   bf16x8 kst[2 * F::LOB];        // this lane's k-hat row pieces of the next chunk
   float coefv = 0.f;             // D + gamma_t (u_t . w_t) of this lane's row
-  float sAv[F::E], sEv[F::E], sFv[F::E];   // wave 0: A_t, 2^{A_t}, 2^{A_last - A_t}
+  float sAv[F::E], sEv[F::E], sFv[F::E], sDv[F::E];   // wave 0: A_t, 2^{A_t}, 2^{A_last - A_t},
+                                                     // 2^{A_strip_end - A_t}
   auto stage_write = [&]() {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
-    const int trow = 16 * wave + (lane & 15);
+    const int trow = 16 * strip + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     if (wave == 0) {
 #pragma unroll
@@ -782,6 +804,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         sA[tt] = sAv[e];
         sExpA[tt] = sEv[e];
         sFac[tt] = sFv[e];
+        sDk[tt] = sDv[e];
       }
     }
 #pragma unroll
@@ -811,12 +834,15 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       }
       const float excl = incl - run;
       const float a_last = __shfl(incl, 63, 64);
+      // A at the last row of this lane's 16-row strip (rows lane E .. lane E + E - 1)
+      const float a_strip = __shfl(incl, lane | (16 / F::E - 1), 64);
 #pragma unroll
       for (int e = 0; e < F::E; ++e) {
         const float A = excl + a[e];
         sAv[e] = A;
         sEv[e] = exp2f(A);
         sFv[e] = exp2f(a_last - A);
+        sDv[e] = exp2f(a_strip - A);
       }
     }
     const int g8 = 8 * (lane >> 4);
@@ -857,23 +883,37 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       f32x4 bql[2], bqh[2], bkl[2], bkh[2];
       load_bias(lb, bql, bqh, bkl, bkh);
       // which of the block's 32 pairs are rotary (n < Nr) is uniform over the wave except
-      // for a block that Nr cuts; only that case tests per pair
-      const bool all_rot = 32 * lb + 32 <= Nr, none_rot = 32 * lb >= Nr;
-      bf16x8 kl8, kh8;
+      // for a block that Nr cuts: one code path per case, chosen by a scalar branch, so
+      // only that block tests per pair (a per-pair test costs an exec-mask branch and
+      // register copies on every pair)
+      auto run = [&](auto mode) {
+        constexpr int M = decltype(mode)::value;   // 0: none rotary, 1: all, 2: n < Nr
+        bf16x8 kl8, kh8;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int n = 32 * lb + g8 + s;
-        float ql, qh, kl, kh;
-        pair(lb, s, bql, bqh, bkl, bkh, ql, qh, kl, kh);
-        uw += ql * kl + qh * kh;
-        if (all_rot || (!none_rot && n < Nr)) rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
-        qf[lb][s] = (bf16)ql;
-        qf[hb][s] = (bf16)qh;
-        kl8[s] = (bf16)(kl * rscale);
-        kh8[s] = (bf16)(kh * rscale);
+        for (int s = 0; s < 8; ++s) {
+          float ql, qh, kl, kh;
+          pair(lb, s, bql, bqh, bkl, bkh, ql, qh, kl, kh);
+          uw += ql * kl + qh * kh;
+          if constexpr (M == 1) {
+            rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
+          } else if constexpr (M == 2) {
+            if (32 * lb + g8 + s < Nr) rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
+          }
+          qf[lb][s] = (bf16)ql;
+          qf[hb][s] = (bf16)qh;
+          kl8[s] = (bf16)(kl * rscale);
+          kh8[s] = (bf16)(kh * rscale);
+        }
+        kst[lb] = kl8;
+        kst[hb] = kh8;
+      };
+      if (32 * lb + 32 <= Nr) {
+        run(IntTag<1>{});
+      } else if (32 * lb >= Nr) {
+        run(IntTag<0>{});
+      } else {
+        run(IntTag<2>{});
       }
-      kst[lb] = kl8;
-      kst[hb] = kh8;
     }
     uw += __shfl_xor(uw, 16, 64);
     uw += __shfl_xor(uw, 32, 64);
@@ -887,7 +927,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
-    const int tb = wave;
+    const int tb = strip;
     const int tcol = tb * 16 + (lane & 15);
     const int g4 = 4 * (lane >> 4);
     const bf16* sV = sVb + (c & 1) * (C * P);
@@ -895,10 +935,29 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // masked, decayed score tile s^T[j][t] for key strip jb (rows j) and this wave's
-    // query strip (columns t), as a sub-fragment with K = j
-    // (all K fragments are read before the first MFMA, and the mask is a select: the
-    // decay 2^{min(A_t - A_j, 0)} is finite for every entry, masked or not)
-    auto score = [&](int jb) {
+    // query strip (columns t), as a sub-fragment with K = j.
+    // Below the diagonal (jb < tb) every entry is causal and the decay factors through
+    // the key strip's last row m: 2^{A_t - A_j} = 2^{A_t - A_m} 2^{A_m - A_j}, both
+    // factors in (0, 1] since A falls along the chunk (t > m >= j); one exp per lane
+    // and tile instead of one per entry. The diagonal tile keeps the exact per-entry
+    // decay and the mask as a select (its decay 2^{min(A_t - A_j, 0)} is finite for
+    // every entry, masked or not). All K fragments are read before the first MFMA.
+    auto score_off = [&](int jb) {
+      bf16x8 kfr[F::NBK];
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk) kfr[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
+      const f32x4 dk = *reinterpret_cast<const f32x4*>(sDk + jb * 16 + g4);
+      const float et = __builtin_amdgcn_exp2f(At - sA[jb * 16 + 15]);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk) mma32x(acc, kfr[blk], qf[blk]);
+      f32x4 sv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = acc[i] * (et * dk[i]);
+      return sub_from_f32<bf16>(sv);
+    };
+    auto score_diag = [&]() {
+      const int jb = tb;
       bf16x8 kfr[F::NBK];
 #pragma unroll
       for (int blk = 0; blk < F::NBK; ++blk) kfr[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
@@ -916,21 +975,34 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       return sub_from_f32<bf16>(sv);
     };
     // intra-chunk: out^T[p][t] += sum_j v^T[p][j] s^T[j][t]   (v^T by transposed reads),
-    // one pair of key strips per step (two steps in flight) so few score tiles are live
-#pragma unroll 2
-    for (int jb = 0; jb <= tb; jb += 2) {
-      const bf16x4 s0 = score(jb);
-      if (jb + 1 <= tb) {
-        const bf16x4 s1 = score(jb + 1);
+    // one pair of key strips per step (K = 32): the pairs wholly below the diagonal, then
+    // the diagonal strip, alone (tb even) or with the strip before it (tb odd)
+    int vo[PB];   // this lane's v^T read offsets in the first 16-row band
 #pragma unroll
-        for (int pb = 0; pb < PB; ++pb)
-          mma32(out[pb], ld_tr4_vz(sV, jb * 16 + g4, pb * 16, lane),
-                ld_tr4_vz(sV, jb * 16 + 16 + g4, pb * 16, lane), s0, s1);
-      } else {
+    for (int pb = 0; pb < PB; ++pb) vo[pb] = vz_tr_off(g4, pb * 16, lane);
+    auto pv_pair = [&](int jb, const bf16x4& s0, const bf16x4& s1) {
 #pragma unroll
-        for (int pb = 0; pb < PB; ++pb)
-          mma16(out[pb], ld_tr4_vz(sV, jb * 16 + g4, pb * 16, lane), s0);
+      for (int pb = 0; pb < PB; ++pb) {
+        const bf16* vp = sV + jb * 16 * 64 + vo[pb];
+        mma32(out[pb], ld_tr4_at(vp), ld_tr4_at(vp + 16 * 64), s0, s1);
       }
+    };
+    const int npair = tb >> 1;
+#pragma unroll 2
+    for (int ip = 0; ip < npair; ++ip) {
+      const int jb = 2 * ip;
+      const bf16x4 s0 = score_off(jb);
+      const bf16x4 s1 = score_off(jb + 1);
+      pv_pair(jb, s0, s1);
+    }
+    if (tb & 1) {
+      const bf16x4 s0 = score_off(tb - 1);
+      const bf16x4 s1 = score_diag();
+      pv_pair(tb - 1, s0, s1);
+    } else {
+      const bf16x4 s0 = score_diag();
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) mma16(out[pb], ld_tr4_at(sV + tb * 16 * 64 + vo[pb]), s0);
     }
     // next chunk's inputs: issued here so the memory-issue waits overlap MFMA work
     if (c + 1 < nc) {
@@ -968,11 +1040,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       for (int i = 0; i < 4; ++i) Sacc[m][i] *= eAl;
     }
     const int g8 = 8 * (lane >> 4);
+    const int vs0 = vz_tr_off(0, pb_w * 16, lane), vs1 = vz_tr_off(4, pb_w * 16, lane);
 #pragma unroll 1
     for (int k0 = 0; k0 < C; k0 += 32) {
       const int kb = k0 + g8;
-      bf16x4 a0 = ld_tr4_vz(sV, kb, pb_w * 16, lane);
-      bf16x4 a1 = ld_tr4_vz(sV, kb + 4, pb_w * 16, lane);
+      bf16x4 a0 = ld_tr4_at(sV + kb * 64 + vs0);   // kb is a multiple of 8
+      bf16x4 a1 = ld_tr4_at(sV + kb * 64 + vs1);
       const f32x4 f0 = *reinterpret_cast<const f32x4*>(sFac + kb);
       const f32x4 f1 = *reinterpret_cast<const f32x4*>(sFac + kb + 4);
       bf16x4 kb0[SPW], kb1[SPW];   // every tile's K fragments first: independent MFMAs
@@ -1044,7 +1117,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   for (int c = 0; c <= nc; ++c) {
     // ---------------- phase A: stage out(c-1), S(c) and chunk c's k-hat / scalars ----
     if (c > 0) {
-      const int tcol = wave * 16 + (lane & 15);
+      const int tcol = strip * 16 + (lane & 15);
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb)
         *reinterpret_cast<f32x4*>(sOut + tcol * LDO + pb * 16 + 4 * (lane >> 4)) = out[pb];
