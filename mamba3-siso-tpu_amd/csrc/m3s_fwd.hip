@@ -558,12 +558,10 @@ struct Fwd2Cfg {
   static constexpr int NSTEP = NW / PB;    // nb stride between a wave's state tiles
   // v / z tiles: C rows of P bf16 (128 bytes), unpadded, the 16-byte pieces of row r
   // stored at slot piece ^ (r & 7) so transposed and row reads hit distinct banks.
-  // They arrive by direct global->LDS loads (1 KiB = 8 rows per instruction) issued by
-  // the first half of the waves -- whose query strips are the short end of the causal
-  // triangle -- and those waves also run the epilogue.
-  static constexpr int VBLK = C * P * 2 / 1024;   // 1 KiB blocks per v (or z) tile
-  static constexpr int NWL = NW / 2;              // light waves
-  static constexpr int VBW = VBLK / NWL;          // blocks per light wave
+  // Every wave prefetches VPL 16-byte pieces of each into registers one phase ahead
+  // and writes them in phase A, so one LDS tile of each suffices.
+  static constexpr int VPL = C * P * 2 / (NT * 16);  // 16-byte pieces per lane per tile
+  static constexpr int NWL = NW / 2;              // light waves: run the epilogue
   static constexpr int VG = P / 8;                // epilogue column groups (16 bytes)
   static constexpr int VT = (C / 2) * VG;         // epilogue tasks: (row pair, group)
   static constexpr int VTH = NWL * 64;            // epilogue threads
@@ -574,10 +572,10 @@ struct Fwd2Cfg {
   static constexpr int SZ_S = P * LDK * 2;
   static constexpr int SZ_O = C * LDO * 4;
   static constexpr int SZ_SC = (5 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb, sDk
-  static constexpr int LDS_BYTES = SZ_K + 4 * SZ_V + SZ_S + SZ_O + SZ_SC;
+  static constexpr int LDS_BYTES = SZ_K + 2 * SZ_V + SZ_S + SZ_O + SZ_SC;
   static_assert(N % 64 == 0 && P == 64 && C % 64 == 0, "tile shape");
   static_assert(NW % PB == 0 && (PB * NB) % NW == 0, "state tiles split evenly over waves");
-  static_assert(VBLK % NWL == 0, "v / z blocks split evenly over the light waves");
+  static_assert(VPL * NT * 16 == C * P * 2, "v / z pieces split evenly over the lanes");
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
 };
 
@@ -618,11 +616,11 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
   auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
   bf16* sK = reinterpret_cast<bf16*>(smem);
-  bf16* sVb = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));                 // [2] v tiles
-  bf16* sZb = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 2 * F::SZ_V));   // [2] z tiles
-  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 4 * F::SZ_V));
-  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + 4 * F::SZ_V + F::SZ_S));
-  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + 4 * F::SZ_V + F::SZ_S + F::SZ_O));
+  bf16* sV = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));                  // v tile
+  bf16* sZ = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + F::SZ_V));        // z tile
+  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 2 * F::SZ_V));
+  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + 2 * F::SZ_V + F::SZ_S));
+  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + 2 * F::SZ_V + F::SZ_S + F::SZ_O));
   float* sExpA = sA + C;   // 2^{A_t}
   float* sFac = sExpA + C; // 2^{A_last - A_t}
   float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
@@ -703,18 +701,38 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
-  // ---- v / z tiles of chunk c: direct global->LDS loads by the light waves ----------
-  auto issue_vz = [&](const __amdgpu_buffer_rsrc_t& r, int64_t st, bf16* tile, int c) {
+  // ---- v / z tiles: 16-byte row pieces prefetched into registers, written in phase A
+  // (plain loads keep every dependency visible to the compiler; a direct global->LDS
+  // load makes it wait for all outstanding loads before any later LDS read)
+  bf16x8 rv[F::VPL], rz[F::VPL];
+  // Loads and writes are unconditional: a chunk that does not exist (v after the last
+  // chunk, z before the first, z of a layer without gate) is read through a zero-size
+  // descriptor, which returns zeros and touches no memory, so every iteration issues
+  // the same loads and the compiler's wait counts stay exact.
+  const auto rNul = make_rsrc(nullptr, 0u);
+  auto prefetch_vz = [&](const __amdgpu_buffer_rsrc_t& srv, int cv,
+                         const __amdgpu_buffer_rsrc_t& srz, int cz) {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
-    const int lane = ln & 63;
 #pragma unroll
-    for (int i = 0; i < F::VBW; ++i) {
-      const int blk = wave * F::VBW + i;           // 1 KiB block = rows 8 blk .. 8 blk + 7
-      const int row = 8 * blk + (lane >> 3);
-      const int piece = (lane & 7) ^ (row & 7);    // LDS slot lane & 7 holds this piece
-      buf_load_lds16(r, tile + blk * 512, (uint32_t)(row * st + 8 * piece) * 2,
-                     (uint32_t)(c * C * st * 2));
+    for (int i = 0; i < F::VPL; ++i) {
+      const int id = ln + i * NT, row = id >> 3, col = 8 * (id & 7);
+      rv[i] = buf_load<bf16x8>(srv, (uint32_t)(row * p.v_st + col) * 2, (uint32_t)(cv * C * p.v_st * 2));
+      rz[i] = buf_load<bf16x8>(srz, (uint32_t)(row * p.z_st + col) * 2, (uint32_t)(cz * C * p.z_st * 2));
+    }
+  };
+  auto write_vz = [&](bool last) {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int i = 0; i < F::VPL; ++i) {
+      const int id = ln + i * NT, row = id >> 3, col = 8 * (id & 7);
+      *reinterpret_cast<bf16x8*>(sV + vz_off(row, col)) = rv[i];
+      *reinterpret_cast<bf16x8*>(sZ + vz_off(row, col)) = rz[i];
+      if (last && row == C - 1) {   // final_v: the sequence's last v row
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p.fv[bh * P + col + e] = (float)rv[i][e];
+      }
     }
   };
 
@@ -726,7 +744,10 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   float radt[F::E];
   const bool phi_vec = (Nr % 4) == 0;
 
-  auto prefetch_qk = [&](int c) {
+  auto prefetch_qk = [&](int c) {   // c >= nc: a chunk that does not exist, read as zeros
+    const bool live = c < nc;
+    const auto dQ = live ? rQ : rNul, dK = live ? rK : rNul;
+    if (!live) c = 0;
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
@@ -735,13 +756,17 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const uint32_t oqk = (uint32_t)(trow * N + g8) * 2;
 #pragma unroll
     for (int blk = 0; blk < F::NBK; ++blk) {
-      rq[blk] = buf_load<bf16x8>(rQ, oqk + 64 * blk, (uint32_t)c * C * N * 2);
-      rk[blk] = buf_load<bf16x8>(rK, oqk + 64 * blk, (uint32_t)c * C * N * 2);
+      rq[blk] = buf_load<bf16x8>(dQ, oqk + 64 * blk, (uint32_t)c * C * N * 2);
+      rk[blk] = buf_load<bf16x8>(dK, oqk + 64 * blk, (uint32_t)c * C * N * 2);
     }
   };
   // the rest of chunk c's inputs; issued from the middle of the products, so that the
   // wait for free memory-request slots overlaps MFMA work instead of stalling a phase
-  auto prefetch_rest = [&](int c) {
+  auto prefetch_rest = [&](int c) {   // c >= nc: read as zeros, as in prefetch_qk
+    const bool live = c < nc;
+    const auto dPhi = live ? rPhi : rNul, dScl = live ? rScl : rNul;
+    const auto dGam = live ? rGam : rNul, dAdt = live ? rAdt : rNul;
+    if (!live) c = 0;
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
@@ -759,7 +784,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       } else if (phi_vec && 32 * lb + 32 <= Nr) {
 #pragma unroll
         for (int qd = 0; qd < 2; ++qd)
-          rphi[lb][qd] = buf_load<f32x4>(rPhi, (uint32_t)(trow * Nr + 32 * lb + g8 + 4 * qd) * 4, sphi);
+          rphi[lb][qd] = buf_load<f32x4>(dPhi, (uint32_t)(trow * Nr + 32 * lb + g8 + 4 * qd) * 4, sphi);
       } else {
 #pragma unroll
         for (int qd = 0; qd < 2; ++qd) {
@@ -767,17 +792,17 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
           const uint32_t o = (uint32_t)(trow * Nr + j) * 4;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            rphi[lb][qd][i] = (j + i < Nr) ? buf_load<float>(rPhi, o + 4 * i, sphi) : 0.f;
+            rphi[lb][qd][i] = (j + i < Nr) ? buf_load<float>(dPhi, o + 4 * i, sphi) : 0.f;
         }
       }
     }
-    rscale = buf_load<float>(rScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
-    rgam = buf_load<float>(rGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
-    if (wave == 0) {
+    rscale = buf_load<float>(dScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+    rgam = buf_load<float>(dGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+    // every wave loads the A-scan inputs (only wave 0 uses them): no wave-dependent
+    // branch around loads (it would cost exact wait counts)
 #pragma unroll
-      for (int e = 0; e < F::E; ++e)
-        radt[e] = buf_load<float>(rAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
-    }
+    for (int e = 0; e < F::E; ++e)
+      radt[e] = buf_load<float>(dAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
   };
 
   bf16x8 qf[F::NBK];                        // q~ of this wave's strip (MFMA B operand)
@@ -930,7 +955,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int tb = strip;
     const int tcol = tb * 16 + (lane & 15);
     const int g4 = 4 * (lane >> 4);
-    const bf16* sV = sVb + (c & 1) * (C * P);
     const float At = sA[tcol];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) out[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -941,34 +965,57 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     // factors in (0, 1] since A falls along the chunk (t > m >= j); one exp per lane
     // and tile instead of one per entry. The diagonal tile keeps the exact per-entry
     // decay and the mask as a select (its decay 2^{min(A_t - A_j, 0)} is finite for
-    // every entry, masked or not). All K fragments are read before the first MFMA.
-    auto score_off = [&](int jb) {
-      bf16x8 kfr[F::NBK];
+    // every entry, masked or not).
+    // Each step reads all its fragments (k-hat rows of both key strips, v^T of both, the
+    // decay factors) before the first MFMA: one LDS round trip per pair of key strips
+    // instead of one per fragment group.
+    struct PairFrags {
+      bf16x8 ka[F::NBK], kb[F::NBK];   // k-hat rows of key strips jb, jb + 1
+      bf16x4 va[PB], vb[PB];           // v^T of the same rows
+      f32x4 da, db;                    // sDk (off-diagonal) or sA (diagonal) of the rows
+      float ma, mb;                    // A at each strip's last row
+    };
+    int vo[PB];   // this lane's v^T read offsets in the first 16-row band
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) kfr[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
-      const f32x4 dk = *reinterpret_cast<const f32x4*>(sDk + jb * 16 + g4);
-      const float et = __builtin_amdgcn_exp2f(At - sA[jb * 16 + 15]);
+    for (int pb = 0; pb < PB; ++pb) vo[pb] = vz_tr_off(g4, pb * 16, lane);
+    // second strip: 0 none, 1 below the diagonal, 2 the diagonal strip (its decay rows
+    // are A itself)
+    auto load_pair = [&](int jb, int second, PairFrags& f) {
+#pragma unroll
+      for (int blk = 0; blk < F::NBK; ++blk) f.ka[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) f.va[pb] = ld_tr4_at(sV + jb * 16 * 64 + vo[pb]);
+      f.da = *reinterpret_cast<const f32x4*>(sDk + jb * 16 + g4);
+      f.ma = sA[jb * 16 + 15];
+      if (second) {
+#pragma unroll
+        for (int blk = 0; blk < F::NBK; ++blk) f.kb[blk] = ld_nat8(sK, LDK, jb * 16 + 16, 32 * blk, lane);
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) f.vb[pb] = ld_tr4_at(sV + (jb + 1) * 16 * 64 + vo[pb]);
+        f.db = *reinterpret_cast<const f32x4*>((second == 2 ? sA : sDk) + jb * 16 + 16 + g4);
+        f.mb = sA[jb * 16 + 31];
+      }
+    };
+    auto qk_acc = [&](const bf16x8 (&kf)[F::NBK]) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) mma32x(acc, kfr[blk], qf[blk]);
+      for (int blk = 0; blk < F::NBK; ++blk) mma32x(acc, kf[blk], qf[blk]);
+      return acc;
+    };
+    // below the diagonal: the factored decay
+    auto decay_off = [&](const f32x4& acc, const f32x4& dk, float m) {
+      const float et = __builtin_amdgcn_exp2f(At - m);
       f32x4 sv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = acc[i] * (et * dk[i]);
       return sub_from_f32<bf16>(sv);
     };
-    auto score_diag = [&]() {
-      const int jb = tb;
-      bf16x8 kfr[F::NBK];
-#pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) kfr[blk] = ld_nat8(sK, LDK, jb * 16, 32 * blk, lane);
-      const f32x4 aj = *reinterpret_cast<const f32x4*>(sA + jb * 16 + g4);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) mma32x(acc, kfr[blk], qf[blk]);
+    // the diagonal strip: exact decay, causal mask as a select
+    auto decay_diag = [&](const f32x4& acc, const f32x4& aj) {
       f32x4 sv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = jb * 16 + g4 + i;
+        const int j = tb * 16 + g4 + i;
         const float dec = __builtin_amdgcn_exp2f(fminf(At - aj[i], 0.f));
         sv[i] = (tcol > j) ? acc[i] * dec : 0.f;
       }
@@ -977,60 +1024,61 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     // intra-chunk: out^T[p][t] += sum_j v^T[p][j] s^T[j][t]   (v^T by transposed reads),
     // one pair of key strips per step (K = 32): the pairs wholly below the diagonal, then
     // the diagonal strip, alone (tb even) or with the strip before it (tb odd)
-    int vo[PB];   // this lane's v^T read offsets in the first 16-row band
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb) vo[pb] = vz_tr_off(g4, pb * 16, lane);
-    auto pv_pair = [&](int jb, const bf16x4& s0, const bf16x4& s1) {
-#pragma unroll
-      for (int pb = 0; pb < PB; ++pb) {
-        const bf16* vp = sV + jb * 16 * 64 + vo[pb];
-        mma32(out[pb], ld_tr4_at(vp), ld_tr4_at(vp + 16 * 64), s0, s1);
-      }
-    };
     const int npair = tb >> 1;
-#pragma unroll 2
+    PairFrags fr;
+#pragma unroll 1
     for (int ip = 0; ip < npair; ++ip) {
-      const int jb = 2 * ip;
-      const bf16x4 s0 = score_off(jb);
-      const bf16x4 s1 = score_off(jb + 1);
-      pv_pair(jb, s0, s1);
+      load_pair(2 * ip, 1, fr);
+      const f32x4 a0 = qk_acc(fr.ka), a1 = qk_acc(fr.kb);
+      const bf16x4 s0 = decay_off(a0, fr.da, fr.ma), s1 = decay_off(a1, fr.db, fr.mb);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) mma32(out[pb], fr.va[pb], fr.vb[pb], s0, s1);
     }
     if (tb & 1) {
-      const bf16x4 s0 = score_off(tb - 1);
-      const bf16x4 s1 = score_diag();
-      pv_pair(tb - 1, s0, s1);
-    } else {
-      const bf16x4 s0 = score_diag();
+      load_pair(tb - 1, 2, fr);
+      const f32x4 a0 = qk_acc(fr.ka), a1 = qk_acc(fr.kb);
+      const bf16x4 s0 = decay_off(a0, fr.da, fr.ma), s1 = decay_diag(a1, fr.db);
 #pragma unroll
-      for (int pb = 0; pb < PB; ++pb) mma16(out[pb], ld_tr4_at(sV + tb * 16 * 64 + vo[pb]), s0);
+      for (int pb = 0; pb < PB; ++pb) mma32(out[pb], fr.va[pb], fr.vb[pb], s0, s1);
+    } else {
+      load_pair(tb, 0, fr);
+      fr.da = *reinterpret_cast<const f32x4*>(sA + tb * 16 + g4);
+      const bf16x4 s0 = decay_diag(qk_acc(fr.ka), fr.da);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) mma16(out[pb], fr.va[pb], s0);
     }
     // next chunk's inputs: issued here so the memory-issue waits overlap MFMA work
-    if (c + 1 < nc) {
-      __builtin_amdgcn_sched_barrier(0);
-      prefetch_rest(c + 1);
-      if (light) issue_vz(rV, p.v_st, sVb + ((c + 1) & 1) * (C * P), c + 1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (zg && light) {  // this chunk's gate, for its epilogue one phase later
-      __builtin_amdgcn_sched_barrier(0);
-      issue_vz(rZ, p.z_st, sZb + (c & 1) * (C * P), c);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    // (the next chunk's v and this chunk's gate z, written in the next phase A)
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_rest(c + 1);
+    prefetch_vz(c + 1 < nc ? rV : rNul, c + 1 < nc ? c + 1 : 0, rZ, c);
+    __builtin_amdgcn_sched_barrier(0);
     // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
+    // (every fragment of S, the diagonal v values and the scalars are read first, then
+    // PB independent MFMA chains: one LDS round trip)
     const float eA = sExpA[tcol];
+    const float coef = sCoef[tcol];
+    bf16x8 sfr[PB][F::NBK];
+    bf16x4 vd[PB];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
-      bf16x8 sfr[F::NBK];   // all K fragments of this row block first, then the chain
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) sfr[blk] = ld_nat8(sS, LDK, pb * 16, 32 * blk, lane);
-      f32x4 it = {0.f, 0.f, 0.f, 0.f};
+      for (int blk = 0; blk < F::NBK; ++blk) sfr[pb][blk] = ld_nat8(sS, LDK, pb * 16, 32 * blk, lane);
+      vd[pb] = *reinterpret_cast<const bf16x4*>(sV + vz_off(tcol, pb * 16 + g4));
+    }
+    f32x4 it[PB];
 #pragma unroll
-      for (int blk = 0; blk < F::NBK; ++blk) mma32x(it, sfr[blk], qf[blk]);
-      // diagonal and skip: (D + gamma_t u_t . w_t) v_t
-      const bf16x4 vd = *reinterpret_cast<const bf16x4*>(sV + vz_off(tcol, pb * 16 + g4));
-      const float coef = sCoef[tcol];
+    for (int pb = 0; pb < PB; ++pb) it[pb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) out[pb][i] = (out[pb][i] + eA * it[i]) + coef * (float)vd[i];
+    for (int blk = 0; blk < F::NBK; ++blk) {
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) mma32x(it[pb], sfr[pb][blk], qf[blk]);
+    }
+    // diagonal and skip: (D + gamma_t u_t . w_t) v_t
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[pb][i] = (out[pb][i] + eA * it[pb][i]) + coef * (float)vd[pb][i];
     }
     // state: S <- 2^{A_last} S + sum_t (v_t 2^{A_last - A_t}) khat_t^T   (K = time)
     const float eAl = sExpA[C - 1];
@@ -1041,27 +1089,43 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
     const int g8 = 8 * (lane >> 4);
     const int vs0 = vz_tr_off(0, pb_w * 16, lane), vs1 = vz_tr_off(4, pb_w * 16, lane);
-#pragma unroll 1
-    for (int k0 = 0; k0 < C; k0 += 32) {
-      const int kb = k0 + g8;
-      bf16x4 a0 = ld_tr4_at(sV + kb * 64 + vs0);   // kb is a multiple of 8
-      bf16x4 a1 = ld_tr4_at(sV + kb * 64 + vs1);
-      const f32x4 f0 = *reinterpret_cast<const f32x4*>(sFac + kb);
-      const f32x4 f1 = *reinterpret_cast<const f32x4*>(sFac + kb + 4);
-      bf16x4 kb0[SPW], kb1[SPW];   // every tile's K fragments first: independent MFMAs
+    // software-pipelined over the C/32 K steps: step i+1's fragments are read into the
+    // other register set before step i's scaling and MFMAs, so LDS latency overlaps them
+    struct StepFrags {
+      bf16x4 a0, a1;
+      f32x4 f0, f1;
+      bf16x4 kb0[SPW], kb1[SPW];
+    };
+    auto load_step = [&](int k0, StepFrags& fr) {
+      const int kb = k0 + g8;                          // a multiple of 8
+      fr.a0 = ld_tr4_at(sV + kb * 64 + vs0);
+      fr.a1 = ld_tr4_at(sV + kb * 64 + vs1);
+      fr.f0 = *reinterpret_cast<const f32x4*>(sFac + kb);
+      fr.f1 = *reinterpret_cast<const f32x4*>(sFac + kb + 4);
 #pragma unroll
       for (int m = 0; m < SPW; ++m) {
         const int nb = nb0 + NSTEP * m;
-        kb0[m] = ld_tr4(sK, LDK, kb, nb * 16, lane);
-        kb1[m] = ld_tr4(sK, LDK, kb + 4, nb * 16, lane);
+        fr.kb0[m] = ld_tr4(sK, LDK, kb, nb * 16, lane);
+        fr.kb1[m] = ld_tr4(sK, LDK, kb + 4, nb * 16, lane);
       }
+    };
+    auto run_step = [&](StepFrags& fr) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        a0[s] = (bf16)((float)a0[s] * f0[s]);
-        a1[s] = (bf16)((float)a1[s] * f1[s]);
+        fr.a0[s] = (bf16)((float)fr.a0[s] * fr.f0[s]);
+        fr.a1[s] = (bf16)((float)fr.a1[s] * fr.f1[s]);
       }
 #pragma unroll
-      for (int m = 0; m < SPW; ++m) mma32(Sacc[m], a0, a1, kb0[m], kb1[m]);
+      for (int m = 0; m < SPW; ++m) mma32(Sacc[m], fr.a0, fr.a1, fr.kb0[m], fr.kb1[m]);
+    };
+    StepFrags fa, fb;
+    load_step(0, fa);
+#pragma unroll
+    for (int k0 = 0; k0 < C; k0 += 64) {
+      if (k0 + 32 < C) load_step(k0 + 32, fb);
+      run_step(fa);
+      if (k0 + 64 < C) load_step(k0 + 64, fa);
+      if (k0 + 32 < C) run_step(fb);
     }
   };
 
@@ -1071,7 +1135,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     asm volatile("" : "+v"(ln));
     const int tid = ln;
     const int t0 = c * C;
-    const bf16* sZ = sZb + (c & 1) * (C * P);
 #pragma unroll
     for (int r = 0; r < F::VR; ++r) {
       const int task = tid + r * F::VTH;
@@ -1107,15 +1170,15 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
-  if (light) issue_vz(rV, p.v_st, sVb, 0);
+  prefetch_vz(rV, 0, rNul, 0);
   prefetch_qk(0);
   prefetch_rest(0);
   vm_wait_all();
-  __syncthreads();  // sQb / sKb, v tile of chunk 0
+  __syncthreads();  // sQb / sKb
   stage_regs();     // chunk 0
-  if (nc > 1) prefetch_qk(1);
-  for (int c = 0; c <= nc; ++c) {
-    // ---------------- phase A: stage out(c-1), S(c) and chunk c's k-hat / scalars ----
+  prefetch_qk(1);
+  // phase A of chunk c (and of the tail): out(c-1) to sOut, S(c) to sS
+  auto phase_a = [&](int c) {
     if (c > 0) {
       const int tcol = strip * 16 + (lane & 15);
 #pragma unroll
@@ -1123,30 +1186,33 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         *reinterpret_cast<f32x4*>(sOut + tcol * LDO + pb * 16 + 4 * (lane >> 4)) = out[pb];
     }
     publish_state(c);
-    if (c < nc) stage_write();
-    if (c + 1 < nc) {
-      vm_wait_keep<2 * F::NBK>();   // all but chunk c+1's q / k rows: v of c, z of c-1
-    } else {
-      vm_wait_all();
-    }
+  };
+  for (int c = 0; c < nc; ++c) {
+    // ---------------- phase A: also chunk c's k-hat and scalars, v of c, z of c-1 --------
+    phase_a(c);
+    stage_write();
+    write_vz(c == nc - 1);   // (zeros where there is no such chunk)
     __syncthreads();
     // ---------------- phase B: epilogue of c-1, products of c, then chunk c+1's rotation
     // into registers (a wave whose products end early rotates while others still run
-    // theirs: the VALU work overlaps the partner wave's MFMA work on the same SIMD)
+    // theirs: the VALU work overlaps the partner wave's MFMA work on the same SIMD).
+    // Every load is issued on every chunk (past the end through a zero-size
+    // descriptor), so the compiler's wait counts stay exact across iterations.
     if (c > 0 && light) epilogue(c - 1);
-    if (c < nc) products(c);
-    if (c + 1 < nc) {
-      stage_regs();
-      if (c + 2 < nc) {
-        __builtin_amdgcn_sched_barrier(0);
-        prefetch_qk(c + 2);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
+    products(c);
+    stage_regs();
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_qk(c + 2);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   }
+  // tail: out and z of the last chunk, its epilogue
+  phase_a(nc);
+  write_vz(false);
+  __syncthreads();
+  if (light) epilogue(nc - 1);
 
-  // final state, and the last v row (still in its LDS tile)
+  // final state
 #pragma unroll
   for (int m = 0; m < SPW; ++m) {
     const int ncol = (nb0 + NSTEP * m) * 16 + (lane & 15);
@@ -1156,8 +1222,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       p.fssm[(bh * P + prow) * N + ncol] = Sacc[m][i];
     }
   }
-  const bf16* sVl = sVb + ((nc - 1) & 1) * (C * P);
-  for (int i = tid; i < P; i += NT) p.fv[bh * P + i] = (float)sVl[vz_off(C - 1, i)];
   // final_k: the sequence's last key row, rotated and unscaled (the same arithmetic as
   // the stage), one rotary pair per lane of wave 0
   if (wave == 0 && lane < H2) {
