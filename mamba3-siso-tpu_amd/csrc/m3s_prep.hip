@@ -119,18 +119,49 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   const RT* tr = static_cast<const RT*>(p.tr.p) + b * p.tr.sb;
   const RT* ang = static_cast<const RT*>(p.ang.p) + b * p.ang.sb;
 
-  for (int i = tid; i < nt1 * H; i += kPrepThreads) {
-    const int t = i / H, h = i % H;
-    const int64_t tg = t0 + t;
-    sDt[i] = softplus_(ldr(dtr, tg * p.dtr.st + h) + p.dt_bias[h]);
-    sLam[i] = sigmoid_(ldr(tr, tg * p.tr.st + h));
-    sA[i] = fminf(-heavy_tail_(ldr(ar, tg * p.ar.st + h)), -p.a_floor);
+  // KU items per thread per round, every load of a round issued before any use: one
+  // memory latency per round instead of one per item
+  constexpr int KU = 4;
+  const int n1 = nt1 * H;
+  for (int i0 = tid; i0 < n1; i0 += KU * kPrepThreads) {
+    float vd[KU], vl[KU], va[KU], vb[KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = min(i0 + u * kPrepThreads, n1 - 1);
+      const int t = i / H, h = i % H;
+      const int64_t tg = t0 + t;
+      vd[u] = ldr(dtr, tg * p.dtr.st + h);
+      vl[u] = ldr(tr, tg * p.tr.st + h);
+      va[u] = ldr(ar, tg * p.ar.st + h);
+      vb[u] = p.dt_bias[h];
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = i0 + u * kPrepThreads;
+      if (i < n1) {
+        sDt[i] = softplus_(vd[u] + vb[u]);
+        sLam[i] = sigmoid_(vl[u]);
+        sA[i] = fminf(-heavy_tail_(va[u]), -p.a_floor);
+      }
+    }
   }
-  for (int i = tid; i < nt * Nr; i += kPrepThreads) {
-    const int t = i / Nr, j = i % Nr;
-    const float tp = tanhf(ldr(ang, (int64_t)(t0 + t) * p.ang.st + j)) * kPiF;
-    sT[i] = tp;
-    p.tpi[((int64_t)b * L + t0) * Nr + i] = tp;
+  const int n2 = nt * Nr;
+  for (int i0 = tid; i0 < n2; i0 += KU * kPrepThreads) {
+    float vg[KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = min(i0 + u * kPrepThreads, n2 - 1);
+      vg[u] = ldr(ang, (int64_t)(t0 + i / Nr) * p.ang.st + i % Nr);
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = i0 + u * kPrepThreads;
+      if (i < n2) {
+        const float tp = tanhf(vg[u]) * kPiF;
+        sT[i] = tp;
+        p.tpi[((int64_t)b * L + t0) * Nr + i] = tp;
+      }
+    }
   }
   __syncthreads();
   for (int i = tid; i < H * nt; i += kPrepThreads) {  // (h, t) order: (b, h) rows
@@ -151,11 +182,17 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
     const int h = pr / J4, j0 = 4 * (pr % J4);
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int t = 0; t < nt; ++t) {
+    auto add_row = [&](int t) {
       const float dt = sDt[t * H + h];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (j0 + i < Nr) s[i] += sT[t * Nr + j0 + i] * dt;
+    };
+    if (nt == kPrepTB) {   // whole blocks: a fixed trip count the compiler can pipeline
+#pragma unroll 16
+      for (int t = 0; t < kPrepTB; ++t) add_row(t);
+    } else {
+      for (int t = 0; t < nt; ++t) add_row(t);
     }
     st_quad(p.tot + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr, s);
   }
@@ -217,13 +254,20 @@ __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdPar
     const int64_t bh = (int64_t)b * H + h;
     const float* dtrow = p.dt + bh * L + t0;
     f32x4 tot = {0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < RPL; ++i) {
-      const int t = r0 + i;
-      if (act && t < nt) {
-        const float dt = dtrow[t];
-        const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+    // this lane's rows in runs of 8, each run's dt loaded together before use
+    constexpr int RUN = 8;
+    for (int i0 = 0; i0 < RPL; i0 += RUN) {
+      float d8[RUN];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) tot[c] += tp[c] * dt;
+      for (int u = 0; u < RUN; ++u) d8[u] = dtrow[min(r0 + i0 + u, nt - 1)];
+#pragma unroll
+      for (int u = 0; u < RUN; ++u) {
+        const int t = r0 + i0 + u;
+        if (act && i0 + u < RPL && t < nt) {
+          const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) tot[c] += tp[c] * d8[u];
+        }
       }
     }
     f32x4 incl = tot;
@@ -241,19 +285,25 @@ __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdPar
 #pragma unroll
     for (int c = 0; c < 4; ++c) run[c] += incl[c] - tot[c];
     float* prow = p.phi + (bh * L + t0) * Nr;
-    for (int i = 0; i < RPL; ++i) {
-      const int t = r0 + i;
-      if (t >= nt) break;
-      const float dt = dtrow[t];
-      const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
-      f32x4 out;
+    for (int i0 = 0; i0 < RPL; i0 += RUN) {
+      float d8[RUN];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        run[c] += tp[c] * dt;
-        out[c] = wrap_(run[c] + init[c]);
+      for (int u = 0; u < RUN; ++u) d8[u] = dtrow[min(r0 + i0 + u, nt - 1)];
+#pragma unroll
+      for (int u = 0; u < RUN; ++u) {
+        const int t = r0 + i0 + u;
+        if (i0 + u < RPL && t < nt) {
+          const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+          f32x4 out;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            run[c] += tp[c] * d8[u];
+            out[c] = wrap_(run[c] + init[c]);
+          }
+          st_quad(prow + t * Nr, j0, Nr, out);
+          if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
+        }
       }
-      st_quad(prow + t * Nr, j0, Nr, out);
-      if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
     }
   }
 }
@@ -330,25 +380,66 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   const RT* ang = static_cast<const RT*>(p.ang.p) + b * p.ang.sb;
 
   // ---- stage: recomputed dt / lambda, incoming cotangents, tanh table -------------
-  for (int i = tid; i < nt * H; i += kPrepThreads) {
-    const int t = i / H, h = i % H;
-    sDt[i] = softplus_(ldr(dtr, (int64_t)(t0 + t) * p.dtr.st + h) + p.dt_bias[h]);
-    sLam[i] = sigmoid_(ldr(tr, (int64_t)(t0 + t) * p.tr.st + h));
-    sPhi[i] = 0.f;
+  // (KU items per thread per round, every load of a round issued before any use)
+  constexpr int KU = 4;
+  const int nh = nt * H;
+  for (int i0 = tid; i0 < nh; i0 += KU * kPrepThreads) {
+    float vd[KU], vl[KU], vb[KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = min(i0 + u * kPrepThreads, nh - 1), t = i / H, h = i % H;
+      vd[u] = ldr(dtr, (int64_t)(t0 + t) * p.dtr.st + h);
+      vl[u] = ldr(tr, (int64_t)(t0 + t) * p.tr.st + h);
+      vb[u] = p.dt_bias[h];
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = i0 + u * kPrepThreads;
+      if (i < nh) {
+        sDt[i] = softplus_(vd[u] + vb[u]);
+        sLam[i] = sigmoid_(vl[u]);
+        sPhi[i] = 0.f;
+      }
+    }
   }
-  for (int i = tid; i < nt * H; i += kPrepThreads) {  // (h, t) order: coalesced reads
-    const int h = i / nt, t = i % nt;
-    const int64_t g = ((int64_t)b * H + h) * L + t0 + t;
-    sDadt[t * H + h] = p.dadt ? p.dadt[g] : 0.f;
-    sDgam[t * H + h] = p.dgamma ? p.dgamma[g] : 0.f;
-    sDscl[t * H + h] = p.dscale ? p.dscale[g] : 0.f;
+  for (int i0 = tid; i0 < nh; i0 += KU * kPrepThreads) {  // (h, t) order: coalesced reads
+    float va[KU], vg[KU], vs[KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = min(i0 + u * kPrepThreads, nh - 1), h = i / nt, t = i % nt;
+      const int64_t g = ((int64_t)b * H + h) * L + t0 + t;
+      va[u] = p.dadt ? p.dadt[g] : 0.f;
+      vg[u] = p.dgamma ? p.dgamma[g] : 0.f;
+      vs[u] = p.dscale ? p.dscale[g] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = i0 + u * kPrepThreads, h = i / nt, t = i % nt;
+      if (i < nh) {
+        sDadt[t * H + h] = va[u];
+        sDgam[t * H + h] = vg[u];
+        sDscl[t * H + h] = vs[u];
+      }
+    }
   }
   for (int h = tid; h < H; h += kPrepThreads)
     sDsPrev[h] = (p.dscale && t0 > 0) ? p.dscale[((int64_t)b * H + h) * L + t0 - 1] : 0.f;
-  for (int i = tid; i < nt * Nr; i += kPrepThreads) {
-    const int t = i / Nr, j = i % Nr;
-    sT[i] = tanhf(ldr(ang, (int64_t)(t0 + t) * p.ang.st + j));
-    sAng[i] = 0.f;
+  const int nj = nt * Nr;
+  for (int i0 = tid; i0 < nj; i0 += KU * kPrepThreads) {
+    float vg[KU];
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = min(i0 + u * kPrepThreads, nj - 1);
+      vg[u] = ldr(ang, (int64_t)(t0 + i / Nr) * p.ang.st + i % Nr);
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int i = i0 + u * kPrepThreads;
+      if (i < nj) {
+        sT[i] = tanhf(vg[u]);
+        sAng[i] = 0.f;
+      }
+    }
   }
   __syncthreads();
 
@@ -431,22 +522,33 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   RT* ddtr = static_cast<RT*>(p.ddtr.p) + b * p.ddtr.sb;
   RT* dar = static_cast<RT*>(p.dar.p) + b * p.dar.sb;
   RT* dtrr = static_cast<RT*>(p.dtrr.p) + b * p.dtrr.sb;
-  for (int i = tid; i < nt * H; i += kPrepThreads) {
+  for (int i0 = tid; i0 < nh; i0 += KU * kPrepThreads) {
+   float vx[KU], vxa[KU], vdd[KU], vdl[KU];
+#pragma unroll
+   for (int u = 0; u < KU; ++u) {
+    const int i = min(i0 + u * kPrepThreads, nh - 1), t = i / H, h = i % H, tg = t0 + t;
+    const int64_t g = ((int64_t)b * H + h) * L + tg;
+    vx[u] = ldr(dtr, (int64_t)tg * p.dtr.st + h) + p.dt_bias[h];
+    vxa[u] = ldr(ar, (int64_t)tg * p.ar.st + h);
+    vdd[u] = p.ddt ? p.ddt[g] : 0.f;
+    vdl[u] = p.dlam ? p.dlam[g] : 0.f;
+   }
+#pragma unroll
+   for (int u = 0; u < KU; ++u) {
+    const int i = i0 + u * kPrepThreads;
+    if (i >= nh) break;
     const int t = i / H, h = i % H;
     const int tg = t0 + t;
-    const int64_t g = ((int64_t)b * H + h) * L + tg;
     const float dt = sDt[i], lam = sLam[i];
-    const float x = ldr(dtr, (int64_t)tg * p.dtr.st + h) + p.dt_bias[h];
-    const float xa = ldr(ar, (int64_t)tg * p.ar.st + h);
+    const float x = vx[u];
+    const float xa = vxa[u];
     const float apre = -heavy_tail_(xa);
     const float a = fminf(apre, -p.a_floor);
     const float dadt = sDadt[i];
     const float dgt = sDgam[i] + sDscl[i];
     const float dsp = tg > 0 ? (t > 0 ? sDscl[i - H] : sDsPrev[h]) : 0.f;
-    float ddt = dadt * a + dgt * lam + dsp * (1.f - lam) + sPhi[i];
-    float dlam = dgt * dt - dsp * dt;
-    if (p.ddt) ddt += p.ddt[g];
-    if (p.dlam) dlam += p.dlam[g];
+    const float ddt = dadt * a + dgt * lam + dsp * (1.f - lam) + sPhi[i] + vdd[u];
+    const float dlam = dgt * dt - dsp * dt + vdl[u];
     // softplus'(x) = sigmoid(x), 1 above the threshold (torch: exp(x) / (exp(x) + 1))
     float dx;
     if (x > 20.f) {
@@ -465,6 +567,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     dar[(int64_t)tg * p.dar.st + h] = (RT)dxa;
     dtrr[(int64_t)tg * p.dtrr.st + h] = (RT)dtrap;
     sBias[i] = dx;
+   }
   }
   __syncthreads();
   for (int h = tid; h < H; h += kPrepThreads) {
