@@ -279,6 +279,24 @@ typedef struct m3s_transpose_args {
   void* out;
 } m3s_transpose_args;
 
+/* The gate of the LM's gated MLP. Replaces the elementwise middle of `gated_mlp`
+ * (model.py:125-140): with h = x @ fc1 split into value | gate halves of `width` columns,
+ * forward a = value * silu(gate); backward, from da, dh = [da * silu(gate) | d gate].
+ * silu(gate) is rounded to the dtype before the product, and each cotangent once, as the
+ * composed framework ops round. All tensors dense, rows of 2 * width (h, dh) or width
+ * (a, da) elements. 16-byte vectors when the width is a multiple of 16 bytes and every
+ * tensor is 16-byte aligned, else one element per thread. */
+typedef struct m3s_swiglu_args {
+  int32_t struct_size;  /* sizeof(m3s_swiglu_args) */
+  int32_t dtype;        /* M3S_DTYPE_* of every tensor */
+  int64_t rows;
+  int32_t width;
+  const void* h;        /* (rows, 2 width): value | gate */
+  void* a;              /* forward out (rows, width) */
+  const void* da;       /* backward in (rows, width) */
+  void* dh;             /* backward out (rows, 2 width) */
+} m3s_swiglu_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -318,6 +336,8 @@ int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
 int32_t m3s_norm_fwd(const m3s_norm_fwd_args* args, void* stream);
 int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
 int32_t m3s_transpose(const m3s_transpose_args* args, void* stream);
+int32_t m3s_swiglu_fwd(const m3s_swiglu_args* args, void* stream);
+int32_t m3s_swiglu_bwd(const m3s_swiglu_args* args, void* stream);
 
 #ifdef __cplusplus
 }

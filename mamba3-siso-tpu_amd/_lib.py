@@ -148,11 +148,19 @@ class TransposeArgs(C.Structure):
     ]
 
 
+class SwigluArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32), ("dtype", i32), ("rows", i64), ("width", i32),
+        ("h", vp), ("a", vp), ("da", vp), ("dh", vp),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
-           "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose")
+           "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
+           "m3s_swiglu_bwd")
 
 _lib = None
 
@@ -199,6 +207,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_norm_fwd.argtypes = [C.POINTER(NormFwdArgs), vp]
     lib.m3s_norm_bwd.restype = i32
     lib.m3s_norm_bwd.argtypes = [C.POINTER(NormBwdArgs), vp]
+    for fn in (lib.m3s_swiglu_fwd, lib.m3s_swiglu_bwd):
+        fn.restype = i32
+        fn.argtypes = [C.POINTER(SwigluArgs), vp]
     ver = lib.m3s_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")

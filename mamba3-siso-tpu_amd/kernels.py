@@ -594,6 +594,46 @@ def bcnorm_backward(xs, weights, rstds, dys, dxs):
     return dws
 
 
+def _swiglu_args(h: Tensor, width: int) -> "_lib.SwigluArgs":
+    if not h.is_cuda:
+        raise ValueError("swiglu: h must be a ROCm device tensor")
+    if h.shape[-1] != 2 * width or not h.is_contiguous():
+        raise ValueError(f"swiglu: h must be a dense (..., {2 * width}) tensor")
+    a = _lib.SwigluArgs()
+    a.struct_size = ctypes.sizeof(_lib.SwigluArgs)
+    a.dtype = _lib.dtype_code(h.dtype)
+    a.rows, a.width = h.numel() // (2 * width), width
+    a.h = h.data_ptr()
+    return a
+
+
+def swiglu_forward(h: Tensor, width: int) -> Tensor:
+    """``h`` (..., 2 width) = value | gate -> ``value * silu(gate)`` (..., width) in h's
+    dtype (one ``m3s_swiglu_fwd`` launch; ``model.py:125-140``'s elementwise middle)."""
+    a = _swiglu_args(h, width)
+    out = torch.empty(*h.shape[:-1], width, device=h.device, dtype=h.dtype)
+    a.a = out.data_ptr()
+    with torch.cuda.device(h.device):
+        _lib.check(_lib.load().m3s_swiglu_fwd(ctypes.byref(a), _lib.stream_handle(h.device)),
+                   "m3s_swiglu_fwd")
+    return out
+
+
+def swiglu_backward(h: Tensor, da: Tensor, width: int) -> Tensor:
+    """Cotangent of `swiglu_forward`: ``da`` (..., width) -> ``dh`` (..., 2 width) =
+    [d value | d gate] (one ``m3s_swiglu_bwd`` launch)."""
+    a = _swiglu_args(h, width)
+    da = da.to(h.dtype).contiguous()
+    if tuple(da.shape) != (*h.shape[:-1], width):
+        raise ValueError("swiglu: da must be (..., width)")
+    dh = torch.empty_like(h)
+    a.da, a.dh = da.data_ptr(), dh.data_ptr()
+    with torch.cuda.device(h.device):
+        _lib.check(_lib.load().m3s_swiglu_bwd(ctypes.byref(a), _lib.stream_handle(h.device)),
+                   "m3s_swiglu_bwd")
+    return dh
+
+
 def transpose_pad(w: Tensor, dtype: torch.dtype, out_rows: int) -> Tensor:
     """``w`` (R, C) -> a dense (out_rows, R) tensor of ``dtype`` holding ``w.T`` in its
     first C rows and zeros below (one ``m3s_transpose`` launch): the projection weights'

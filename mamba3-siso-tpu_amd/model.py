@@ -27,6 +27,7 @@ from typing import Any, NamedTuple, Optional
 import torch
 import torch.nn.functional as F
 
+from . import kernels as K
 from . import layer as LY
 from . import layout as L
 from .scan_prep import SISOState, zero_state
@@ -97,13 +98,32 @@ def _mm(x: Tensor, w: Tensor, dt: torch.dtype) -> Tensor:
     return x.to(dt) @ w.to(dt)
 
 
+class _GateFn(torch.autograd.Function):
+    """``value * silu(gate)`` of the fc1 product ``h`` = value | gate as one autograd node:
+    one HIP pass each way (``m3s_swiglu_fwd`` / ``m3s_swiglu_bwd``), whose backward writes
+    both halves' cotangents into one dense ``dh`` (the composed ops' backward builds them
+    apart and concatenates)."""
+
+    @staticmethod
+    def forward(ctx, h, width):
+        ctx.save_for_backward(h)
+        ctx.width = width
+        return K.swiglu_forward(h, width)
+
+    @staticmethod
+    def backward(ctx, da):
+        (h,) = ctx.saved_tensors
+        return K.swiglu_backward(h, da, ctx.width), None
+
+
 def gated_mlp(p: MLPParams, x: Tensor, mm_dtype: Optional[torch.dtype] = None) -> Tensor:
-    """``fc2(value * silu(gate))`` (``model.py:128-141``); value is the first half of
+    """``fc2(value * silu(gate))`` (``model.py:125-140``); value is the first half of
     ``fc1``'s output, gate the second (upstream's ``chunk(2, dim=-1)`` order). Products
-    run in ``mm_dtype`` (default: ``x``'s dtype); the result is in that dtype."""
+    run in ``mm_dtype`` (default: ``x``'s dtype); the result is in that dtype. The gate
+    runs as one HIP kernel each way (`_GateFn`)."""
     dt = x.dtype if mm_dtype is None else mm_dtype
-    value, gate = _mm(x, p.fc1, dt).chunk(2, dim=-1)
-    return _mm(value * F.silu(gate), p.fc2, dt)
+    h = _mm(x, p.fc1, dt)
+    return _mm(_GateFn.apply(h.contiguous(), p.fc1.shape[1] // 2), p.fc2, dt)
 
 
 def init_lm(cfg: LMConfig, key: Any = 0, dtype=torch.float32, device=None) -> LMParams:

@@ -57,6 +57,8 @@ int main(void) {
          offsetof(m3s_decode_layer_args, y));
   printf("%zu %zu %zu\n", sizeof(m3s_transpose_args), offsetof(m3s_transpose_args, in_stride),
          offsetof(m3s_transpose_args, out));
+  printf("%zu %zu %zu\n", sizeof(m3s_swiglu_args), offsetof(m3s_swiglu_args, rows),
+         offsetof(m3s_swiglu_args, dh));
   return 0;
 }
 """
@@ -80,8 +82,10 @@ int main(void) {
                             lib.NormBwdArgs.dx.offset, lib.NormBwdArgs.workspace.offset]
     assert sizes[19:22] == [ctypes.sizeof(lib.DecodeLayerArgs), lib.DecodeLayerArgs.proj_stride.offset,
                             lib.DecodeLayerArgs.y.offset]
-    assert sizes[22:] == [ctypes.sizeof(lib.TransposeArgs), lib.TransposeArgs.in_stride.offset,
-                          lib.TransposeArgs.out.offset]
+    assert sizes[22:25] == [ctypes.sizeof(lib.TransposeArgs), lib.TransposeArgs.in_stride.offset,
+                            lib.TransposeArgs.out.offset]
+    assert sizes[25:] == [ctypes.sizeof(lib.SwigluArgs), lib.SwigluArgs.rows.offset,
+                          lib.SwigluArgs.dh.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -208,3 +212,26 @@ def test_transpose_arguments_are_checked_without_a_launch(lib):
     a.out_rows, a.in_stride = 128, 50                        # row stride shorter than a row
     assert h.m3s_transpose(ctypes.byref(a), None) == lib.ERR_INVALID
     assert b"in_stride" in h.m3s_last_error()
+
+
+def test_swiglu_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_swiglu_fwd(None, None) == lib.ERR_INVALID
+    a = lib.SwigluArgs()
+    a.struct_size = 7
+    assert h.m3s_swiglu_bwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"ABI mismatch" in h.m3s_last_error()
+    a.struct_size = ctypes.sizeof(lib.SwigluArgs)
+    a.dtype, a.rows, a.width = lib.DTYPE_BF16, 16, 0           # empty width
+    a.h, a.a = 0x1000, 0x2000
+    assert h.m3s_swiglu_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"width" in h.m3s_last_error()
+    a.width = 12
+    a.a = 0x2001                                                # not bf16-aligned
+    assert h.m3s_swiglu_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"aligned" in h.m3s_last_error()
+    a.a = 0x2000                                                # backward needs da and dh
+    assert h.m3s_swiglu_bwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"NULL" in h.m3s_last_error()
+    a.rows = 0                                                  # nothing to do: no launch,
+    assert h.m3s_swiglu_bwd(ctypes.byref(a), None) == lib.OK    # NULL tensors allowed
