@@ -297,6 +297,29 @@ typedef struct m3s_swiglu_args {
   void* dh;             /* backward out (rows, 2 width) */
 } m3s_swiglu_args;
 
+/* The LM's block norms. Replaces `rms_norm` (layer.py:190-198) as the LM applies it to
+ * the residual stream (model.py:194-232), and its autograd, in f32:
+ * rstd = 1 / sqrt(mean(x^2) + eps), y = (x rstd w) cast to y_dtype;
+ * s = sum(dy w x), dx = rstd (dy w - x rstd^2 s / width) in x_dtype,
+ * dw = sum over rows of dy x rstd, summed in a fixed order. Rows are dense and aligned to
+ * 4 elements; width a multiple of 4, at most 4096. */
+typedef struct m3s_rms_args {
+  int32_t struct_size;  /* sizeof(m3s_rms_args) */
+  int32_t x_dtype;      /* M3S_DTYPE_* of x and dx (the stream) */
+  int32_t y_dtype;      /* M3S_DTYPE_* of y and dy (the normalised rows) */
+  int32_t width;
+  int64_t rows;
+  float eps;
+  const void* x;        /* (rows, width) */
+  const float* weight;  /* (width), 16-byte aligned */
+  void* y;              /* forward out (rows, width) */
+  float* rstd;          /* forward out (rows) or NULL; backward in */
+  const void* dy;       /* backward in (rows, width) */
+  void* dx;             /* backward out (rows, width) */
+  float* dweight;       /* backward out (width) */
+  void* workspace;      /* backward scratch, m3s_rms_bwd_workspace_bytes() bytes */
+} m3s_rms_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -326,6 +349,9 @@ int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nhea
 /* Bytes of m3s_norm_bwd_args.workspace: per-block gain partials (1024, 2, width) f32.
  * No counterpart in the reference. -1 on a bad width. */
 int64_t m3s_norm_bwd_workspace_bytes(int32_t width);
+/* Bytes of m3s_rms_args.workspace: per-block gain partials (1024, width) f32. No
+ * counterpart in the reference. -1 on a bad width. */
+int64_t m3s_rms_bwd_workspace_bytes(int32_t width);
 
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
@@ -338,6 +364,8 @@ int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
 int32_t m3s_transpose(const m3s_transpose_args* args, void* stream);
 int32_t m3s_swiglu_fwd(const m3s_swiglu_args* args, void* stream);
 int32_t m3s_swiglu_bwd(const m3s_swiglu_args* args, void* stream);
+int32_t m3s_rms_fwd(const m3s_rms_args* args, void* stream);
+int32_t m3s_rms_bwd(const m3s_rms_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -155,12 +155,21 @@ class SwigluArgs(C.Structure):
     ]
 
 
+class RmsArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32), ("x_dtype", i32), ("y_dtype", i32), ("width", i32),
+        ("rows", i64), ("eps", C.c_float),
+        ("x", vp), ("weight", vp), ("y", vp), ("rstd", vp), ("dy", vp), ("dx", vp),
+        ("dweight", vp), ("workspace", vp),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
-           "m3s_swiglu_bwd")
+           "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes")
 
 _lib = None
 
@@ -207,6 +216,11 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_norm_fwd.argtypes = [C.POINTER(NormFwdArgs), vp]
     lib.m3s_norm_bwd.restype = i32
     lib.m3s_norm_bwd.argtypes = [C.POINTER(NormBwdArgs), vp]
+    lib.m3s_rms_bwd_workspace_bytes.restype = i64
+    lib.m3s_rms_bwd_workspace_bytes.argtypes = [i32]
+    for fn in (lib.m3s_rms_fwd, lib.m3s_rms_bwd):
+        fn.restype = i32
+        fn.argtypes = [C.POINTER(RmsArgs), vp]
     for fn in (lib.m3s_swiglu_fwd, lib.m3s_swiglu_bwd):
         fn.restype = i32
         fn.argtypes = [C.POINTER(SwigluArgs), vp]

@@ -594,6 +594,51 @@ def bcnorm_backward(xs, weights, rstds, dys, dxs):
     return dws
 
 
+def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
+    """LM block norm: ``x`` (..., D) in f32 or bf16 -> ``(y (..., D) in out_dtype, rstd
+    (...,) f32)`` with ``y = x rstd w``, ``rstd = 1/sqrt(mean(x^2) + eps)`` in f32 (one
+    ``m3s_rms_fwd`` launch; ``layer.py:190-198`` as ``model.py:194-232`` applies it)."""
+    if not x.is_cuda:
+        raise ValueError("rms_forward: x must be a ROCm device tensor")
+    x = x.contiguous()
+    w = weight.float().contiguous()
+    d = x.shape[-1]
+    y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
+    rstd = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    a = _lib.RmsArgs()
+    a.struct_size = ctypes.sizeof(_lib.RmsArgs)
+    a.x_dtype, a.y_dtype = _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype)
+    a.width, a.rows, a.eps = d, x.numel() // d, float(eps)
+    a.x, a.weight, a.y, a.rstd = x.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr()
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().m3s_rms_fwd(ctypes.byref(a), _lib.stream_handle(x.device)),
+                   "m3s_rms_fwd")
+    return y, rstd
+
+
+def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor):
+    """Cotangents of `rms_forward`: ``dy`` (..., D) in y's dtype -> ``(dx in x's dtype,
+    dweight (D,) f32)``, dweight summed in a fixed order (one ``m3s_rms_bwd`` call)."""
+    x = x.contiguous()
+    dy = dy.contiguous()
+    w = weight.float().contiguous()
+    d = x.shape[-1]
+    dx = torch.empty_like(x)
+    dw = torch.empty(d, device=x.device, dtype=torch.float32)
+    ws = torch.empty(max(_lib.load().m3s_rms_bwd_workspace_bytes(d), 0) // 4 + 1,
+                     device=x.device, dtype=torch.float32)
+    a = _lib.RmsArgs()
+    a.struct_size = ctypes.sizeof(_lib.RmsArgs)
+    a.x_dtype, a.y_dtype = _lib.dtype_code(x.dtype), _lib.dtype_code(dy.dtype)
+    a.width, a.rows = d, x.numel() // d
+    a.x, a.weight, a.rstd, a.dy = x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr()
+    a.dx, a.dweight, a.workspace = dx.data_ptr(), dw.data_ptr(), ws.data_ptr()
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().m3s_rms_bwd(ctypes.byref(a), _lib.stream_handle(x.device)),
+                   "m3s_rms_bwd")
+    return dx, dw
+
+
 def _swiglu_args(h: Tensor, width: int) -> "_lib.SwigluArgs":
     if not h.is_cuda:
         raise ValueError("swiglu: h must be a ROCm device tensor")

@@ -228,12 +228,32 @@ def _logits(x: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
     return xn.float() @ _head(params, cfg).to(dt).float()
 
 
+class _NormFn(torch.autograd.Function):
+    """The block norm as one autograd node over ``m3s_rms_fwd`` / ``m3s_rms_bwd``: the
+    stream row in, the normalised row out in the next product's dtype, and back, each one
+    HBM pass (the backward takes dy in that dtype, with no cast pass)."""
+
+    @staticmethod
+    def forward(ctx, x, gain, eps, dt):
+        y, rstd = K.rms_forward(x, gain, eps, dt)
+        ctx.save_for_backward(x, gain, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, gain, rstd = ctx.saved_tensors
+        dx, dw = K.rms_backward(x, gain, rstd, dy)
+        return dx, dw.to(gain.dtype), None, None
+
+
 def _norm(x: Tensor, gain: Tensor, eps: float, dt: torch.dtype) -> Tensor:
     """``rms_norm(x, gain, eps)`` (``layer.py:190-198``: float32 statistics, gain after
-    scaling) returned in ``dt``, as the next product takes it. ``F.rms_norm`` on a float32
-    row is one fused kernel each way on the device, where the composed form launches about
-    seven elementwise and reduction kernels per direction."""
-    return F.rms_norm(x.float(), (x.shape[-1],), gain.float(), eps).to(dt)
+    scaling) returned in ``dt``, as the next product takes it: one HIP pass each way
+    (`_NormFn`). Rows wider than 4096 or not a multiple of 4 go through ``F.rms_norm``."""
+    d = x.shape[-1]
+    if x.is_cuda and d % 4 == 0 and d <= 4096 and x.dtype in (torch.float32, torch.bfloat16):
+        return _NormFn.apply(x, gain, eps, dt)
+    return F.rms_norm(x.float(), (d,), gain.float(), eps).to(dt)
 
 
 def _embed(table: Tensor, tokens: Tensor) -> Tensor:

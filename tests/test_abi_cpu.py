@@ -59,6 +59,8 @@ int main(void) {
          offsetof(m3s_transpose_args, out));
   printf("%zu %zu %zu\n", sizeof(m3s_swiglu_args), offsetof(m3s_swiglu_args, rows),
          offsetof(m3s_swiglu_args, dh));
+  printf("%zu %zu %zu\n", sizeof(m3s_rms_args), offsetof(m3s_rms_args, x),
+         offsetof(m3s_rms_args, workspace));
   return 0;
 }
 """
@@ -84,8 +86,10 @@ int main(void) {
                             lib.DecodeLayerArgs.y.offset]
     assert sizes[22:25] == [ctypes.sizeof(lib.TransposeArgs), lib.TransposeArgs.in_stride.offset,
                             lib.TransposeArgs.out.offset]
-    assert sizes[25:] == [ctypes.sizeof(lib.SwigluArgs), lib.SwigluArgs.rows.offset,
-                          lib.SwigluArgs.dh.offset]
+    assert sizes[25:28] == [ctypes.sizeof(lib.SwigluArgs), lib.SwigluArgs.rows.offset,
+                            lib.SwigluArgs.dh.offset]
+    assert sizes[28:] == [ctypes.sizeof(lib.RmsArgs), lib.RmsArgs.x.offset,
+                          lib.RmsArgs.workspace.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -235,3 +239,25 @@ def test_swiglu_arguments_are_checked_without_a_launch(lib):
     assert b"NULL" in h.m3s_last_error()
     a.rows = 0                                                  # nothing to do: no launch,
     assert h.m3s_swiglu_bwd(ctypes.byref(a), None) == lib.OK    # NULL tensors allowed
+
+
+def test_rms_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_rms_bwd_workspace_bytes(768) == 1024 * 768 * 4
+    assert h.m3s_rms_bwd_workspace_bytes(0) == -1
+    a = lib.RmsArgs()
+    a.struct_size = ctypes.sizeof(lib.RmsArgs)
+    a.x_dtype, a.y_dtype, a.width, a.rows, a.eps = lib.DTYPE_F32, lib.DTYPE_BF16, 770, 8, 1e-5
+    a.x, a.weight, a.y = 0x1000, 0x2000, 0x3000
+    assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.ERR_INVALID       # width % 4
+    assert b"width" in h.m3s_last_error()
+    a.width = 8192
+    assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.ERR_INVALID       # too wide
+    a.width = 768
+    assert h.m3s_rms_bwd(ctypes.byref(a), None) == lib.ERR_INVALID       # no rstd / dy / dx
+    assert b"NULL" in h.m3s_last_error()
+    a.x = 0x1004                                                          # f32 rows need 16 B
+    assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"aligned" in h.m3s_last_error()
+    a.rows = 0
+    assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.OK
