@@ -571,8 +571,11 @@ struct Fwd2Cfg {
   static constexpr int SZ_V = C * P * 2;          // one v or z tile
   static constexpr int SZ_S = P * LDK * 2;
   static constexpr int SZ_O = C * LDO * 4;
-  static constexpr int SZ_SC = (5 * C + 2 * N) * 4;  // sA, sExpA, sFac, sCoef, sQb, sKb, sDk
-  static constexpr int LDS_BYTES = SZ_K + 2 * SZ_V + SZ_S + SZ_O + SZ_SC;
+  // sQb, sKb, then two buffers of the row scalars [A, 2^A, 2^(A_last - A), coef, dk]
+  static constexpr int SZ_SC = (10 * C + 2 * N) * 4;
+  // k-hat tiles and row scalars are double-buffered: chunk c+1's are written at the end
+  // of chunk c's phase B, while the products of chunk c read the other buffer
+  static constexpr int LDS_BYTES = 2 * SZ_K + 2 * SZ_V + SZ_S + SZ_O + SZ_SC;
   static_assert(N % 64 == 0 && P == 64 && C % 64 == 0, "tile shape");
   static_assert(NW % PB == 0 && (PB * NB) % NW == 0, "state tiles split evenly over waves");
   static_assert(VPL * NT * 16 == C * P * 2, "v / z pieces split evenly over the lanes");
@@ -615,18 +618,23 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 
   __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
   auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
-  bf16* sK = reinterpret_cast<bf16*>(smem);
-  bf16* sV = reinterpret_cast<bf16*>(smem + opq(F::SZ_K));                  // v tile
-  bf16* sZ = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + F::SZ_V));        // z tile
-  bf16* sS = reinterpret_cast<bf16*>(smem + opq(F::SZ_K + 2 * F::SZ_V));
-  float* sOut = reinterpret_cast<float*>(smem + opq(F::SZ_K + 2 * F::SZ_V + F::SZ_S));
-  float* sA = reinterpret_cast<float*>(smem + opq(F::SZ_K + 2 * F::SZ_V + F::SZ_S + F::SZ_O));
-  float* sExpA = sA + C;   // 2^{A_t}
-  float* sFac = sExpA + C; // 2^{A_last - A_t}
-  float* sCoef = sFac + C; // D + gamma_t (u_t . w_t)
-  float* sQb = sCoef + C;
+  bf16* sK2 = reinterpret_cast<bf16*>(smem);                                // [2] k-hat tiles
+  bf16* sV = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_K));              // v tile
+  bf16* sZ = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_K + F::SZ_V));    // z tile
+  bf16* sS = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_K + 2 * F::SZ_V));
+  float* sOut = reinterpret_cast<float*>(smem + opq(2 * F::SZ_K + 2 * F::SZ_V + F::SZ_S));
+  float* sQb = reinterpret_cast<float*>(smem + opq(2 * F::SZ_K + 2 * F::SZ_V + F::SZ_S + F::SZ_O));
   float* sKb = sQb + N;
-  float* sDk = sKb + N;    // 2^{A_{16 s + 15} - A_j}, s = j's strip: a key row's decay to its strip end
+  float* sSc2 = sKb + N;   // [2] row scalar blocks, laid out as in `scalars` below
+  // buffer b's k-hat tile, and its row scalars: A_t, 2^{A_t}, 2^{A_last - A_t},
+  // D + gamma_t (u_t . w_t), and 2^{A_{16 s + 15} - A_j} (s = j's strip: a key row's
+  // decay to its strip end)
+  auto khat = [&](int b) { return sK2 + b * (F::SZ_K / 2); };
+  struct Scalars { float *A, *ExpA, *Fac, *Coef, *Dk; };
+  auto scalars = [&](int b) {
+    float* base = sSc2 + b * 5 * C;
+    return Scalars{base, base + C, base + 2 * C, base + 3 * C, base + 4 * C};
+  };
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -816,7 +824,10 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   float coefv = 0.f;             // D + gamma_t (u_t . w_t) of this lane's row
   float sAv[F::E], sEv[F::E], sFv[F::E], sDv[F::E];   // wave 0: A_t, 2^{A_t}, 2^{A_last - A_t},
                                                      // 2^{A_strip_end - A_t}
-  auto stage_write = [&]() {
+  auto stage_write = [&](int buf) {
+    bf16* sK = khat(buf);
+    const Scalars sc = scalars(buf);
+    float *sA = sc.A, *sExpA = sc.ExpA, *sFac = sc.Fac, *sCoef = sc.Coef, *sDk = sc.Dk;
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
@@ -947,6 +958,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 
   // ---- phase G: scores, intra + inter + diagonal output, state update -------------
   auto products = [&](int c) {
+    const bf16* sK = khat(c & 1);
+    const Scalars sc = scalars(c & 1);
+    const float *sA = sc.A, *sExpA = sc.ExpA, *sFac = sc.Fac, *sCoef = sc.Coef, *sDk = sc.Dk;
     // lane index re-derived opaquely: the per-lane LDS addresses below are recomputed
     // each chunk instead of being hoisted out of the chunk loop (and spilled)
     int ln = threadIdx.x;
@@ -1176,6 +1190,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   vm_wait_all();
   __syncthreads();  // sQb / sKb
   stage_regs();     // chunk 0
+  stage_write(0);
   prefetch_qk(1);
   // phase A of chunk c (and of the tail): out(c-1) to sOut, S(c) to sS
   auto phase_a = [&](int c) {
@@ -1190,7 +1205,6 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   for (int c = 0; c < nc; ++c) {
     // ---------------- phase A: also chunk c's k-hat and scalars, v of c, z of c-1 --------
     phase_a(c);
-    stage_write();
     write_vz(c == nc - 1);   // (zeros where there is no such chunk)
     __syncthreads();
     // ---------------- phase B: epilogue of c-1, products of c, then chunk c+1's rotation
@@ -1201,6 +1215,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     if (c > 0 && light) epilogue(c - 1);
     products(c);
     stage_regs();
+    stage_write((c + 1) & 1);   // chunk c+1's k-hat rows and scalars, into the other buffer
     __builtin_amdgcn_sched_barrier(0);
     prefetch_qk(c + 2);
     __builtin_amdgcn_sched_barrier(0);
