@@ -1025,7 +1025,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
       }
     }
   };
-  auto prefetch_rest = [&](int c) {
+  // part 1: v, dy, z rows; part 2: ybar rows, the state and the row scalars
+  auto prefetch_rest = [&](int c, int part) {
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int tid = ln, lane = ln & 63;
@@ -1037,15 +1038,20 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int t = 2 * tp + e;
-          rv[r][e] = gld<vec>(vg, (uint32_t)(c * C * p.v_st * 2) + (uint32_t)(t * p.v_st + p0) * 2);
-          rdy[r][e] = gld<vec>(dyg, (uint32_t)(c * C * p.dy_st * 2) + (uint32_t)(t * p.dy_st + p0) * 2);
-          rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
+          if (part & 1) {
+            rv[r][e] = gld<vec>(vg, (uint32_t)(c * C * p.v_st * 2) + (uint32_t)(t * p.v_st + p0) * 2);
+            rdy[r][e] = gld<vec>(dyg, (uint32_t)(c * C * p.dy_st * 2) + (uint32_t)(t * p.dy_st + p0) * 2);
+            rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
+          }
+          if (part & 2) {
 #pragma unroll
-          for (int i = 0; i < VEC; i += 4)
-            ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
+            for (int i = 0; i < VEC; i += 4)
+              ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
+          }
         }
       }
     }
+    if (!(part & 2)) return;
 #pragma unroll
     for (int r = 0; r < F::SR; ++r) {
       const int f = tid + r * NT;
@@ -1063,7 +1069,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   };
 
   prefetch_qk(nc - 1);
-  prefetch_rest(nc - 1);
+  prefetch_rest(nc - 1, 3);
   __syncthreads();
 
   for (int c = nc - 1; c >= 0; --c) {
@@ -1540,6 +1546,12 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             sDA[2 * tp + e] = dA;
             dsc_r[(uint32_t)(t0 + 2 * tp + e)] = dsc;
           }
+          // The previous chunk's v, dy and z rows, for its phase L, into registers this
+          // row has freed: the loads overlap the second row's arithmetic. Issued on every
+          // iteration (chunk 0 reloads itself on the last one): a conditional prefetch
+          // would keep the consumed registers alive through the whole loop body for the
+          // skipped path. The rest waits for phase S.
+          if (r == F::QKR - 1 && e == 0) prefetch_rest(c > 0 ? c - 1 : 0, 1);
         }
         // The lanes that share j0 differ in lane bits log2(QKG)..5. A transposing
         // butterfly over those bits halves the entries a lane keeps each round (it sends
@@ -1571,11 +1583,10 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     }
     __syncthreads();
 
-    // the previous chunk's v, dy, z, ybar, state. Issued on every iteration (chunk 0
-    // reloads itself on the last one): a conditional prefetch would keep the consumed
-    // registers alive through the whole loop body for the skipped path.
+    // the previous chunk's q, k, phi rows for its phase L, into the registers phase R
+    // has just consumed, and its ybar rows, state and row scalars
     prefetch_qk(c > 0 ? c - 1 : 0);
-    prefetch_rest(c > 0 ? c - 1 : 0);
+    prefetch_rest(c > 0 ? c - 1 : 0, 2);
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
       int ln = threadIdx.x;
