@@ -1574,6 +1574,9 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           }
           base += up ? half : 0;
         }
+        // the previous chunk's ybar rows, state and row scalars, into registers the
+        // butterfly has freed
+        if (r == F::QKR - 1) prefetch_rest(c > 0 ? c - 1 : 0, 2);
 #pragma unroll
         for (int k = 0; k < BFIN; ++k) {
           const int idx = base + k, u = idx & 3;
@@ -1584,9 +1587,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     __syncthreads();
 
     // the previous chunk's q, k, phi rows for its phase L, into the registers phase R
-    // has just consumed, and its ybar rows, state and row scalars
+    // has just consumed
     prefetch_qk(c > 0 ? c - 1 : 0);
-    prefetch_rest(c > 0 ? c - 1 : 0, 2);
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
       int ln = threadIdx.x;
