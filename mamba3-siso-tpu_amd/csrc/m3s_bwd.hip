@@ -1550,7 +1550,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           // row has freed: the loads overlap the second row's arithmetic. Issued on every
           // iteration (chunk 0 reloads itself on the last one): a conditional prefetch
           // would keep the consumed registers alive through the whole loop body for the
-          // skipped path. The rest waits for phase S.
+          // skipped path. The rest follows the bias butterfly.
           if (r == F::QKR - 1 && e == 0) prefetch_rest(c > 0 ? c - 1 : 0, 1);
         }
         // The lanes that share j0 differ in lane bits log2(QKG)..5. A transposing
