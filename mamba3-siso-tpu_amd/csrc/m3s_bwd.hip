@@ -827,9 +827,10 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
 //    strip) is consumed by its products as soon as it is built: only two tiles live.
 //  * Global traffic through per-(b, h) buffer descriptors (32-bit offsets), and the
 //    lane index re-derived per phase, so nothing spills.
-//  * v, dy, z, ybar and the chunk state of the previous chunk are prefetched after the
-//    pullback (their registers never coexist with the product accumulators or the
-//    pullback's); q, k, phi are loaded at the start of the chunk that uses them.
+//  * The previous chunk's raw rows are prefetched during the pullback, into registers
+//    it frees as it goes: v, dy, z after its first row, ybar and the chunk state after
+//    the bias butterfly, q, k, phi after the pullback. None of them coexists with the
+//    product accumulators. Phase R reloads q, k, phi before the staging barrier.
 // ===================================================================================
 
 template <int C, int N, int P>
