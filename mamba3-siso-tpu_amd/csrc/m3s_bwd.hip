@@ -1076,8 +1076,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   for (int c = nc - 1; c >= 0; --c) {
     const int t0 = c * C;
     // ============ phase L: raw -> LDS (q~, khat, g, v, S^T), dz, dqk, uw ==============
-    // Both register prefetches of this chunk (q/k/phi/scale and v/dy/z/ybar/state) were
-    // issued in the previous iteration's tail; the second set is consumed first.
+    // This chunk's raw rows were prefetched during the previous iteration's pullback and
+    // tail, v/dy/z first and q/k/phi/scale last; they are consumed in that order.
     {
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
