@@ -829,7 +829,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
 //    lane index re-derived per phase, so nothing spills.
 //  * The previous chunk's raw rows are prefetched during the pullback, into registers
 //    it frees as it goes: v, dy, z after its first row, ybar and the chunk state after
-//    the bias butterfly, q, k, phi after the pullback. None of them coexists with the
+//    the bias butterfly, q, k, phi before the pullback's closing barrier. None of them coexists with the
 //    product accumulators. Phase R reloads q, k, phi before the staging barrier.
 // ===================================================================================
 
@@ -1585,11 +1585,11 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         }
       }
     }
+    // the previous chunk's q, k, phi rows for its phase L, into the registers phase R
+    // has just consumed: in flight during the barrier wait
+    prefetch_qk(c > 0 ? c - 1 : 0);
     __syncthreads();
 
-    // the previous chunk's q, k, phi rows for its phase L, into the registers phase R
-    // has just consumed
-    prefetch_qk(c > 0 ? c - 1 : 0);
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
       int ln = threadIdx.x;
