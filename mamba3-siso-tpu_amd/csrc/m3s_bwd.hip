@@ -1453,7 +1453,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           __builtin_amdgcn_sched_barrier(0);   // rows one after the other: fewer live values
-          float dA = 0.f, dsc = 0.f;
+          // dA = sum(q~ . dq~) - sc * sum(k~ . dk^) over the row; dsc is the second sum
+          float dqq = 0.f, dsc = 0.f;
           if (valid) {
             const int t = 2 * tp + e;
             const uint32_t o = (uint32_t)(t * N + j0) * 2;
@@ -1491,7 +1492,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               const float klo = wlo * cs - whi * sn, khi = whi * cs + wlo * sn;
               const float dqlo = dql[i / 4][i % 4], dqhi = dqh[i / 4][i % 4];
               const float dklo = dkl[i / 4][i % 4], dkhi = dkh[i / 4][i % 4];
-              dA += qlo * dqlo + qhi * dqhi - (klo * sc) * dklo - (khi * sc) * dkhi;
+              dqq += qlo * dqlo + qhi * dqhi;
               dsc += dklo * klo + dkhi * khi;
               const float dtlo = dklo * sc, dthi = dkhi * sc;   // d k~
               // R^T = R(-phi): lo' = lo cos + hi sin, hi' = hi cos - lo sin
@@ -1541,10 +1542,10 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             gst<vec>(dwg, sqk + o, dw0);
             gst<vec>(dwg, sqk + o + 2 * H2, dw1);
           }
-          dA = group_sum<F::QKG>(dA);
+          dqq = group_sum<F::QKG>(dqq);
           dsc = group_sum<F::QKG>(dsc);
           if (valid && j0 == 0) {
-            sDA[2 * tp + e] = dA;
+            sDA[2 * tp + e] = dqq - sScl[2 * tp + e] * dsc;
             dsc_r[(uint32_t)(t0 + 2 * tp + e)] = dsc;
           }
           // The previous chunk's v, dy and z rows, for its phase L, into registers this
