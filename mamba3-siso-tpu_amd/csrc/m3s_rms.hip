@@ -74,7 +74,10 @@ __global__ void __launch_bounds__(kRmsThreads) rms_fwd_kernel(const TX* __restri
   if (lane == 0 && rstd) rstd[r] = rs;
 }
 
-template <typename TX, typename TY>
+// MAXK >= D / 256 column passes per lane (4, 8 or 16 by width): the column partials
+// take 4 * MAXK registers, which sets the occupancy. Up to MAXK = 8 the row's x and dy
+// stay in registers for the second pass; past that it reads them again.
+template <typename TX, typename TY, int MAXK>
 __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restrict__ x,
                                                               const float* __restrict__ w,
                                                               const float* __restrict__ rstd,
@@ -82,23 +85,29 @@ __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restri
                                                               TX* __restrict__ dx,
                                                               float* __restrict__ part,
                                                               int64_t M, int D) {
-  __shared__ float sAcc[kRmsWaves * 4096];
+  extern __shared__ float sAcc[];   // [kRmsWaves][D]: sized at launch, for occupancy
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nk = D / 256 + ((4 * lane) < (D % 256) ? 1 : 0);   // this lane's column passes
-  f32x4 acc[kRmsMaxChunks];
+  f32x4 acc[MAXK];
 #pragma unroll
-  for (int k = 0; k < kRmsMaxChunks; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < MAXK; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int64_t nw = (int64_t)gridDim.x * kRmsWaves;
   for (int64_t r = (int64_t)blockIdx.x * kRmsWaves + wave; r < M; r += nw) {
     const TX* xr = x + r * D;
     const TY* dr = dy + r * D;
     const float rs = rstd[r];
+    constexpr bool HOLD = MAXK <= 8;
+    f32x4 hv[HOLD ? MAXK : 1], hd[HOLD ? MAXK : 1];
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < kRmsMaxChunks; ++k) {
+    for (int k = 0; k < MAXK; ++k) {
       if (k < nk) {
         const int c = 4 * (lane + 64 * k);
         const f32x4 v = ld4(xr + c), d = ld4(dr + c);
+        if constexpr (HOLD) {
+          hv[k] = v;
+          hd[k] = d;
+        }
         const f32x4 g = *reinterpret_cast<const f32x4*>(w + c);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -111,10 +120,11 @@ __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restri
     const float cr = rs * rs * s / (float)D;
     TX* xo = dx + r * D;
 #pragma unroll
-    for (int k = 0; k < kRmsMaxChunks; ++k) {
+    for (int k = 0; k < MAXK; ++k) {
       if (k < nk) {
         const int c = 4 * (lane + 64 * k);
-        const f32x4 v = ld4(xr + c), d = ld4(dr + c);
+        const f32x4 v = HOLD ? hv[HOLD ? k : 0] : ld4(xr + c);
+        const f32x4 d = HOLD ? hd[HOLD ? k : 0] : ld4(dr + c);
         const f32x4 g = *reinterpret_cast<const f32x4*>(w + c);
         f32x4 o;
 #pragma unroll
@@ -125,14 +135,14 @@ __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restri
   }
   // the block's waves in a fixed order, then one partial row per block
 #pragma unroll
-  for (int k = 0; k < kRmsMaxChunks; ++k) {
-    if (k < nk) *reinterpret_cast<f32x4*>(sAcc + wave * 4096 + 4 * (lane + 64 * k)) = acc[k];
+  for (int k = 0; k < MAXK; ++k) {
+    if (k < nk) *reinterpret_cast<f32x4*>(sAcc + wave * D + 4 * (lane + 64 * k)) = acc[k];
   }
   __syncthreads();
   for (int c = threadIdx.x; c < D; c += kRmsThreads) {
     float t = 0.f;
 #pragma unroll
-    for (int v = 0; v < kRmsWaves; ++v) t += sAcc[v * 4096 + c];
+    for (int v = 0; v < kRmsWaves; ++v) t += sAcc[v * D + c];
     part[(int64_t)blockIdx.x * D + c] = t;
   }
 }
@@ -194,10 +204,15 @@ template <typename TX, typename TY>
 static void launch_rms_bwd(const m3s_rms_args* a, hipStream_t s) {
   const int nblk = (int)std::min<int64_t>(kRmsBwdBlocks, (a->rows + kRmsWaves - 1) / kRmsWaves);
   float* part = static_cast<float*>(a->workspace);
-  hipLaunchKernelGGL((rms_bwd_kernel<TX, TY>), dim3(nblk), dim3(kRmsThreads), 0, s,
-                     static_cast<const TX*>(a->x), a->weight, a->rstd,
-                     static_cast<const TY*>(a->dy), static_cast<TX*>(a->dx), part, a->rows,
-                     a->width);
+  const size_t lds = (size_t)kRmsWaves * a->width * sizeof(float);
+  const auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(nblk), dim3(kRmsThreads), lds, s, static_cast<const TX*>(a->x),
+                       a->weight, a->rstd, static_cast<const TY*>(a->dy), static_cast<TX*>(a->dx),
+                       part, a->rows, a->width);
+  };
+  if (a->width <= 1024) go(rms_bwd_kernel<TX, TY, 4>);
+  else if (a->width <= 2048) go(rms_bwd_kernel<TX, TY, 8>);
+  else go(rms_bwd_kernel<TX, TY, kRmsMaxChunks>);
   hipLaunchKernelGGL(rms_dw_kernel, dim3((a->width + 63) / 64), dim3(kRmsThreads), 0, s, part,
                      a->dweight, nblk, a->width);
 }

@@ -20,7 +20,7 @@ def maxrel(a, b):
     return ((a - b).abs().max() / b.abs().max()).item()
 
 
-@pytest.mark.parametrize("rows,d", [(4096, 768), (333, 1024), (5, 12), (64, 4096)])
+@pytest.mark.parametrize("rows,d", [(4096, 768), (333, 1024), (5, 12), (100, 1536), (64, 4096)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
                                      (torch.bfloat16, torch.bfloat16)])
 def test_norm_matches_torch_and_float64(m3, dev, rows, d, xdt, ydt):
