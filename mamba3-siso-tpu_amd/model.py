@@ -302,6 +302,14 @@ def zero_states(cfg: LMConfig, batch: int, dtype=torch.float32, device=None) -> 
     return out
 
 
+def _add_residual(x: Tensor, y: Tensor) -> Tensor:
+    """``x + y`` for a one-token step: a block output of another dtype is cast to the
+    stream's first. That is the cast the mixed-dtype add does inside, so the sum is the
+    same; PyTorch's mixed-dtype add kernel needs scratch memory and costs ~40 us per
+    launch on ROCm whatever its size, against a few us for a cast and a plain add."""
+    return x + (y if y.dtype == x.dtype else y.to(x.dtype))
+
+
 def lm_decode_step(params: LMParams, token: Tensor, states: list, cfg: LMConfig,
                    interpret: Any = False):
     """One token through the stack (``model.py:244-296``): ``(B,)`` -> ``((B, vocab)
@@ -316,7 +324,7 @@ def lm_decode_step(params: LMParams, token: Tensor, states: list, cfg: LMConfig,
         y, st = LY.mamba3_siso_decode_step(b.siso, _norm(x, b.norm_gain, c.norm_eps, dt), c,
                                            states[i])
         out_states.append(st)
-        x = x + y
+        x = _add_residual(x, y)
         if b.mlp is not None:
-            x = x + gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, c.norm_eps, dt), dt)
+            x = _add_residual(x, gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, c.norm_eps, dt), dt))
     return _logits(x, params, cfg), out_states
