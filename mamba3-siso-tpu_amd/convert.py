@@ -1,28 +1,33 @@
-"""Weight layout conversion between an upstream torch ``state_dict`` and `SISOParams`.
+"""Upstream torch checkpoints <-> this package's parameter trees.
 
-Restates ``convert.py:58-176`` of the reference (host-side format conversion, not a
-compute path): transpose the two linears from torch's ``(out, in)`` to ``(in, out)``;
-apply the de-interleave permutation to every tensor on the state axis (the B and C
-column blocks of ``in_proj``, the two norm gains, the two biases); squeeze the MIMO
-rank of the biases (``(H, 1, N)`` -> ``(H, N)``). ``dt_bias``, ``D`` and ``out_proj``
-pass through. The names ``torch_to_jax`` / ``jax_to_torch`` are kept so code written
-against the reference runs unchanged; ``params_from_state_dict`` /
-``state_dict_from_params`` are the descriptive aliases.
+The on-disk format is upstream's (``convert.py:58-356`` of the reference reads and
+writes the same one): the two linears are stored torch-style ``(out, in)``, the
+state-axis tensors in the interleaved rotary layout, the B/C biases with a MIMO rank
+axis of 1. The kernels want ``(in, out)`` linears and the permuted half-split rotary
+layout (``layout.py:299-337``).
 
-Whole released checkpoints (``convert.py:179-356``): `config_from_hf` reads a released
-``config.json`` (vocab padding, chunk override, MIMO / hybrid / ngroups refusal) and
-`load_lm_state_dict` maps a ``MambaLMHeadModel`` state dict (``backbone.``-prefixed keys)
-onto `model.LMParams`, widening bf16 tensors on the torch side. `load_pretrained` reads a
-LOCAL checkpoint directory (``config.json`` plus ``model.safetensors`` or
-``pytorch_model.bin``); there is no network download.
+Design: every difference between the two sides is data, not code. `MIXER_LEAVES` lists,
+per `SISOParams` field, its torch key(s) and the three things that can happen to it --
+a transpose, the state-axis permutation (on the last axis, or on the B and C column
+blocks of the projection), and the rank axis. One pair of functions (`_leaf_in`,
+`_leaf_out`) applies a table row in either direction, and the whole-model mapping is a
+second table (`BLOCK_LEAVES`, `TOP_LEAVES`) of `LMParams` paths to released key names,
+walked by the same loop for import and export. Released ``config.json`` files are read
+through a field table and a list of refusal rules.
+
+The reference's names are kept (``torch_to_jax`` / ``jax_to_torch`` /
+``config_from_state_dict`` / ``config_from_hf`` / ``load_lm_state_dict`` /
+``load_pretrained``) so code written against it runs unchanged.
+``params_from_state_dict`` / ``state_dict_from_params`` are descriptive aliases.
+`load_pretrained` reads a LOCAL directory only; there is no network download.
 """
 
 from __future__ import annotations
 
-from typing import Any, Mapping
-
+import dataclasses
 import json
 import os
+from typing import Any, Mapping, Optional
 
 import numpy as np
 import torch
@@ -31,100 +36,134 @@ from . import layout as LY
 from .layer import SISOConfig, SISOParams
 
 
-def _to_numpy(x: Any) -> np.ndarray:
-    """``convert.py:39-51``: torch tensors (bf16 included) widen on the torch side."""
-    if hasattr(x, "detach"):
-        x = x.detach().cpu()
-        if hasattr(x, "float"):
-            x = x.float()
-    return np.asarray(x, dtype=np.float32)
+# ------------------------------------------------------------------------------------
+# one layer (the "mixer")
+# ------------------------------------------------------------------------------------
 
 
-def _perm(n: int) -> np.ndarray:
-    return LY.deinterleave_perm(n).numpy()
+@dataclasses.dataclass(frozen=True)
+class Leaf:
+    """How one `SISOParams` field is stored in an upstream state dict.
+
+    ``keys``: accepted torch names, the first one written on export. ``transpose``:
+    torch keeps ``(out, in)``. ``perm``: where the state-axis permutation applies --
+    ``"last"`` (the trailing N axis) or ``"bc_blocks"`` (the B and C column blocks of the
+    projection). ``rank_axis``: stored as ``(H, rank, N)`` with rank 1 (SISO)."""
+
+    field: str
+    keys: tuple
+    transpose: bool = False
+    perm: Optional[str] = None
+    rank_axis: bool = False
+
+
+MIXER_LEAVES = (
+    Leaf("in_proj", ("in_proj.weight",), transpose=True, perm="bc_blocks"),
+    Leaf("out_proj", ("out_proj.weight",), transpose=True),
+    Leaf("dt_bias", ("dt_bias",)),
+    Leaf("b_norm_weight", ("B_norm.weight", "B_norm_weight"), perm="last"),
+    Leaf("c_norm_weight", ("C_norm.weight", "C_norm_weight"), perm="last"),
+    Leaf("b_bias", ("B_bias",), perm="last", rank_axis=True),
+    Leaf("c_bias", ("C_bias",), perm="last", rank_axis=True),
+    Leaf("d_skip", ("D",)),
+)
+assert tuple(leaf.field for leaf in MIXER_LEAVES) == SISOParams._fields
+
+
+def _f32(x: Any) -> np.ndarray:
+    """A float32 numpy copy of a tensor or array. Torch tensors are widened by torch
+    first, so bf16 checkpoints (which numpy cannot represent) convert too."""
+    if isinstance(x, torch.Tensor):
+        x = x.detach().to("cpu", torch.float32).numpy()
+    return np.array(x, dtype=np.float32, copy=True)
+
+
+def _state_index(leaf: Leaf, cfg: SISOConfig, width: int) -> np.ndarray:
+    """Index array over the permuted axis: position i of our layout reads position
+    ``idx[i]`` of upstream's. Only the B and C blocks move for ``bc_blocks``."""
+    n = cfg.d_state
+    perm = LY.deinterleave_perm(n).numpy()
+    if leaf.perm == "last":
+        return perm
+    idx = np.arange(width)
+    for start in (2 * cfg.d_inner, 2 * cfg.d_inner + n):
+        idx[start:start + n] = start + perm
+    return idx
+
+
+def _leaf_in(leaf: Leaf, raw: np.ndarray, cfg: SISOConfig) -> np.ndarray:
+    """Upstream array -> ours, per the table row."""
+    a = raw
+    if leaf.rank_axis and a.ndim == 3:
+        if a.shape[1] != 1:
+            raise ValueError(f"{leaf.keys[0]} has shape {a.shape}: mimo_rank={a.shape[1]}, "
+                             "but only rank-1 (SISO) layers convert")
+        a = a[:, 0, :]
+    if leaf.transpose:
+        a = a.T
+    if leaf.perm is not None:
+        a = a[..., _state_index(leaf, cfg, a.shape[-1])]
+    return np.ascontiguousarray(a)
+
+
+def _leaf_out(leaf: Leaf, ours: np.ndarray, cfg: SISOConfig) -> np.ndarray:
+    """Ours -> upstream array: the inverse of `_leaf_in`."""
+    a = ours
+    if leaf.perm is not None:
+        a = a[..., np.argsort(_state_index(leaf, cfg, a.shape[-1]))]
+    if leaf.transpose:
+        a = a.T
+    if leaf.rank_axis:
+        a = a[:, None, :]
+    return np.ascontiguousarray(a)
+
+
+def _lookup(sd: Mapping[str, Any], names, where: str = ""):
+    for name in names:
+        if name in sd:
+            return sd[name]
+    raise KeyError(f"state dict{where} has none of {list(names)}")
 
 
 def config_from_state_dict(sd: Mapping[str, Any], headdim: int = 64, **overrides) -> SISOConfig:
-    """``convert.py:58-89``: ``d_model``/``d_in_proj`` from ``in_proj.weight``,
-    ``d_state``/``nheads`` from ``B_bias``; ``headdim`` must be supplied."""
-    in_proj = _to_numpy(sd["in_proj.weight"])
-    d_in_proj, d_model = in_proj.shape
-    b_bias = _to_numpy(sd["B_bias"])
-    nheads, d_state = b_bias.shape[0], b_bias.shape[-1]
-    d_inner = nheads * headdim
-    if d_inner % d_model != 0:
-        raise ValueError(
-            f"nheads*headdim = {d_inner} is not a multiple of d_model = {d_model}; "
-            f"headdim={headdim} is probably wrong for this checkpoint")
-    cfg = SISOConfig(d_model=d_model, d_state=d_state, headdim=headdim,
-                     expand=d_inner // d_model, **overrides)
-    if cfg.d_in_proj != d_in_proj:
-        raise ValueError(
-            f"in_proj width {d_in_proj} does not match the config's {cfg.d_in_proj}. "
-            f"This checkpoint may be MIMO (mimo_rank > 1), which is out of scope, or "
-            f"headdim is not {headdim}.")
+    """Infer a `SISOConfig` from a layer's torch state dict (``convert.py:58-89``).
+
+    ``in_proj.weight`` gives ``d_model`` and the projection width, ``B_bias`` gives
+    ``nheads`` and ``d_state``; ``headdim`` cannot be read off the weights and must be
+    supplied. The projection width is then checked against the config, which catches a
+    wrong ``headdim`` and MIMO checkpoints (whose B/C blocks are rank times wider)."""
+    rows, d_model = tuple(_lookup(sd, ("in_proj.weight",)).shape)
+    bias_shape = tuple(_lookup(sd, ("B_bias",)).shape)
+    nheads, d_state = bias_shape[0], bias_shape[-1]
+    expand, rem = divmod(nheads * headdim, d_model)
+    if rem or expand == 0:
+        raise ValueError(f"{nheads} heads of headdim {headdim} give d_inner={nheads * headdim}, "
+                         f"not a whole multiple of d_model={d_model}: wrong headdim?")
+    cfg = SISOConfig(d_model=d_model, d_state=d_state, headdim=headdim, expand=expand, **overrides)
+    if cfg.d_in_proj != rows:
+        raise ValueError(f"in_proj.weight has {rows} output rows; a SISO layer with this "
+                         f"config has {cfg.d_in_proj}. MIMO layers (rank > 1) are not "
+                         f"supported, and a wrong headdim (here {headdim}) also shows up this way")
     return cfg
 
 
 def torch_to_jax(sd: Mapping[str, Any], cfg: SISOConfig, dtype=torch.float32,
                  device=None) -> SISOParams:
-    """``convert.py:92-149``: a torch ``state_dict`` -> `SISOParams` (permuted layout).
-
-    Norm gains are accepted as ``B_norm.weight`` (upstream) or ``B_norm_weight``.
-    """
-    n = cfg.d_state
-    perm = _perm(n)
-    in_proj = _to_numpy(sd["in_proj.weight"]).T.copy()
-    out_proj = _to_numpy(sd["out_proj.weight"]).T.copy()
-    b_start = 2 * cfg.d_inner
-    for start in (b_start, b_start + n):
-        in_proj[:, start:start + n] = in_proj[:, start:start + n][:, perm]
-
-    def norm_gain(prefix: str) -> np.ndarray:
-        for key in (f"{prefix}_norm.weight", f"{prefix}_norm_weight"):
-            if key in sd:
-                return _to_numpy(sd[key])
-        raise KeyError(f"missing {prefix} norm weight ({prefix}_norm.weight)")
-
-    def bias(prefix: str) -> np.ndarray:
-        arr = _to_numpy(sd[f"{prefix}_bias"])
-        if arr.ndim == 3:
-            if arr.shape[1] != 1:
-                raise ValueError(f"{prefix}_bias has mimo_rank {arr.shape[1]}; MIMO is out of scope")
-            arr = arr[:, 0]
-        return arr
-
-    def t(a):
-        return torch.as_tensor(np.ascontiguousarray(a), dtype=dtype, device=device)
-
-    return SISOParams(
-        in_proj=t(in_proj), out_proj=t(out_proj),
-        dt_bias=t(_to_numpy(sd["dt_bias"])),
-        b_norm_weight=t(norm_gain("B")[perm]), c_norm_weight=t(norm_gain("C")[perm]),
-        b_bias=t(bias("B")[:, perm]), c_bias=t(bias("C")[:, perm]),
-        d_skip=t(_to_numpy(sd["D"])),
-    )
+    """A layer's torch state dict -> `SISOParams` in the kernels' layout
+    (``convert.py:92-149``). Norm gains are found as ``B_norm.weight`` (upstream) or
+    ``B_norm_weight``."""
+    out = {}
+    for leaf in MIXER_LEAVES:
+        arr = _leaf_in(leaf, _f32(_lookup(sd, leaf.keys)), cfg)
+        out[leaf.field] = torch.as_tensor(arr, dtype=dtype, device=device)
+    return SISOParams(**out)
 
 
 def jax_to_torch(params: SISOParams, cfg: SISOConfig) -> dict:
-    """``convert.py:152-176``: inverse of `torch_to_jax`, as float32 numpy arrays in
-    torch's shapes and order."""
-    n = cfg.d_state
-    inv = LY.interleave_perm(n).numpy()
-    in_proj = _to_numpy(params.in_proj).copy()
-    b_start = 2 * cfg.d_inner
-    for start in (b_start, b_start + n):
-        in_proj[:, start:start + n] = in_proj[:, start:start + n][:, inv]
-    return {
-        "in_proj.weight": in_proj.T.copy(),
-        "out_proj.weight": _to_numpy(params.out_proj).T.copy(),
-        "dt_bias": _to_numpy(params.dt_bias),
-        "B_norm.weight": _to_numpy(params.b_norm_weight)[inv],
-        "C_norm.weight": _to_numpy(params.c_norm_weight)[inv],
-        "B_bias": _to_numpy(params.b_bias)[:, inv][:, None, :],
-        "C_bias": _to_numpy(params.c_bias)[:, inv][:, None, :],
-        "D": _to_numpy(params.d_skip),
-    }
+    """`SISOParams` -> a torch-format state dict of float32 numpy arrays
+    (``convert.py:152-176``); the exact inverse of `torch_to_jax`."""
+    return {leaf.keys[0]: _leaf_out(leaf, _f32(getattr(params, leaf.field)), cfg)
+            for leaf in MIXER_LEAVES}
 
 
 params_from_state_dict = torch_to_jax
@@ -132,134 +171,177 @@ state_dict_from_params = jax_to_torch
 
 
 # ------------------------------------------------------------------------------------
-# whole released checkpoints (convert.py:179-356)
+# whole released checkpoints
 # ------------------------------------------------------------------------------------
-#
-# A released ``MambaLMHeadModel`` state dict, per block i:
-#   backbone.layers.{i}.norm.weight (d_model,); backbone.layers.{i}.mixer.* (the layer's
-#   torch state dict); with an MLP: backbone.layers.{i}.norm2.weight (d_model,),
-#   backbone.layers.{i}.mlp.fc1.weight (2*d_int, d_model), .mlp.fc2.weight (d_model, d_int)
-# plus backbone.embedding.weight (vocab_padded, d_model), backbone.norm_f.weight and
-# lm_head.weight (vocab_padded, d_model; the embedding itself when tied).
 
+#: Per-block leaves of a released ``MambaLMHeadModel``: (path in `model.BlockParams`,
+#: key template, transposed, present only with an MLP). The mixer itself is the
+#: `MIXER_LEAVES` table under ``MIXER_PREFIX``.
+BLOCK_LEAVES = (
+    ("norm_gain", "backbone.layers.{i}.norm.weight", False, False),
+    ("mlp_norm_gain", "backbone.layers.{i}.norm2.weight", False, True),
+    ("mlp.fc1", "backbone.layers.{i}.mlp.fc1.weight", True, True),
+    ("mlp.fc2", "backbone.layers.{i}.mlp.fc2.weight", True, True),
+)
+#: Model-level leaves: (path in `model.LMParams`, key, transposed).
+TOP_LEAVES = (
+    ("embed", "backbone.embedding.weight", False),
+    ("final_norm", "backbone.norm_f.weight", False),
+    ("head", "lm_head.weight", True),
+)
 MIXER_PREFIX = "backbone.layers.{i}.mixer."
+
+#: ``config.json`` fields read into `SISOConfig`: (key under ``ssm_cfg``, field, type).
+#: Fields absent from the file keep `SISOConfig`'s defaults.
+HF_SSM_FIELDS = (
+    ("d_state", "d_state", int),
+    ("headdim", "headdim", int),
+    ("expand", "expand", int),
+    ("rope_fraction", "rope_fraction", float),
+    ("A_floor", "a_floor", float),
+    ("dt_min", "dt_min", float),
+    ("dt_max", "dt_max", float),
+    ("dt_init_floor", "dt_init_floor", float),
+)
+
+#: Released configurations this package does not implement: (test on (config.json,
+#: ssm_cfg), message). Each names what the checkpoint has that a SISO stack lacks.
+HF_REFUSALS: tuple = (
+    (lambda top, ssm: ssm.get("layer", "Mamba3") != "Mamba3",
+     lambda top, ssm: f"ssm_cfg.layer={ssm.get('layer')!r}: only Mamba3 layers load"),
+    (lambda top, ssm: bool(ssm.get("mimo")) or (ssm.get("mimo_rank") or 1) != 1,
+     lambda top, ssm: "a MIMO checkpoint (mimo / mimo_rank > 1); only SISO layers load"),
+    (lambda top, ssm: bool(top.get("attn_layer_idx")),
+     lambda top, ssm: f"attention layers at {top['attn_layer_idx']}: hybrid attention "
+                      "stacks do not load"),
+    (lambda top, ssm: ssm.get("ngroups", 1) != 1,
+     lambda top, ssm: f"ngroups={ssm['ngroups']}: only the SISO grouping (1) loads"),
+)
 
 
 def config_from_hf(cfg_json: Mapping[str, Any], **overrides):
     """A released ``config.json`` -> `model.LMConfig` (``convert.py:202-267``).
 
-    ``vocab_size`` is padded up to ``pad_vocab_size_multiple`` (upstream pads inside the
-    model, so the checkpoint's embedding has the padded width). ``chunk`` defaults to
-    128, as in the reference, whatever the file says; ``overrides`` replace any
-    `SISOConfig` field. Raises ``ValueError`` for a non-Mamba3 layer, MIMO, attention
-    layers or ``ngroups != 1``."""
+    The vocabulary is rounded up to ``pad_vocab_size_multiple``, the width the released
+    embedding has. The chunk is 128 unless overridden: the file's ``chunk_size`` is the
+    upstream kernel's tiling, not a property of the weights. ``overrides`` replace any
+    `SISOConfig` field. Refused with ``ValueError``: see `HF_REFUSALS`."""
     from . import model as M
 
-    ssm = dict(cfg_json.get("ssm_cfg", {}))
-    layer_name = ssm.pop("layer", "Mamba3")
-    if layer_name != "Mamba3":
-        raise ValueError(f"ssm_cfg.layer is {layer_name!r}, expected 'Mamba3'")
-    if ssm.get("mimo", False) or ssm.get("mimo_rank", 1) not in (1, None):
-        raise ValueError("this checkpoint is MIMO; only SISO is implemented")
-    if cfg_json.get("attn_layer_idx"):
-        raise ValueError(f"checkpoint has attention layers at {cfg_json['attn_layer_idx']}; "
-                         "hybrid attention/SSM stacks are not implemented")
-    if ssm.get("ngroups", 1) != 1:
-        raise ValueError(f"ngroups={ssm['ngroups']}, only ngroups=1 (SISO) is implemented")
-    vocab = int(cfg_json["vocab_size"])
-    mult = int(cfg_json.get("pad_vocab_size_multiple", 1) or 1)
-    vocab += (-vocab) % mult
-    kw: dict[str, Any] = {
-        "d_model": int(cfg_json["d_model"]),
-        "d_state": int(ssm.get("d_state", 128)),
-        "headdim": int(ssm.get("headdim", 64)),
-        "expand": int(ssm.get("expand", 2)),
-        "rope_fraction": float(ssm.get("rope_fraction", 0.5)),
-        "chunk": 128,
-    }
-    for src, dst in (("A_floor", "a_floor"), ("dt_min", "dt_min"), ("dt_max", "dt_max"),
-                     ("dt_init_floor", "dt_init_floor")):
-        if src in ssm:
-            kw[dst] = float(ssm[src])
-    kw.update({k: v for k, v in overrides.items() if k != "d_intermediate"})
+    ssm = dict(cfg_json.get("ssm_cfg") or {})
+    for test, message in HF_REFUSALS:
+        if test(cfg_json, ssm):
+            raise ValueError(f"cannot load this checkpoint: {message(cfg_json, ssm)}")
+    fields: dict = {"d_model": int(cfg_json["d_model"]), "chunk": 128}
+    fields.update({dst: kind(ssm[src]) for src, dst, kind in HF_SSM_FIELDS if src in ssm})
+    fields.update({k: v for k, v in overrides.items() if k != "d_intermediate"})
+    multiple = max(1, int(cfg_json.get("pad_vocab_size_multiple") or 1))
+    vocab = -(-int(cfg_json["vocab_size"]) // multiple) * multiple
     return M.LMConfig(vocab_size=vocab, n_layers=int(cfg_json["n_layer"]),
-                      siso=SISOConfig(**kw), tie_head=bool(cfg_json.get("tie_embeddings", True)),
+                      siso=SISOConfig(**fields),
+                      tie_head=bool(cfg_json.get("tie_embeddings", True)),
                       d_intermediate=int(cfg_json.get("d_intermediate", 0)))
+
+
+def _get_path(obj, path: str):
+    for part in path.split("."):
+        obj = None if obj is None else getattr(obj, part)
+    return obj
+
+
+def _model_leaves(cfg):
+    """(path, key, transposed) of every non-mixer tensor the config implies, in a fixed
+    order; block paths are prefixed ``blocks.{i}.``."""
+    out = []
+    for i in range(cfg.n_layers):
+        for path, key, tr, mlp_only in BLOCK_LEAVES:
+            if cfg.d_intermediate or not mlp_only:
+                out.append((f"blocks.{i}.{path}", key.format(i=i), tr))
+    for path, key, tr in TOP_LEAVES:
+        if path != "head" or not cfg.tie_head:
+            out.append((path, key, tr))
+    return out
 
 
 def load_lm_state_dict(sd: Mapping[str, Any], cfg, dtype=torch.float32, device=None):
     """A released ``MambaLMHeadModel`` state dict -> `model.LMParams`
-    (``convert.py:270-330``). Linear weights are transposed to ``(in, out)``; each mixer
-    goes through `torch_to_jax`; bf16 tensors are widened on the torch side. Strict: a
-    key the config implies but the dict lacks raises ``KeyError`` naming it, and an
-    embedding whose width disagrees with the (padded) vocabulary raises ``ValueError``."""
+    (``convert.py:270-330``). Strict: a tensor the config implies but the dict lacks
+    raises ``KeyError`` with its name, and an embedding whose width is not the padded
+    vocabulary raises ``ValueError``."""
     from . import model as M
 
-    def get(key: str) -> np.ndarray:
+    def tensor(arr):
+        return torch.as_tensor(np.ascontiguousarray(arr), dtype=dtype, device=device)
+
+    flat = {}
+    for path, key, tr in _model_leaves(cfg):
         if key not in sd:
-            raise KeyError(f"checkpoint is missing {key!r}")
-        return _to_numpy(sd[key])
-
-    def t(a):
-        return torch.as_tensor(np.ascontiguousarray(a), dtype=dtype, device=device)
-
-    embed = get("backbone.embedding.weight")
-    if embed.shape != (cfg.vocab_size, cfg.d_model):
-        raise ValueError(f"embedding is {embed.shape}, config implies "
-                         f"{(cfg.vocab_size, cfg.d_model)}; check pad_vocab_size_multiple")
+            raise KeyError(f"released state dict lacks {key!r}, which the config implies")
+        arr = _f32(sd[key])
+        flat[path] = tensor(arr.T if tr else arr)
+    want = (cfg.vocab_size, cfg.d_model)
+    if tuple(flat["embed"].shape) != want:
+        raise ValueError(f"backbone.embedding.weight is {tuple(flat['embed'].shape)} but the "
+                         f"config needs {want} (vocab_size rounded up to "
+                         "pad_vocab_size_multiple)")
     blocks = []
     for i in range(cfg.n_layers):
-        pre = MIXER_PREFIX.format(i=i)
-        mixer = {k[len(pre):]: sd[k] for k in sd if k.startswith(pre)}
+        prefix = MIXER_PREFIX.format(i=i)
+        mixer = {k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)}
         if not mixer:
-            raise KeyError(f"no keys under {pre!r}; is this a Mamba-3 checkpoint?")
-        siso = torch_to_jax(mixer, cfg.siso, dtype, device)
-        mlp = mlp_norm = None
+            raise KeyError(f"released state dict has no {prefix}* tensors (layer {i} of "
+                           f"{cfg.n_layers})")
+        mlp = None
         if cfg.d_intermediate:
-            mlp = M.MLPParams(fc1=t(get(f"backbone.layers.{i}.mlp.fc1.weight").T),
-                              fc2=t(get(f"backbone.layers.{i}.mlp.fc2.weight").T))
-            mlp_norm = t(get(f"backbone.layers.{i}.norm2.weight"))
-        blocks.append(M.BlockParams(norm_gain=t(get(f"backbone.layers.{i}.norm.weight")),
-                                    siso=siso, mlp_norm_gain=mlp_norm, mlp=mlp))
-    head = None if cfg.tie_head else t(get("lm_head.weight").T)
-    return M.LMParams(embed=t(embed), blocks=blocks, final_norm=t(get("backbone.norm_f.weight")),
-                      head=head)
+            mlp = M.MLPParams(fc1=flat[f"blocks.{i}.mlp.fc1"], fc2=flat[f"blocks.{i}.mlp.fc2"])
+        blocks.append(M.BlockParams(
+            norm_gain=flat[f"blocks.{i}.norm_gain"],
+            siso=torch_to_jax(mixer, cfg.siso, dtype, device),
+            mlp_norm_gain=flat.get(f"blocks.{i}.mlp_norm_gain"), mlp=mlp))
+    return M.LMParams(embed=flat["embed"], blocks=blocks, final_norm=flat["final_norm"],
+                      head=flat.get("head"))
 
 
 def lm_state_dict(params, cfg) -> dict:
-    """Inverse of `load_lm_state_dict`: `model.LMParams` -> a released-format state dict
-    of float32 numpy arrays (``lm_head.weight`` is the embedding when the head is tied,
-    as upstream's shared tensor is)."""
-    sd: dict[str, np.ndarray] = {"backbone.embedding.weight": _to_numpy(params.embed)}
-    for i, b in enumerate(params.blocks):
-        pre = MIXER_PREFIX.format(i=i)
-        for k, v in jax_to_torch(b.siso, cfg.siso).items():
-            sd[pre + k] = v
-        sd[f"backbone.layers.{i}.norm.weight"] = _to_numpy(b.norm_gain)
-        if b.mlp is not None:
-            sd[f"backbone.layers.{i}.norm2.weight"] = _to_numpy(b.mlp_norm_gain)
-            sd[f"backbone.layers.{i}.mlp.fc1.weight"] = _to_numpy(b.mlp.fc1).T.copy()
-            sd[f"backbone.layers.{i}.mlp.fc2.weight"] = _to_numpy(b.mlp.fc2).T.copy()
-    sd["backbone.norm_f.weight"] = _to_numpy(params.final_norm)
-    sd["lm_head.weight"] = (sd["backbone.embedding.weight"] if params.head is None
-                            else _to_numpy(params.head).T.copy())
+    """`model.LMParams` -> a released-format state dict of float32 numpy arrays; the
+    inverse of `load_lm_state_dict`. With a tied head ``lm_head.weight`` is the
+    embedding, as upstream stores one shared tensor under both names."""
+    sd: dict = {}
+    for path, key, tr in _model_leaves(cfg):
+        arr = _f32(_get_path_indexed(params, path))
+        sd[key] = np.ascontiguousarray(arr.T) if tr else arr
+    for i, blk in enumerate(params.blocks):
+        prefix = MIXER_PREFIX.format(i=i)
+        sd.update({prefix + k: v for k, v in jax_to_torch(blk.siso, cfg.siso).items()})
+    if cfg.tie_head:
+        sd["lm_head.weight"] = sd["backbone.embedding.weight"]
     return sd
 
 
-def load_pretrained(path: str, dtype=torch.float32, device=None, **cfg_overrides):
-    """A released checkpoint from a LOCAL directory -> ``(params, cfg)``
-    (``convert.py:333-356`` without the Hub download). Reads ``config.json`` and
-    ``model.safetensors`` (preferred) or ``pytorch_model.bin`` (loaded with
-    ``weights_only=True``: no code in the file runs)."""
-    if not os.path.isdir(path):
-        raise ValueError(f"{path!r} is not a local checkpoint directory (no network here)")
-    with open(os.path.join(path, "config.json")) as fh:
-        cfg = config_from_hf(json.load(fh), **cfg_overrides)
+def _get_path_indexed(params, path: str):
+    if path.startswith("blocks."):
+        _, i, rest = path.split(".", 2)
+        return _get_path(params.blocks[int(i)], rest)
+    return _get_path(params, path)
+
+
+def _read_weights(path: str) -> Mapping[str, Any]:
     st = os.path.join(path, "model.safetensors")
     if os.path.exists(st):
         from safetensors.torch import load_file
-        sd = load_file(st, device="cpu")
-    else:
-        sd = torch.load(os.path.join(path, "pytorch_model.bin"), map_location="cpu",
-                        weights_only=True)
-    return load_lm_state_dict(sd, cfg, dtype, device), cfg
+        return load_file(st, device="cpu")
+    # weights_only: tensors and containers only, no code in the file runs
+    return torch.load(os.path.join(path, "pytorch_model.bin"), map_location="cpu",
+                      weights_only=True)
+
+
+def load_pretrained(path: str, dtype=torch.float32, device=None, **cfg_overrides):
+    """A released checkpoint in a LOCAL directory -> ``(params, cfg)``
+    (``convert.py:333-356``, without the Hub download): ``config.json`` plus
+    ``model.safetensors`` (preferred) or ``pytorch_model.bin``."""
+    if not os.path.isdir(path):
+        raise ValueError(f"{path!r}: expected a local checkpoint directory (config.json + "
+                         "weights); hub names are not fetched")
+    with open(os.path.join(path, "config.json")) as fh:
+        cfg = config_from_hf(json.load(fh), **cfg_overrides)
+    return load_lm_state_dict(_read_weights(path), cfg, dtype, device), cfg

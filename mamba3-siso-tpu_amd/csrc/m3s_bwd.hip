@@ -1670,7 +1670,7 @@ static bool bwd_fits_rsrc(const BwdParams& p, int N, int P) {
 template <typename MT, int C, int N, int P>
 static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   bool done = false;
-  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
+  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0 && C <= N) {
     if (bwd_fits_rsrc(prm, N, P)) {
       hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
       done = true;
@@ -1693,15 +1693,22 @@ static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   X(bf16, 128, 128, 64)    \
   X(bf16, 64, 128, 64)     \
   X(bf16, 32, 128, 64)     \
+  X(bf16, 128, 64, 64)     \
   X(bf16, 64, 64, 64)      \
+  X(bf16, 32, 64, 64)      \
+  X(bf16, 128, 32, 16)     \
   X(bf16, 64, 32, 16)      \
   X(bf16, 32, 32, 16)      \
+  X(bf16, 128, 16, 16)     \
   X(bf16, 64, 16, 16)      \
   X(bf16, 32, 16, 16)      \
   X(float, 32, 128, 64)    \
   X(float, 64, 64, 64)     \
+  X(float, 32, 64, 64)     \
+  X(float, 128, 32, 16)    \
   X(float, 64, 32, 16)     \
   X(float, 32, 32, 16)     \
+  X(float, 128, 16, 16)    \
   X(float, 64, 16, 16)     \
   X(float, 32, 16, 16)
 

@@ -208,9 +208,11 @@ static int32_t launch_dec(const DecParams& prm, int grid, hipStream_t stream) {
 #define M3S_DEC_CONFIGS(X) \
   X(bf16, 128, 64)         \
   X(bf16, 64, 64)          \
+  X(bf16, 32, 16)          \
   X(bf16, 16, 16)          \
   X(float, 128, 64)        \
   X(float, 64, 64)         \
+  X(float, 32, 16)         \
   X(float, 16, 16)
 
 template <typename MT> constexpr int dcode();

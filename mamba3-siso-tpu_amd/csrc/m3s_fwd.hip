@@ -1287,16 +1287,23 @@ static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   X(bf16, 128, 128, 64)     \
   X(bf16, 64, 128, 64)      \
   X(bf16, 32, 128, 64)      \
+  X(bf16, 128, 64, 64)      \
   X(bf16, 64, 64, 64)       \
+  X(bf16, 32, 64, 64)       \
+  X(bf16, 128, 32, 16)      \
   X(bf16, 64, 32, 16)       \
   X(bf16, 32, 32, 16)       \
+  X(bf16, 128, 16, 16)      \
   X(bf16, 64, 16, 16)       \
   X(bf16, 32, 16, 16)       \
   X(float, 64, 128, 64)     \
   X(float, 32, 128, 64)     \
   X(float, 64, 64, 64)      \
+  X(float, 32, 64, 64)      \
+  X(float, 128, 32, 16)     \
   X(float, 64, 32, 16)      \
   X(float, 32, 32, 16)      \
+  X(float, 128, 16, 16)     \
   X(float, 64, 16, 16)      \
   X(float, 32, 16, 16)
 

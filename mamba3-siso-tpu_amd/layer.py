@@ -49,8 +49,11 @@ Tensor = torch.Tensor
 class SISOConfig:
     """Shapes and hyperparameters (``layer.py:39-99``); same fields and defaults.
 
-    ``chunk`` follows the GPU rule of `layout.validate_chunk` (32/64/128/256) instead of
-    the reference's Mosaic rule (multiple of 128).
+    ``chunk`` follows the GPU rule of `layout.validate_chunk` (32/64/128) instead of the
+    reference's Mosaic rule (multiple of 128), and the config is rejected at construction,
+    as the reference rejects a bad chunk (``layer.py:97-99``), unless a forward, backward
+    and decode kernel is compiled for its (policy, chunk, d_state, headdim)
+    (`layout.validate_kernel_shape`).
     """
 
     d_model: int
@@ -98,6 +101,7 @@ class SISOConfig:
         LY.validate_chunk(self.chunk)
         LY.policy(self.policy_name)
         _ = self.nheads, self.n_angles
+        LY.validate_kernel_shape(self.policy_name, self.chunk, self.d_state, self.headdim)
 
 
 class SISOParams(NamedTuple):

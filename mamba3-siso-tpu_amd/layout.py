@@ -116,14 +116,78 @@ def num_chunks(seqlen: int, chunk: int) -> int:
     return seqlen // chunk
 
 
-#: Chunk lengths the HIP kernels are instantiated for.
-SUPPORTED_CHUNKS = (32, 64, 128, 256)
+#: Chunk lengths the HIP kernels are instantiated for (the union over shapes; which
+#: (chunk, d_state, headdim) exist per policy is `KERNELS`).
+SUPPORTED_CHUNKS = (32, 64, 128)
+
+#: The compiled kernel instantiations: role -> {(policy, chunk, d_state, headdim)}; decode
+#: has no chunk (0). Mirrors the instantiation tables of ``csrc/m3s_fwd.hip``,
+#: ``m3s_bwd.hip`` and ``m3s_decode.hip``; ``tests/test_abi_cpu.py`` checks this mirror
+#: against the library's ``m3s_supported`` entry by entry, so `SISOConfig` can reject an
+#: unsupported shape at construction without loading the library.
+KERNELS = {
+    "forward": frozenset({
+        ("bf16", 128, 128, 64), ("bf16", 64, 128, 64), ("bf16", 32, 128, 64),
+        ("bf16", 128, 64, 64), ("bf16", 64, 64, 64), ("bf16", 32, 64, 64),
+        ("bf16", 128, 32, 16), ("bf16", 64, 32, 16), ("bf16", 32, 32, 16),
+        ("bf16", 128, 16, 16), ("bf16", 64, 16, 16), ("bf16", 32, 16, 16),
+        ("f32", 64, 128, 64), ("f32", 32, 128, 64),
+        ("f32", 64, 64, 64), ("f32", 32, 64, 64),
+        ("f32", 128, 32, 16), ("f32", 64, 32, 16), ("f32", 32, 32, 16),
+        ("f32", 128, 16, 16), ("f32", 64, 16, 16), ("f32", 32, 16, 16),
+    }),
+    "backward": frozenset({
+        ("bf16", 128, 128, 64), ("bf16", 64, 128, 64), ("bf16", 32, 128, 64),
+        ("bf16", 128, 64, 64), ("bf16", 64, 64, 64), ("bf16", 32, 64, 64),
+        ("bf16", 128, 32, 16), ("bf16", 64, 32, 16), ("bf16", 32, 32, 16),
+        ("bf16", 128, 16, 16), ("bf16", 64, 16, 16), ("bf16", 32, 16, 16),
+        ("f32", 32, 128, 64),
+        ("f32", 64, 64, 64), ("f32", 32, 64, 64),
+        ("f32", 128, 32, 16), ("f32", 64, 32, 16), ("f32", 32, 32, 16),
+        ("f32", 128, 16, 16), ("f32", 64, 16, 16), ("f32", 32, 16, 16),
+    }),
+    "decode": frozenset({
+        (pol, 0, n, p) for pol in ("bf16", "f32") for n, p in ((128, 64), (64, 64), (32, 16), (16, 16))
+    }),
+}
+
+
+def missing_kernels(policy_name: str, chunk: int, d_state: int, headdim: int) -> list:
+    """The roles (forward, backward, decode) with no compiled kernel for this shape."""
+    pol = policy(policy_name).name
+    want = {"forward": (pol, chunk, d_state, headdim), "backward": (pol, chunk, d_state, headdim),
+            "decode": (pol, 0, d_state, headdim)}
+    return [role for role, key in want.items() if key not in KERNELS[role]]
+
+
+def compiled_chunks(policy_name: str, d_state: int, headdim: int) -> tuple:
+    """Chunks with both a forward and a backward kernel for (policy, d_state, headdim)."""
+    pol = policy(policy_name).name
+    return tuple(c for c in SUPPORTED_CHUNKS
+                 if (pol, c, d_state, headdim) in KERNELS["forward"]
+                 and (pol, c, d_state, headdim) in KERNELS["backward"])
 
 
 def validate_chunk(chunk: int) -> None:
     """GPU chunk rule, replacing the reference's Mosaic rule ``chunk % 128 == 0``
-    (``layout.py:225-236``): any of `SUPPORTED_CHUNKS`. The reference's chunked maths
-    (``reference.siso_chunked``) accepts any divisor of L; 32..256 are the tile sizes
-    the MFMA kernels are built for."""
+    (``layout.py:225-236``): one of `SUPPORTED_CHUNKS`. The reference's chunked maths
+    (``reference.siso_chunked``) accepts any divisor of L; 32, 64 and 128 are the tile
+    sizes the MFMA kernels are built for."""
     if chunk not in SUPPORTED_CHUNKS:
         raise ValueError(f"chunk must be one of {SUPPORTED_CHUNKS}, got {chunk}")
+
+
+def validate_kernel_shape(policy_name: str, chunk: int, d_state: int, headdim: int) -> None:
+    """Raise ``ValueError`` unless forward, backward and decode kernels are all compiled
+    for this (policy, chunk, d_state, headdim) -- the check the reference makes on its
+    chunk when the config is built (``layer.py:97-99``), widened to the whole shape
+    because the HIP kernels are compiled per shape."""
+    validate_chunk(chunk)
+    missing = missing_kernels(policy_name, chunk, d_state, headdim)
+    if missing:
+        ok = compiled_chunks(policy_name, d_state, headdim)
+        hint = (f"chunks compiled for this policy and shape: {list(ok)}" if ok else
+                "no chunk is compiled for this policy and shape")
+        raise ValueError(
+            f"no {'/'.join(missing)} kernel for policy={policy(policy_name).name} "
+            f"chunk={chunk} d_state={d_state} headdim={headdim}; {hint}")

@@ -303,11 +303,16 @@ def zero_states(cfg: LMConfig, batch: int, dtype=torch.float32, device=None) -> 
 
 
 def _add_residual(x: Tensor, y: Tensor) -> Tensor:
-    """``x + y`` for a one-token step: a block output of another dtype is cast to the
-    stream's first. That is the cast the mixed-dtype add does inside, so the sum is the
-    same; PyTorch's mixed-dtype add kernel needs scratch memory and costs ~40 us per
-    launch on ROCm whatever its size, against a few us for a cast and a plain add."""
-    return x + (y if y.dtype == x.dtype else y.to(x.dtype))
+    """``x + y`` for a one-token step, with PyTorch's type promotion: both operands are
+    cast to the promoted dtype first, then added. That is what the mixed-dtype add
+    computes (a bf16 stream plus an f32 block output becomes an f32 stream, as the
+    reference's JAX add promotes), but the mixed-dtype add kernel needs scratch memory and
+    costs ~40 us per launch on ROCm whatever its size, against a few us for a cast and a
+    plain add."""
+    if x.dtype == y.dtype:
+        return x + y
+    wide = torch.promote_types(x.dtype, y.dtype)
+    return x.to(wide) + y.to(wide)
 
 
 def lm_decode_step(params: LMParams, token: Tensor, states: list, cfg: LMConfig,

@@ -18,7 +18,10 @@
 
 from __future__ import annotations
 
+import codecs
+import collections
 import math
+import sys
 from typing import Any, Callable, Iterable, Optional
 
 import numpy as np
@@ -316,31 +319,50 @@ def generate(params: M.LMParams, cfg: M.LMConfig, key: Any, prompt_ids,
     for t in ids[n_whole:]:
         logits, _ = step(torch.tensor([t], device=dev))
         last = logits[0]
-    stops = set(int(s) for s in stop_ids) if stop_ids else set()
-    seen = torch.zeros(cfg.vocab_size, dtype=torch.bool, device=dev)
-    window = ids[-rep_window:] if rep_window > 0 else []
-    for t in window:
-        seen[t] = True
+    stops = frozenset(int(s) for s in stop_ids) if stop_ids else frozenset()
+    penalty = _RecentIds(rep_window, cfg.vocab_size, dev, ids)
     out = list(ids)
     filt = (temperature, top_p, rep_penalty)
     for _ in range(n_tokens):
-        nxt_t = _pick_token(last, seen, gen, filt, cfg.vocab_size)
+        nxt_t = _pick_token(last, penalty.mask, gen, filt, cfg.vocab_size)
         nxt = int(nxt_t)
         out.append(nxt)
         if on_token is not None:
             on_token(nxt)
         if nxt in stops:
             break
-        if rep_window > 0:
-            window.append(nxt)
-            if len(window) > rep_window:
-                dropped = window.pop(0)
-                if dropped not in window:
-                    seen[dropped] = False
-            seen[nxt] = True
+        penalty.push(nxt)
         logits, _ = step(nxt_t.reshape(1))
         last = logits[0]
     return out
+
+
+class _RecentIds:
+    """The ids the repetition penalty applies to: those among the last ``window``
+    tokens. Host-side counts over a bounded deque decide membership; the device mask
+    that `_pick_token` reads changes only when an id enters or leaves the window."""
+
+    def __init__(self, window: int, vocab: int, device, history) -> None:
+        self.window = max(0, int(window))
+        self.mask = torch.zeros(vocab, dtype=torch.bool, device=device)
+        self.recent: collections.deque = collections.deque()
+        self.count: collections.Counter = collections.Counter()
+        for t in list(history)[-self.window:] if self.window else []:
+            self.push(t)
+
+    def push(self, tok: int) -> None:
+        if not self.window:
+            return
+        self.recent.append(tok)
+        self.count[tok] += 1
+        if self.count[tok] == 1:
+            self.mask[tok] = True
+        if len(self.recent) > self.window:
+            old = self.recent.popleft()
+            self.count[old] -= 1
+            if self.count[old] == 0:
+                del self.count[old]
+                self.mask[old] = False
 
 
 def sample(params: M.LMParams, cfg: M.LMConfig, key: Any, prompt: bytes = b"the ",
@@ -351,14 +373,20 @@ def sample(params: M.LMParams, cfg: M.LMConfig, key: Any, prompt: bytes = b"the 
     as they arrive."""
     emit = None
     if stream:
-        print(prompt.decode("utf-8", errors="replace"), end="", flush=True)
+        # bytes arrive one at a time; an incremental decoder holds back the leading
+        # bytes of a multi-byte character until it is complete
+        text = codecs.getincrementaldecoder("utf-8")(errors="replace")
+        sys.stdout.write(text.decode(prompt))
+        sys.stdout.flush()
 
         def emit(t: int) -> None:
-            print(bytes([t]).decode("utf-8", errors="replace"), end="", flush=True)
+            sys.stdout.write(text.decode(bytes((t,))))
+            sys.stdout.flush()
 
     ids = generate(params, cfg, key, np.frombuffer(prompt, dtype=np.uint8), n_tokens=n_tokens,
                    temperature=temperature, top_p=top_p, rep_penalty=rep_penalty,
                    rep_window=rep_window, on_token=emit)
     if stream:
-        print(flush=True)
+        sys.stdout.write(text.decode(b"", final=True) + "\n")
+        sys.stdout.flush()
     return bytes(ids)

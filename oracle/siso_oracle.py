@@ -373,25 +373,36 @@ def rms_norm(x, weight, eps):
 
 
 def layer_forward(params: dict, u: Tensor, d_state, headdim, expand=2, rope_fraction=0.5,
-                  chunk=128, a_floor=1e-4, norm_eps=1e-5, state=None, mm_dtype=None):
+                  chunk=128, a_floor=1e-4, norm_eps=1e-5, state=None, mm_dtype=None,
+                  act_dtype=None):
     """``layer.py:201-262``: in_proj -> split -> BCNorm -> siso_segment -> out_proj.
 
-    ``params`` holds the reference's `SISOParams` fields by name, permuted layout."""
+    ``params`` holds the reference's `SISOParams` fields by name, permuted layout.
+
+    ``act_dtype=torch.bfloat16`` is the layer's bf16 rounding model, computed in the
+    working precision of ``u`` (float64 for the checks): the projection weights are
+    rounded as ``params.in_proj.astype(u.dtype)`` rounds them (``layer.py:233, 256``),
+    and every activation the bf16 layer stores is rounded where it is stored -- the
+    projection output, the normalised B and C (``rms_norm`` casts back,
+    ``layer.py:196``), the scan output y (``v.dtype``, ``kernel_fwd.py:193``) and the
+    layer output. Pair it with ``mm_dtype=torch.bfloat16`` for the scan's own MFMA
+    operand roundings."""
     bsz, seqlen, d_model = u.shape
     d_inner, h, nr, _ = layer_dims(d_model, d_state, headdim, expand, rope_fraction)
-    proj = u @ params["in_proj"].to(u.dtype)
+    act = _bf16 if act_dtype == torch.bfloat16 else (lambda x: x)
+    proj = act(act(u) @ act(params["in_proj"].to(u.dtype)))
     z, x, bb, cc, dt_raw, a_raw, trap_raw, angles = split_in_proj(
         proj, d_inner, d_state, h, nr, headdim)
-    bb = rms_norm(bb, params["b_norm_weight"], norm_eps)
-    cc = rms_norm(cc, params["c_norm_weight"], norm_eps)
+    bb = act(rms_norm(bb, params["b_norm_weight"], norm_eps))
+    cc = act(rms_norm(cc, params["c_norm_weight"], norm_eps))
     f = torch.float64 if u.dtype == torch.float64 else torch.float32
     y, st = siso_segment(
         cc, bb, x.permute(0, 2, 1, 3), dt_raw.to(f), a_raw.to(f), trap_raw.to(f),
         angles.to(f), params["dt_bias"].to(f), params["c_bias"].to(f), params["b_bias"].to(f),
         d_skip=params["d_skip"].to(f), z=z.permute(0, 2, 1, 3),
         state=state, a_floor=a_floor, chunk=chunk, mm_dtype=mm_dtype)
-    y = y.permute(0, 2, 1, 3).reshape(bsz, seqlen, d_inner)
-    return y.to(u.dtype) @ params["out_proj"].to(u.dtype), st
+    y = act(y.permute(0, 2, 1, 3).reshape(bsz, seqlen, d_inner))
+    return act(y.to(u.dtype) @ act(params["out_proj"].to(u.dtype))), st
 
 
 def layer_decode_step(params: dict, token_embed: Tensor, state: SISOState, d_state, headdim,

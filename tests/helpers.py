@@ -5,13 +5,19 @@ Tolerances (stated once, used by every GPU test):
   * f32 policy vs the float64 oracle: p95 relative error over |ref| >= 1e-2
     (``tests.py:60-88``) <= 2e-5 for forward/decode outputs and <= 2e-4 for gradients
     (the reference's own bars, ``tests.py:533, 612``).
-  * bf16 policy: against the oracle's bf16 rounding model (same rounding points as the
-    reference kernel) p95 <= 2e-3 for f32 outputs (ybar, state) and <= 5e-3 for outputs
-    stored in bf16 (one bf16 rounding is up to 2^-8 relative); against the float64
-    maths, max |got - ref| /
-    max |ref| <= 2e-2 on outputs and states and <= 2e-2 on gradients (the north_star
-    bound is 5e-2 relative on gradients), and the reference's bf16 p95 bar of 5e-2 on
-    forward outputs (``tests.py:533``).
+  * bf16 policy against the oracle's bf16 rounding model (the same rounding points as the
+    reference kernel): p95 <= 2e-3 for f32 outputs (ybar, state) and <= 5e-3 for outputs
+    stored in bf16 (one bf16 rounding is up to 2^-8 relative); elementwise, a bf16
+    output is within one bf16 ulp of |ref| plus 4e-3 max|ref| (the operand roundings of
+    the products, which the model reproduces only up to accumulation order).
+  * bf16 policy against the float64 maths:
+      - max |got - ref| / max |ref| <= 1e-2 on outputs (y);
+      - max |got - ref| <= 2e-2 on the float32 final state (the north_star bound);
+      - max |got - ref| / max |ref| <= 2e-2 on every gradient (north_star: 5e-2);
+      - p95 <= 5e-2 on the kernel's y, the reference's bf16 bar (``tests.py:533``).
+    At the layer level the bf16 projections round the weights and every stored
+    activation (``layer.py:233, 256``); the layer's y is held to the rounding model of the
+    whole bf16 layer (`siso_oracle.layer_forward(act_dtype=bf16)`), p95 <= 1e-2.
 """
 
 import torch
@@ -26,8 +32,13 @@ FWD_F32_P95 = 2e-5
 GRAD_F32_P95 = 2e-4
 BF16_MODEL_P95 = 2e-3
 BF16_OUT_MODEL_P95 = 5e-3
+BF16_LAYER_MODEL_P95 = 1e-2
+BF16_Y_MAXREL = 1e-2
 BF16_MAXREL = 2e-2
+BF16_GRAD_MAXREL = 2e-2
 BF16_P95 = 5e-2
+STATE_MAXABS = 2e-2
+BF16_MODEL_ABS_REL = 4e-3
 
 
 def mt_of(policy):
@@ -72,6 +83,13 @@ def cpu(t):
     return t.detach().float().cpu().double()
 
 
+def report(what, got, ref):
+    """Print the error figures of one comparison (visible with ``pytest -s``)."""
+    g, r = cpu(got), ref.detach().double()
+    print(f"[parity] {what}: p95 {O.rel_error(g, r):.3e}  max-norm {O.max_rel(g, r):.3e}  "
+          f"max-abs {O.max_abs(g, r):.3e}  (max|ref| {float(r.abs().max()):.3e})", flush=True)
+
+
 def assert_p95(got, ref, tol, what=""):
     e = O.rel_error(cpu(got), ref)
     assert e <= tol, f"{what}: p95 rel error {e:.3e} > {tol:.1e}"
@@ -80,3 +98,23 @@ def assert_p95(got, ref, tol, what=""):
 def assert_maxrel(got, ref, tol, what=""):
     e = O.max_rel(cpu(got), ref)
     assert e <= tol, f"{what}: max-normalised error {e:.3e} > {tol:.1e}"
+
+
+def assert_maxabs(got, ref, tol, what=""):
+    e = O.max_abs(cpu(got), ref)
+    assert e <= tol, f"{what}: max-abs error {e:.3e} > {tol:.1e}"
+
+
+def bf16_ulp(x):
+    """Spacing of bfloat16 numbers at |x| (8 significant bits); 2^-133 at zero."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -126)))
+    return torch.pow(2.0, e - 7)
+
+
+def assert_bf16_bound(got, ref, rel=BF16_MODEL_ABS_REL, what=""):
+    """Elementwise |got - ref| <= ulp_bf16(|ref|) + rel * max|ref|: one rounding of the
+    stored bf16 value plus the operand roundings of the products feeding it."""
+    g, r = cpu(got), ref.detach().double()
+    bound = bf16_ulp(r) + rel * float(r.abs().max())
+    over = ((g - r).abs() / bound).max()
+    assert float(over) <= 1.0, f"{what}: |err| reaches {float(over):.2f}x the bf16 bound"

@@ -165,7 +165,23 @@ def test_capability_table(lib):
                 for p in (16, 64):
                     if lib.supported(1, dt, c, n, p):
                         assert lib.supported(0, dt, c, n, p)
-    assert not lib.supported(0, lib.DTYPE_F32, 128, 128, 64)   # does not fit in LDS
+    assert not lib.supported(0, lib.DTYPE_BF16, 256, 128, 64)
+
+
+def test_python_kernel_table_mirrors_the_library(lib):
+    """layout.KERNELS (what SISOConfig validates against without loading the library)
+    equals the library's m3s_supported answer on every (role, policy, chunk, N, P) of a
+    grid wider than both tables."""
+    from mamba3_siso_tpu_amd import layout as LY
+    codes = {"bf16": lib.DTYPE_BF16, "f32": lib.DTYPE_F32}
+    roles = {"forward": 0, "backward": 1, "decode": 2}
+    for role, which in roles.items():
+        for pol, code in codes.items():
+            for c in ((0,) if role == "decode" else (16, 32, 64, 128, 256, 512)):
+                for n in (16, 32, 64, 128, 256):
+                    for p in (16, 32, 64, 128):
+                        want = bool(lib.supported(which, code, c, n, p))
+                        assert ((pol, c, n, p) in LY.KERNELS[role]) == want, (role, pol, c, n, p)
 
 
 def test_norm_arguments_are_checked_without_a_launch(lib):

@@ -35,8 +35,36 @@ def test_config_fields_defaults_and_rules(m3):
         m3.SISOConfig(d_model=64, policy_name="fp8")
 
 
+@pytest.mark.parametrize("kw,match", [
+    (dict(d_model=1024, chunk=256), "chunk must be one of"),            # no 256 kernel
+    (dict(d_model=1024, chunk=512), "chunk must be one of"),            # the reference's TPU chunk
+    (dict(d_model=1024, policy_name="f32"), "forward/backward kernel"),  # f32 at chunk 128, N 128
+    (dict(d_model=1024, chunk=64, policy_name="f32"), "backward kernel"),
+    (dict(d_model=256, d_state=32, headdim=32), "forward/backward/decode"),
+    (dict(d_model=256, d_state=256), "forward/backward/decode"),
+    (dict(d_model=256, headdim=128), "forward/backward/decode"),
+])
+def test_config_rejects_shapes_without_compiled_kernels(m3, kw, match):
+    """The reference rejects a bad chunk when the config is built (layer.py:97-99); here
+    the whole (policy, chunk, d_state, headdim) must have forward, backward and decode
+    kernels, and the error names the chunks that do exist."""
+    with pytest.raises(ValueError, match=match):
+        m3.SISOConfig(**kw)
+
+
+def test_config_accepts_every_compiled_shape(m3):
+    from mamba3_siso_tpu_amd import layout as LY
+    both = LY.KERNELS["forward"] & LY.KERNELS["backward"]
+    for pol, c, n, p in sorted(both):
+        if (pol, 0, n, p) in LY.KERNELS["decode"]:
+            cfg = m3.SISOConfig(d_model=4 * p, d_state=n, headdim=p, chunk=c, policy_name=pol)
+            assert (cfg.chunk, cfg.d_state, cfg.headdim) == (c, n, p)
+    assert LY.compiled_chunks("f32", 128, 64) == (32,)
+    assert LY.compiled_chunks("bf16", 128, 64) == (32, 64, 128)
+
+
 def test_init_params_distributions(m3):
-    cfg = m3.SISOConfig(d_model=256, d_state=32, headdim=32)
+    cfg = m3.SISOConfig(d_model=256, d_state=32, headdim=16)
     p = m3.init_params(cfg, 0)
     assert p.in_proj.shape == (256, cfg.d_in_proj) and p.out_proj.shape == (512, 256)
     assert float(p.in_proj.abs().max()) <= 1 / math.sqrt(256)

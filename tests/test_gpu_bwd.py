@@ -6,8 +6,9 @@ import math
 import pytest
 import torch
 
-from helpers import (BF16, BF16_MAXREL, GRAD_F32_P95, assert_maxrel, assert_p95,
-                     boundary_inputs, fwd_args)
+from helpers import (BF16, BF16_GRAD_MAXREL, BF16_MAXREL, GRAD_F32_P95, STATE_MAXABS,
+                     assert_maxabs, assert_maxrel, assert_p95, boundary_inputs, fwd_args,
+                     report)
 from oracle import siso_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -80,6 +81,22 @@ def test_backward_bf16_state64_and_no_gate(m3, n, chunk):
     assert gr.dz is None and gr.dd_skip is None
     for name, w in want.items():
         assert_maxrel(getattr(gr, GRAD_FIELD[name]), w, BF16_MAXREL, f"d{name} (no gate)")
+
+
+@pytest.mark.parametrize("policy,n,p,chunk", [
+    ("bf16", 64, 64, 128), ("bf16", 64, 64, 32), ("bf16", 32, 16, 128), ("bf16", 16, 16, 128),
+    ("f32", 64, 64, 32), ("f32", 32, 16, 128), ("f32", 16, 16, 128),
+])
+def test_backward_every_table_shape(m3, policy, n, p, chunk):
+    """Instantiations of the kernel table not covered above, against autograd of the
+    float64 oracle."""
+    want, gr = run_case(m3, 2, 2, 256, n, p, n // 4, chunk, policy, True, True, seed=19)
+    for name, w in want.items():
+        got = getattr(gr, GRAD_FIELD[name])
+        if policy == "f32":
+            assert_p95(got, w, GRAD_F32_P95, f"d{name}")
+        else:
+            assert_maxrel(got, w, BF16_GRAD_MAXREL, f"d{name}")
 
 
 def test_backward_matches_finite_differences_of_the_kernel_forward(m3):
@@ -161,4 +178,19 @@ def test_backward_full_size_cfg3_head_slices_and_head_sum(m3):
     got = dict(v=full.dv, z=full.dz, adt=full.dadt, gamma=full.dgamma, scale=full.dscale,
                phi=full.dphi)
     for name, t in got.items():
-        assert_maxrel(t[b_:b_ + 1, hs], want[name], BF16_MAXREL, f"d{name} (slice)")
+        report(f"cfg3 d{name} (slice) vs float64", t[b_:b_ + 1, hs], want[name])
+        assert_maxrel(t[b_:b_ + 1, hs], want[name], BF16_GRAD_MAXREL, f"d{name} (slice)")
+    # the same two heads through the kernel alone, at the full length: the head-summed
+    # dq/dk, the bias and skip gradients and the seed adjoint are then the oracle's too
+    a = [q[b_:b_ + 1], k[b_:b_ + 1], v[b_:b_ + 1, hs], pre.adt[b_:b_ + 1, hs],
+         pre.gamma[b_:b_ + 1, hs], pre.scale[b_:b_ + 1, hs], pre.phi[b_:b_ + 1, hs], qb[hs],
+         kb[hs], dsk[hs], z[b_:b_ + 1, hs]]
+    out = m3.siso_forward(*a, chunk=128, save_residuals=True)
+    two = m3.siso_backward(dy[b_:b_ + 1, hs], *a[:9], out[4].ybar, out[4].chunk_states,
+                           d_skip=dsk[hs], z=z[b_:b_ + 1, hs], chunk=128)
+    for name in ("q", "k", "q_bias", "k_bias", "d_skip", "v", "adt", "phi"):
+        report(f"cfg3 d{name} (2-head run) vs float64", getattr(two, GRAD_FIELD[name]), want[name])
+        assert_maxrel(getattr(two, GRAD_FIELD[name]), want[name], BF16_GRAD_MAXREL,
+                      f"d{name} (2-head run)")
+    assert_maxabs(out[1], O.siso_boundary_forward(**inputs, chunk=128)[1], STATE_MAXABS,
+                  "final ssm (2-head run)")

@@ -27,6 +27,10 @@ def make_lm(m3, policy, d_intermediate=48, tie_head=True, n_layers=2, vocab=40, 
     if policy == "f32":
         scfg = m3.SISOConfig(d_model=64, d_state=16, headdim=16, expand=2, chunk=64,
                              policy_name="f32")
+    elif policy == "bf16_cfg5":
+        # BASELINE configs[4] widths: d_model 768, N 128, P 64, chunk 128 (the
+        # <128, 128, 64> scan kernels and the MLP / norm kernels at widths 768 and 1536)
+        scfg = m3.SISOConfig(d_model=768, d_state=128, headdim=64, expand=2, chunk=128)
     else:
         scfg = m3.SISOConfig(d_model=128, d_state=64, headdim=64, expand=2, chunk=64)
     cfg = m3.model.LMConfig(vocab_size=vocab, n_layers=n_layers, siso=scfg,
@@ -52,15 +56,16 @@ def tokens_for(cfg, b, l, seed):
     return torch.randint(0, cfg.vocab_size, (b, l), generator=g)
 
 
-@pytest.mark.parametrize("policy,tie,di", [("f32", True, 48), ("f32", False, 0),
-                                           ("bf16", True, 96)])
-def test_lm_loss_and_grads_match_oracle(m3, dev, policy, tie, di):
-    cfg, params, lay = make_lm(m3, policy, d_intermediate=di, tie_head=tie)
-    xs = tokens_for(cfg, 2, 192, 1)
-    ys = tokens_for(cfg, 2, 192, 2)
+@pytest.mark.parametrize("policy,tie,di,vocab,seqlen", [
+    ("f32", True, 48, 40, 192), ("f32", False, 0, 40, 192), ("bf16", True, 96, 40, 192),
+    ("bf16_cfg5", True, 1536, 256, 256)])
+def test_lm_loss_and_grads_match_oracle(m3, dev, policy, tie, di, vocab, seqlen):
+    cfg, params, lay = make_lm(m3, policy, d_intermediate=di, tie_head=tie, vocab=vocab)
+    xs = tokens_for(cfg, 2, seqlen, 1)
+    ys = tokens_for(cfg, 2, seqlen, 2)
     p_dev = m3.train.train_params(m3.model.lm_to(params, device=dev))
     logits = m3.model.lm_forward(p_dev, xs.to(dev), cfg)
-    assert logits.dtype == torch.float32 and logits.shape == (2, 192, cfg.vocab_size)
+    assert logits.dtype == torch.float32 and logits.shape == (2, seqlen, cfg.vocab_size)
     loss = m3.model.lm_loss(p_dev, xs.to(dev), ys.to(dev), cfg)
     loss.backward()
 
@@ -122,6 +127,24 @@ def test_decode_chain_matches_prefill_and_oracle(m3, dev):
     assert_maxrel(dec, cpu(full[:, 64:]), 1e-4, "decode vs forward")
     ref = LO.lm_forward(LO.from_lm_params(params), toks.cpu(), lay)
     assert_maxrel(dec, ref[:, 64:], 1e-4, "decode vs oracle")
+
+
+def test_decode_matches_forward_with_bf16_params_under_f32_policy(m3, dev):
+    """bf16 parameters give a bf16 embedding stream; under the f32 policy the block
+    outputs are f32, and the forward's ``x + y`` promotes the stream to f32. The decode
+    step's residual add must promote the same way (not round the block output to the
+    stream's bf16), so decode equals the no-state forward at every position."""
+    cfg, params, _ = make_lm(m3, "f32")
+    p_dev = m3.model.lm_map(lambda t: t.to(torch.bfloat16), m3.model.lm_to(params, device=dev))
+    toks = tokens_for(cfg, 2, 64, 12).to(dev)
+    with torch.no_grad():
+        full = m3.model.lm_forward(p_dev, toks, cfg)
+        states = m3.model.zero_states(cfg, 2, device=dev)
+        steps = []
+        for t in range(toks.shape[1]):
+            lg, states = m3.model.lm_decode_step(p_dev, toks[:, t], states, cfg)
+            steps.append(lg)
+    assert_maxrel(torch.stack(steps, dim=1), cpu(full), 1e-4, "decode vs forward (bf16 params)")
 
 
 @pytest.mark.parametrize("policy", ["f32", "bf16"])

@@ -212,3 +212,24 @@ def test_zipf_bytes_and_bigram(m3):
     xs, ys = next(T.batches(data, 4, 64, seed=1))
     assert xs.shape == ys.shape == (4, 64) and xs.dtype == torch.int64
     assert torch.equal(xs[:, 1:], ys[:, :-1])
+
+
+def test_repetition_window_tracks_the_last_ids(m3):
+    """The sampler's penalty set is exactly the ids among the last ``window`` tokens
+    (prompt included), as a brute-force recount over the history says after each push,
+    and a zero window penalises nothing."""
+    RI = m3.train._RecentIds
+    g = torch.Generator().manual_seed(3)
+    history = torch.randint(0, 12, (9,), generator=g).tolist()
+    win = 5
+    rec = RI(win, 12, "cpu", history)
+    hist = list(history)
+    for tok in torch.randint(0, 12, (40,), generator=g).tolist():
+        want = torch.zeros(12, dtype=torch.bool)
+        want[list(set(hist[-win:]))] = True
+        assert torch.equal(rec.mask, want), hist[-win:]
+        rec.push(tok)
+        hist.append(tok)
+    off = RI(0, 12, "cpu", history)
+    off.push(3)
+    assert not bool(off.mask.any())
