@@ -15,8 +15,9 @@
  *    in views of the fused in_proj output (B, L, H*P) without a transpose.
  *  - All other tensors are dense row-major in the shape given in the comment.
  *  - Calls are stream-ordered on `stream` (a hipStream_t, NULL = default stream). No
- *    call allocates, synchronises, or keeps state between calls; concurrent calls on
- *    different streams are safe.
+ *    call allocates or synchronises. Every call but m3s_norm_bwd_noalloc keeps no state
+ *    between calls, and concurrent calls on different streams are safe; that one shares
+ *    a library-owned scratch array per GPU (see its declaration).
  *  - Return value: M3S_OK (0) or a negative M3S_ERR_*; `m3s_last_error()` then holds
  *    a message (thread-local).
  */
@@ -361,6 +362,14 @@ int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
 int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);
 int32_t m3s_norm_fwd(const m3s_norm_fwd_args* args, void* stream);
 int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
+/* m3s_norm_bwd without a caller workspace: no counterpart in the reference. For callers
+ * that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). The gain partials live in a library-owned device array of 4 MiB per GPU
+ * (enough for every width m3s_norm_bwd accepts, at most 512), held until the process
+ * ends; args->workspace is ignored and nothing is allocated or freed. Calls that overlap
+ * on one GPU (different streams, or threads) share that array and race: serialise them.
+ * Widths the array cannot hold are rejected with M3S_ERR_INVALID. */
+int32_t m3s_norm_bwd_noalloc(const m3s_norm_bwd_args* args, void* stream);
 int32_t m3s_transpose(const m3s_transpose_args* args, void* stream);
 int32_t m3s_swiglu_fwd(const m3s_swiglu_args* args, void* stream);
 int32_t m3s_swiglu_bwd(const m3s_swiglu_args* args, void* stream);

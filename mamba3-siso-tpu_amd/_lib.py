@@ -169,7 +169,8 @@ EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_worksp
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
-           "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes")
+           "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes",
+           "m3s_norm_bwd_noalloc")
 
 _lib = None
 
@@ -216,6 +217,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_norm_fwd.argtypes = [C.POINTER(NormFwdArgs), vp]
     lib.m3s_norm_bwd.restype = i32
     lib.m3s_norm_bwd.argtypes = [C.POINTER(NormBwdArgs), vp]
+    lib.m3s_norm_bwd_noalloc.restype = i32
+    lib.m3s_norm_bwd_noalloc.argtypes = [C.POINTER(NormBwdArgs), vp]
     lib.m3s_rms_bwd_workspace_bytes.restype = i64
     lib.m3s_rms_bwd_workspace_bytes.argtypes = [i32]
     for fn in (lib.m3s_rms_fwd, lib.m3s_rms_bwd):

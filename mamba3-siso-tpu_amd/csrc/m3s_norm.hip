@@ -16,6 +16,7 @@
 // gradient is summed per block in a fixed order, then over blocks by a second launch,
 // so it does not depend on the order in which blocks finish. HBM-bound.
 #include <algorithm>
+#include <mutex>
 
 #include "m3s_common.h"
 #include "m3s_internal.h"
@@ -245,46 +246,126 @@ extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
   return launch_status("m3s_norm_fwd");
 }
 
-extern "C" int32_t m3s_norm_bwd(const m3s_norm_bwd_args* a, void* stream) {
-  clear_error();
-  M3S_REQUIRE(a != nullptr, "m3s_norm_bwd: args is NULL");
+namespace m3s {
+
+// Argument checks shared by m3s_norm_bwd and m3s_norm_bwd_noalloc: fills every field of
+// `p` but the gain-partials buffer, and the backward's block count. `what` names the
+// entry point in error messages.
+static int32_t norm_bwd_prepare(const m3s_norm_bwd_args* a, const char* what,
+                                bool need_workspace, NormBwdParams* p, int* nblk) {
+  M3S_REQUIRE(a != nullptr, "%s: args is NULL", what);
   M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_norm_bwd_args),
-              "m3s_norm_bwd: struct_size %d != %d (ABI mismatch)", a->struct_size,
+              "%s: struct_size %d != %d (ABI mismatch)", what, a->struct_size,
               (int)sizeof(m3s_norm_bwd_args));
   const int B = a->batch, L = a->seqlen, N = a->width, cnt = a->count;
-  M3S_REQUIRE(B > 0 && L > 0 && N > 0 && (cnt == 1 || cnt == 2), "m3s_norm_bwd: bad dimension");
+  M3S_REQUIRE(B > 0 && L > 0 && N > 0 && (cnt == 1 || cnt == 2), "%s: bad dimension", what);
   M3S_REQUIRE(a->dtype == M3S_DTYPE_BF16 || a->dtype == M3S_DTYPE_F32,
-              "m3s_norm_bwd: bad dtype %d", a->dtype);
+              "%s: bad dtype %d", what, a->dtype);
   const int vec = a->dtype == M3S_DTYPE_BF16 ? 8 : 4;
   M3S_REQUIRE(N % vec == 0 && N / vec <= 64,
-              "m3s_norm_bwd: width %d must be a multiple of %d and at most %d", N, vec, 64 * vec);
-  M3S_REQUIRE((int64_t)B * L < (1ll << 31), "m3s_norm_bwd: B*L too large");
-  M3S_REQUIRE(a->workspace && aligned16(a->workspace), "m3s_norm_bwd: workspace NULL or misaligned");
-  NormBwdParams p{};
+              "%s: width %d must be a multiple of %d and at most %d", what, N, vec, 64 * vec);
+  M3S_REQUIRE((int64_t)B * L < (1ll << 31), "%s: B*L too large", what);
+  M3S_REQUIRE(!need_workspace || (a->workspace && aligned16(a->workspace)),
+              "%s: workspace NULL or misaligned", what);
+  *p = NormBwdParams{};
   for (int i = 0; i < cnt; ++i) {
-    M3S_REQUIRE(blx_ok(a->x[i], vec), "m3s_norm_bwd: x[%d] must be 16-byte aligned rows", i);
-    M3S_REQUIRE(blx_ok(a->dx[i], vec), "m3s_norm_bwd: dx[%d] must be 16-byte aligned rows", i);
+    M3S_REQUIRE(blx_ok(a->x[i], vec), "%s: x[%d] must be 16-byte aligned rows", what, i);
+    M3S_REQUIRE(blx_ok(a->dx[i], vec), "%s: dx[%d] must be 16-byte aligned rows", what, i);
     M3S_REQUIRE(a->weight[i] && a->rstd[i] && a->dy[i] && aligned16(a->dy[i]) && a->dweight[i],
-                "m3s_norm_bwd: weight/rstd/dy/dweight[%d] NULL or dy misaligned", i);
-    p.in.x[i] = a->x[i].ptr; p.in.xsb[i] = a->x[i].stride_b; p.in.xst[i] = a->x[i].stride_t;
-    p.in.w[i] = a->weight[i];
-    p.rstd[i] = a->rstd[i];
-    p.dy[i] = a->dy[i];
-    p.dx[i] = a->dx[i].ptr; p.dxsb[i] = a->dx[i].stride_b; p.dxst[i] = a->dx[i].stride_t;
+                "%s: weight/rstd/dy/dweight[%d] NULL or dy misaligned", what, i);
+    p->in.x[i] = a->x[i].ptr; p->in.xsb[i] = a->x[i].stride_b; p->in.xst[i] = a->x[i].stride_t;
+    p->in.w[i] = a->weight[i];
+    p->rstd[i] = a->rstd[i];
+    p->dy[i] = a->dy[i];
+    p->dx[i] = a->dx[i].ptr; p->dxsb[i] = a->dx[i].stride_b; p->dxst[i] = a->dx[i].stride_t;
   }
-  p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec);
-  p.part = static_cast<float*>(a->workspace);
-  const int64_t rows_per_pass = kNormThreads / p.G;
-  const int nblk = (int)std::min<int64_t>(kNormBwdBlocks, ((int64_t)B * L + rows_per_pass - 1) / rows_per_pass);
+  p->B = B; p->L = L; p->N = N; p->G = norm_group(N, vec);
+  const int64_t rows_per_pass = kNormThreads / p->G;
+  *nblk = (int)std::min<int64_t>(kNormBwdBlocks, ((int64_t)B * L + rows_per_pass - 1) / rows_per_pass);
+  return M3S_OK;
+}
+
+// The two kernels, with p.part as the gain-partials buffer ((nblk, count, width) f32;
+// every entry the second kernel reads is written by the first, so it needs no clearing).
+static int32_t norm_bwd_run(const m3s_norm_bwd_args* a, const NormBwdParams& p, int nblk,
+                            const char* what, void* stream) {
+  const int cnt = a->count;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->dtype == M3S_DTYPE_BF16)
     hipLaunchKernelGGL(norm_bwd_kernel<bf16>, dim3(nblk, cnt), dim3(kNormThreads), 0, s, p);
   else
     hipLaunchKernelGGL(norm_bwd_kernel<float>, dim3(nblk, cnt), dim3(kNormThreads), 0, s, p);
-  int32_t rc = launch_status("m3s_norm_bwd");
+  int32_t rc = launch_status(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(norm_gain_kernel, dim3((N + 63) / 64, cnt),
+  hipLaunchKernelGGL(norm_gain_kernel, dim3((p.N + 63) / 64, cnt),
                      dim3(kNormThreads), 0, s, p.part, a->dweight[0], cnt > 1 ? a->dweight[1] : nullptr,
-                     nblk, N);
-  return launch_status("m3s_norm_bwd");
+                     nblk, p.N);
+  return launch_status(what);
+}
+
+// ---- scratch of m3s_norm_bwd_noalloc ------------------------------------------------
+// The gain partials at the widest accepted width (64 16-byte vectors of bf16 = 512):
+// (kNormBwdBlocks, 2, 512) f32 = 4 MiB. A __device__ array exists once per device and
+// lives until the process ends. In host code its name is only a stand-in for the symbol,
+// so the device address is looked up (hipGetSymbolAddress) once per device, with that
+// device current, and only that address is handed to kernels.
+constexpr int kNormScratchWidth = 512;
+constexpr int64_t kNormScratchBytes = (int64_t)kNormBwdBlocks * 2 * kNormScratchWidth * 4;
+static __device__ __align__(256) float scratch[kNormBwdBlocks * 2 * kNormScratchWidth];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices];
+
+static int32_t scratch_for_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("m3s_norm_bwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return M3S_ERR_LAUNCH;
+  }
+  M3S_REQUIRE(dev >= 0 && dev < kMaxDevices, "m3s_norm_bwd_noalloc: device ordinal %d past %d",
+              dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("m3s_norm_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return M3S_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return M3S_OK;
+}
+
+}  // namespace m3s
+
+extern "C" int32_t m3s_norm_bwd(const m3s_norm_bwd_args* a, void* stream) {
+  clear_error();
+  NormBwdParams p;
+  int nblk = 0;
+  int32_t rc = norm_bwd_prepare(a, "m3s_norm_bwd", true, &p, &nblk);
+  if (rc != M3S_OK) return rc;
+  p.part = static_cast<float*>(a->workspace);
+  return norm_bwd_run(a, p, nblk, "m3s_norm_bwd", stream);
+}
+
+extern "C" int32_t m3s_norm_bwd_noalloc(const m3s_norm_bwd_args* a, void* stream) {
+  clear_error();
+  NormBwdParams p;
+  int nblk = 0;
+  int32_t rc = norm_bwd_prepare(a, "m3s_norm_bwd_noalloc", false, &p, &nblk);
+  if (rc != M3S_OK) return rc;
+  const int64_t need = (int64_t)nblk * 2 * p.N * 4;
+  M3S_REQUIRE(need <= kNormScratchBytes,
+              "m3s_norm_bwd_noalloc: width %d needs %lld bytes of scratch, past the %lld reserved",
+              p.N, (long long)need, (long long)kNormScratchBytes);
+  float* part = nullptr;
+  rc = scratch_for_current_device(&part);
+  if (rc != M3S_OK) return rc;
+  p.part = part;
+  return norm_bwd_run(a, p, nblk, "m3s_norm_bwd_noalloc", stream);
 }
