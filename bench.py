@@ -62,17 +62,51 @@ def gpu_time_ms(fn, iters, torch):
 
 def scan_inputs(m3, params16, cfg, u, torch):
     """Kernel-boundary operands of the configs[1] layer: the projections of ``u`` through
-    split_in_proj, BCNorm and preprocess, exactly as the layer hands them to the scan."""
+    split_in_proj, BCNorm and preprocess, as the layer hands them to the scan -- phi in
+    the compact form the layer uses (``kernels.PhiStrips``), and the same phi
+    materialised (``phi_full``) for the phi-reading mode."""
+    from mamba3_siso_tpu_amd import scan_prep as SP
+
     with torch.no_grad():
         proj = u @ params16.in_proj
         z, x, bb, cc, dt_raw, a_raw, trap_raw, angles = m3.split_in_proj(proj, cfg)
         kq = m3.rms_norm(cc, params16.c_norm_weight, cfg.norm_eps)
         kk = m3.rms_norm(bb, params16.b_norm_weight, cfg.norm_eps)
-        pre, _ = m3.preprocess(dt_raw, a_raw, trap_raw, angles, params16.dt_bias)
+        bias = params16.dt_bias.float().contiguous()
+        adt, gamma, scale, _, _, strips, _ = SP.prep_forward_launch(
+            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=True)
+        phi_full = SP.prep_forward_launch(dt_raw, a_raw, trap_raw, angles, bias, None,
+                                          cfg.a_floor)[5]
         kv, kz = x.permute(0, 2, 1, 3), z.permute(0, 2, 1, 3)
-    return dict(q=kq, k=kk, v=kv, adt=pre.adt, gamma=pre.gamma, scale=pre.scale, phi=pre.phi,
+    return dict(q=kq, k=kk, v=kv, adt=adt, gamma=gamma, scale=scale, phi=strips,
                 q_bias=params16.c_bias.float(), k_bias=params16.b_bias.float(),
-                d_skip=params16.d_skip.float(), z=kz)
+                d_skip=params16.d_skip.float(), z=kz), phi_full
+
+
+def layer_roofline(B, L, DM, cfg, scan_bytes, scan_flops, measured_ms):
+    """The layer forward's time floor: for each kernel, its algorithmic flops at the bf16
+    MFMA peak or its algorithmic bytes at the HBM peak, whichever takes longer, summed
+    over the kernels of the step; ``frac`` = floor / measured."""
+    M, d_in, dpad = B * L, cfg.d_in_proj, (cfg.d_in_proj + 255) // 256 * 256
+    H, N, Nr = cfg.nheads, cfg.d_state, cfg.n_angles
+
+    def floor_ms(flops, nbytes):
+        return max(flops / (BF16_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
+
+    parts = {
+        "in_proj": floor_ms(2 * M * DM * d_in, M * DM * 2 + DM * dpad * 2 + M * dpad * 2),
+        "bcnorm": floor_ms(0, 4 * M * N * 2),
+        "preprocess": floor_ms(0, M * (3 * H + Nr) * 2 + 5 * M * H * 4 + M * Nr * 4
+                               + M * H * Nr * 4),
+        "scan": floor_ms(scan_flops, scan_bytes),
+        "out_proj": floor_ms(2 * M * cfg.d_inner * DM, M * cfg.d_inner * 2 + cfg.d_inner * DM * 2
+                             + M * DM * 2),
+    }
+    floor = sum(parts.values())
+    return {"floor_ms": round(floor, 4), "measured_ms": round(measured_ms, 4),
+            "frac": round(floor / measured_ms, 4),
+            "per_kernel_floor_ms": {k: round(v, 4) for k, v in parts.items()},
+            "peaks": {"bf16_mfma_tflops": BF16_PEAK_TFLOPS, "hbm_gbs": HBM_PEAK_GBS}}
 
 
 def main():
@@ -121,13 +155,20 @@ def main():
     line = {}
 
     # ---------------- the scan kernels alone, kernel boundary -------------------------
-    # algorithmic bytes of one forward launch: q, k once (head-shared), v, z, y bf16;
-    # adt/gamma/scale f32; phi f32; final ssm f32 (+ k, v rows)
-    scan_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * H * L * 4
-                  + B * H * L * Nr * 4 + B * H * P * N * 4 + B * H * (N + P) * 4)
+    # Algorithmic bytes of one forward launch as the layer runs it (phi read): q, k once
+    # (head-shared), v, z, y bf16; adt/gamma/scale f32; phi (B, H, L, Nr) f32; the final
+    # ssm f32 (+ k, v rows). With phi built in the kernel (phi_in_kernel) the tanh(angles)
+    # pi table (head-shared), dt and one phi row per 16 tokens replace phi.
+    phi_compact = B * L * Nr * 4 + B * H * L * 4 + B * H * (L // 16) * Nr * 4
+    phi_read = B * H * L * Nr * 4
+    scan_fixed = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * H * L * 4
+                  + B * H * P * N * 4 + B * H * (N + P) * 4)
+    scan_bytes = scan_fixed + phi_read
     scan_flops = B * H * L * 2 * (2 * N * P + cfg.chunk * N + cfg.chunk * P)
     if args.leg in ("all", "scan", "bwd"):
-        ka = scan_inputs(m3, params16, cfg, u, torch)
+        ka, phi_full = scan_inputs(m3, params16, cfg, u, torch)
+        kc = ka
+        ka = dict(kc, phi=phi_full)
         if args.leg in ("all", "scan"):
             scan = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
             # a kernel-boundary micro-measurement: enough launches that the clocks have
@@ -137,16 +178,24 @@ def main():
             scan_ms = gpu_time_ms(scan, max(args.steps, 50), torch)
             scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
             scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
+            scan_c = lambda: K.siso_forward(**kc, chunk=128)  # noqa: E731
+            for _ in range(5):
+                scan_c()
+            comp_ms = gpu_time_ms(scan_c, max(args.steps, 50), torch)
             line.update(scan_kernel_ms=round(scan_ms, 4),
                         scan_kernel_tok_s=round(tokens / (scan_ms * 1e-3), 1),
                         scan_kernel_gbs=round(scan_gbs, 1),
                         scan_kernel_tflops=round(scan_tflops, 2),
-                        scan_kernel_mfma_frac=round(scan_tflops / BF16_PEAK_TFLOPS, 5))
+                        scan_kernel_mfma_frac=round(scan_tflops / BF16_PEAK_TFLOPS, 5),
+                        scan_kernel_phi_in_kernel_ms=round(comp_ms, 4),
+                        scan_kernel_phi_in_kernel_gbs=round((scan_fixed + phi_compact) / (comp_ms * 1e-3) / 1e9, 1))
             line["roofline"] = {
-                "kernel": "fwd_bf16_kernel<128,128,64> (m3s_fwd, kernel boundary)",
+                "kernel": "fwd_bf16_kernel<128,128,64> (m3s_fwd, kernel boundary, phi read)",
                 "bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic_figure("fwd_bf16_kernel"), "algorithmic_bytes": scan_bytes}
+                "traffic": traffic_figure("fwd_bf16_kernel"),
+                "traffic_source": TRAFFIC_SOURCE, "algorithmic_bytes": scan_bytes,
+                "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5)}
         if args.leg in ("all", "bwd"):
             with torch.no_grad():
                 y, fs, fk, fv, res = K.siso_forward(**ka, chunk=128, save_residuals=True)
@@ -160,10 +209,25 @@ def main():
                     bw()
                 bwd_ms = gpu_time_ms(bw, max(10, args.steps // 2), torch)
             bwd_flops = B * H * L * (2 * cfg.chunk * (3 * N + 2 * P) + 8 * P * N)
+            # The backward's necessary bytes (no per-head rows): reads q, k (head-shared),
+            # v, z, dy bf16, ybar f32, adt/gamma/scale f32, phi f32, the chunk states
+            # bf16; writes dv, dz bf16, dadt/dqk/dscale/uw f32, dphi f32, dq/dk f32.
+            nc = L // cfg.chunk
+            bwd_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + B * H * L * P * 4
+                         + 3 * B * H * L * 4 + phi_read + B * H * nc * N * P * 2
+                         + 2 * B * H * L * P * 2 + 4 * B * H * L * 4 + B * H * L * Nr * 4
+                         + 2 * B * L * N * 4)
+            bwd_gbs = bwd_bytes / (bwd_ms * 1e-3) / 1e9
             line.update(bwd_kernel_ms=round(bwd_ms, 4),
                         bwd_kernel_tflops=round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2))
+            line["bwd_roofline"] = {
+                "kernel": "bwd_bf16_kernel<128,128,64> + headsum_kernel (m3s_bwd)",
+                "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
+                "algorithmic_bytes": bwd_bytes,
+                "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 5)}
             del y, res, dyk
-        del ka
+        del ka, kc, phi_full
         torch.cuda.empty_cache()
         if args.leg != "all":
             print(json.dumps({"leg": args.leg, **line}))
@@ -272,6 +336,7 @@ def main():
         "fwd_bwd_tok_s": round(tokens / (fb_ms * 1e-3), 1),
         "decode_ms_per_token": round(dec_ms, 4),
         **{k: v for k, v in line.items() if k != "roofline"},
+        "layer_roofline": layer_roofline(B, L, DM, cfg, scan_bytes, scan_flops, fwd_ms),
         "lm": lm,
         "reference_tpu_v5e": {"fwd_kernel_ms_chunk128_pinned": 21.66, "fwd_bwd_ms": 80.1,
                               "decode_ms_per_token_b256": 1.4},
@@ -345,6 +410,11 @@ def _zipf_entropy(s):
     return -sum(x / z * math.log(x / z) for x in p)
 
 
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of "
+                  "`bench.py --leg scan`, each scaled by its ratio on `bench.py --leg copy`; "
+                  "measured in its own runs, not in this one")
+
+
 def traffic_figure(kernel):
     """HBM bytes per launch of ``kernel`` from the committed counter summary
     (profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the
@@ -364,7 +434,8 @@ def cpu_baseline(m3, params32, cfg, torch):
     the workload, repeated until ~10 s of CPU work; reported, never a gate."""
     from oracle import siso_oracle as O
 
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
     pd = {f: getattr(params32, f).detach().float().cpu() for f in params32._fields}
     g = torch.Generator().manual_seed(0)
     u = torch.randn(1, 8192, cfg.d_model, generator=g).to(torch.bfloat16).float()
@@ -377,7 +448,7 @@ def cpu_baseline(m3, params32, cfg, torch):
             t_total += time.perf_counter() - t0
             reps += 1
     return {"value": round(reps * u.shape[1] / t_total, 1), "unit": "tok/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": os.cpu_count(), "threads": torch.get_num_threads(), "kind": "port",
             "sample": f"{reps} x one sequence (B=1, L=8192, d_model=1024) of the configs[1] layer "
                       f"forward through oracle.siso_oracle.layer_forward in float32 on "
                       f"{platform.processor() or platform.machine()}"}

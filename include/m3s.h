@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 4
+#define M3S_ABI_VERSION 5
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -66,7 +66,13 @@ typedef struct m3s_fwd_args {
   const float* adt;                    /* (B, H, L)                                   */
   const float* gamma;                  /* (B, H, L)                                   */
   const float* scale;                  /* (B, H, L)                                   */
-  const float* phi;                    /* (B, H, L, Nr)                               */
+  const float* phi;                    /* (B, H, L, Nr), or NULL with phi_strips      */
+  /* phi built in the kernel instead of read (reference.py:134-157 fused into the scan):
+   * phi_t = phi_strips[t / 16] + sum over t' in [16 (t / 16), t] of theta_table[t'] dt[t'],
+   * angles taken mod 2 pi. Give all three (and phi = NULL) or none; L % 16 == 0. */
+  const float* theta_table;            /* (B, L, Nr) tanh(angles) pi, shared by heads */
+  const float* phi_dt;                 /* (B, H, L) dt                                */
+  const float* phi_strips;             /* (B, H, L / 16, Nr) phi entering each strip  */
   const float* q_bias;                 /* (H, N)                                      */
   const float* k_bias;                 /* (H, N)                                      */
   const float* d_skip;                 /* (H), if has_d                               */
@@ -101,7 +107,10 @@ typedef struct m3s_bwd_args {
   const float* adt;            /* (B, H, L)                                            */
   const float* gamma;          /* (B, H, L)                                            */
   const float* scale;          /* (B, H, L)                                            */
-  const float* phi;            /* (B, H, L, Nr)                                        */
+  const float* phi;            /* (B, H, L, Nr), or NULL with phi_strips               */
+  const float* theta_table;    /* phi built in the kernel, as in m3s_fwd_args          */
+  const float* phi_dt;
+  const float* phi_strips;
   const float* q_bias;         /* (H, N)                                               */
   const float* k_bias;         /* (H, N)                                               */
   const float* d_skip;         /* (H), if has_d                                        */
@@ -199,8 +208,14 @@ typedef struct m3s_prep_fwd_args {
   float* scale;        /* out (B, H, L)                   */
   float* lam;          /* out (B, H, L)                   */
   float* dt;           /* out (B, H, L)                   */
-  float* phi;          /* out (B, H, L, Nr)               */
+  float* phi;          /* out (B, H, L, Nr), or NULL      */
   float* phi_final;    /* out (B, H, Nr) = phi[:, :, L-1] */
+  /* The compact form m3s_fwd / m3s_bwd rebuild phi from (their phi_strips mode):
+   * theta_table = tanh(angles) pi, and phi_strips[s] = wrap(phi_init + sum over t < 16 s
+   * of theta_t), the angle entering token 16 s. NULL = not written; phi_strips needs
+   * L % 16 == 0. At least one of phi and phi_strips is given. */
+  float* theta_table;  /* out (B, L, Nr), or NULL          */
+  float* phi_strips;   /* out (B, H, L / 16, Nr), or NULL  */
   void* workspace;     /* scratch, m3s_prep_fwd_workspace_bytes() bytes, 16-aligned */
 } m3s_prep_fwd_args;
 

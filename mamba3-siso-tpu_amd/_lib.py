@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -39,6 +39,7 @@ class FwdArgs(C.Structure):
         ("has_d", i32), ("has_z", i32), ("has_seed", i32), ("save_residuals", i32),
         ("q", vp), ("k", vp), ("v", Bhlp), ("z", Bhlp),
         ("adt", vp), ("gamma", vp), ("scale", vp), ("phi", vp),
+        ("theta_table", vp), ("phi_dt", vp), ("phi_strips", vp),
         ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
         ("seed_ssm", vp), ("seed_k", vp), ("seed_v", vp), ("seed_coef", vp),
         ("y", Bhlp), ("ybar", vp), ("chunk_states", vp),
@@ -55,6 +56,7 @@ class BwdArgs(C.Structure):
         ("has_d", i32), ("has_z", i32),
         ("dy", Bhlp), ("ybar", vp), ("z", Bhlp), ("q", vp), ("k", vp), ("v", Bhlp),
         ("adt", vp), ("gamma", vp), ("scale", vp), ("phi", vp),
+        ("theta_table", vp), ("phi_dt", vp), ("phi_strips", vp),
         ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
         ("chunk_states", vp), ("dfinal_ssm", vp), ("dfinal_v", vp),
         ("dq", vp), ("dk", vp), ("dv", Bhlp), ("dz", Bhlp),
@@ -101,7 +103,8 @@ class PrepFwdArgs(C.Structure):
         ("dt_raw", Blx), ("a_raw", Blx), ("trap_raw", Blx), ("angles", Blx),
         ("dt_bias", vp), ("phi_init", vp),
         ("adt", vp), ("gamma", vp), ("scale", vp), ("lam", vp), ("dt", vp),
-        ("phi", vp), ("phi_final", vp), ("workspace", vp),
+        ("phi", vp), ("phi_final", vp), ("theta_table", vp), ("phi_strips", vp),
+        ("workspace", vp),
     ]
 
 

@@ -47,6 +47,9 @@ struct BwdParams {
   const float* gamma;
   const float* scale;
   const float* phi;
+  const float* tht;    // phi_strips mode (see FwdParams); else NULL
+  const float* pdt;
+  const float* pstr;
   const float* qb;
   const float* kb;
   const float* dsk;
@@ -127,7 +130,7 @@ __device__ __forceinline__ sub_t<MT> zero_sub() {
   return sub_from_f32<MT>(f32x4{0.f, 0.f, 0.f, 0.f});
 }
 
-template <typename MT, int C, int N, int P, int NW>
+template <typename MT, int C, int N, int P, int NW, bool STRIPS>
 __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   using F = BwdCfg<MT, C, N, P, NW>;
   using vec = typename BV16<MT>::type;
@@ -192,11 +195,32 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   const float* adtg = p.adt + bh * L;
   const float* gamg = p.gamma + bh * L;
   const float* sclg = p.scale + bh * L;
-  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  const float* phig = STRIPS ? nullptr : p.phi + bh * (int64_t)L * Nr;
   const MT* csg = static_cast<const MT*>(p.cstates) + bh * (int64_t)nc * N * P;
   MT* dug = static_cast<MT*>(p.part) + bh * (int64_t)L * N;                 // du rows of (b, h)
   MT* dwg = static_cast<MT*>(p.part) + ((int64_t)p.B * p.H + bh) * L * N;   // dw rows of (b, h)
   const bool phi_vec = (Nr % 4) == 0;
+  // phi of row t (global index) at angles j0 .. j0 + VEC - 1, 0 past Nr: read, or
+  // (phi_strips mode) the strip's entering angle plus theta = tanh(angles) pi dt over the
+  // strip's rows up to t (at most 16)
+  auto phi_row = [&](int64_t t, int j0, float (&out)[VEC]) {
+    if constexpr (STRIPS) {
+      const int64_t s16 = t >> 4;
+      const float* ps = p.pstr + (bh * (L / 16) + s16) * Nr;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) out[i] = (j0 + i < Nr) ? ps[j0 + i] : 0.f;
+      for (int64_t u = 16 * s16; u <= t; ++u) {
+        const float du = p.pdt[bh * L + u];
+        const float* tr = p.tht + ((int64_t)b * L + u) * Nr;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          if (j0 + i < Nr) out[i] += tr[j0 + i] * du;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) out[i] = (j0 + i < Nr) ? phig[t * Nr + j0 + i] : 0.f;
+    }
+  };
 
   // ---- adjoint G (registers, MFMA layout [p][n]) -----------------------------------
   f32x4 Gacc[F::SPW];
@@ -248,15 +272,22 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
           q_[r][e][1] = *reinterpret_cast<const vec*>(qg + t * N + H2 + j0);
           k_[r][e][0] = *reinterpret_cast<const vec*>(kg + t * N + j0);
           k_[r][e][1] = *reinterpret_cast<const vec*>(kg + t * N + H2 + j0);
-          const float* pr = phig + t * Nr;
+          if constexpr (STRIPS) {
+            float pv[VEC];
+            phi_row(t, j0, pv);
 #pragma unroll
-          for (int qd = 0; qd < VEC / 4; ++qd) {
-            const int j = j0 + 4 * qd;
-            if (phi_vec && j + 4 <= Nr) {
-              ph_[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
-            } else {
+            for (int i = 0; i < VEC; ++i) ph_[r][e][i / 4][i % 4] = pv[i];
+          } else {
+            const float* pr = phig + t * Nr;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) ph_[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+            for (int qd = 0; qd < VEC / 4; ++qd) {
+              const int j = j0 + 4 * qd;
+              if (phi_vec && j + 4 <= Nr) {
+                ph_[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
+              } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ph_[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+              }
             }
           }
           sc_[r][e] = sclg[t];
@@ -691,7 +722,8 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
           const vec k1 = *reinterpret_cast<const vec*>(kg + tg * N + H2 + j0);
           const float sc = sScl[t];
           const float cd = sDqk[t] * sGam[t];
-          const float* pr = phig + tg * Nr;
+          float pr[VEC];
+          phi_row(tg, j0, pr);
           vec du0, du1, dw0, dw1;
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
@@ -701,7 +733,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
             const float wlo = (float)k0[i] + sKb[j];
             const float whi = (float)k1[i] + sKb[H2 + j];
             float sn = 0.f, cs = 1.f;
-            if (j < Nr) sincosf(pr[j], &sn, &cs);
+            if (j < Nr) sincosf(pr[i], &sn, &cs);
             const float qlo = ulo * cs - uhi * sn, qhi = uhi * cs + ulo * sn;
             const float klo = wlo * cs - whi * sn, khi = whi * cs + wlo * sn;
             const float dqlo = sDQ[t * LDF + j], dqhi = sDQ[t * LDF + H2 + j];
@@ -870,7 +902,7 @@ struct Bwd2Cfg {
   static_assert(C <= N, "the dv rows are staged in the adjoint's N-row slot");
 };
 
-template <int C, int N, int P>
+template <int C, int N, int P, bool STRIPS>
 __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p) {
   using F = Bwd2Cfg<C, N, P>;
   using vec = bf16x8;
@@ -926,7 +958,11 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   bf16* dzg = p.has_z ? static_cast<bf16*>(p.dz) + b * p.dz_sb + h * p.dz_sh : nullptr;
   bf16* dvg = static_cast<bf16*>(p.dv) + b * p.dv_sb + h * p.dv_sh;
   const float* ybg = p.ybar + bh * (int64_t)L * P;
-  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  // phi rows of this (b, h), or (phi_strips mode) the head-shared tanh(angles) pi rows of
+  // batch element b with the same addressing, plus dt and the strips' entering angles
+  const float* phig = STRIPS ? p.tht + (int64_t)b * L * Nr : p.phi + bh * (int64_t)L * Nr;
+  const float* pdtg = STRIPS ? p.pdt + bh * L : nullptr;
+  const float* pstrg = STRIPS ? p.pstr + bh * (int64_t)(L / 16) * Nr : nullptr;
   const bf16* csg = static_cast<const bf16*>(p.cstates) + bh * (int64_t)nc * N * P;
   bf16* dug = static_cast<bf16*>(p.part) + bh * (int64_t)L * N;                 // du rows of (b, h)
   bf16* dwg = static_cast<bf16*>(p.part) + ((int64_t)p.B * p.H + bh) * L * N;   // dw rows of (b, h)
@@ -993,7 +1029,9 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 
   // ---- register prefetch of one chunk's raw inputs, in two parts -------------------
   vec rq[F::QKR][2][2], rk[F::QKR][2][2];
-  f32x4 rphi[F::QKR][2][VEC / 4];
+  f32x4 rphi[F::QKR][2][VEC / 4];   // phi (or the tanh(angles) pi rows), then turns
+  float rpdt[F::QKR][2];             // phi_strips mode: dt of the two rows
+  f32x4 rstr[STRIPS ? F::QKR : 1][VEC / 4];   // phi_strips mode: the strip's entering angles
   float rscale[F::QKR][2];
   vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2];
   f32x4 ryb[F::VR][2][VEC / 4];
@@ -1022,6 +1060,59 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
           for (int qd = 0; qd < VEC / 4; ++qd)
             rphi[r][e][qd] = phi_quad(t, j0 + 4 * qd, sphi);
           rscale[r][e] = scl_r[(uint32_t)(c * C + t)];
+          if constexpr (STRIPS) rpdt[r][e] = pdtg[(uint32_t)(c * C + t)];
+        }
+        if constexpr (STRIPS) {
+          // both rows of the pair lie in strip (c C + 2 tp) / 16
+          const uint32_t so = (uint32_t)((c * C + 2 * tp) >> 4) * Nr;
+#pragma unroll
+          for (int qd = 0; qd < VEC / 4; ++qd) {
+            const int j = j0 + 4 * qd;
+            if (phi_vec) {
+              rstr[r][qd] = gld<f32x4>(pstrg, (so + (j + 4 <= Nr ? (uint32_t)j : 0u)) * 4);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                rstr[r][qd][i] = (j + i < Nr) ? gld<float>(pstrg, (so + j + i) * 4) : 0.f;
+            }
+          }
+        }
+      }
+    }
+  };
+  // rphi -> the rows' angles in turns, in place, once the loads have landed. phi mode:
+  // phi / (2 pi) (phi is wrapped). phi_strips mode: the strip's entering angle plus the
+  // inclusive prefix of theta = table * dt over the strip's rows; a lane holds two rows
+  // (a row pair), and the strip's eight row pairs are the lanes QKG apart that share
+  // j0, so the exclusive part is a shuffle scan over those lanes. Quads past Nr (never
+  // used) hold junk.
+  auto angles_to_turns = [&]() {
+    int ln = threadIdx.x;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln & 63;
+    const int pos = (lane / F::QKG) & 7;   // row pair within the strip
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+#pragma unroll
+      for (int qd = 0; qd < VEC / 4; ++qd) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (STRIPS) {
+            const float t0v = rphi[r][0][qd][i] * rpdt[r][0];
+            const float t1v = rphi[r][1][qd][i] * rpdt[r][1];
+            float incl = t0v + t1v;
+#pragma unroll
+            for (int k = 1; k < 8; k <<= 1) {
+              const float o = __shfl_up(incl, k * F::QKG, 64);
+              incl += (pos >= k) ? o : 0.f;
+            }
+            const float before = rstr[r][qd][i] + (incl - (t0v + t1v));
+            rphi[r][0][qd][i] = __builtin_amdgcn_fractf((before + t0v) * 0.15915494309189535f);
+            rphi[r][1][qd][i] = __builtin_amdgcn_fractf((before + t0v + t1v) * 0.15915494309189535f);
+          } else {
+            rphi[r][0][qd][i] *= 0.15915494309189535f;
+            rphi[r][1][qd][i] *= 0.15915494309189535f;
+          }
         }
       }
     }
@@ -1161,6 +1252,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+      angles_to_turns();
 #pragma unroll
       for (int r = 0; r < F::QKR; ++r) {
         const int task = tid + r * NT;
@@ -1183,7 +1275,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               uw[e] += ulo * wlo + uhi * whi;
               // phi in [0, 2 pi): hardware sin / cos, argument in turns; the identity past
               // Nr by select (no divergent branch: half of every wave's lanes rotate)
-              const float turns = rphi[r][e][i / 4][i % 4] * 0.15915494309189535f;
+              const float turns = rphi[r][e][i / 4][i % 4];
               const float sn = (j < Nr) ? __builtin_amdgcn_sinf(turns) : 0.f;
               const float cs = (j < Nr) ? __builtin_amdgcn_cosf(turns) : 1.f;
               const float sc = rscale[r][e];
@@ -1435,6 +1527,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
 
     // ============ phase R: rotation pullback, per-row reductions, head sum ============
     {
+      angles_to_turns();
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
       const int tid = ln, lane = ln & 63;
@@ -1485,7 +1578,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
               const float uhi = (float)q1[i] + sQb[H2 + j];
               const float wlo = (float)k0[i] + sKb[j];
               const float whi = (float)k1[i] + sKb[H2 + j];
-              const float turns = ph[i] * 0.15915494309189535f;
+              const float turns = ph[i];
               const float sn = (j < Nr) ? __builtin_amdgcn_sinf(turns) : 0.f;
               const float cs = (j < Nr) ? __builtin_amdgcn_cosf(turns) : 1.f;
               const float qlo = ulo * cs - uhi * sn, qhi = uhi * cs + ulo * sn;
@@ -1670,15 +1763,22 @@ static bool bwd_fits_rsrc(const BwdParams& p, int N, int P) {
 template <typename MT, int C, int N, int P>
 static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   bool done = false;
+  const bool strips = prm.pstr != nullptr;
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0 && C <= N) {
     if (bwd_fits_rsrc(prm, N, P)) {
-      hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      if (strips)
+        hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      else
+        hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P, false>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
       done = true;
     }
   }
   if (!done) {
     constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
-    hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+    if (strips)
+      hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW, true>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+    else
+      hipLaunchKernelGGL((bwd_kernel<MT, C, N, P, NW, false>), dim3(grid), dim3(NW * 64), 0, stream, prm);
   }
   int32_t rc = launch_status("m3s_bwd");
   if (rc != M3S_OK) return rc;
@@ -1759,9 +1859,15 @@ extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
                             aligned16(a->ybar)),
               "m3s_bwd: has_z needs z, dz and an aligned ybar");
   M3S_REQUIRE(a->q && a->k && aligned16(a->q) && aligned16(a->k), "m3s_bwd: q/k null or misaligned");
-  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->phi && a->q_bias && a->k_bias,
+  const bool strips = a->theta_table || a->phi_dt || a->phi_strips;
+  M3S_REQUIRE(!strips || (a->theta_table && a->phi_dt && a->phi_strips && !a->phi),
+              "m3s_bwd: give phi, or theta_table, phi_dt and phi_strips (not both)");
+  M3S_REQUIRE(!strips || L % 16 == 0, "m3s_bwd: phi_strips needs seqlen %% 16 == 0");
+  M3S_REQUIRE(a->adt && a->gamma && a->scale && (a->phi || strips) && a->q_bias && a->k_bias,
               "m3s_bwd: a required input pointer is NULL");
-  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 || aligned16(a->phi), "m3s_bwd: phi misaligned");
+  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 ||
+                  (strips ? aligned16(a->theta_table) && aligned16(a->phi_strips) : aligned16(a->phi)),
+              "m3s_bwd: phi (or theta_table / phi_strips) misaligned");
   M3S_REQUIRE(a->chunk_states && aligned16(a->chunk_states), "m3s_bwd: chunk_states null or misaligned");
   M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_bwd: has_d but d_skip is NULL");
   M3S_REQUIRE(a->dq && a->dk && aligned16(a->dq) && aligned16(a->dk) && a->dadt && a->dqk_diag &&
@@ -1780,6 +1886,9 @@ extern "C" int32_t m3s_bwd(const m3s_bwd_args* a, void* stream) {
   prm.q = a->q; prm.k = a->k;
   prm.v = a->v.ptr; prm.v_sb = a->v.stride_b; prm.v_sh = a->v.stride_h; prm.v_st = a->v.stride_t;
   prm.adt = a->adt; prm.gamma = a->gamma; prm.scale = a->scale; prm.phi = a->phi;
+  prm.tht = strips ? a->theta_table : nullptr;
+  prm.pdt = strips ? a->phi_dt : nullptr;
+  prm.pstr = strips ? a->phi_strips : nullptr;
   prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
   prm.cstates = a->chunk_states; prm.dfs = a->dfinal_ssm; prm.dfv = a->dfinal_v;
   prm.dq = a->dq; prm.dk = a->dk;

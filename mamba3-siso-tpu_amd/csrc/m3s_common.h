@@ -220,6 +220,24 @@ __device__ __forceinline__ float dpp_mov(float v) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
 }
 
+// row_shr:n -- lane i of a 16-lane row reads lane i - n of that row; the first n lanes
+// of the row read 0 (their write is masked off and they keep the `old` operand, 0).
+template <int n>
+__device__ __forceinline__ float dpp_row_shr(float v) {
+  static_assert(n >= 1 && n <= 15, "row_shr range");
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 + n, 0xF, 0xF, false));
+}
+// Inclusive prefix sum along each 16-lane row: lane i of a row gets the sum of lanes
+// 0 .. i of that row (Hillis-Steele, four DPP adds).
+__device__ __forceinline__ float row_prefix16(float v) {
+  v += dpp_row_shr<1>(v);
+  v += dpp_row_shr<2>(v);
+  v += dpp_row_shr<4>(v);
+  v += dpp_row_shr<8>(v);
+  return v;
+}
+
 // Sum over aligned groups of W lanes (W a power of two <= 64), in every lane of the
 // group: after the quad swaps each quad holds its sum, the half mirror pairs the two
 // quads of an 8-lane half, the row mirror the two halves of a row; across rows, lane

@@ -42,6 +42,9 @@ struct FwdParams {
   const float* gamma;
   const float* scale;
   const float* phi;
+  const float* tht;    // phi_strips mode: tanh(angles) pi (B, L, Nr), dt (B, H, L),
+  const float* pdt;    // phi entering each 16-token strip (B, H, L / 16, Nr); else NULL
+  const float* pstr;
   const float* qb;
   const float* kb;
   const float* dsk;
@@ -95,7 +98,7 @@ struct FwdCfg {
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
 };
 
-template <typename MT, int C, int N, int P, int NW>
+template <typename MT, int C, int N, int P, int NW, bool STRIPS>
 __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   using F = FwdCfg<MT, C, N, P, NW>;
   using vec = typename V16<MT>::type;
@@ -142,7 +145,7 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   const float* adtg = p.adt + bh * L;
   const float* gamg = p.gamma + bh * L;
   const float* sclg = p.scale + bh * L;
-  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  const float* phig = STRIPS ? nullptr : p.phi + bh * (int64_t)L * Nr;
   MT* csg = p.save ? static_cast<MT*>(p.cstates) + bh * (int64_t)nc * N * P : nullptr;
 
   // ---- carried state: registers, MFMA layout ------------------------------------
@@ -204,15 +207,43 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
           rq[r][e][1] = *reinterpret_cast<const vec*>(qg + t * N + H2 + j0);
           rk[r][e][0] = *reinterpret_cast<const vec*>(kg + t * N + j0);
           rk[r][e][1] = *reinterpret_cast<const vec*>(kg + t * N + H2 + j0);
-          const float* pr = phig + t * Nr;
+          if constexpr (STRIPS) {
+            // the strip's entering angle plus theta = tanh(angles) pi dt over the strip's
+            // rows up to t (at most 16)
+            const int64_t s16 = t >> 4;
+            const float* ps = p.pstr + (bh * (L / 16) + s16) * Nr;
+            const float* tb = p.tht + (int64_t)b * L * Nr;
+            const float* db = p.pdt + bh * L;
 #pragma unroll
-          for (int qd = 0; qd < VEC / 4; ++qd) {
-            const int j = j0 + 4 * qd;
-            if (phi_vec && j + 4 <= Nr) {
-              rphi[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
-            } else {
+            for (int qd = 0; qd < VEC / 4; ++qd) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) rphi[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+              for (int i = 0; i < 4; ++i) {
+                const int j = j0 + 4 * qd + i;
+                rphi[r][e][qd][i] = j < Nr ? ps[j] : 0.f;
+              }
+            }
+            for (int64_t u = s16 * 16; u <= t; ++u) {
+              const float du = db[u];
+#pragma unroll
+              for (int qd = 0; qd < VEC / 4; ++qd) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  const int j = j0 + 4 * qd + i;
+                  if (j < Nr) rphi[r][e][qd][i] += tb[u * Nr + j] * du;
+                }
+              }
+            }
+          } else {
+            const float* pr = phig + t * Nr;
+#pragma unroll
+            for (int qd = 0; qd < VEC / 4; ++qd) {
+              const int j = j0 + 4 * qd;
+              if (phi_vec && j + 4 <= Nr) {
+                rphi[r][e][qd] = *reinterpret_cast<const f32x4*>(pr + j);
+              } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rphi[r][e][qd][i] = (j + i < Nr) ? pr[j + i] : 0.f;
+              }
             }
           }
           rscale[r][e] = sclg[t];
@@ -610,7 +641,7 @@ __device__ __forceinline__ bf16x4 ld_tr4_at(const bf16* ptr) {
   return __builtin_bit_cast(bf16x4, r);
 }
 
-template <int C, int N, int P>
+template <int C, int N, int P, bool STRIPS>
 __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p) {
   using F = Fwd2Cfg<C, N, P>;
   constexpr int NT = F::NT, LDK = F::LDK, LDO = F::LDO;
@@ -663,12 +694,18 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   const float* adtg = p.adt + bh * L;
   const float* gamg = p.gamma + bh * L;
   const float* sclg = p.scale + bh * L;
-  const float* phig = p.phi + bh * (int64_t)L * Nr;
+  // phi rows of this (b, h), or (phi_strips mode) the head-shared tanh(angles) pi rows of
+  // batch element b, read with the same row addressing; then dt and the strip values
+  const float* phig = STRIPS ? p.tht + (int64_t)b * L * Nr : p.phi + bh * (int64_t)L * Nr;
   bf16* csg = p.save ? static_cast<bf16*>(p.cstates) + bh * (int64_t)nc * N * P : nullptr;
   // buffer descriptors of this (b, h)'s streams (the host checked every extent < 2^31)
   const auto rQ = make_rsrc(qg, (uint32_t)L * N * 2);
   const auto rK = make_rsrc(kg, (uint32_t)L * N * 2);
   const auto rPhi = make_rsrc(phig, (uint32_t)L * Nr * 4);
+  // dt and the strip angles through SGPR-base global loads (two SGPRs per base where a
+  // buffer descriptor takes four): past the last chunk they read chunk 0 again, unused
+  const float* pdtg = STRIPS ? p.pdt + bh * L : nullptr;
+  const float* pstrg = STRIPS ? p.pstr + bh * (int64_t)(L / 16) * Nr : nullptr;
   const auto rScl = make_rsrc(sclg, (uint32_t)L * 4);
   const auto rGam = make_rsrc(gamg, (uint32_t)L * 4);
   const auto rAdt = make_rsrc(adtg, (uint32_t)L * 4);
@@ -747,7 +784,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // ---- raw q, k, phi, scale, gamma of one chunk, prefetched into registers ---------
   // Strip layout: lane row 16 strip + (lane & 15), K group 8 (lane >> 4).
   bf16x8 rq[F::NBK], rk[F::NBK];
-  f32x4 rphi[F::LOB][2];
+  f32x4 rphi[F::LOB][2];          // phi, or (phi_strips mode) tanh(angles) pi of the row
+  f32x4 rstr[STRIPS ? F::LOB : 1][2];   // phi_strips mode: phi entering this lane's strip
+  float rpdt = 0.f;                 // phi_strips mode: dt of the row
   float rscale, rgam;
   float radt[F::E];
   const bool phi_vec = (Nr % 4) == 0;
@@ -781,6 +820,30 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int trow = 16 * strip + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     const uint32_t sphi = (uint32_t)c * C * Nr * 4;
+    if constexpr (STRIPS) {
+      // the strip's entering angles: one 32-byte piece per lane group (16 lanes read it)
+      const uint32_t sstr = (uint32_t)(c * (C / 16) + strip) * Nr * 4;
+#pragma unroll
+      for (int lb = 0; lb < F::LOB; ++lb) {
+        if (32 * lb >= Nr) {
+#pragma unroll
+          for (int qd = 0; qd < 2; ++qd) rstr[lb][qd] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else if (phi_vec && 32 * lb + 32 <= Nr) {
+#pragma unroll
+          for (int qd = 0; qd < 2; ++qd)
+            rstr[lb][qd] = gld<f32x4>(pstrg, sstr + (uint32_t)(32 * lb + g8 + 4 * qd) * 4);
+        } else {
+#pragma unroll
+          for (int qd = 0; qd < 2; ++qd) {
+            const int j = 32 * lb + g8 + 4 * qd;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              rstr[lb][qd][i] = (j + i < Nr) ? gld<float>(pstrg, sstr + (uint32_t)(j + i) * 4) : 0.f;
+          }
+        }
+      }
+      rpdt = gld<float>(pdtg, (uint32_t)(c * C + trow) * 4);
+    }
 #pragma unroll
     for (int lb = 0; lb < F::LOB; ++lb) {
       // wave-uniform cases first: a block of 32 columns wholly past Nr needs no load, one
@@ -893,10 +956,22 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       kl = (float)rk[lb][s] + bkl[s >> 2][s & 3];
       kh = (float)rk[hb][s] + bkh[s >> 2][s & 3];
     };
-    // rotate (lo, hi) by phi: the hardware sin / cos with the argument in turns (phi is
-    // wrapped to [0, 2 pi)); accurate far below the bf16 rounding of what they feed
-    auto rotate = [](float phi, float& ql, float& qh, float& kl, float& kh) {
-      const float turns = phi * 0.15915494309189535f;
+    // angle s of this lane's block lb, in turns: phi is read wrapped to [0, 2 pi); in
+    // phi_strips mode it is the strip's entering angle plus the inclusive prefix of
+    // theta = tanh(angles) pi dt over the strip's rows -- the 16 lanes of a DPP row are the
+    // strip's 16 rows -- keeping the fraction of a turn. Evaluated only on the rotary
+    // paths below, so blocks past Nr cost nothing.
+    auto turns_of = [&](int lb, int s) {
+      if constexpr (STRIPS) {
+        const float th = row_prefix16(rphi[lb][s >> 2][s & 3] * rpdt);
+        return __builtin_amdgcn_fractf((rstr[lb][s >> 2][s & 3] + th) * 0.15915494309189535f);
+      } else {
+        return rphi[lb][s >> 2][s & 3] * 0.15915494309189535f;
+      }
+    };
+    // rotate (lo, hi) by an angle given in turns, with the hardware sin / cos; accurate
+    // far below the bf16 rounding of what they feed
+    auto rotate = [](float turns, float& ql, float& qh, float& kl, float& kh) {
       const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
       const float q0 = ql * cs - qh * sn, q1 = qh * cs + ql * sn;
       const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
@@ -924,6 +999,11 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       // register copies on every pair)
       auto run = [&](auto mode) {
         constexpr int M = decltype(mode)::value;   // 0: none rotary, 1: all, 2: n < Nr
+        float trn[8];
+        if constexpr (M != 0) {
+#pragma unroll
+          for (int s = 0; s < 8; ++s) trn[s] = turns_of(lb, s);
+        }
         bf16x8 kl8, kh8;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -931,9 +1011,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
           pair(lb, s, bql, bqh, bkl, bkh, ql, qh, kl, kh);
           uw += ql * kl + qh * kh;
           if constexpr (M == 1) {
-            rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
+            rotate(trn[s], ql, qh, kl, kh);
           } else if constexpr (M == 2) {
-            if (32 * lb + g8 + s < Nr) rotate(rphi[lb][s >> 2][s & 3], ql, qh, kl, kh);
+            if (32 * lb + g8 + s < Nr) rotate(trn[s], ql, qh, kl, kh);
           }
           qf[lb][s] = (bf16)ql;
           qf[hb][s] = (bf16)qh;
@@ -1244,7 +1324,14 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int64_t row = (int64_t)(L - 1) * N;
     float kl = (float)kg[row + j] + sKb[j], kh = (float)kg[row + H2 + j] + sKb[H2 + j];
     if (j < Nr) {
-      const float turns = phig[(int64_t)(L - 1) * Nr + j] * 0.15915494309189535f;
+      float turns;
+      if constexpr (STRIPS) {   // the last strip's entering angle plus its 16 thetas
+        float ph = p.pstr[(bh * (L / 16) + L / 16 - 1) * Nr + j];
+        for (int t = L - 16; t < L; ++t) ph += phig[(int64_t)t * Nr + j] * p.pdt[bh * L + t];
+        turns = __builtin_amdgcn_fractf(ph * 0.15915494309189535f);
+      } else {
+        turns = phig[(int64_t)(L - 1) * Nr + j] * 0.15915494309189535f;
+      }
       const float sn = __builtin_amdgcn_sinf(turns), cs = __builtin_amdgcn_cosf(turns);
       const float k0 = kl * cs - kh * sn, k1 = kh * cs + kl * sn;
       kl = k0;
@@ -1268,15 +1355,22 @@ static bool fits_rsrc(const FwdParams& p, int N, int P) {
 
 template <typename MT, int C, int N, int P>
 static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
+  const bool strips = prm.pstr != nullptr;
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
     if (fits_rsrc(prm, N, P)) {
-      hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      if (strips)
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      else
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, false>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
       return launch_status("m3s_fwd");
     }
   }
   {
     constexpr int NW = (C / 16) > 4 ? (C / 16) : 4;
-    hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+    if (strips)
+      hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW, true>), dim3(grid), dim3(NW * 64), 0, stream, prm);
+    else
+      hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NW, false>), dim3(grid), dim3(NW * 64), 0, stream, prm);
   }
   return launch_status("m3s_fwd");
 }
@@ -1346,9 +1440,15 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
   M3S_REQUIRE(bhlp_ok(a->v, vec), "m3s_fwd: v null, misaligned or strides not multiples of %d", vec);
   M3S_REQUIRE(!a->has_z || bhlp_ok(a->z, vec), "m3s_fwd: z null, misaligned or bad strides");
   M3S_REQUIRE(bhlp_ok(a->y, vec), "m3s_fwd: y null, misaligned or bad strides");
-  M3S_REQUIRE(a->adt && a->gamma && a->scale && a->phi && a->q_bias && a->k_bias,
+  const bool strips = a->theta_table || a->phi_dt || a->phi_strips;
+  M3S_REQUIRE(!strips || (a->theta_table && a->phi_dt && a->phi_strips && !a->phi),
+              "m3s_fwd: give phi, or theta_table, phi_dt and phi_strips (not both)");
+  M3S_REQUIRE(!strips || L % 16 == 0, "m3s_fwd: phi_strips needs seqlen %% 16 == 0");
+  M3S_REQUIRE(a->adt && a->gamma && a->scale && (a->phi || strips) && a->q_bias && a->k_bias,
               "m3s_fwd: a required input pointer is NULL");
-  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 || aligned16(a->phi), "m3s_fwd: phi misaligned");
+  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 ||
+                  (strips ? aligned16(a->theta_table) && aligned16(a->phi_strips) : aligned16(a->phi)),
+              "m3s_fwd: phi (or theta_table / phi_strips) misaligned");
   M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_fwd: has_d but d_skip is NULL");
   M3S_REQUIRE(!a->has_seed || (a->seed_ssm && a->seed_k && a->seed_v && a->seed_coef),
               "m3s_fwd: seed_ssm, seed_k, seed_v and seed_coef must be given together");
@@ -1367,6 +1467,9 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
   prm.z = a->has_z ? a->z.ptr : nullptr;
   prm.z_sb = a->z.stride_b; prm.z_sh = a->z.stride_h; prm.z_st = a->z.stride_t;
   prm.adt = a->adt; prm.gamma = a->gamma; prm.scale = a->scale; prm.phi = a->phi;
+  prm.tht = strips ? a->theta_table : nullptr;
+  prm.pdt = strips ? a->phi_dt : nullptr;
+  prm.pstr = strips ? a->phi_strips : nullptr;
   prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
   prm.seed_ssm = a->seed_ssm; prm.seed_k = a->seed_k; prm.seed_v = a->seed_v;
   prm.seed_coef = a->seed_coef;

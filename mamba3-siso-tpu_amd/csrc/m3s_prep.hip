@@ -93,8 +93,9 @@ struct PrepFwdParams {
   const float* dt_bias;
   const float* phi_init;
   float* adt; float* gamma; float* scale; float* lam; float* dt;
-  float* phi;
+  float* phi;         // (B, H, L, Nr) or NULL
   float* phi_final;
+  float* strips;      // (B, H, L / 16, Nr) phi entering each 16-token strip, or NULL
   float* tpi;  // (B, L, Nr) tanh(angles) * pi
   float* tot;  // (B, nblk, H, Nr) block totals of theta, then exclusive carries
 };
@@ -232,8 +233,10 @@ prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
 // so a store instruction covers whole rows of one head's contiguous (t, Nr) slab. Lane
 // (row group rg, column quad q) owns RPL consecutive rows of that quad: a first pass
 // sums them, a shuffle scan over the row groups of the column gives each lane's
-// exclusive prefix, a second pass writes the running sum wrapped to [0, 2 pi). The
-// block's tanh(angles) pi rows, shared by the heads, are staged in LDS once.
+// exclusive prefix, a second pass writes the running sum wrapped to [0, 2 pi) -- every
+// row into phi, and/or, into strips, the sum before each row whose index is a multiple
+// of 16 (the angle entering that 16-token strip). The block's tanh(angles) pi rows,
+// shared by the heads, are staged in LDS once.
 __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdParams p) {
   extern __shared__ float sT[];   // [kPrepTB][Nr]
   const int H = p.H, Nr = p.Nr, L = p.L;
@@ -284,7 +287,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdPar
     if (p.phi_init) init = ld_quad(p.phi_init + bh * Nr, j0, Nr);
 #pragma unroll
     for (int c = 0; c < 4; ++c) run[c] += incl[c] - tot[c];
-    float* prow = p.phi + (bh * L + t0) * Nr;
+    float* prow = p.phi ? p.phi + (bh * L + t0) * Nr : nullptr;
     for (int i0 = 0; i0 < RPL; i0 += RUN) {
       float d8[RUN];
 #pragma unroll
@@ -294,13 +297,19 @@ __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdPar
         const int t = r0 + i0 + u;
         if (i0 + u < RPL && t < nt) {
           const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+          if (p.strips && ((t0 + t) & 15) == 0) {
+            f32x4 enter;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) enter[c] = wrap_(run[c] + init[c]);
+            st_quad(p.strips + (bh * (L >> 4) + ((t0 + t) >> 4)) * Nr, j0, Nr, enter);
+          }
           f32x4 out;
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             run[c] += tp[c] * d8[u];
             out[c] = wrap_(run[c] + init[c]);
           }
-          st_quad(prow + t * Nr, j0, Nr, out);
+          if (prow) st_quad(prow + t * Nr, j0, Nr, out);
           if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
         }
       }
@@ -639,12 +648,17 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
               "m3s_prep_fwd: a required input pointer is NULL");
   M3S_REQUIRE(!a->has_phi_init || a->phi_init, "m3s_prep_fwd: has_phi_init but phi_init is NULL");
   M3S_REQUIRE(a->adt && a->gamma && a->scale && a->lam && a->dt &&
-                  (Nr == 0 || (a->phi && a->phi_final && a->workspace)),
-              "m3s_prep_fwd: an output pointer or the workspace is NULL");
+                  (Nr == 0 || ((a->phi || a->phi_strips) && a->phi_final && a->workspace)),
+              "m3s_prep_fwd: an output pointer or the workspace is NULL (phi or phi_strips "
+              "is needed)");
   M3S_REQUIRE(Nr == 0 || aligned16(a->workspace), "m3s_prep_fwd: workspace must be 16-byte aligned");
-  M3S_REQUIRE(Nr % 4 != 0 || (aligned16(a->phi) && aligned16(a->phi_final) &&
+  M3S_REQUIRE(Nr % 4 != 0 || ((!a->phi || aligned16(a->phi)) && aligned16(a->phi_final) &&
+                              (!a->phi_strips || aligned16(a->phi_strips)) &&
+                              (!a->theta_table || aligned16(a->theta_table)) &&
                               (!a->has_phi_init || aligned16(a->phi_init))),
               "m3s_prep_fwd: phi buffers must be 16-byte aligned");
+  M3S_REQUIRE(!a->phi_strips || L % 16 == 0,
+              "m3s_prep_fwd: phi_strips needs seqlen %% 16 == 0, got %d", L);
   const size_t lds = (size_t)prep_fwd_lds_floats(H, Nr) * 4;
   M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_fwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
   M3S_REQUIRE(Nr <= 256, "m3s_prep_fwd: n_angles %d > 256 (a phi row must fit one wave)", Nr);
@@ -657,8 +671,8 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
   p.dt_bias = a->dt_bias;
   p.phi_init = a->has_phi_init ? a->phi_init : nullptr;
   p.adt = a->adt; p.gamma = a->gamma; p.scale = a->scale; p.lam = a->lam; p.dt = a->dt;
-  p.phi = a->phi; p.phi_final = a->phi_final;
-  p.tpi = static_cast<float*>(a->workspace);
+  p.phi = a->phi; p.phi_final = a->phi_final; p.strips = a->phi_strips;
+  p.tpi = a->theta_table ? a->theta_table : static_cast<float*>(a->workspace);
   p.tot = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
                                    align256((int64_t)B * L * Nr * 4));
   hipStream_t s = static_cast<hipStream_t>(stream);

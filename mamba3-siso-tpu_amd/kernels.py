@@ -14,6 +14,7 @@ CPU: every tensor must already be on the ROCm device, and a missing library rais
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Any, NamedTuple, Optional
 
 import torch
@@ -22,6 +23,44 @@ from . import _lib
 from . import layout as LY
 
 Tensor = torch.Tensor
+
+
+class PhiStrips(NamedTuple):
+    """phi in the compact form the scan kernels rebuild it from (the cumulative angle of
+    ``reference.py:134-157`` fused into the scan): ``phi[t] = strips[t // 16] +
+    sum_{16 (t // 16) <= t' <= t} table[t'] * dt[t']`` taken mod 2 pi. ``table`` is
+    ``tanh(angles) pi`` ``(B, L, Nr)`` (shared by the heads), ``dt`` ``(B, H, L)``,
+    ``strips`` ``(B, H, L / 16, Nr)`` the wrapped angle entering each 16-token strip. The
+    kernels accept it wherever they take ``phi``; it is 1/16 of phi's bytes plus the
+    head-shared table."""
+
+    table: Tensor
+    dt: Tensor
+    strips: Tensor
+
+    @property
+    def shape(self):
+        b, h, l = self.dt.shape
+        return (b, h, l, self.table.shape[-1])
+
+    def last(self) -> Tensor:
+        """phi at the last position, ``(B, H, Nr)`` in [0, 2 pi)."""
+        theta = torch.einsum("bln,bhl->bhn", self.table[:, -16:].float(), self.dt[:, :, -16:].float())
+        return torch.remainder(self.strips[:, :, -1, :] + theta, 2 * math.pi)
+
+
+def _phi_fields(a, phi, dev) -> list:
+    """Fill ``a.phi`` or the three ``phi_strips`` fields of an args struct; returns the
+    converted tensors, which must stay alive until the launch."""
+    if isinstance(phi, PhiStrips):
+        tab, dt, st = _f32c(phi.table), _f32c(phi.dt), _f32c(phi.strips)
+        _device_of(tab, dt, st)
+        a.phi = None
+        a.theta_table, a.phi_dt, a.phi_strips = tab.data_ptr(), dt.data_ptr(), st.data_ptr()
+        return [tab, dt, st]
+    ph = _f32c(phi)
+    a.phi = ph.data_ptr()
+    return [ph]
 
 
 class ForwardResiduals(NamedTuple):
@@ -116,7 +155,8 @@ def siso_forward(
             f"phi must be (B, H, L, Nr) = {(batch, nheads, seqlen, n_angles)}, got {tuple(phi.shape)}")
     if z is not None and tuple(z.shape) != tuple(v.shape):
         raise ValueError(f"z shape {tuple(z.shape)} must match v {tuple(v.shape)}")
-    dev = _device_of(q, k, v, adt, gamma, scale, phi, q_bias, k_bias, d_skip, z, *seeds)
+    dev = _device_of(q, k, v, adt, gamma, scale, q_bias, k_bias, d_skip, z, *seeds,
+                     *(phi if isinstance(phi, PhiStrips) else (phi,)))
     mt = pol.matmul
     dcode = _lib.dtype_code(mt)
     if not _lib.supported(0, dcode, chunk, state_dim, headdim):
@@ -126,7 +166,7 @@ def siso_forward(
 
     qc, kc = _mt(q, mt), _mt(k, mt)
     vc, zc = _bhlp_operand(v, mt), _bhlp_operand(z, mt)
-    adt_c, gam_c, scl_c, phi_c = _f32c(adt), _f32c(gamma), _f32c(scale), _f32c(phi)
+    adt_c, gam_c, scl_c = _f32c(adt), _f32c(gamma), _f32c(scale)
     qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
     s_ssm, s_k, s_v, s_c = (_f32c(s) for s in seeds)
 
@@ -151,7 +191,8 @@ def siso_forward(
     a.save_residuals = int(save_residuals)
     a.q, a.k = qc.data_ptr(), kc.data_ptr()
     a.v, a.z = _lib.bhlp(vc), _lib.bhlp(zc)
-    a.adt, a.gamma, a.scale, a.phi = (t.data_ptr() for t in (adt_c, gam_c, scl_c, phi_c))
+    a.adt, a.gamma, a.scale = (t.data_ptr() for t in (adt_c, gam_c, scl_c))
+    keep = _phi_fields(a, phi, dev)  # noqa: F841  (alive until the launch)
     a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
     a.seed_ssm, a.seed_k, a.seed_v, a.seed_coef = (_lib.ptr(s) for s in (s_ssm, s_k, s_v, s_c))
     a.y = _lib.bhlp(y)
@@ -392,7 +433,8 @@ def siso_backward_kernel(
     if tuple(chunk_states.shape) != (batch, nheads, nc, headdim, state_dim):
         raise ValueError(f"chunk_states must be (B, H, nc, P, N) = "
                          f"{(batch, nheads, nc, headdim, state_dim)}, got {tuple(chunk_states.shape)}")
-    dev = _device_of(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias,
+    dev = _device_of(dy, ybar, z, q, k, v, adt, gamma, scale, q_bias, k_bias,
+                     *(phi if isinstance(phi, PhiStrips) else (phi,)),
                      chunk_states, d_skip, dfinal_ssm, dfinal_v)
     mt = pol.matmul
     dcode = _lib.dtype_code(mt)
@@ -403,7 +445,7 @@ def siso_backward_kernel(
     dyc, zc, vc = _bhlp_operand(dy, mt), _bhlp_operand(z, mt), _bhlp_operand(v, mt)
     qc, kc = _mt(q, mt), _mt(k, mt)
     ybc = _f32c(ybar)
-    adt_c, gam_c, scl_c, phi_c = _f32c(adt), _f32c(gamma), _f32c(scale), _f32c(phi)
+    adt_c, gam_c, scl_c = _f32c(adt), _f32c(gamma), _f32c(scale)
     qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
     cs = _nmajor_states(chunk_states, mt)
     dfs, dfv = _f32c(dfinal_ssm), _f32c(dfinal_v)
@@ -433,7 +475,8 @@ def siso_backward_kernel(
     a.has_d, a.has_z = int(d_c is not None), int(zc is not None)
     a.dy, a.ybar, a.z = _lib.bhlp(dyc), ybc.data_ptr(), _lib.bhlp(zc)
     a.q, a.k, a.v = qc.data_ptr(), kc.data_ptr(), _lib.bhlp(vc)
-    a.adt, a.gamma, a.scale, a.phi = (t.data_ptr() for t in (adt_c, gam_c, scl_c, phi_c))
+    a.adt, a.gamma, a.scale = (t.data_ptr() for t in (adt_c, gam_c, scl_c))
+    keep = _phi_fields(a, phi, dev)  # noqa: F841  (alive until the launch)
     a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
     a.chunk_states, a.dfinal_ssm, a.dfinal_v = cs.data_ptr(), _lib.ptr(dfs), _lib.ptr(dfv)
     a.dq, a.dk, a.dv, a.dz = dq.data_ptr(), dk.data_ptr(), _lib.bhlp(dv), _lib.bhlp(dz)
@@ -495,7 +538,8 @@ def siso_backward(
     dgamma = kg.dqk_diag * kg.uw
     dd_skip = kg.dqk_diag.sum(dim=(0, 2)) if d_skip is not None else None
     if dfinal_k is not None:
-        cos_l, sin_l = LY.rope_cos_sin(phi[:, :, -1, :].float(), state_dim)
+        phi_last = phi.last() if isinstance(phi, PhiStrips) else phi[:, :, -1, :].float()
+        cos_l, sin_l = LY.rope_cos_sin(phi_last, state_dim)
         dk_rot = LY.rope_apply(dfinal_k.float(), cos_l, -sin_l)     # (B, H, N)
         dk = dk.clone()
         dk[:, -1, :] += dk_rot.sum(dim=1)

@@ -192,7 +192,7 @@ class _LayerFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, in_proj, out_proj, dt_bias, b_norm_weight, c_norm_weight, b_bias,
-                c_bias, d_skip, cfg):
+                c_bias, d_skip, cfg, phi_in_kernel=False):
         dt = u.dtype
         batch, seqlen, dm = u.shape
         m = batch * seqlen
@@ -206,8 +206,10 @@ class _LayerFn(torch.autograd.Function):
         z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
         (k, q), (rk, rq) = K.bcnorm_forward([b, c], [b_norm_weight, c_norm_weight], cfg.norm_eps)
         bias = dt_bias.float().contiguous()
+        # phi_in_kernel: phi stays compact (kernels.PhiStrips) and the scans rebuild it per
+        # row; otherwise the preprocess materialises it (B, H, L, Nr)
         adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
-            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor)
+            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=phi_in_kernel)
         need = any(ctx.needs_input_grad[:9])   # all False under no_grad
         outs = K.siso_forward(q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias,
                               b_bias, d_skip=d_skip, z=z.permute(0, 2, 1, 3), chunk=cfg.chunk,
@@ -218,17 +220,22 @@ class _LayerFn(torch.autograd.Function):
         out = (y2 @ wo_t.t()).view(batch, seqlen, dm)
         if need:
             res = outs[4]
-            ctx.save_for_backward(u, proj, q, k, rk, rq, adt, gamma, scale, phi, y, res.ybar,
+            phis = tuple(phi) if isinstance(phi, K.PhiStrips) else (phi,)
+            ctx.n_phi = len(phis)
+            ctx.save_for_backward(u, proj, q, k, rk, rq, adt, gamma, scale, y, res.ybar,
                                   res.chunk_states, in_proj, out_proj, bias, b_norm_weight,
-                                  c_norm_weight, b_bias, c_bias, d_skip)
+                                  c_norm_weight, b_bias, c_bias, d_skip, *phis)
         ctx.cfg = cfg
         ctx.set_materialize_grads(False)
         return out, fs, fk, fv, phi_final
 
     @staticmethod
     def backward(ctx, dout, dfs, dfk, dfv, dphi_final):
-        (u, proj, q, k, rk, rq, adt, gamma, scale, phi, y, ybar, cstates, in_proj, out_proj,
-         bias, wb, wc, b_bias, c_bias, d_skip) = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        (u, proj, q, k, rk, rq, adt, gamma, scale, y, ybar, cstates, in_proj, out_proj,
+         bias, wb, wc, b_bias, c_bias, d_skip) = saved[:-ctx.n_phi]
+        phis = saved[-ctx.n_phi:]
+        phi = K.PhiStrips(*phis) if ctx.n_phi == 3 else phis[0]
         cfg = ctx.cfg
         dt = u.dtype
         batch, seqlen, dm = u.shape
@@ -271,19 +278,27 @@ class _LayerFn(torch.autograd.Function):
             return None if (t is None or p_ is None) else t.to(p_.dtype)
 
         return (du, d_in_proj, d_out_proj, like(d_bias, bias), like(dwb, wb), like(dwc, wc),
-                like(g.dk_bias, b_bias), like(g.dq_bias, c_bias), like(g.dd_skip, d_skip), None)
+                like(g.dk_bias, b_bias), like(g.dq_bias, c_bias), like(g.dd_skip, d_skip), None,
+                None)
 
 
 def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
                       state: Optional[SISOState] = None, interpret: Any = False,
-                      device_kind: str | None = None):
+                      device_kind: str | None = None, phi_in_kernel: bool = False):
     """Forward of one layer (``layer.py:201-262``). ``u`` is ``(B, L, d_model)`` on the
     ROCm device; returns ``(out (B, L, d_model), SISOState)``. Differentiable w.r.t.
-    ``u`` and every `SISOParams` field through torch autograd."""
+    ``u`` and every `SISOParams` field through torch autograd.
+
+    ``phi_in_kernel`` (no counterpart in the reference; same results to float rounding):
+    the cumulative rotary angle is not materialised as ``(B, H, L, Nr)``; the scan kernels
+    rebuild it per token from the head-shared ``tanh(angles) pi`` table, dt and one angle
+    per 16 tokens. It moves 1/16 of phi's bytes, but on the current kernels the in-kernel
+    prefix costs more time than those bytes save, so it is off by default."""
     if _fused_ok(u, cfg, state):
         out, fs, fk, fv, phi_final = _LayerFn.apply(
             u, params.in_proj, params.out_proj, params.dt_bias, params.b_norm_weight,
-            params.c_norm_weight, params.b_bias, params.c_bias, params.d_skip, cfg)
+            params.c_norm_weight, params.b_bias, params.c_bias, params.d_skip, cfg,
+            phi_in_kernel)
         return out, SISOState(ssm=fs, k=fk, v=fv, phi=phi_final)
     batch, seqlen, _ = u.shape
     proj = u @ params.in_proj.to(u.dtype)

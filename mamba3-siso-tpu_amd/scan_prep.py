@@ -131,16 +131,21 @@ def _f32c(t: Optional[Tensor]) -> Optional[Tensor]:
 
 
 def prep_forward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
-                        bias: Tensor, init: Optional[Tensor], a_floor: float):
+                        bias: Tensor, init: Optional[Tensor], a_floor: float,
+                        compact: bool = False):
     """One ``m3s_prep_fwd`` call on raw ``(B, L, X)`` operands with a unit last stride and
     one dtype (bf16 or f32); ``bias`` and ``init`` f32 contiguous. Returns fresh
-    ``(adt, gamma, scale, lam, dt, phi, phi_final)``."""
+    ``(adt, gamma, scale, lam, dt, phi, phi_final)``. With ``compact`` (needs
+    ``L % 16 == 0``) phi is not materialised: the sixth entry is a `kernels.PhiStrips`
+    (the head-shared ``tanh(angles) pi`` table, dt and the angle entering each 16-token
+    strip), which the scan kernels take in place of phi."""
+    from .kernels import PhiStrips
+
     batch, seqlen, nheads = r_dt.shape
     n_angles = r_ang.shape[-1]
     dev = r_dt.device
     f32 = dict(device=dev, dtype=torch.float32)
     adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
-    phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
     phi_final = torch.empty(batch, nheads, n_angles, **f32)
     lib = _lib.load()
     ws = torch.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
@@ -154,7 +159,15 @@ def prep_forward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
     a.dt_raw, a.a_raw, a.trap_raw, a.angles = (_lib.blx(t) for t in (r_dt, r_a, r_tr, r_ang))
     a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
     a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
-    a.phi, a.phi_final = phi.data_ptr(), phi_final.data_ptr()
+    if compact:
+        table = torch.empty(batch, seqlen, n_angles, **f32)
+        strips = torch.empty(batch, nheads, seqlen // 16, n_angles, **f32)
+        a.theta_table, a.phi_strips = table.data_ptr(), strips.data_ptr()
+        phi = PhiStrips(table, dt, strips)
+    else:
+        phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
+        a.phi = phi.data_ptr()
+    a.phi_final = phi_final.data_ptr()
     a.workspace = ws.data_ptr()
     with torch.cuda.device(dev):
         _lib.check(lib.m3s_prep_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_prep_fwd")

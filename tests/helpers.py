@@ -118,3 +118,14 @@ def assert_bf16_bound(got, ref, rel=BF16_MODEL_ABS_REL, what=""):
     bound = bf16_ulp(r) + rel * float(r.abs().max())
     over = ((g - r).abs() / bound).max()
     assert float(over) <= 1.0, f"{what}: |err| reaches {float(over):.2f}x the bf16 bound"
+
+
+def phi_strips_of(c, m3):
+    """The compact phi (kernels.PhiStrips) of `boundary_inputs`' oracle preprocess, on the
+    device: tanh(angles) pi, dt, and the angle entering each 16-token strip (the oracle's
+    phi at token 16 s - 1; 0 for the first strip, since these inputs start from 0)."""
+    b, h, l, nr = c["phi"].shape
+    strips = torch.zeros(b, h, l // 16, nr, dtype=F64)
+    strips[:, :, 1:] = c["phi"][:, :, 15:-1:16]
+    return m3.kernels.PhiStrips((torch.tanh(c["angles"]) * torch.pi).float().cuda(),
+                                c["dt"].float().cuda(), strips.float().cuda())

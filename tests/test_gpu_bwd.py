@@ -8,7 +8,7 @@ import torch
 
 from helpers import (BF16, BF16_GRAD_MAXREL, BF16_MAXREL, GRAD_F32_P95, STATE_MAXABS,
                      assert_maxabs, assert_maxrel, assert_p95, boundary_inputs, fwd_args,
-                     report)
+                     phi_strips_of, report)
 from oracle import siso_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -91,6 +91,36 @@ def test_backward_every_table_shape(m3, policy, n, p, chunk):
     """Instantiations of the kernel table not covered above, against autograd of the
     float64 oracle."""
     want, gr = run_case(m3, 2, 2, 256, n, p, n // 4, chunk, policy, True, True, seed=19)
+    for name, w in want.items():
+        got = getattr(gr, GRAD_FIELD[name])
+        if policy == "f32":
+            assert_p95(got, w, GRAD_F32_P95, f"d{name}")
+        else:
+            assert_maxrel(got, w, BF16_GRAD_MAXREL, f"d{name}")
+
+
+@pytest.mark.parametrize("policy,n,p,chunk", [
+    ("bf16", 128, 64, 128), ("bf16", 64, 64, 64), ("bf16", 32, 16, 32),
+    ("f32", 128, 64, 32), ("f32", 16, 16, 64),
+])
+def test_backward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
+    """phi_strips mode of the backward: every gradient (dphi included, which the caller
+    turns into theta and angle gradients) against autograd of the float64 oracle, with
+    the seeds and final-state cotangents on."""
+    c, d = boundary_inputs(2, 2, 256, n, p, n // 4, policy, seed=29, seeds=True)
+    g = torch.Generator().manual_seed(101)
+    dfs = torch.randn(2, 2, p, n, generator=g, dtype=torch.float64).float().double()
+    dfk = torch.randn(2, 2, n, generator=g, dtype=torch.float64).float().double()
+    dfv = torch.randn(2, 2, p, generator=g, dtype=torch.float64).float().double()
+    want = O.boundary_grads({k_: c[k_] for k_ in NAMES if k_ in c}, c["dy"], dfs, dfk, dfv,
+                            chunk=chunk)
+    args = fwd_args(d)
+    args[6] = phi_strips_of(c, m3)
+    out = m3.siso_forward(*args, chunk=chunk, dtype_policy=policy, save_residuals=True)
+    dev = lambda t: t.float().cuda()  # noqa: E731
+    gr = m3.siso_backward(d["dy"], *args[:9], out[4].ybar, out[4].chunk_states, d["d_skip"],
+                          d["z"], d["seed_ssm"], d["seed_k"], d["seed_v"], d["seed_coef"],
+                          dev(dfs), dev(dfk), dev(dfv), chunk=chunk, dtype_policy=policy)
     for name, w in want.items():
         got = getattr(gr, GRAD_FIELD[name])
         if policy == "f32":

@@ -8,7 +8,7 @@ import torch
 from helpers import (BF16, BF16_MAXREL, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_P95,
                      BF16_Y_MAXREL, F32, FWD_F32_P95, STATE_MAXABS, assert_bf16_bound,
                      assert_maxabs, assert_maxrel, assert_p95, boundary_inputs, cpu, fwd_args,
-                     report)
+                     phi_strips_of, report)
 from oracle import siso_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -103,6 +103,38 @@ def test_forward_every_table_shape(m3, policy, n, p, chunk):
         assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
         assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
     assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+
+
+@pytest.mark.parametrize("policy,n,p,chunk", [
+    ("bf16", 128, 64, 128), ("bf16", 128, 64, 64), ("bf16", 64, 64, 64), ("bf16", 32, 16, 32),
+    ("f32", 128, 64, 32), ("f32", 16, 16, 64),
+])
+def test_forward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
+    """phi_strips mode (the cumulative angle fused into the scan): the kernel rebuilds
+    phi from tanh(angles) pi, dt and one angle per 16-token strip. Against the oracle
+    with the same bars as when phi is read, and against the phi-reading run of the same
+    kernel (the rebuilt phi differs from the read one by float rounding only)."""
+    c, d = boundary_inputs(2, 3, 256, n, p, n // 4, policy, seed=23)
+    yr, sr, dbg = oracle_fwd(c, chunk)
+    args = fwd_args(d)
+    base = m3.siso_forward(*args, chunk=chunk, dtype_policy=policy, save_residuals=True)
+    args[6] = phi_strips_of(c, m3)
+    y, fs, fk, fv, res = m3.siso_forward(*args, chunk=chunk, dtype_policy=policy,
+                                         save_residuals=True)
+    if policy == "f32":
+        assert_p95(y, yr, FWD_F32_P95, "y")
+        assert_p95(fs, sr.ssm, FWD_F32_P95, "final ssm")
+        assert_p95(res.chunk_states, dbg["chunk_states"], FWD_F32_P95, "chunk_states")
+        assert_p95(y, cpu(base[0]), FWD_F32_P95, "y vs phi read")
+    else:
+        ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
+        assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+        assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
+        assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
+        assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
+        assert_p95(res.ybar, cpu(base[4].ybar), BF16_MODEL_P95, "ybar vs phi read")
+    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+    assert O.max_rel(cpu(fv), cpu(base[3])) == 0.0
 
 
 def test_forward_bf16_with_carried_state(m3):

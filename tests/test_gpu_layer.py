@@ -192,3 +192,35 @@ def test_layer_decode_fused_matches_composed_over_steps(m3, policy, monkeypatch)
     for name in ("ssm", "k", "v"):
         assert_maxrel(getattr(s1, name), cpu(getattr(s0, name)), tol, name)
     assert O.rel_error(cpu(s1.phi), cpu(s0.phi), angle=True) <= 1e-5
+
+
+@pytest.mark.parametrize("policy", ["bf16", "f32"])
+def test_layer_with_phi_built_in_the_kernels(m3, policy):
+    """phi_in_kernel=True (the preprocess writes the compact phi, both scan kernels rebuild
+    it per token) against the default (phi materialised): outputs, state and every
+    gradient agree to float rounding, and the bf16 run stays within its float64 bars."""
+    if policy == "bf16":
+        cfg = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=128)
+        dt, tol = BF16, 2e-3
+    else:
+        cfg = m3.SISOConfig(d_model=64, d_state=16, headdim=16, expand=1, chunk=64,
+                            policy_name="f32")
+        dt, tol = torch.float32, 2e-5
+    p_cpu = m3.init_params(cfg, 13)
+    g = torch.Generator().manual_seed(14)
+    u = torch.randn(2, 512, cfg.d_model, generator=g).to(dt)
+    gy = torch.randn(2, 512, cfg.d_model, generator=g).to(dt)
+    runs = []
+    for flag in (False, True):
+        params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+        ud = u.cuda().requires_grad_(True)
+        y, st = m3.mamba3_siso_layer(params, ud, cfg, phi_in_kernel=flag)
+        (y.float() * gy.cuda().float()).sum().backward()
+        runs.append((y, st, ud.grad, [getattr(params, f).grad for f in p_cpu._fields]))
+    (y0, s0, du0, g0), (y1, s1, du1, g1) = runs
+    assert_maxrel(y1, cpu(y0), tol, "y")
+    assert_maxrel(s1.ssm, cpu(s0.ssm), tol, "ssm")
+    assert O.rel_error(cpu(s1.phi), cpu(s0.phi), angle=True) <= 1e-5
+    assert_maxrel(du1, cpu(du0), 10 * tol, "du")
+    for f, a, b in zip(p_cpu._fields, g1, g0):
+        assert_maxrel(a, cpu(b), 10 * tol, f"d{f}")

@@ -173,3 +173,38 @@ def test_prep_backward_final_phi_only(m3, dev):
     got = torch.autograd.grad(fin.cos().sum() + pre.adt.sum(), d_in + [d_bias, d_p0])
     for gv, wv in zip(got, want):
         assert O.max_abs(gv, wv) <= 1e-4 * max(1.0, float(wv.abs().max()))
+
+
+@pytest.mark.parametrize("b,l,h,nr,init", [(2, 256, 8, 32, True), (1, 1024, 4, 6, False),
+                                           (2, 64, 3, 4, True)])
+def test_prep_compact_phi_matches_oracle(m3, dev, b, l, h, nr, init):
+    """The compact phi (kernels.PhiStrips): the table is tanh(angles) pi, dt is the
+    preprocess's dt, and strip s holds the angle entering token 16 s -- the oracle's
+    phi at token 16 s - 1, or phi_init for the first strip. Rebuilt per token with the
+    same rule the scan kernels use, it reproduces the oracle's phi."""
+    dtr, ar, tr, ang, bias = raw_inputs(b, l, h, nr, seed=l + nr + 1)
+    g = torch.Generator().manual_seed(4)
+    phi0 = (torch.rand(b, h, nr, generator=g, dtype=F64) * 6.0) if init else None
+    ref, rfin = O.preprocess(dtr, ar, tr, ang, bias, phi_init=phi0)
+    lim, lim_fin = phi_limit(dtr, ar, tr, ang, bias, phi0=phi0)
+    d_dt, d_a, d_tr, d_ang = as_proj(dev, torch.float32, dtr, ar, tr, ang)
+    out = m3.scan_prep.prep_forward_launch(
+        d_dt, d_a, d_tr, d_ang, bias.float().to(dev).contiguous(),
+        None if phi0 is None else phi0.float().to(dev).contiguous(), 1e-4, compact=True)
+    adt, gamma, scale, lam, dt, ph, fin = out
+    assert isinstance(ph, m3.kernels.PhiStrips)
+    torch.testing.assert_close(ph.table.cpu().double(), torch.tanh(ang) * torch.pi,
+                               rtol=2e-6, atol=2e-6)
+    assert ph.dt is dt
+    want = torch.zeros(b, h, l // 16, nr, dtype=F64)
+    want[:, :, 1:] = ref.phi[:, :, 15:-1:16]
+    if phi0 is not None:
+        want[:, :, 0] = phi0
+    assert O.rel_error(ph.strips.cpu().double(), want, angle=True) <= lim
+    assert O.rel_error(fin.cpu().double(), rfin, angle=True) <= lim_fin
+    # the per-token rule of the scan kernels
+    theta = ph.table.cpu().double()[:, None] * dt.cpu().double()[..., None]   # (B, H, L, Nr)
+    within = torch.cumsum(theta.reshape(b, h, l // 16, 16, nr), dim=3).reshape(b, h, l, nr)
+    rebuilt = ph.strips.cpu().double().repeat_interleave(16, dim=2) + within
+    assert O.rel_error(rebuilt, ref.phi, angle=True) <= lim
+    assert O.rel_error(ph.last().cpu().double(), rebuilt[:, :, -1], angle=True, pct=100.0) <= 1e-5
