@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=512)
     ap.add_argument("--no-lm", action="store_true", help="skip the LM-stack legs")
+    ap.add_argument("--default-gemms", action="store_true",
+                    help="leave the library GEMMs on hipBLASLt's default heuristic instead of "
+                         "the recorded solutions (gemm_tuning.enable)")
     ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy", "lm"), default="all",
                     help="run one leg alone (for rocprofv3 counter passes): 'scan' = the forward "
                          "scan kernel at the kernel boundary, 'bwd' = the backward scan kernel, "
@@ -121,7 +124,13 @@ def main():
     import __graft_entry__
 
     m3 = __graft_entry__.load_package()
+    from mamba3_siso_tpu_amd import gemm_tuning
     from mamba3_siso_tpu_amd import kernels as K
+
+    # the library GEMMs around the scan run the hipBLASLt / rocBLAS solutions recorded for
+    # these shapes (mamba3-siso-tpu_amd/tuned_gemms.csv); --default-gemms keeps hipBLASLt's
+    # own heuristic
+    tuned = False if args.default_gemms else gemm_tuning.enable()
 
     dev = torch.device("cuda:0")
     if args.leg == "copy":
@@ -332,6 +341,8 @@ def main():
                                "preprocess, HIP chunked scan, out_proj)",
                    "batch": B, "seq_len": L, "nheads": H, "headdim": P, "d_state": N,
                    "d_model": DM, "chunk": 128, "n_angles": Nr},
+        "gemm_solutions": "recorded (mamba3-siso-tpu_amd/tuned_gemms.csv)" if tuned
+                          else "hipBLASLt default heuristic",
         "fwd_bwd_ms": round(fb_ms, 3),
         "fwd_bwd_tok_s": round(tokens / (fb_ms * 1e-3), 1),
         "decode_ms_per_token": round(dec_ms, 4),

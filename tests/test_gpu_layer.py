@@ -218,9 +218,36 @@ def test_layer_with_phi_built_in_the_kernels(m3, policy):
         (y.float() * gy.cuda().float()).sum().backward()
         runs.append((y, st, ud.grad, [getattr(params, f).grad for f in p_cpu._fields]))
     (y0, s0, du0, g0), (y1, s1, du1, g1) = runs
-    assert_maxrel(y1, cpu(y0), tol, "y")
+    if policy == "bf16":   # y is stored in bf16: a rounding may flip by one ulp
+        assert_bf16_bound(y1, cpu(y0), rel=tol, what="y")
+    else:
+        assert_maxrel(y1, cpu(y0), tol, "y")
     assert_maxrel(s1.ssm, cpu(s0.ssm), tol, "ssm")
     assert O.rel_error(cpu(s1.phi), cpu(s0.phi), angle=True) <= 1e-5
     assert_maxrel(du1, cpu(du0), 10 * tol, "du")
     for f, a, b in zip(p_cpu._fields, g1, g0):
         assert_maxrel(a, cpu(b), 10 * tol, f"d{f}")
+
+
+def test_recorded_gemm_solutions_change_only_gemm_rounding(m3):
+    """gemm_tuning.enable() picks other library kernels for the projections; the layer's
+    output and input gradient stay within bf16 rounding of the default solutions'."""
+    from mamba3_siso_tpu_amd import gemm_tuning
+
+    cfg = m3.SISOConfig(d_model=1024, d_state=128, headdim=64, expand=2, chunk=128)
+    params = m3.SISOParams(*(t.cuda() for t in m3.init_params(cfg, 17)))
+    g = torch.Generator().manual_seed(18)
+    u = torch.randn(8, 8192, 1024, generator=g).to(BF16).cuda()   # a recorded shape
+    outs = []
+    for tuned in (False, True):
+        if tuned:
+            assert gemm_tuning.enable()
+        try:
+            ud = u.clone().requires_grad_(True)
+            y, _ = m3.mamba3_siso_layer(params, ud, cfg)
+            y.float().square().mean().backward()
+            outs.append((y.detach(), ud.grad))
+        finally:
+            gemm_tuning.disable()
+    assert_maxrel(outs[1][0], cpu(outs[0][0]), 1e-2, "y")
+    assert_maxrel(outs[1][1], cpu(outs[0][1]), 2e-2, "du")
