@@ -641,9 +641,13 @@ __device__ __forceinline__ bf16x4 ld_tr4_at(const bf16* ptr) {
   return __builtin_bit_cast(bf16x4, r);
 }
 
-template <int C, int N, int P, bool STRIPS>
+// NRB = 0: phi is read. NRB > 0 (phi_strips mode): phi is built from the compact form,
+// and NRB is the number of 32-column blocks that hold rotary pairs (Nr <= 32 NRB).
+template <int C, int N, int P, int NRB>
 __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p) {
   using F = Fwd2Cfg<C, N, P>;
+  constexpr bool STRIPS = NRB > 0;
+  static_assert(NRB <= F::LOB, "rotary blocks lie in the rotated half");
   constexpr int NT = F::NT, LDK = F::LDK, LDO = F::LDO;
   constexpr int H2 = N / 2, PB = F::PB, SPW = F::SPW, NSTEP = F::NSTEP;
 
@@ -784,9 +788,12 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // ---- raw q, k, phi, scale, gamma of one chunk, prefetched into registers ---------
   // Strip layout: lane row 16 strip + (lane & 15), K group 8 (lane >> 4).
   bf16x8 rq[F::NBK], rk[F::NBK];
-  f32x4 rphi[F::LOB][2];          // phi, or (phi_strips mode) tanh(angles) pi of the row
-  f32x4 rstr[STRIPS ? F::LOB : 1][2];   // phi_strips mode: phi entering this lane's strip
-  float rpdt = 0.f;                 // phi_strips mode: dt of the row
+  f32x4 rphi[STRIPS ? 1 : F::LOB][2];   // phi of the row (phi read)
+  // phi_strips mode: tanh(angles) pi of the row, the angle entering its strip, its dt, and
+  // the turns built from them (for the next chunk, from the middle of the products on)
+  f32x4 rtab[STRIPS ? NRB : 1][2], rstr[STRIPS ? NRB : 1][2];
+  float rpdt = 0.f;
+  float trn_pre[STRIPS ? NRB : 1][8];
   float rscale, rgam;
   float radt[F::E];
   const bool phi_vec = (Nr % 4) == 0;
@@ -820,32 +827,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const int trow = 16 * strip + (lane & 15);
     const int g8 = 8 * (lane >> 4);
     const uint32_t sphi = (uint32_t)c * C * Nr * 4;
-    if constexpr (STRIPS) {
-      // the strip's entering angles: one 32-byte piece per lane group (16 lanes read it)
-      const uint32_t sstr = (uint32_t)(c * (C / 16) + strip) * Nr * 4;
+
 #pragma unroll
-      for (int lb = 0; lb < F::LOB; ++lb) {
-        if (32 * lb >= Nr) {
-#pragma unroll
-          for (int qd = 0; qd < 2; ++qd) rstr[lb][qd] = f32x4{0.f, 0.f, 0.f, 0.f};
-        } else if (phi_vec && 32 * lb + 32 <= Nr) {
-#pragma unroll
-          for (int qd = 0; qd < 2; ++qd)
-            rstr[lb][qd] = gld<f32x4>(pstrg, sstr + (uint32_t)(32 * lb + g8 + 4 * qd) * 4);
-        } else {
-#pragma unroll
-          for (int qd = 0; qd < 2; ++qd) {
-            const int j = 32 * lb + g8 + 4 * qd;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              rstr[lb][qd][i] = (j + i < Nr) ? gld<float>(pstrg, sstr + (uint32_t)(j + i) * 4) : 0.f;
-          }
-        }
-      }
-      rpdt = gld<float>(pdtg, (uint32_t)(c * C + trow) * 4);
-    }
-#pragma unroll
-    for (int lb = 0; lb < F::LOB; ++lb) {
+    for (int lb = 0; lb < (STRIPS ? 0 : F::LOB); ++lb) {
       // wave-uniform cases first: a block of 32 columns wholly past Nr needs no load, one
       // wholly inside takes 16-byte loads; only a block that Nr cuts tests per lane (a
       // per-lane choice between load widths makes the compiler drain the load queue)
@@ -874,6 +858,57 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 #pragma unroll
     for (int e = 0; e < F::E; ++e)
       radt[e] = buf_load<float>(dAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+  };
+
+  // phi_strips mode: chunk c's table rows, strip angles and dt (issued at the start of the
+  // previous chunk's products), and the turns built from them in the middle of those
+  // products, where the DPP prefix interleaves with the inter-chunk and state MFMAs
+  // instead of lengthening the end of the long strips' phase
+  auto prefetch_angles = [&](int c) {
+    if constexpr (STRIPS) {
+      if (c >= nc) c = 0;   // past the end: chunk 0 again, never used
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63;
+      const int trow = 16 * strip + (lane & 15);
+      const int g8 = 8 * (lane >> 4);
+      const uint32_t sphi = (uint32_t)c * C * Nr * 4;
+      const uint32_t sstr = (uint32_t)(c * (C / 16) + strip) * Nr * 4;
+#pragma unroll
+      for (int lb = 0; lb < NRB; ++lb) {
+        if (phi_vec && 32 * lb + 32 <= Nr) {
+#pragma unroll
+          for (int qd = 0; qd < 2; ++qd) {
+            rtab[lb][qd] = buf_load<f32x4>(rPhi, (uint32_t)(trow * Nr + 32 * lb + g8 + 4 * qd) * 4, sphi);
+            rstr[lb][qd] = gld<f32x4>(pstrg, sstr + (uint32_t)(32 * lb + g8 + 4 * qd) * 4);
+          }
+        } else {
+#pragma unroll
+          for (int qd = 0; qd < 2; ++qd) {
+            const int j = 32 * lb + g8 + 4 * qd;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const bool in = j + i < Nr;
+              rtab[lb][qd][i] = in ? buf_load<float>(rPhi, (uint32_t)(trow * Nr + j + i) * 4, sphi) : 0.f;
+              rstr[lb][qd][i] = in ? gld<float>(pstrg, sstr + (uint32_t)(j + i) * 4) : 0.f;
+            }
+          }
+        }
+      }
+      rpdt = gld<float>(pdtg, (uint32_t)(c * C + trow) * 4);
+    }
+  };
+  auto build_turns = [&]() {
+    if constexpr (STRIPS) {
+#pragma unroll
+      for (int lb = 0; lb < NRB; ++lb) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const float th = row_prefix16(rtab[lb][s >> 2][s & 3] * rpdt);
+          trn_pre[lb][s] = __builtin_amdgcn_fractf((rstr[lb][s >> 2][s & 3] + th) * 0.15915494309189535f);
+        }
+      }
+    }
   };
 
   bf16x8 qf[F::NBK];                        // q~ of this wave's strip (MFMA B operand)
@@ -957,14 +992,13 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       kh = (float)rk[hb][s] + bkh[s >> 2][s & 3];
     };
     // angle s of this lane's block lb, in turns: phi is read wrapped to [0, 2 pi); in
-    // phi_strips mode it is the strip's entering angle plus the inclusive prefix of
-    // theta = tanh(angles) pi dt over the strip's rows -- the 16 lanes of a DPP row are the
-    // strip's 16 rows -- keeping the fraction of a turn. Evaluated only on the rotary
-    // paths below, so blocks past Nr cost nothing.
+    // phi_strips mode build_turns made it during the previous products (the strip's
+    // entering angle plus the inclusive prefix of theta = tanh(angles) pi dt over the
+    // strip's rows -- the 16 lanes of a DPP row are the strip's 16 rows -- keeping the
+    // fraction of a turn); blocks at or past NRB hold no rotary pair.
     auto turns_of = [&](int lb, int s) {
       if constexpr (STRIPS) {
-        const float th = row_prefix16(rphi[lb][s >> 2][s & 3] * rpdt);
-        return __builtin_amdgcn_fractf((rstr[lb][s >> 2][s & 3] + th) * 0.15915494309189535f);
+        return lb < NRB ? trn_pre[lb < NRB ? lb : 0][s] : 0.f;
       } else {
         return rphi[lb][s >> 2][s & 3] * 0.15915494309189535f;
       }
@@ -1043,6 +1077,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     const float *sA = sc.A, *sExpA = sc.ExpA, *sFac = sc.Fac, *sCoef = sc.Coef, *sDk = sc.Dk;
     // lane index re-derived opaquely: the per-lane LDS addresses below are recomputed
     // each chunk instead of being hoisted out of the chunk loop (and spilled)
+    prefetch_angles(c + 1);
     int ln = threadIdx.x;
     asm volatile("" : "+v"(ln));
     const int lane = ln & 63;
@@ -1147,6 +1182,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     prefetch_rest(c + 1);
     prefetch_vz(c + 1 < nc ? rV : rNul, c + 1 < nc ? c + 1 : 0, rZ, c);
     __builtin_amdgcn_sched_barrier(0);
+    build_turns();   // chunk c+1's angles (phi_strips mode)
     // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
     // (every fragment of S, the diagonal v values and the scalars are read first, then
     // PB independent MFMA chains: one LDS round trip)
@@ -1267,7 +1303,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   prefetch_vz(rV, 0, rNul, 0);
   prefetch_qk(0);
   prefetch_rest(0);
+  prefetch_angles(0);
   vm_wait_all();
+  build_turns();
   __syncthreads();  // sQb / sKb
   stage_regs();     // chunk 0
   stage_write(0);
@@ -1358,10 +1396,12 @@ static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   const bool strips = prm.pstr != nullptr;
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
     if (fits_rsrc(prm, N, P)) {
-      if (strips)
-        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      if (strips && (prm.Nr <= 32 || N / 64 < 2))
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 1>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+      else if (strips)
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, (N / 64 >= 2 ? 2 : 1)>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
       else
-        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, false>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 0>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
       return launch_status("m3s_fwd");
     }
   }

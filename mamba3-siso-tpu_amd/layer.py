@@ -192,7 +192,7 @@ class _LayerFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, in_proj, out_proj, dt_bias, b_norm_weight, c_norm_weight, b_bias,
-                c_bias, d_skip, cfg, phi_in_kernel=False):
+                c_bias, d_skip, cfg, phi_in_kernel=None):
         dt = u.dtype
         batch, seqlen, dm = u.shape
         m = batch * seqlen
@@ -206,11 +206,13 @@ class _LayerFn(torch.autograd.Function):
         z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
         (k, q), (rk, rq) = K.bcnorm_forward([b, c], [b_norm_weight, c_norm_weight], cfg.norm_eps)
         bias = dt_bias.float().contiguous()
-        # phi_in_kernel: phi stays compact (kernels.PhiStrips) and the scans rebuild it per
-        # row; otherwise the preprocess materialises it (B, H, L, Nr)
-        adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
-            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=phi_in_kernel)
         need = any(ctx.needs_input_grad[:9])   # all False under no_grad
+        # compact: phi stays compact (kernels.PhiStrips) and the scans rebuild it per row;
+        # otherwise the preprocess materialises it (B, H, L, Nr). By default compact exactly
+        # when no gradient is taken (the forward is faster that way, the backward slower).
+        compact = (not need) if phi_in_kernel is None else bool(phi_in_kernel)
+        adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
+            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=compact)
         outs = K.siso_forward(q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias,
                               b_bias, d_skip=d_skip, z=z.permute(0, 2, 1, 3), chunk=cfg.chunk,
                               dtype_policy=cfg.policy_name, save_residuals=need)
@@ -284,16 +286,18 @@ class _LayerFn(torch.autograd.Function):
 
 def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
                       state: Optional[SISOState] = None, interpret: Any = False,
-                      device_kind: str | None = None, phi_in_kernel: bool = False):
+                      device_kind: str | None = None, phi_in_kernel: Optional[bool] = None):
     """Forward of one layer (``layer.py:201-262``). ``u`` is ``(B, L, d_model)`` on the
     ROCm device; returns ``(out (B, L, d_model), SISOState)``. Differentiable w.r.t.
     ``u`` and every `SISOParams` field through torch autograd.
 
     ``phi_in_kernel`` (no counterpart in the reference; same results to float rounding):
-    the cumulative rotary angle is not materialised as ``(B, H, L, Nr)``; the scan kernels
-    rebuild it per token from the head-shared ``tanh(angles) pi`` table, dt and one angle
-    per 16 tokens. It moves 1/16 of phi's bytes, but on the current kernels the in-kernel
-    prefix costs more time than those bytes save, so it is off by default."""
+    when True the cumulative rotary angle is not materialised as ``(B, H, L, Nr)``; the
+    scan kernels rebuild it per token from the head-shared ``tanh(angles) pi`` table, dt
+    and one angle per 16 tokens, which moves 1/16 of phi's bytes. The forward scan is then
+    faster as a whole (the preprocess writes no phi), the backward scan slower (its
+    in-kernel prefix sits on its critical path). ``None`` (the default) picks the compact
+    form exactly when no gradient will be taken; True / False force either form."""
     if _fused_ok(u, cfg, state):
         out, fs, fk, fv, phi_final = _LayerFn.apply(
             u, params.in_proj, params.out_proj, params.dt_bias, params.b_norm_weight,
