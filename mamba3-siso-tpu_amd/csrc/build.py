@@ -3,7 +3,7 @@
     python mamba3-siso-tpu_amd/csrc/build.py [--jobs N]
 
 Every source is rebuilt on each call. Flags: gfx950 only; packed-FP32 ops disabled
-(the compiler must not emit v_pk_{add,mul,fma}_f32); hardware float atomics.
+(the compiler must not emit v_pk_{add,mul,fma}_f32).
 """
 
 from __future__ import annotations
@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
-    "-Wno-unused-function", "-munsafe-fp-atomics",
+    "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

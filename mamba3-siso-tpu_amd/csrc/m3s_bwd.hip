@@ -164,9 +164,10 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   float* sDA = sCoef + C;
   float* sQb = sDA + C;
   float* sKb = sQb + N;
-  float* sDqb = sKb + N;
-  float* sDkb = sDqb + N;
-  float* sRed = sDkb + N;  // [0]: 2^{A_last}<G,S> + <v, dv_inter> for the current chunk
+  // [w]: wave w's share of 2^{A_last}<G,S> + <v, dv_inter> for the current chunk, summed
+  // in wave order (no float atomics: the result does not depend on wave timing)
+  float* sRed = sKb + 3 * N;
+  static_assert(NW <= 16, "one sRed slot per wave");
 
   const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -178,11 +179,14 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   for (int i = tid; i < N; i += NT) {
     sQb[i] = p.qb[h * N + i];
     sKb[i] = p.kb[h * N + i];
-    sDqb[i] = 0.f;
-    sDkb[i] = 0.f;
   }
-  if (tid == 0) sRed[0] = 0.f;
   const float dsk = p.has_d ? p.dsk[h] : 0.f;
+  // this lane's running bias-gradient partials over its row pairs of every chunk: a lane
+  // keeps the same columns j0.. in every chunk (NT is a multiple of QKG), so the sums
+  // stay in registers and are reduced once, in a fixed order, after the last chunk
+  float bqa[2][F::VEC], bka[2][F::VEC];
+#pragma unroll
+  for (int i = 0; i < F::VEC; ++i) bqa[0][i] = bqa[1][i] = bka[0][i] = bka[1][i] = 0.f;
 
   const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * L * N;
   const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * L * N;
@@ -581,7 +585,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
       red += sExpA[C - 1] * gs;
     }
     red = group_sum<64>(red);
-    if (lane == 0) atomicAdd(sRed, red);
+    if (lane == 0) sRed[wave] = red;
     __syncthreads();
 
     // ============ transpose pass: q~, khat, g to [x][position], one tile at a time =====
@@ -779,22 +783,13 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
           p.dscale[bh * L + t0 + 2 * tp + e] = dsc[e];
         }
       }
-      // bias partials: sum over the row pairs of this wave that share the pair group,
-      // then one LDS atomic per element from the first of them
+      // bias partials: into this lane's running sums (zero for an idle task)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          float vq = bq[hh][i], vk = bk[hh][i];
-#pragma unroll
-          for (int m = F::QKG; m < 64; m <<= 1) {
-            vq += __shfl_xor(vq, m, 64);
-            vk += __shfl_xor(vk, m, 64);
-          }
-          if (valid && lane < F::QKG) {
-            atomicAdd(sDqb + hh * H2 + j0 + i, vq);
-            atomicAdd(sDkb + hh * H2 + j0 + i, vk);
-          }
+          bqa[hh][i] += bq[hh][i];
+          bka[hh][i] += bk[hh][i];
         }
       }
     }
@@ -802,7 +797,9 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
 
     // ============ phase S: dadt = suffix_sum(dA) + A_last share; publish G ============
     if (wave == 0) {
-      const float extra = sRed[0];
+      float extra = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) extra += sRed[w];
       float a[F::E];
       float run = 0.f;
 #pragma unroll
@@ -827,7 +824,6 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
     }
     publish_adjoint();
     __syncthreads();
-    if (tid == 0) sRed[0] = 0.f;
   }
 
   // ---- per-(b, h) outputs ------------------------------------------------------------
@@ -841,10 +837,36 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
         p.dseed[(bh * P + pb * 16 + 4 * g4 + i) * N + nb * 16 + l16] = Gacc[m][i];
     }
   }
+  // bias gradients: the lanes sharing columns j0.. (lane bits log2(QKG)..5) summed by a
+  // butterfly, each wave's totals into its own LDS slot (the staging area is free now),
+  // then the slots summed in wave order
   __syncthreads();
-  for (int i = tid; i < N; i += NT) {
-    p.dqb[bh * N + i] = sDqb[i];
-    p.dkb[bh * N + i] = sDkb[i];
+  {
+    float* sBias = sDQ;   // [NW][2N]: q's N entries, then k's
+    const int j0 = (tid % F::QKG) * VEC;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float vq = bqa[hh][i], vk = bka[hh][i];
+#pragma unroll
+        for (int m = F::QKG; m < 64; m <<= 1) {
+          vq += __shfl_xor(vq, m, 64);
+          vk += __shfl_xor(vk, m, 64);
+        }
+        if (lane < F::QKG) {
+          sBias[wave * 2 * N + hh * H2 + j0 + i] = vq;
+          sBias[wave * 2 * N + N + hh * H2 + j0 + i] = vk;
+        }
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < 2 * N; i += NT) {
+      float acc = 0.f;
+      for (int w = 0; w < NW; ++w) acc += sBias[w * 2 * N + i];
+      if (i < N) p.dqb[bh * N + i] = acc;
+      else p.dkb[bh * N + i - N] = acc;
+    }
   }
 }
 
@@ -930,9 +952,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   float* sDA = sCoef + C;
   float* sQb = sDA + C;
   float* sKb = sQb + N;
-  float* sDqb = sKb + N;
-  float* sDkb = sDqb + N;
-  float* sRed = sDkb + N;  // [0]: 2^{A_last}<G,S> + <v, dv_inter> for the current chunk
+  // [w]: wave w's share of 2^{A_last}<G,S> + <v, dv_inter> for the current chunk, summed
+  // in wave order (no float atomics: the result does not depend on wave timing)
+  float* sRed = sKb + 3 * N;
+  static_assert(NW <= 16, "one sRed slot per wave");
+  // bias butterfly: BROUNDS rounds leave each lane the group sums of BFIN entries (below)
+  constexpr int BFIN = VEC * 4 * F::QKG / 64;
+  constexpr int BROUNDS = (F::QKG == 4) ? 4 : (F::QKG == 8) ? 3 : (F::QKG == 16) ? 2 : 1;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -944,10 +970,13 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   for (int i = tid; i < N; i += NT) {
     sQb[i] = p.qb[h * N + i];
     sKb[i] = p.kb[h * N + i];
-    sDqb[i] = 0.f;
-    sDkb[i] = 0.f;
   }
-  if (tid == 0) sRed[0] = 0.f;
+  // this lane's running bias-gradient sums: the butterfly leaves a lane the same BFIN
+  // entries in every row and chunk (its columns j0.. and `base` depend on lane bits only),
+  // so they are summed in registers and reduced once, in a fixed order, at the end
+  float bsum[BFIN];
+#pragma unroll
+  for (int k = 0; k < BFIN; ++k) bsum[k] = 0.f;
   const float dsk = p.has_d ? p.dsk[h] : 0.f;
 
   const bf16* qg = static_cast<const bf16*>(p.q) + (int64_t)b * L * N;
@@ -1441,7 +1470,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         red += sExpA[C - 1] * gs;
       }
       red = wave_total(red);
-      if (lane == 0) atomicAdd(sRed, red);
+      if (lane == 0) sRed[wave] = red;
       // G <- 2^{A_last} G + sum_t (2^{A_t} g[t][p]) q~[t][n]   (K = time, both by columns)
       const float eAl = sExpA[C - 1];
 #pragma unroll
@@ -1651,13 +1680,11 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
         // The lanes that share j0 differ in lane bits log2(QKG)..5. A transposing
         // butterfly over those bits halves the entries a lane keeps each round (it sends
         // the half its partner keeps), so each lane ends with the group sums of
-        // BFIN consecutive entries starting at `base`: one LDS atomic each, no idle lanes.
-        constexpr int BFIN = VEC * 4 * F::QKG / 64;
-        constexpr int ROUNDS = (F::QKG == 4) ? 4 : (F::QKG == 8) ? 3 : (F::QKG == 16) ? 2 : 1;
-        static_assert((VEC * 4) >> ROUNDS == BFIN && BFIN >= 1, "bias butterfly shape");
-        int base = 0;
+        // BFIN consecutive entries (which ones: the epilogue recomputes it from the lane
+        // bits), added to its running sums.
+        static_assert((VEC * 4) >> BROUNDS == BFIN && BFIN >= 1, "bias butterfly shape");
 #pragma unroll
-        for (int rd = 0; rd < ROUNDS; ++rd) {
+        for (int rd = 0; rd < BROUNDS; ++rd) {
           const int m = 32 >> rd, half = (VEC * 2) >> rd;
           const bool up = (lane & m) != 0;
 #pragma unroll
@@ -1667,16 +1694,12 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             const float keep = up ? hi : lo;
             bacc[k] = keep + __shfl_xor(send, m, 64);
           }
-          base += up ? half : 0;
         }
         // the previous chunk's ybar rows, state and row scalars, into registers the
         // butterfly has freed
         if (r == F::QKR - 1) prefetch_rest(c > 0 ? c - 1 : 0, 2);
 #pragma unroll
-        for (int k = 0; k < BFIN; ++k) {
-          const int idx = base + k, u = idx & 3;
-          atomicAdd((u < 2 ? sDqb : sDkb) + (u & 1) * H2 + j0 + (idx >> 2), bacc[k]);
-        }
+        for (int k = 0; k < BFIN; ++k) bsum[k] += bacc[k];
       }
     }
     // the previous chunk's q, k, phi rows for its phase L, into the registers phase R
@@ -1689,7 +1712,9 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
       const int lane = ln & 63;
-      const float extra = sRed[0];
+      float extra = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) extra += sRed[w];
       float a[F::E];
       float run = 0.f;
 #pragma unroll
@@ -1710,7 +1735,6 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     }
     publish_adjoint();
     __syncthreads();
-    if (tid == 0) sRed[0] = 0.f;
   }
 
   // ---- per-(b, h) outputs ------------------------------------------------------------
@@ -1721,10 +1745,30 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
     for (int i = 0; i < 4; ++i)
       p.dseed[(bh * P + pb_w * 16 + 4 * (lane >> 4) + i) * N + nb * 16 + (lane & 15)] = Gacc[m][i];
   }
+  // bias gradients: each wave's sums into its own LDS slot (the staging area is free
+  // now; every entry is held by exactly one lane of each wave), then the slots summed in
+  // wave order
   __syncthreads();
-  for (int i = tid; i < N; i += NT) {
-    p.dqb[bh * N + i] = sDqb[i];
-    p.dkb[bh * N + i] = sDkb[i];
+  {
+    float* sBias = sDQ;   // [NW][2N]: q's N entries, then k's
+    static_assert(NW * 2 * N * 4 <= F::SZ_STAGE, "bias slots fit the staging area");
+    const int j0 = (tid % F::QKG) * VEC;
+    int base = 0;
+#pragma unroll
+    for (int rd = 0; rd < BROUNDS; ++rd)   // the butterfly keeps the upper half on a set bit
+      base += (lane & (32 >> rd)) ? ((VEC * 2) >> rd) : 0;
+#pragma unroll
+    for (int k = 0; k < BFIN; ++k) {
+      const int idx = base + k, u = idx & 3;
+      sBias[wave * 2 * N + (u >> 1) * N + (u & 1) * H2 + j0 + (idx >> 2)] = bsum[k];
+    }
+    __syncthreads();
+    for (int i = tid; i < 2 * N; i += NT) {
+      float acc = 0.f;
+      for (int w = 0; w < NW; ++w) acc += sBias[w * 2 * N + i];
+      if (i < N) p.dqb[bh * N + i] = acc;
+      else p.dkb[bh * N + i - N] = acc;
+    }
   }
 }
 

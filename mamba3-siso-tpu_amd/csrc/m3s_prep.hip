@@ -357,10 +357,16 @@ struct PrepBwdParams {
   float* bias_part;    // (B * nblk, H)
 };
 
+// Tokens per run of prep_bwd_kernel's reverse walk over dphi: a run's loads are issued
+// before its first use, and the waves' angle-cotangent partials of a run are summed in
+// wave order at its end.
+constexpr int kPrepRun = 8;
+
 // LDS of prep_bwd_kernel (floats): six TB x H tables, the TB x Nr tanh table and
-// angle-cotangent accumulator, and dscale just before the block for each head.
+// angle-cotangent accumulator, dscale just before the block for each head, and each
+// wave's angle-cotangent partials of one run.
 __host__ __device__ inline int prep_bwd_lds_floats(int H, int Nr) {
-  return 6 * kPrepTB * H + 2 * kPrepTB * Nr + H;
+  return 6 * kPrepTB * H + 2 * kPrepTB * Nr + H + (kPrepThreads / 64) * kPrepRun * Nr;
 }
 
 template <typename RT>
@@ -378,6 +384,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   float* sT = sPhi + kPrepTB * H;      // [TB][Nr] tanh(angles)
   float* sAng = sT + kPrepTB * Nr;     // [TB][Nr] sum_h dtheta dt
   float* sDsPrev = sAng + kPrepTB * Nr;  // [H] dscale at t0 - 1
+  float* sStage = sDsPrev + H;           // [wave][kPrepRun][Nr] this run's partials
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int blk = blockIdx.x, b = blockIdx.y;
@@ -454,66 +461,75 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
 
   // ---- dtheta_t = carry + sum_{s >= t in block} dphi_s, walked in reverse; per t:
   //      sPhi[t][h] = sum_j dtheta tanh pi and sAng[t][j] = sum_h dtheta dt -----------
+  // A lane takes one (head, group of 4 angles) pair; the J4 groups of a head are
+  // consecutive lanes (J4 rounded up to a power of two, the groups past Nr idle), so the
+  // sum over j is a butterfly inside a wave. The sum over h: a butterfly over the wave's
+  // heads, then the waves' partials summed in wave order at the end of every run of
+  // tokens -- a fixed order, so the result does not depend on wave timing.
   if (Nr > 0 && p.carry) {
-    const int J4 = (Nr + 3) / 4;
-    const bool pow2 = (J4 & (J4 - 1)) == 0 && J4 <= 64;
+    int J4 = 1;
+    while (4 * J4 < Nr) J4 <<= 1;   // <= 64: n_angles <= 256
     const int npair = H * J4;
-    // every lane of a wave runs the same iterations (the shuffles need all lanes)
+    const int wave = tid >> 6;
+    // every lane of a wave runs the same iterations (the shuffles and barriers need all)
     const int iters = (npair + kPrepThreads - 1) / kPrepThreads;
     for (int it = 0; it < iters; ++it) {
       const int pr = tid + it * kPrepThreads;
       const bool valid = pr < npair;
-      const int h = valid ? pr / J4 : 0, jg = valid ? pr % J4 : 0, j0 = 4 * jg;
+      // jg = pr % J4 even past npair: lanes 0..J4-1 then cover every angle group, so
+      // each wave writes every stage entry of the run (zeros from idle lanes)
+      const int h = valid ? pr / J4 : 0, jg = pr % J4, j0 = 4 * jg;
+      const bool live = valid && j0 < Nr;
       const int64_t bh = (int64_t)b * H + h;
       f32x4 run = {0.f, 0.f, 0.f, 0.f};
-      if (valid) run = ld_quad(p.carry + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
+      if (live) run = ld_quad(p.carry + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
       const float* src = p.dphi ? p.dphi + (bh * L + t0) * Nr : nullptr;
-      // rows in runs of kRun, all of a run's loads issued before its first use (idle lanes
-      // load head 0's row and drop it: the loads stay unconditional per lane)
-      constexpr int kRun = 8;
-      for (int tr = nt - 1; tr >= 0; tr -= kRun) {
-        f32x4 dq[kRun];
+      for (int tr = nt - 1; tr >= 0; tr -= kPrepRun) {
+        // all of a run's loads issued before its first use (idle lanes load nothing)
+        f32x4 dq[kPrepRun];
 #pragma unroll
-        for (int u = 0; u < kRun; ++u) {
+        for (int u = 0; u < kPrepRun; ++u) {
           dq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (src && tr - u >= 0) dq[u] = ld_quad(src + (tr - u) * Nr, j0, Nr);
+          if (src && live && tr - u >= 0) dq[u] = ld_quad(src + (tr - u) * Nr, j0, Nr);
         }
 #pragma unroll
-        for (int u = 0; u < kRun; ++u) {
+        for (int u = 0; u < kPrepRun; ++u) {
           const int t = tr - u;
           if (t < 0) break;
-          if (valid) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) run[i] += dq[u][i];
-          }
-          const float dt = valid ? sDt[t * H + h] : 0.f;
+          for (int i = 0; i < 4; ++i) run[i] += dq[u][i];
+          const float dt = live ? sDt[t * H + h] : 0.f;
           float ph = 0.f;
           f32x4 ag;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float tq = (valid && j0 + i < Nr) ? sT[t * Nr + j0 + i] : 0.f;
+            const float tq = (live && j0 + i < Nr) ? sT[t * Nr + j0 + i] : 0.f;
             ph += run[i] * (tq * kPiF);
-            ag[i] = valid ? run[i] * dt : 0.f;
+            ag[i] = run[i] * dt;
           }
-          if (pow2) {
-            for (int off = 1; off < J4; off <<= 1) ph += __shfl_xor(ph, off, 64);
-            if (valid && jg == 0) sPhi[t * H + h] = ph;
-            for (int off = J4; off < 64; off <<= 1) {
+          for (int off = 1; off < J4; off <<= 1) ph += __shfl_xor(ph, off, 64);
+          if (valid && jg == 0) sPhi[t * H + h] = ph;
+          for (int off = J4; off < 64; off <<= 1) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) ag[i] += __shfl_xor(ag[i], off, 64);
-            }
-            if (lane < J4) {   // lanes jg = lane of head group 0 hold this wave's sum
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
-            }
-          } else if (valid) {
-            atomicAdd(sPhi + t * H + h, ph);
+            for (int i = 0; i < 4; ++i) ag[i] += __shfl_xor(ag[i], off, 64);
+          }
+          if (lane < J4) {   // lanes jg = lane hold this wave's sum over its heads
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (j0 + i < Nr) atomicAdd(sAng + t * Nr + j0 + i, ag[i]);
+              if (j0 + i < Nr) sStage[(wave * kPrepRun + u) * Nr + j0 + i] = ag[i];
           }
         }
+        __syncthreads();
+        for (int e = tid; e < kPrepRun * Nr; e += kPrepThreads) {
+          const int u = e / Nr, j = e % Nr, t = tr - u;
+          if (t >= 0) {
+            float acc = sAng[t * Nr + j];
+#pragma unroll
+            for (int w = 0; w < kPrepThreads / 64; ++w) acc += sStage[(w * kPrepRun + u) * Nr + j];
+            sAng[t * Nr + j] = acc;
+          }
+        }
+        __syncthreads();
       }
     }
   }
@@ -718,6 +734,7 @@ extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
                               (!a->dphi_final || aligned16(a->dphi_final)) &&
                               (!a->dphi_init || aligned16(a->dphi_init))),
               "m3s_prep_bwd: phi cotangent buffers must be 16-byte aligned");
+  M3S_REQUIRE(Nr <= 256, "m3s_prep_bwd: n_angles %d > 256 (a head's angle groups must fit one wave)", Nr);
   const size_t lds = (size_t)prep_bwd_lds_floats(H, Nr) * 4;
   M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_bwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_prep_bwd: B*H too large");
