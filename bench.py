@@ -184,17 +184,19 @@ def main():
         ka = dict(kc, phi=phi_full)
         if args.leg in ("all", "scan"):
             scan = lambda: K.siso_forward(**kc, chunk=128)  # noqa: E731
+            scan_r = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
             # a kernel-boundary micro-measurement: enough launches that the clocks have
-            # settled (a few ms of warmup), whatever --steps says for the headline
+            # settled (a few ms of warmup), whatever --steps says for the headline; the two
+            # phi forms alternate, and each keeps the better of its two averages
             for _ in range(max(args.warmup, 10)):
                 scan()
-            scan_ms = gpu_time_ms(scan, max(args.steps, 50), torch)
+                scan_r()
+            n = max(args.steps, 50)
+            times = [(gpu_time_ms(scan, n, torch), gpu_time_ms(scan_r, n, torch)) for _ in range(2)]
+            scan_ms = min(t[0] for t in times)
+            read_ms = min(t[1] for t in times)
             scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
             scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
-            scan_r = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
-            for _ in range(5):
-                scan_r()
-            read_ms = gpu_time_ms(scan_r, max(args.steps, 50), torch)
             line.update(scan_kernel_ms=round(scan_ms, 4),
                         scan_kernel_tok_s=round(tokens / (scan_ms * 1e-3), 1),
                         scan_kernel_gbs=round(scan_gbs, 1),

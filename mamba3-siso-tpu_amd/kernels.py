@@ -118,6 +118,17 @@ def _empty_like_layout(v: Tensor, dtype: torch.dtype) -> Tensor:
     return torch.empty(b, h, l, p, device=v.device, dtype=dtype)
 
 
+def _tile(pol: LY.DtypePolicy, chunk: int, state_dim: int, headdim: int, role: str) -> int:
+    """`layout.kernel_chunk`, or the error naming what is compiled."""
+    tile = LY.kernel_chunk(pol.name, chunk, state_dim, headdim)
+    if tile is None:
+        raise ValueError(
+            f"no {role} kernel for policy={pol.name} chunk={chunk} d_state={state_dim} "
+            f"headdim={headdim}; chunks compiled for this shape: "
+            f"{list(LY.compiled_chunks(pol.name, state_dim, headdim))}")
+    return tile
+
+
 def siso_forward(
     q: Tensor, k: Tensor, v: Tensor, adt: Tensor, gamma: Tensor, scale: Tensor,
     phi: Tensor, q_bias: Tensor, k_bias: Tensor, d_skip: Optional[Tensor] = None,
@@ -131,13 +142,17 @@ def siso_forward(
 
     Returns ``(y, final_ssm, final_k, final_v)`` and, with ``save_residuals``, a
     `ForwardResiduals`. ``y`` has ``v``'s memory layout (see `_empty_like_layout`).
+    A ``chunk`` with no kernel of its own runs as tiles of `layout.kernel_chunk`; the
+    residual ``chunk_states`` are then per tile.
     """
     pol = LY.policy(dtype_policy)
     LY.validate_chunk(chunk)
     batch, seqlen, state_dim = q.shape
     nheads, headdim = v.shape[1], v.shape[3]
     n_angles = phi.shape[-1]
-    nc = LY.num_chunks(seqlen, chunk)
+    LY.num_chunks(seqlen, chunk)
+    chunk = _tile(pol, chunk, state_dim, headdim, "forward")
+    nc = seqlen // chunk
     if q.shape != k.shape:
         raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} must match")
     if tuple(v.shape) != (batch, nheads, seqlen, headdim):
@@ -427,7 +442,9 @@ def siso_backward_kernel(
     batch, seqlen, state_dim = q.shape
     nheads, headdim = v.shape[1], v.shape[3]
     n_angles = phi.shape[-1]
-    nc = LY.num_chunks(seqlen, chunk)
+    LY.num_chunks(seqlen, chunk)
+    chunk = _tile(pol, chunk, state_dim, headdim, "backward")
+    nc = seqlen // chunk
     if tuple(dy.shape) != tuple(v.shape) or tuple(ybar.shape) != tuple(v.shape):
         raise ValueError("dy and ybar must be (B, H, L, P) like v")
     if tuple(chunk_states.shape) != (batch, nheads, nc, headdim, state_dim):

@@ -49,11 +49,13 @@ Tensor = torch.Tensor
 class SISOConfig:
     """Shapes and hyperparameters (``layer.py:39-99``); same fields and defaults.
 
-    ``chunk`` follows the GPU rule of `layout.validate_chunk` (32/64/128) instead of the
-    reference's Mosaic rule (multiple of 128), and the config is rejected at construction,
-    as the reference rejects a bad chunk (``layer.py:97-99``), unless a forward, backward
-    and decode kernel is compiled for its (policy, chunk, d_state, headdim)
-    (`layout.validate_kernel_shape`).
+    ``chunk`` follows the reference's rule (a positive multiple of 128) widened to the
+    shorter kernel tiles 32 and 64 (`layout.validate_chunk`); a chunk with no kernel of
+    its own is scanned in tiles of the largest compiled chunk dividing it
+    (`layout.kernel_chunk`: the chunked form is exact for any chunk length). The config is
+    rejected at construction, as the reference rejects a bad chunk (``layer.py:97-99``),
+    unless forward, backward and decode kernels are compiled to run its (policy, chunk,
+    d_state, headdim) (`layout.validate_kernel_shape`).
     """
 
     d_model: int

@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import dataclasses
 import functools
+from typing import Optional
 
 import torch
 
@@ -117,7 +118,8 @@ def num_chunks(seqlen: int, chunk: int) -> int:
 
 
 #: Chunk lengths the HIP kernels are instantiated for (the union over shapes; which
-#: (chunk, d_state, headdim) exist per policy is `KERNELS`).
+#: (chunk, d_state, headdim) exist per policy is `KERNELS`). A longer chunk is scanned
+#: in tiles of one of these (`kernel_chunk`).
 SUPPORTED_CHUNKS = (32, 64, 128)
 
 #: The compiled kernel instantiations: role -> {(policy, chunk, d_state, headdim)}; decode
@@ -152,12 +154,33 @@ KERNELS = {
 }
 
 
-def missing_kernels(policy_name: str, chunk: int, d_state: int, headdim: int) -> list:
-    """The roles (forward, backward, decode) with no compiled kernel for this shape."""
+def kernel_chunk(policy_name: str, chunk: int, d_state: int, headdim: int) -> Optional[int]:
+    """The chunk the scan kernels run for a requested ``chunk``: the largest compiled
+    chunk (forward and backward both, so the forward's per-chunk states are the ones the
+    backward reads) that divides ``chunk``; None if there is none.
+
+    The chunked form is exact for any chunk length -- the intra-chunk quadratic form plus
+    the carried state reproduce the recurrence (``reference.py:217-330``) -- so a chunk of
+    512 scanned as four 128-token tiles gives the same results to float rounding. The
+    caller's chunk still has to divide the sequence (``layout.py:500-506``)."""
     pol = policy(policy_name).name
-    want = {"forward": (pol, chunk, d_state, headdim), "backward": (pol, chunk, d_state, headdim),
-            "decode": (pol, 0, d_state, headdim)}
-    return [role for role, key in want.items() if key not in KERNELS[role]]
+    for c in sorted(SUPPORTED_CHUNKS, reverse=True):
+        if (chunk % c == 0 and (pol, c, d_state, headdim) in KERNELS["forward"]
+                and (pol, c, d_state, headdim) in KERNELS["backward"]):
+            return c
+    return None
+
+
+def missing_kernels(policy_name: str, chunk: int, d_state: int, headdim: int) -> list:
+    """The roles (forward, backward, decode) with no compiled kernel to run this shape
+    (for the scans, at `kernel_chunk`)."""
+    pol = policy(policy_name).name
+    out = []
+    if kernel_chunk(pol, chunk, d_state, headdim) is None:
+        out += ["forward", "backward"]
+    if (pol, 0, d_state, headdim) not in KERNELS["decode"]:
+        out.append("decode")
+    return out
 
 
 def compiled_chunks(policy_name: str, d_state: int, headdim: int) -> tuple:
@@ -169,17 +192,16 @@ def compiled_chunks(policy_name: str, d_state: int, headdim: int) -> tuple:
 
 
 def validate_chunk(chunk: int) -> None:
-    """GPU chunk rule, replacing the reference's Mosaic rule ``chunk % 128 == 0``
-    (``layout.py:225-236``): one of `SUPPORTED_CHUNKS`. The reference's chunked maths
-    (``reference.siso_chunked``) accepts any divisor of L; 32, 64 and 128 are the tile
-    sizes the MFMA kernels are built for."""
-    if chunk not in SUPPORTED_CHUNKS:
-        raise ValueError(f"chunk must be one of {SUPPORTED_CHUNKS}, got {chunk}")
+    """The reference's rule, a positive multiple of 128 (``layout.py:225-236``), widened
+    to the shorter kernel tiles 32 and 64. A multiple of 128 above 128 runs as 128-token
+    (or shorter) tiles (`kernel_chunk`)."""
+    if not isinstance(chunk, int) or chunk <= 0 or (chunk % 128 and chunk not in SUPPORTED_CHUNKS):
+        raise ValueError(f"chunk must be 32, 64 or a positive multiple of 128, got {chunk}")
 
 
 def validate_kernel_shape(policy_name: str, chunk: int, d_state: int, headdim: int) -> None:
     """Raise ``ValueError`` unless forward, backward and decode kernels are all compiled
-    for this (policy, chunk, d_state, headdim) -- the check the reference makes on its
+    to run this (policy, chunk, d_state, headdim) -- the check the reference makes on its
     chunk when the config is built (``layer.py:97-99``), widened to the whole shape
     because the HIP kernels are compiled per shape."""
     validate_chunk(chunk)

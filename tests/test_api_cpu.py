@@ -36,10 +36,10 @@ def test_config_fields_defaults_and_rules(m3):
 
 
 @pytest.mark.parametrize("kw,match", [
-    (dict(d_model=1024, chunk=256), "chunk must be one of"),            # no 256 kernel
-    (dict(d_model=1024, chunk=512), "chunk must be one of"),            # the reference's TPU chunk
-    (dict(d_model=1024, policy_name="f32"), "forward/backward kernel"),  # f32 at chunk 128, N 128
-    (dict(d_model=1024, chunk=64, policy_name="f32"), "backward kernel"),
+    (dict(d_model=1024, chunk=96), "multiple of 128"),     # neither a tile nor a 128 multiple
+    (dict(d_model=1024, chunk=192), "multiple of 128"),
+    (dict(d_model=1024, chunk=0), "multiple of 128"),
+    (dict(d_model=1024, chunk=16), "multiple of 128"),
     (dict(d_model=256, d_state=32, headdim=32), "forward/backward/decode"),
     (dict(d_model=256, d_state=256), "forward/backward/decode"),
     (dict(d_model=256, headdim=128), "forward/backward/decode"),
@@ -61,6 +61,25 @@ def test_config_accepts_every_compiled_shape(m3):
             assert (cfg.chunk, cfg.d_state, cfg.headdim) == (c, n, p)
     assert LY.compiled_chunks("f32", 128, 64) == (32,)
     assert LY.compiled_chunks("bf16", 128, 64) == (32, 64, 128)
+
+
+@pytest.mark.parametrize("pol,chunk,n,p,tile", [
+    ("bf16", 128, 128, 64, 128), ("bf16", 64, 128, 64, 64), ("bf16", 32, 128, 64, 32),
+    ("bf16", 256, 128, 64, 128), ("bf16", 512, 128, 64, 128), ("bf16", 1024, 64, 64, 128),
+    ("f32", 128, 128, 64, 32), ("f32", 64, 128, 64, 32),     # f32 backward only at 32
+    ("f32", 512, 32, 16, 128), ("f32", 128, 64, 64, 64),
+])
+def test_long_chunks_run_as_compiled_tiles(m3, pol, chunk, n, p, tile):
+    """The reference's chunks (any multiple of 128, layout.py:225-236; its headline runs
+    chunk 512) and the f32 policy at the default chunk build, and the scans run them as
+    the largest compiled tile dividing the chunk that has both a forward and a backward
+    kernel, so the forward's per-tile states are the ones the backward reads."""
+    from mamba3_siso_tpu_amd import layout as LY
+    cfg = m3.SISOConfig(d_model=4 * p, d_state=n, headdim=p, chunk=chunk, policy_name=pol)
+    assert cfg.chunk == chunk
+    assert LY.kernel_chunk(pol, chunk, n, p) == tile
+    assert (pol, tile, n, p) in LY.KERNELS["forward"] & LY.KERNELS["backward"]
+    assert chunk % tile == 0
 
 
 def test_init_params_distributions(m3):
@@ -169,7 +188,7 @@ def test_kernel_shape_errors_match_the_reference(m3):
          x["q_bias"], x["k_bias"])
     with pytest.raises(ValueError, match="multiple of chunk"):
         m3.siso_forward(*a, chunk=128)                       # L=64 (layout.py:500-506)
-    with pytest.raises(ValueError, match="chunk must be one of"):
+    with pytest.raises(ValueError, match="multiple of 128"):
         m3.siso_forward(*a, chunk=48)
     with pytest.raises(ValueError, match="must match"):
         m3.siso_forward(a[0], a[1][:, :, :8], *a[2:], chunk=64)   # kernel_fwd.py:255-256

@@ -129,6 +129,28 @@ def test_backward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
             assert_maxrel(got, w, BF16_GRAD_MAXREL, f"d{name}")
 
 
+@pytest.mark.parametrize("policy,n,p,chunk,compact", [
+    ("bf16", 128, 64, 128, False), ("bf16", 128, 64, 128, True), ("bf16", 32, 16, 64, False),
+    ("f32", 128, 64, 32, False), ("f32", 64, 64, 64, True),
+])
+def test_backward_is_bit_reproducible(m3, policy, n, p, chunk, compact):
+    """Every gradient, the head-summed dq/dk, the bias and the dadt shares included, is
+    bit-identical between two runs on the same inputs: the cross-wave sums are taken in
+    wave order, not by float atomics in arrival order."""
+    c, d = boundary_inputs(2, 8, 512, n, p, n // 4, policy, seed=5)
+    phi = phi_strips_of(c, m3) if compact else d["phi"]
+    a = fwd_args(dict(d, phi=phi))
+    out = m3.siso_forward(*a, chunk=chunk, dtype_policy=policy, save_residuals=True)
+    runs = [m3.siso_backward(d["dy"], *a[:9], out[4].ybar, out[4].chunk_states,
+                             d_skip=d["d_skip"], z=d["z"], chunk=chunk, dtype_policy=policy)
+            for _ in range(3)]
+    for name in runs[0]._fields:
+        x = getattr(runs[0], name)
+        if isinstance(x, torch.Tensor):
+            for r in runs[1:]:
+                assert torch.equal(x, getattr(r, name)), name
+
+
 def test_backward_matches_finite_differences_of_the_kernel_forward(m3):
     """Central differences of the HIP forward itself (f32, tiny): the VJP is checked
     against the function it differentiates, as tests.py:614-645 does."""

@@ -31,6 +31,11 @@ def oracle_fwd(c, chunk, mm=None, with_seed=False):
     (2, 2, 192, 32, 16, 8, 32),
 ])
 def test_forward_f32_matches_oracle(m3, b, h, L, n, p, nr, chunk):
+    """A chunk with no f32 kernel of its own (64 at N=128) runs as 32-token tiles: the
+    states saved per tile are the oracle's states at the tile chunk, and every
+    (chunk/tile)-th of them the state entering each requested chunk."""
+    from mamba3_siso_tpu_amd import layout as LY
+    tile = LY.kernel_chunk("f32", chunk, n, p)
     c, d = boundary_inputs(b, h, L, n, p, nr, "f32", seed=1)
     yr, sr, dbg = oracle_fwd(c, chunk)
     y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy="f32",
@@ -40,8 +45,12 @@ def test_forward_f32_matches_oracle(m3, b, h, L, n, p, nr, chunk):
     assert_p95(fk, sr.k, FWD_F32_P95, "final k")
     assert O.max_rel(cpu(fv), sr.v) == 0.0
     assert_p95(res.ybar, dbg["ybar"], FWD_F32_P95, "ybar")
-    assert_p95(res.chunk_states, dbg["chunk_states"], FWD_F32_P95, "chunk_states")
-    assert tuple(res.chunk_states.shape) == (b, h, L // chunk, p, n)
+    assert tuple(res.chunk_states.shape) == (b, h, L // tile, p, n)
+    assert_p95(res.chunk_states[:, :, ::chunk // tile], dbg["chunk_states"], FWD_F32_P95,
+               "chunk_states")
+    if tile != chunk:
+        _, _, dbg_t = oracle_fwd(c, tile)
+        assert_p95(res.chunk_states, dbg_t["chunk_states"], FWD_F32_P95, "tile states")
 
 
 @pytest.mark.parametrize("chunk", [128, 64, 32])

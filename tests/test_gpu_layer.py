@@ -130,6 +130,55 @@ def test_layer_bf16_forward_and_grads(m3, d_model, batch, seqlen, seed):
         assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
 
 
+@pytest.mark.parametrize("policy,chunk", [("bf16", 256), ("bf16", 512), ("f32", 128),
+                                          ("f32", 64)])
+def test_layer_at_chunks_without_a_kernel_of_their_own(m3, policy, chunk):
+    """The reference's chunks (a multiple of 128; its headline runs 512) and the f32
+    policy at the default chunk run as compiled tiles (layout.kernel_chunk): the output,
+    final state and every gradient against autograd of the float64 layer at the requested
+    chunk, and bit-equal to the same layer configured at the tile itself."""
+    from mamba3_siso_tpu_amd import layout as LY
+    cfg = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=chunk,
+                        policy_name=policy)
+    tile = LY.kernel_chunk(policy, chunk, 128, 64)
+    assert tile < chunk
+    cfg_t = m3.SISOConfig(d_model=256, d_state=128, headdim=64, expand=2, chunk=tile,
+                          policy_name=policy)
+    dt = BF16 if policy == "bf16" else torch.float32
+    p_cpu = m3.init_params(cfg, 21)
+    g = torch.Generator().manual_seed(22)
+    u = torch.randn(2, 1024, 256, generator=g).to(dt)
+    gy = torch.randn(2, 1024, 256, generator=g).to(dt)
+    runs = []
+    for c in (cfg, cfg_t):
+        params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+        ud = u.cuda().requires_grad_(True)
+        y, st = m3.mamba3_siso_layer(params, ud, c)
+        (y.float() * gy.cuda().float()).sum().backward()
+        runs.append((y, st, ud.grad, params))
+    (y, st, du, params), (y_t, st_t, du_t, params_t) = runs
+    assert torch.equal(y, y_t) and torch.equal(st.ssm, st_t.ssm) and torch.equal(du, du_t)
+    for f in p_cpu._fields:
+        assert torch.equal(getattr(params, f).grad, getattr(params_t, f).grad), f
+    pd = {k_: v_.requires_grad_(True) for k_, v_ in params_dict(p_cpu).items()}
+    uo = u.double().requires_grad_(True)
+    yr, sr = O.layer_forward(pd, uo, d_state=128, headdim=64, expand=2, chunk=chunk)
+    (yr * gy.double()).sum().backward()
+    report(f"layer y ({policy}, chunk {chunk} as {tile}) vs float64", y, yr.detach())
+    if policy == "f32":
+        assert_p95(y, yr.detach(), 2e-5, "y")
+        assert_p95(st.ssm, sr.ssm.detach(), 2e-5, "final ssm")
+        assert_p95(du, uo.grad, GRAD_F32_P95, "du")
+        for f in p_cpu._fields:
+            assert_p95(getattr(params, f).grad, pd[f].grad, GRAD_F32_P95, f"d{f}")
+    else:
+        assert_maxrel(y, yr.detach(), BF16_Y_MAXREL, "y")
+        assert_maxabs(st.ssm, sr.ssm.detach(), STATE_MAXABS, "final ssm")
+        assert_maxrel(du, uo.grad, BF16_GRAD_MAXREL, "du")
+        for f in p_cpu._fields:
+            assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
+
+
 @pytest.mark.parametrize("policy", ["f32", "bf16"])
 def test_layer_decode_step_matches_oracle(m3, policy):
     # decode does not depend on the chunk; f32 at N=128 is compiled at chunk 32

@@ -99,7 +99,7 @@ def test_prep_forward_full_length(m3, dev):
 @pytest.mark.parametrize("b,l,h,nr,a_floor,init,raw_dtype", [
     (2, 40, 3, 4, 1e-4, True, torch.float32),
     (1, 200, 4, 6, 1e-4, False, torch.float32),
-    (1, 150, 5, 12, 1e-4, True, torch.float32),    # 3 angle quads: the LDS-atomic reductions
+    (1, 150, 5, 12, 1e-4, True, torch.float32),    # 3 angle groups, padded to 4
     (2, 130, 8, 32, 0.5, True, torch.float32),
     (2, 256, 4, 16, 1e-4, True, torch.bfloat16),
 ])
@@ -136,6 +136,28 @@ def test_prep_backward_matches_oracle_autograd(m3, dev, b, l, h, nr, a_floor, in
             assert O.rel_error(gv, wv) < 1e-4, (name, O.rel_error(gv, wv))
         else:
             assert O.max_rel(gv, wv) < 2e-2, (name, O.max_rel(gv, wv))
+
+
+@pytest.mark.parametrize("h,nr", [(32, 32), (64, 32), (5, 12)])
+def test_prep_backward_is_bit_reproducible(m3, dev, h, nr):
+    """The raw-slice gradients are bit-identical between runs: the angle cotangent's sum
+    over heads is taken in wave order at the end of each run of tokens (one and two
+    rounds of heads per workgroup, and a padded angle-group count)."""
+    dtr, ar, tr, ang, bias = raw_inputs(2, 300, h, nr, seed=3)
+    g = torch.Generator().manual_seed(4)
+    cot = {k: torch.randn(2, h, 300, generator=g).to(dev)
+           for k in ("adt", "gamma", "scale", "lam", "dt")}
+    cphi = torch.randn(2, h, 300, nr, generator=g).to(dev)
+    d_in = [t.detach().requires_grad_(True) for t in as_proj(dev, torch.float32, dtr, ar, tr, ang)]
+    d_bias = bias.float().to(dev).requires_grad_(True)
+    runs = []
+    for _ in range(3):
+        pre, fin = m3.preprocess(*d_in, d_bias)
+        dl = sum((getattr(pre, k) * cot[k]).sum() for k in cot) + (pre.phi * cphi).sum()
+        runs.append(torch.autograd.grad(dl, d_in + [d_bias]))
+    for r in runs[1:]:
+        for name, x, y in zip(["dt_raw", "a_raw", "trap_raw", "angles", "dt_bias"], runs[0], r):
+            assert torch.equal(x, y), name
 
 
 def test_prep_backward_with_partial_cotangents(m3, dev):
