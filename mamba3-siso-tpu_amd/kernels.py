@@ -129,6 +129,50 @@ def _tile(pol: LY.DtypePolicy, chunk: int, state_dim: int, headdim: int, role: s
     return tile
 
 
+def _width(pol: LY.DtypePolicy, chunk: int, state_dim: int, headdim: int, role: str) -> int:
+    """`layout.kernel_headdim`, or the error naming the shape."""
+    width = LY.kernel_headdim(pol.name, chunk, state_dim, headdim)
+    if width is None:
+        raise ValueError(
+            f"no {role} kernel for policy={pol.name} chunk={chunk} d_state={state_dim} "
+            f"headdim={headdim}; chunks compiled for this shape: "
+            f"{list(LY.compiled_chunks(pol.name, state_dim, headdim))}")
+    return width
+
+
+# A head of width P runs as r = P / P' sub-heads of a compiled width P' (layout.kernel_headdim):
+# sub-head h*r + s takes columns s*P'.. of head h and shares every other input of head h.
+def _rep(t: Optional[Tensor], r: int, dim: int = 1) -> Optional[Tensor]:
+    """A per-head input, repeated for each of the head's r sub-heads."""
+    return None if t is None else t.repeat_interleave(r, dim=dim)
+
+
+def _split_cols(t: Optional[Tensor], r: int) -> Optional[Tensor]:
+    """``(B, H, L, P)`` -> ``(B, H*r, L, P/r)``: a view when a head's columns are adjacent in
+    memory (the layer's ``(B, L, H*P)`` layout), else a copy."""
+    if t is None:
+        return None
+    b, h, l, p = t.shape
+    return t.unflatten(3, (r, p // r)).permute(0, 1, 3, 2, 4).reshape(b, h * r, l, p // r)
+
+
+def _merge_cols(t: Tensor, r: int) -> Tensor:
+    """Inverse of `_split_cols`: ``(B, H*r, L, P')`` -> ``(B, H, L, r*P')``."""
+    b, hr, l, pp = t.shape
+    return t.unflatten(1, (hr // r, r)).permute(0, 1, 3, 2, 4).reshape(b, hr // r, l, r * pp)
+
+
+def _rep_phi(phi, r: int):
+    if isinstance(phi, PhiStrips):
+        return PhiStrips(phi.table, _rep(phi.dt, r), _rep(phi.strips, r))
+    return _rep(phi, r)
+
+
+def _head_sum(t: Tensor, r: int, dim: int = 1) -> Tensor:
+    """Sum a per-sub-head gradient over each head's r sub-heads (in sub-head order)."""
+    return t.unflatten(dim, (t.shape[dim] // r, r)).sum(dim + 1)
+
+
 def siso_forward(
     q: Tensor, k: Tensor, v: Tensor, adt: Tensor, gamma: Tensor, scale: Tensor,
     phi: Tensor, q_bias: Tensor, k_bias: Tensor, d_skip: Optional[Tensor] = None,
@@ -151,6 +195,25 @@ def siso_forward(
     nheads, headdim = v.shape[1], v.shape[3]
     n_angles = phi.shape[-1]
     LY.num_chunks(seqlen, chunk)
+    width = _width(pol, chunk, state_dim, headdim, "forward")
+    if width != headdim and tuple(v.shape) == (batch, nheads, seqlen, headdim):
+        r = headdim // width
+        sd = lambda t, *s: None if t is None else t.reshape(batch, nheads * r, *s)  # noqa: E731
+        outs = siso_forward(
+            q, k, _split_cols(v, r), _rep(adt, r), _rep(gamma, r), _rep(scale, r),
+            _rep_phi(phi, r), _rep(q_bias, r, 0), _rep(k_bias, r, 0), _rep(d_skip, r, 0),
+            _split_cols(z, r), sd(seed_ssm, width, state_dim), _rep(seed_k, r),
+            sd(seed_v, width), _rep(seed_coef, r), chunk=chunk, dtype_policy=pol,
+            save_residuals=save_residuals)
+        y, fs, fk, fv = outs[:4]
+        res = (_merge_cols(y, r), fs.reshape(batch, nheads, headdim, state_dim),
+               fk[:, ::r].contiguous(), fv.reshape(batch, nheads, headdim))
+        if save_residuals:
+            cs = outs[4].chunk_states   # (B, H*r, nc, P', N)
+            cs = cs.unflatten(1, (nheads, r)).permute(0, 1, 3, 2, 4, 5).reshape(
+                batch, nheads, cs.shape[2], headdim, state_dim)
+            res += (ForwardResiduals(ybar=_merge_cols(outs[4].ybar, r), chunk_states=cs),)
+        return res
     chunk = _tile(pol, chunk, state_dim, headdim, "forward")
     nc = seqlen // chunk
     if q.shape != k.shape:
@@ -267,8 +330,24 @@ def siso_decode(q: Tensor, k: Tensor, v: Tensor, adt: Tensor, dt: Tensor, lam: T
     dev = _device_of(q, k, v, adt, dt, lam, angles, q_bias, k_bias, d_skip, z, *state)
     mt = pol.matmul
     dcode = _lib.dtype_code(mt)
-    if not _lib.supported(2, dcode, 0, state_dim, headdim):
+    width = LY.decode_headdim(pol.name, state_dim, headdim)
+    if width is None:
         raise ValueError(f"no decode kernel for policy={pol.name} d_state={state_dim} headdim={headdim}")
+    if width != headdim:   # sub-heads (see _split_cols): ssm and v update in place as views
+        r = headdim // width
+        ssm = _state_buf(state.ssm, (batch, nheads, headdim, state_dim), dev)
+        vst = _state_buf(state.v, (batch, nheads, headdim), dev)
+        kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
+        phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
+        sub = SISOState(ssm=ssm.view(batch, nheads * r, width, state_dim), k=_rep(kst, r),
+                        v=vst.view(batch, nheads * r, width), phi=_rep(phist, r))
+        cut = lambda t: None if t is None else t.reshape(batch, nheads * r, width)  # noqa: E731
+        y, st = siso_decode(q, k, cut(v), _rep(adt, r), _rep(dt, r), _rep(lam, r), angles,
+                            _rep(q_bias, r, 0), _rep(k_bias, r, 0), sub,
+                            d_skip=_rep(d_skip, r, 0), z=cut(z), dtype_policy=pol)
+        kst.copy_(st.k[:, ::r])
+        phist.copy_(st.phi[:, ::r])
+        return y.reshape(batch, nheads, headdim), SISOState(ssm=ssm, k=kst, v=vst, phi=phist)
     ssm = _state_buf(state.ssm, (batch, nheads, headdim, state_dim), dev)
     kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
     vst = _state_buf(state.v, (batch, nheads, headdim), dev)
@@ -443,6 +522,11 @@ def siso_backward_kernel(
     nheads, headdim = v.shape[1], v.shape[3]
     n_angles = phi.shape[-1]
     LY.num_chunks(seqlen, chunk)
+    width = _width(pol, chunk, state_dim, headdim, "backward")
+    if width != headdim and tuple(v.shape) == (batch, nheads, seqlen, headdim):
+        return _backward_split(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias,
+                               chunk_states, d_skip, dfinal_ssm, chunk, pol, dfinal_v, dv_out,
+                               dz_out, headdim // width)
     chunk = _tile(pol, chunk, state_dim, headdim, "backward")
     nc = seqlen // chunk
     if tuple(dy.shape) != tuple(v.shape) or tuple(ybar.shape) != tuple(v.shape):
@@ -506,6 +590,52 @@ def siso_backward_kernel(
     return KernelGrads(dq=dq, dk=dk, dv=dv, dadt=dadt, dqk_diag=dqk, dscale=dscale, dphi=dphi,
                        dz=dz, uw=uw, dq_bias=dqb.sum(0), dk_bias=dkb.sum(0), k_final=kfin,
                        dseed_ssm=dseed)
+
+
+def _backward_split(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias, chunk_states,
+                    d_skip, dfinal_ssm, chunk, pol, dfinal_v, dv_out, dz_out, r):
+    """`siso_backward_kernel` for heads run as r sub-heads (see `_split_cols`): the
+    sub-heads' gradients of the inputs they share are summed per head."""
+    batch, nheads, seqlen, headdim = v.shape
+    state_dim = q.shape[-1]
+    width = headdim // r
+    cs = chunk_states.unflatten(3, (r, width)).permute(0, 1, 3, 2, 4, 5).reshape(
+        batch, nheads * r, chunk_states.shape[2], width, state_dim)
+
+    def in_place(out):   # a sub-head view of the caller's buffer, or None
+        if out is None:
+            return None
+        sv = _split_cols(out, r)
+        return sv if sv.data_ptr() == out.data_ptr() and sv._base is not None else None
+
+    dv_v, dz_v = in_place(dv_out), in_place(dz_out)
+    kg = siso_backward_kernel(
+        _split_cols(dy, r), _split_cols(ybar, r), _split_cols(z, r), q, k, _split_cols(v, r),
+        _rep(adt, r), _rep(gamma, r), _rep(scale, r), _rep_phi(phi, r), _rep(q_bias, r, 0),
+        _rep(k_bias, r, 0), cs, d_skip=_rep(d_skip, r, 0),
+        dfinal_ssm=None if dfinal_ssm is None else dfinal_ssm.reshape(batch, nheads * r, width, state_dim),
+        chunk=chunk, dtype_policy=pol,
+        dfinal_v=None if dfinal_v is None else dfinal_v.reshape(batch, nheads * r, width),
+        dv_out=dv_v, dz_out=dz_v)
+
+    def merged(g, out, out_v):
+        if g is None:
+            return None
+        if out_v is not None:
+            return out
+        m = _merge_cols(g, r)
+        if out is not None:
+            out.copy_(m)
+            return out
+        return m
+
+    return KernelGrads(
+        dq=kg.dq, dk=kg.dk, dv=merged(kg.dv, dv_out, dv_v), dadt=_head_sum(kg.dadt, r),
+        dqk_diag=_head_sum(kg.dqk_diag, r), dscale=_head_sum(kg.dscale, r),
+        dphi=_head_sum(kg.dphi, r), dz=merged(kg.dz, dz_out, dz_v),
+        uw=kg.uw[:, ::r].contiguous(), dq_bias=_head_sum(kg.dq_bias, r, 0),
+        dk_bias=_head_sum(kg.dk_bias, r, 0), k_final=kg.k_final[:, ::r].contiguous(),
+        dseed_ssm=kg.dseed_ssm.reshape(batch, nheads, headdim, state_dim))
 
 
 class SISOGrads(NamedTuple):

@@ -322,8 +322,10 @@ def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
 
 def _decode_fused_ok(u: Tensor, cfg: SISOConfig) -> bool:
     """Whether the decode step runs as one ``m3s_decode_layer`` launch: ``u`` on the
-    device in the policy's operand dtype (otherwise the composed step casts as needed)."""
-    return u.is_cuda and u.dtype == LY.policy(cfg.policy_name).matmul
+    device in the policy's operand dtype, and a decode kernel of the head's own width
+    (otherwise the composed step casts as needed and runs sub-heads)."""
+    return (u.is_cuda and u.dtype == LY.policy(cfg.policy_name).matmul
+            and LY.decode_headdim(cfg.policy_name, cfg.d_state, cfg.headdim) == cfg.headdim)
 
 
 def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,

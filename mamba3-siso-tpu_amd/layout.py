@@ -171,10 +171,51 @@ def kernel_chunk(policy_name: str, chunk: int, d_state: int, headdim: int) -> Op
     return None
 
 
+def kernel_headdim(policy_name: str, chunk: int, d_state: int, headdim: int) -> Optional[int]:
+    """The head width the kernels run for ``headdim``: ``headdim`` itself when it has
+    scan (`kernel_chunk`) and decode kernels, else the largest compiled width dividing
+    it; None if there is none.
+
+    Given a head's scores ``q~ . k^`` and decays, its output and state are independent
+    across the P columns of v (``reference.py:217-330``): a head of width P runs exactly
+    as P / P' heads of width P' that share its q, k, scalars, phi and biases, with the
+    shared inputs' gradients summed over them."""
+    pol = policy(policy_name).name
+
+    def ok(p):
+        return (kernel_chunk(pol, chunk, d_state, p) is not None
+                and (pol, 0, d_state, p) in KERNELS["decode"])
+
+    if ok(headdim):
+        return headdim
+    widths = sorted({p for (q, _, n, p) in KERNELS["forward"] if q == pol and n == d_state},
+                    reverse=True)
+    for p in widths:
+        if p < headdim and headdim % p == 0 and ok(p):
+            return p
+    return None
+
+
+def decode_headdim(policy_name: str, d_state: int, headdim: int) -> Optional[int]:
+    """`kernel_headdim` for the decode kernels alone (no chunk)."""
+    pol = policy(policy_name).name
+    widths = sorted({p for (q, _, n, p) in KERNELS["decode"] if q == pol and n == d_state},
+                    reverse=True)
+    if headdim in widths:
+        return headdim
+    for p in widths:
+        if p < headdim and headdim % p == 0:
+            return p
+    return None
+
+
 def missing_kernels(policy_name: str, chunk: int, d_state: int, headdim: int) -> list:
     """The roles (forward, backward, decode) with no compiled kernel to run this shape
-    (for the scans, at `kernel_chunk`)."""
+    (for the scans at `kernel_chunk`, as heads of `kernel_headdim`)."""
     pol = policy(policy_name).name
+    width = kernel_headdim(pol, chunk, d_state, headdim)
+    if width is not None:
+        return []
     out = []
     if kernel_chunk(pol, chunk, d_state, headdim) is None:
         out += ["forward", "backward"]

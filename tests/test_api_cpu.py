@@ -40,9 +40,9 @@ def test_config_fields_defaults_and_rules(m3):
     (dict(d_model=1024, chunk=192), "multiple of 128"),
     (dict(d_model=1024, chunk=0), "multiple of 128"),
     (dict(d_model=1024, chunk=16), "multiple of 128"),
-    (dict(d_model=256, d_state=32, headdim=32), "forward/backward/decode"),
     (dict(d_model=256, d_state=256), "forward/backward/decode"),
-    (dict(d_model=256, headdim=128), "forward/backward/decode"),
+    (dict(d_model=256, headdim=32), "forward/backward/decode"),      # 32 < the compiled 64
+    (dict(d_model=192, d_state=32, headdim=24), "forward/backward/decode"),
 ])
 def test_config_rejects_shapes_without_compiled_kernels(m3, kw, match):
     """The reference rejects a bad chunk when the config is built (layer.py:97-99); here
@@ -61,6 +61,21 @@ def test_config_accepts_every_compiled_shape(m3):
             assert (cfg.chunk, cfg.d_state, cfg.headdim) == (c, n, p)
     assert LY.compiled_chunks("f32", 128, 64) == (32,)
     assert LY.compiled_chunks("bf16", 128, 64) == (32, 64, 128)
+
+
+@pytest.mark.parametrize("pol,n,p,width", [
+    ("bf16", 128, 64, 64), ("bf16", 128, 128, 64), ("bf16", 128, 256, 64), ("f32", 128, 192, 64),
+    ("bf16", 64, 128, 64), ("bf16", 32, 32, 16), ("f32", 16, 48, 16),
+])
+def test_wide_heads_run_as_compiled_sub_heads(m3, pol, n, p, width):
+    """A head width with no kernel of its own runs as sub-heads of the largest compiled
+    width dividing it (the scan is independent across a head's v columns given its
+    scores), for the scans and the decode alike."""
+    from mamba3_siso_tpu_amd import layout as LY
+    cfg = m3.SISOConfig(d_model=4 * p, d_state=n, headdim=p, chunk=64, policy_name=pol)
+    assert cfg.headdim == p
+    assert LY.kernel_headdim(pol, 64, n, p) == width
+    assert LY.decode_headdim(pol, n, p) == width
 
 
 @pytest.mark.parametrize("pol,chunk,n,p,tile", [

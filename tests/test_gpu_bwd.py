@@ -151,6 +151,42 @@ def test_backward_is_bit_reproducible(m3, policy, n, p, chunk, compact):
                 assert torch.equal(x, getattr(r, name)), name
 
 
+@pytest.mark.parametrize("policy,n,p,chunk,compact", [("bf16", 128, 128, 128, False),
+                                                    ("f32", 32, 48, 64, True)])
+def test_forward_and_backward_with_sub_heads(m3, policy, n, p, chunk, compact):
+    """A head width with no kernel runs as sub-heads of a compiled width: forward outputs
+    and every gradient (the shared inputs' summed over sub-heads) against the oracle,
+    with seeds and final-state cotangents, and dv / dz written into caller buffers laid
+    out like the layer's (B, L, H*P) projection gradient."""
+    want, gr = run_case(m3, 2, 2, 256, n, p, n // 4, chunk, policy, True, True, seed=3)
+    c, d = boundary_inputs(2, 2, 256, n, p, n // 4, policy, seed=3, seeds=True)
+    for name, w in want.items():
+        g_ = getattr(gr, GRAD_FIELD[name])
+        if policy == "f32":
+            assert_p95(g_, w, GRAD_F32_P95, f"d{name}")
+        else:
+            assert_maxrel(g_, w, BF16_GRAD_MAXREL, f"d{name}")
+    # in place into (B, L, H*P) buffers, phi built in the kernel
+    phi = phi_strips_of(c, m3) if compact else d["phi"]
+    a = fwd_args(dict(d, phi=phi))
+    out = m3.siso_forward(*a, chunk=chunk, dtype_policy=policy, save_residuals=True)
+    mt = d["v"].dtype
+    buf = torch.zeros(2, 256, 2 * 2 * p, device="cuda", dtype=mt)
+    dv_out = buf[..., :2 * p].unflatten(-1, (2, p)).permute(0, 2, 1, 3)
+    dz_out = buf[..., 2 * p:].unflatten(-1, (2, p)).permute(0, 2, 1, 3)
+    g2 = m3.siso_backward(d["dy"], *a[:9], out[4].ybar, out[4].chunk_states,
+                          d_skip=d["d_skip"], z=d["z"], seed_ssm=d["seed_ssm"],
+                          seed_k=d["seed_k"], seed_v=d["seed_v"], seed_coef=d["seed_coef"],
+                          chunk=chunk, dtype_policy=policy, dv_out=dv_out, dz_out=dz_out)
+    assert g2.dv.data_ptr() == dv_out.data_ptr() and g2.dz.data_ptr() == dz_out.data_ptr()
+    ref = m3.siso_backward(d["dy"], *a[:9], out[4].ybar, out[4].chunk_states,
+                           d_skip=d["d_skip"], z=d["z"], seed_ssm=d["seed_ssm"],
+                           seed_k=d["seed_k"], seed_v=d["seed_v"], seed_coef=d["seed_coef"],
+                           chunk=chunk, dtype_policy=policy)
+    assert torch.equal(g2.dv, ref.dv) and torch.equal(g2.dz, ref.dz)
+    assert torch.equal(g2.dq, ref.dq) and torch.equal(g2.dadt, ref.dadt)
+
+
 def test_backward_matches_finite_differences_of_the_kernel_forward(m3):
     """Central differences of the HIP forward itself (f32, tiny): the VJP is checked
     against the function it differentiates, as tests.py:614-645 does."""

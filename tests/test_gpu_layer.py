@@ -179,6 +179,66 @@ def test_layer_at_chunks_without_a_kernel_of_their_own(m3, policy, chunk):
             assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
 
 
+@pytest.mark.parametrize("policy,n,p,chunk", [("bf16", 128, 128, 128), ("f32", 32, 32, 64),
+                                            ("bf16", 64, 192, 64)])
+def test_layer_with_heads_wider_than_a_kernel(m3, policy, n, p, chunk):
+    """Head widths with no kernel of their own (a checkpoint with headdim 128) run as
+    sub-heads of a compiled width (layout.kernel_headdim): the output, final state and
+    every gradient against autograd of the float64 layer, then a decode step from the
+    final state against the oracle's."""
+    from mamba3_siso_tpu_amd import layout as LY
+    cfg = m3.SISOConfig(d_model=2 * p, d_state=n, headdim=p, expand=2, chunk=chunk,
+                        policy_name=policy)
+    assert LY.kernel_headdim(policy, chunk, n, p) < p
+    dt = BF16 if policy == "bf16" else torch.float32
+    p_cpu = m3.init_params(cfg, 31)
+    g = torch.Generator().manual_seed(32)
+    u = torch.randn(2, 256, cfg.d_model, generator=g).to(dt)
+    gy = torch.randn(2, 256, cfg.d_model, generator=g).to(dt)
+    params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+    ud = u.cuda().requires_grad_(True)
+    y, st = m3.mamba3_siso_layer(params, ud, cfg)
+    (y.float() * gy.cuda().float()).sum().backward()
+    pd = {k_: v_.requires_grad_(True) for k_, v_ in params_dict(p_cpu).items()}
+    uo = u.double().requires_grad_(True)
+    yr, sr = O.layer_forward(pd, uo, d_state=n, headdim=p, expand=2, chunk=chunk)
+    (yr * gy.double()).sum().backward()
+    report(f"layer y ({policy}, N {n}, P {p}) vs float64", y, yr.detach())
+    if policy == "f32":
+        assert_p95(y, yr.detach(), 2e-5, "y")
+        assert_p95(st.ssm, sr.ssm.detach(), 2e-5, "final ssm")
+        assert_p95(ud.grad, uo.grad, GRAD_F32_P95, "du")
+        for f in p_cpu._fields:
+            assert_p95(getattr(params, f).grad, pd[f].grad, GRAD_F32_P95, f"d{f}")
+    else:
+        assert_maxrel(y, yr.detach(), BF16_Y_MAXREL, "y")
+        assert_maxabs(st.ssm, sr.ssm.detach(), STATE_MAXABS, "final ssm")
+        assert_maxrel(ud.grad, uo.grad, BF16_GRAD_MAXREL, "du")
+        for f in p_cpu._fields:
+            assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
+    # bf16: the angles and dt come from the bf16 projection, 2^-9 relative per token
+    assert O.rel_error(cpu(st.phi), sr.phi.detach(), angle=True) <= (1e-4 if policy == "f32" else 1e-2)
+    # one decode step from the final state (composed path: sub-heads of the decode kernel)
+    g2 = torch.Generator().manual_seed(33)
+    u1 = torch.randn(2, cfg.d_model, generator=g2).to(dt)
+    st_o = O.SISOState(*(t.detach().double() for t in (sr.ssm, sr.k, sr.v, sr.phi)))
+    with torch.no_grad():
+        y1, s1 = m3.mamba3_siso_decode_step(
+            m3.SISOParams(*(t.detach() for t in params)), u1.cuda(), cfg,
+            m3.SISOState(*(t.float().cuda().contiguous() for t in st_o)))
+    y1r, s1r = O.layer_decode_step(params_dict(p_cpu), u1.double(), st_o, d_state=n, headdim=p,
+                                   mm_dtype=BF16 if policy == "bf16" else None)
+    if policy == "f32":
+        assert_p95(y1, y1r, 1e-4, "decode y")
+        assert_p95(s1.ssm, s1r.ssm, 2e-5, "decode ssm")
+    else:
+        assert_maxrel(y1, y1r, BF16_MAXREL, "decode y")
+        assert_maxrel(s1.ssm, s1r.ssm, BF16_MAXREL, "decode ssm")
+    # bf16: the token's k row and angles come from the bf16 projection
+    assert O.max_rel(cpu(s1.k), s1r.k) <= (1e-5 if policy == "f32" else BF16_MAXREL)
+    assert O.rel_error(cpu(s1.phi), s1r.phi, angle=True) <= (1e-5 if policy == "f32" else 1e-2)
+
+
 @pytest.mark.parametrize("policy", ["f32", "bf16"])
 def test_layer_decode_step_matches_oracle(m3, policy):
     # decode does not depend on the chunk; f32 at N=128 is compiled at chunk 32
