@@ -1846,6 +1846,7 @@ static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   X(bf16, 128, 16, 16)     \
   X(bf16, 64, 16, 16)      \
   X(bf16, 32, 16, 16)      \
+  X(bf16, 32, 256, 64)     \
   X(float, 32, 128, 64)    \
   X(float, 64, 64, 64)     \
   X(float, 32, 64, 64)     \

@@ -105,51 +105,75 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
     dt = p.dt[bh];
     lam = p.lam[bh];
   }
-  // ---- angle advance + rotation (one thread per rotary pair; wave 0) ------------
+  // ---- angle advance + rotation (wave 0; lane l takes the pairs j = l + 64 u) ---------
   if (tid < 64) {
-    const int j = tid;
-    const bool act = j < H2;
-    float qlo = 0.f, qhi = 0.f, klo = 0.f, khi = 0.f;
+    constexpr int JP = (H2 + 63) / 64;   // pairs per lane
+    float qlo[JP], qhi[JP], klo[JP], khi[JP];
     if constexpr (LAYER) {
       // BCNorm of the C (query) and B (key) rows, f32, output rounded to MT
       const MT* crow = prow + 2 * HP + N;
       const MT* brow = prow + 2 * HP;
-      float cl = 0.f, ch = 0.f, bl = 0.f, bh_ = 0.f;
-      if (act) {
-        cl = (float)crow[j]; ch = (float)crow[H2 + j];
-        bl = (float)brow[j]; bh_ = (float)brow[H2 + j];
+      float cl[JP], ch[JP], bl[JP], bh_[JP];
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int u = 0; u < JP; ++u) {
+        const int j = tid + 64 * u;
+        cl[u] = ch[u] = bl[u] = bh_[u] = 0.f;
+        if (j < H2) {
+          cl[u] = (float)crow[j]; ch[u] = (float)crow[H2 + j];
+          bl[u] = (float)brow[j]; bh_[u] = (float)brow[H2 + j];
+        }
+        sq += cl[u] * cl[u] + ch[u] * ch[u];
+        sk += bl[u] * bl[u] + bh_[u] * bh_[u];
       }
-      const float sq = group_sum<64>(cl * cl + ch * ch), sk = group_sum<64>(bl * bl + bh_ * bh_);
+      sq = group_sum<64>(sq);
+      sk = group_sum<64>(sk);
       const float rq = 1.f / sqrtf(sq / (float)N + p.eps), rk = 1.f / sqrtf(sk / (float)N + p.eps);
-      if (act) {
-        qlo = (float)(MT)(cl * rq * p.wc[j]);
-        qhi = (float)(MT)(ch * rq * p.wc[H2 + j]);
-        klo = (float)(MT)(bl * rk * p.wb[j]);
-        khi = (float)(MT)(bh_ * rk * p.wb[H2 + j]);
+#pragma unroll
+      for (int u = 0; u < JP; ++u) {
+        const int j = tid + 64 * u;
+        qlo[u] = qhi[u] = klo[u] = khi[u] = 0.f;
+        if (j < H2) {
+          qlo[u] = (float)(MT)(cl[u] * rq * p.wc[j]);
+          qhi[u] = (float)(MT)(ch[u] * rq * p.wc[H2 + j]);
+          klo[u] = (float)(MT)(bl[u] * rk * p.wb[j]);
+          khi[u] = (float)(MT)(bh_[u] * rk * p.wb[H2 + j]);
+        }
       }
-    } else if (act) {
+    } else {
       const MT* qg = static_cast<const MT*>(p.q) + (int64_t)b * N;
       const MT* kg = static_cast<const MT*>(p.k) + (int64_t)b * N;
-      qlo = (float)qg[j]; qhi = (float)qg[H2 + j];
-      klo = (float)kg[j]; khi = (float)kg[H2 + j];
+#pragma unroll
+      for (int u = 0; u < JP; ++u) {
+        const int j = tid + 64 * u;
+        qlo[u] = qhi[u] = klo[u] = khi[u] = 0.f;
+        if (j < H2) {
+          qlo[u] = (float)qg[j]; qhi[u] = (float)qg[H2 + j];
+          klo[u] = (float)kg[j]; khi[u] = (float)kg[H2 + j];
+        }
+      }
     }
-    if (act) {
-    const float ulo = qlo + p.qb[h * N + j];
-    const float uhi = qhi + p.qb[h * N + H2 + j];
-    const float wlo = klo + p.kb[h * N + j];
-    const float whi = khi + p.kb[h * N + H2 + j];
-    float sn = 0.f, cs = 1.f;
-    if (j < p.Nr) {
-      const float ang = LAYER ? (float)prow[2 * HP + 2 * N + 3 * p.H + j] : p.angles[(int64_t)b * p.Nr + j];
-      const float th = tanhf(ang) * kPi * dt;
-      const float phi = wrap_2pi(p.phist[bh * p.Nr + j] + th);
-      p.phist[bh * p.Nr + j] = phi;
-      sincosf(phi, &sn, &cs);
-    }
-    sQt[j] = (float)(MT)(ulo * cs - uhi * sn);
-    sQt[H2 + j] = (float)(MT)(uhi * cs + ulo * sn);
-    sKt[j] = wlo * cs - whi * sn;
-    sKt[H2 + j] = whi * cs + wlo * sn;
+#pragma unroll
+    for (int u = 0; u < JP; ++u) {
+      const int j = tid + 64 * u;
+      if (j < H2) {
+        const float ulo = qlo[u] + p.qb[h * N + j];
+        const float uhi = qhi[u] + p.qb[h * N + H2 + j];
+        const float wlo = klo[u] + p.kb[h * N + j];
+        const float whi = khi[u] + p.kb[h * N + H2 + j];
+        float sn = 0.f, cs = 1.f;
+        if (j < p.Nr) {
+          const float ang = LAYER ? (float)prow[2 * HP + 2 * N + 3 * p.H + j] : p.angles[(int64_t)b * p.Nr + j];
+          const float th = tanhf(ang) * kPi * dt;
+          const float phi = wrap_2pi(p.phist[bh * p.Nr + j] + th);
+          p.phist[bh * p.Nr + j] = phi;
+          sincosf(phi, &sn, &cs);
+        }
+        sQt[j] = (float)(MT)(ulo * cs - uhi * sn);
+        sQt[H2 + j] = (float)(MT)(uhi * cs + ulo * sn);
+        sKt[j] = wlo * cs - whi * sn;
+        sKt[H2 + j] = whi * cs + wlo * sn;
+      }
     }
   }
   const MT* vrow = LAYER ? prow + HP + h * P : static_cast<const MT*>(p.v) + bh * P;
@@ -210,6 +234,7 @@ static int32_t launch_dec(const DecParams& prm, int grid, hipStream_t stream) {
   X(bf16, 64, 64)          \
   X(bf16, 32, 16)          \
   X(bf16, 16, 16)          \
+  X(bf16, 256, 64)         \
   X(float, 128, 64)        \
   X(float, 64, 64)         \
   X(float, 32, 16)         \

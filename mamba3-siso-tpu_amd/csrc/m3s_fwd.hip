@@ -1430,6 +1430,7 @@ static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   X(bf16, 128, 16, 16)      \
   X(bf16, 64, 16, 16)       \
   X(bf16, 32, 16, 16)       \
+  X(bf16, 32, 256, 64)     \
   X(float, 64, 128, 64)     \
   X(float, 32, 128, 64)     \
   X(float, 64, 64, 64)      \

@@ -133,6 +133,7 @@ KERNELS = {
         ("bf16", 128, 64, 64), ("bf16", 64, 64, 64), ("bf16", 32, 64, 64),
         ("bf16", 128, 32, 16), ("bf16", 64, 32, 16), ("bf16", 32, 32, 16),
         ("bf16", 128, 16, 16), ("bf16", 64, 16, 16), ("bf16", 32, 16, 16),
+        ("bf16", 32, 256, 64),
         ("f32", 64, 128, 64), ("f32", 32, 128, 64),
         ("f32", 64, 64, 64), ("f32", 32, 64, 64),
         ("f32", 128, 32, 16), ("f32", 64, 32, 16), ("f32", 32, 32, 16),
@@ -143,6 +144,7 @@ KERNELS = {
         ("bf16", 128, 64, 64), ("bf16", 64, 64, 64), ("bf16", 32, 64, 64),
         ("bf16", 128, 32, 16), ("bf16", 64, 32, 16), ("bf16", 32, 32, 16),
         ("bf16", 128, 16, 16), ("bf16", 64, 16, 16), ("bf16", 32, 16, 16),
+        ("bf16", 32, 256, 64),
         ("f32", 32, 128, 64),
         ("f32", 64, 64, 64), ("f32", 32, 64, 64),
         ("f32", 128, 32, 16), ("f32", 64, 32, 16), ("f32", 32, 32, 16),
@@ -150,7 +152,7 @@ KERNELS = {
     }),
     "decode": frozenset({
         (pol, 0, n, p) for pol in ("bf16", "f32") for n, p in ((128, 64), (64, 64), (32, 16), (16, 16))
-    }),
+    } | {("bf16", 0, 256, 64)}),
 }
 
 

@@ -40,7 +40,7 @@ def test_config_fields_defaults_and_rules(m3):
     (dict(d_model=1024, chunk=192), "multiple of 128"),
     (dict(d_model=1024, chunk=0), "multiple of 128"),
     (dict(d_model=1024, chunk=16), "multiple of 128"),
-    (dict(d_model=256, d_state=256), "forward/backward/decode"),
+    (dict(d_model=256, d_state=256, policy_name="f32"), "forward/backward/decode"),
     (dict(d_model=256, headdim=32), "forward/backward/decode"),      # 32 < the compiled 64
     (dict(d_model=192, d_state=32, headdim=24), "forward/backward/decode"),
 ])
@@ -65,7 +65,7 @@ def test_config_accepts_every_compiled_shape(m3):
 
 @pytest.mark.parametrize("pol,n,p,width", [
     ("bf16", 128, 64, 64), ("bf16", 128, 128, 64), ("bf16", 128, 256, 64), ("f32", 128, 192, 64),
-    ("bf16", 64, 128, 64), ("bf16", 32, 32, 16), ("f32", 16, 48, 16),
+    ("bf16", 64, 128, 64), ("bf16", 32, 32, 16), ("f32", 16, 48, 16), ("bf16", 256, 128, 64),
 ])
 def test_wide_heads_run_as_compiled_sub_heads(m3, pol, n, p, width):
     """A head width with no kernel of its own runs as sub-heads of the largest compiled

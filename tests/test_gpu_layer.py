@@ -180,16 +180,18 @@ def test_layer_at_chunks_without_a_kernel_of_their_own(m3, policy, chunk):
 
 
 @pytest.mark.parametrize("policy,n,p,chunk", [("bf16", 128, 128, 128), ("f32", 32, 32, 64),
-                                            ("bf16", 64, 192, 64)])
+                                            ("bf16", 64, 192, 64), ("bf16", 256, 64, 128),
+                                            ("bf16", 256, 128, 128)])
 def test_layer_with_heads_wider_than_a_kernel(m3, policy, n, p, chunk):
     """Head widths with no kernel of their own (a checkpoint with headdim 128) run as
-    sub-heads of a compiled width (layout.kernel_headdim): the output, final state and
-    every gradient against autograd of the float64 layer, then a decode step from the
-    final state against the oracle's."""
+    sub-heads of a compiled width (layout.kernel_headdim), and d_state 256 runs the
+    generic kernels at 32-token tiles: the output, final state and every gradient
+    against autograd of the float64 layer, then a decode step from the final state
+    against the oracle's."""
     from mamba3_siso_tpu_amd import layout as LY
     cfg = m3.SISOConfig(d_model=2 * p, d_state=n, headdim=p, expand=2, chunk=chunk,
                         policy_name=policy)
-    assert LY.kernel_headdim(policy, chunk, n, p) < p
+    assert LY.kernel_headdim(policy, chunk, n, p) < p or LY.kernel_chunk(policy, chunk, n, p) < chunk
     dt = BF16 if policy == "bf16" else torch.float32
     p_cpu = m3.init_params(cfg, 31)
     g = torch.Generator().manual_seed(32)
