@@ -467,9 +467,22 @@ def cpu_baseline(m3, params32, cfg, torch):
             reps += 1
     return {"value": round(reps * u.shape[1] / t_total, 1), "unit": "tok/s",
             "cores": os.cpu_count(), "threads": torch.get_num_threads(), "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"{reps} x one sequence (B=1, L=8192, d_model=1024) of the configs[1] layer "
                       f"forward through oracle.siso_oracle.layer_forward in float32 on "
                       f"{platform.processor() or platform.machine()}"}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (Linux /proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 if __name__ == "__main__":
