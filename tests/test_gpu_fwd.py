@@ -238,8 +238,8 @@ def test_forward_full_size_cfg2_against_head_slices(m3):
     z = rn(B, H, L, P).to(BF16)
     dt_raw = torch.log(torch.expm1(torch.exp(torch.rand(B, L, H, generator=g, device="cuda")
                                              * (math.log(0.1) - math.log(0.001)) + math.log(0.001))))
-    pre, _ = m3.preprocess(dt_raw, rn(B, L, H), rn(B, L, H), 0.5 * rn(B, L, Nr),
-                           torch.zeros(H, device="cuda"))
+    a_raw, trap_raw, ang = rn(B, L, H), rn(B, L, H), 0.5 * rn(B, L, Nr)
+    pre, _ = m3.preprocess(dt_raw, a_raw, trap_raw, ang, torch.zeros(H, device="cuda"))
     qb, kb, dsk = 0.1 * rn(H, N), 0.1 * rn(H, N), rn(H)
     args = [q, k, v, pre.adt, pre.gamma, pre.scale, pre.phi, qb, kb, dsk, z]
     y, fs, fk, fv = m3.siso_forward(*args, chunk=128)
@@ -247,6 +247,17 @@ def test_forward_full_size_cfg2_against_head_slices(m3):
     assert bool(torch.isfinite(y.float()).all()) and bool(torch.isfinite(fs).all())
     assert O.rel_error(y64.float().cpu()[::3], y.float().cpu()[::3]) <= BF16_P95
     assert O.max_rel(fs64.cpu(), fs.cpu()) <= BF16_MAXREL
+    # the headline forward's kernel: phi built from the compact form at full length, against
+    # the phi-reading run (they differ by the float rounding of phi only) and the oracle
+    # slices below
+    compact = m3.scan_prep.prep_forward_launch(dt_raw, a_raw, trap_raw, ang,
+                                               torch.zeros(H, device="cuda"), None, 1e-4,
+                                               compact=True)[5]
+    yc, fsc, fkc, fvc = m3.siso_forward(*args[:6], compact, *args[7:], chunk=128)
+    report("cfg2 y, phi built vs read", yc, y.double())
+    assert O.rel_error(yc.float().cpu()[::2], y.float().cpu()[::2]) <= BF16_MODEL_P95
+    assert O.max_rel(fsc.cpu(), fs.cpu()) <= 1e-3
+    assert O.max_rel(fkc.cpu(), fk.cpu()) <= 1e-4 and torch.equal(fvc, fv)
     for b_, hs in ((0, [0, 31]), (7, [5, 17])):
         sl = lambda t: t[b_:b_ + 1, hs].double().cpu()  # noqa: E731
         args_cpu = (q[b_:b_ + 1].double().cpu(), k[b_:b_ + 1].double().cpu(), sl(v),
@@ -267,6 +278,9 @@ def test_forward_full_size_cfg2_against_head_slices(m3):
         assert_maxabs(fk[b_:b_ + 1, hs], sr.k, 1e-4, f"final k {tag}")
         assert_maxrel(y[b_:b_ + 1, hs], yr, BF16_Y_MAXREL, f"y {tag}")
         assert_p95(y[b_:b_ + 1, hs], yr, BF16_P95, f"y {tag}")
+        assert_bf16_bound(yc[b_:b_ + 1, hs], ym, what=f"y {tag} (phi built) vs bf16 model")
+        assert_maxabs(fsc[b_:b_ + 1, hs], sr.ssm, STATE_MAXABS, f"final ssm {tag} (phi built)")
+        assert_maxrel(yc[b_:b_ + 1, hs], yr, BF16_Y_MAXREL, f"y {tag} (phi built)")
 
 
 def _golden(name):
