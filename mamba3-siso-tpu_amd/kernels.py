@@ -602,11 +602,12 @@ def _backward_split(dy, ybar, z, q, k, v, adt, gamma, scale, phi, q_bias, k_bias
     cs = chunk_states.unflatten(3, (r, width)).permute(0, 1, 3, 2, 4, 5).reshape(
         batch, nheads * r, chunk_states.shape[2], width, state_dim)
 
-    def in_place(out):   # a sub-head view of the caller's buffer, or None
+    def in_place(out):   # a sub-head view of the caller's buffer, or None (reshape copied)
         if out is None:
             return None
         sv = _split_cols(out, r)
-        return sv if sv.data_ptr() == out.data_ptr() and sv._base is not None else None
+        same = sv.untyped_storage().data_ptr() == out.untyped_storage().data_ptr()
+        return sv if same else None
 
     dv_v, dz_v = in_place(dv_out), in_place(dz_out)
     kg = siso_backward_kernel(
