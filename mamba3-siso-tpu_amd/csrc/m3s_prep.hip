@@ -101,7 +101,7 @@ struct PrepFwdParams {
 };
 
 __host__ __device__ inline int prep_fwd_lds_floats(int H, int Nr) {
-  return 3 * (kPrepTB + 1) * H + kPrepTB * Nr;
+  return 3 * (kPrepTB + 1) * (H + 1) + kPrepTB * Nr;
 }
 
 template <typename RT>
@@ -111,10 +111,13 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * kPrepTB;
   const int nt = min(kPrepTB, L - t0), nt1 = min(kPrepTB + 1, L - t0);
-  float* sDt = lds;                          // [TB + 1][H]
-  float* sLam = sDt + (kPrepTB + 1) * H;     // [TB + 1][H]
-  float* sA = sLam + (kPrepTB + 1) * H;      // [TB + 1][H]
-  float* sT = sA + (kPrepTB + 1) * H;        // [TB][Nr]  tanh(angles) * pi
+  // [t][h] tables with a padded row stride HS = H + 1: written in (t, h) order and read in
+  // (h, t) order, so that the reads of consecutive t fall in distinct LDS banks
+  const int HS = H + 1;
+  float* sDt = lds;                          // [TB + 1][HS]
+  float* sLam = sDt + (kPrepTB + 1) * HS;    // [TB + 1][HS]
+  float* sA = sLam + (kPrepTB + 1) * HS;     // [TB + 1][HS]
+  float* sT = sA + (kPrepTB + 1) * HS;       // [TB][Nr]  tanh(angles) * pi
   const RT* dtr = static_cast<const RT*>(p.dtr.p) + b * p.dtr.sb;
   const RT* ar = static_cast<const RT*>(p.ar.p) + b * p.ar.sb;
   const RT* tr = static_cast<const RT*>(p.tr.p) + b * p.tr.sb;
@@ -140,9 +143,10 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
     for (int u = 0; u < KU; ++u) {
       const int i = i0 + u * kPrepThreads;
       if (i < n1) {
-        sDt[i] = softplus_(vd[u] + vb[u]);
-        sLam[i] = sigmoid_(vl[u]);
-        sA[i] = fminf(-heavy_tail_(va[u]), -p.a_floor);
+        const int k = (i / H) * HS + i % H;
+        sDt[k] = softplus_(vd[u] + vb[u]);
+        sLam[k] = sigmoid_(vl[u]);
+        sA[k] = fminf(-heavy_tail_(va[u]), -p.a_floor);
       }
     }
   }
@@ -167,9 +171,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   __syncthreads();
   for (int i = tid; i < H * nt; i += kPrepThreads) {  // (h, t) order: (b, h) rows
     const int h = i / nt, t = i % nt;
-    const int k = t * H + h;
+    const int k = t * HS + h;
     const float dt = sDt[k], lam = sLam[k];
-    const float nxt = (t0 + t + 1 < L) ? sDt[k + H] * (1.f - sLam[k + H]) : 0.f;
+    const float nxt = (t0 + t + 1 < L) ? sDt[k + HS] * (1.f - sLam[k + HS]) : 0.f;
     const float gam = dt * lam;
     const int64_t o = ((int64_t)b * H + h) * L + t0 + t;
     p.adt[o] = sA[k] * dt;
@@ -184,7 +188,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
     const int h = pr / J4, j0 = 4 * (pr % J4);
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     auto add_row = [&](int t) {
-      const float dt = sDt[t * H + h];
+      const float dt = sDt[t * HS + h];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (j0 + i < Nr) s[i] += sT[t * Nr + j0 + i] * dt;
@@ -366,20 +370,25 @@ constexpr int kPrepRun = 8;
 // angle-cotangent accumulator, dscale just before the block for each head, and each
 // wave's angle-cotangent partials of one run.
 __host__ __device__ inline int prep_bwd_lds_floats(int H, int Nr) {
-  return 6 * kPrepTB * H + 2 * kPrepTB * Nr + H + (kPrepThreads / 64) * kPrepRun * Nr;
+  return 3 * kPrepTB * H + 3 * kPrepTB * (H + 1) + 2 * kPrepTB * Nr + H +
+         (kPrepThreads / 64) * kPrepRun * Nr;
 }
 
 template <typename RT>
 __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdParams p) {
   extern __shared__ float lds[];
   const int H = p.H, Nr = p.Nr, L = p.L;
+  // the incoming cotangents are read from HBM in (h, t) order (coalesced) and stored
+  // t-major: their tables have a padded row stride HS = H + 1, so that consecutive t of
+  // one head fall in distinct LDS banks
+  const int HS = H + 1;
   float* sDt = lds;                    // [TB][H] dt
   float* sLam = sDt + kPrepTB * H;     // [TB][H] lambda
-  float* sDadt = sLam + kPrepTB * H;   // [TB][H] incoming cotangents (t-major)
-  float* sDgam = sDadt + kPrepTB * H;
-  float* sDscl = sDgam + kPrepTB * H;
-  float* sPhi = sDscl + kPrepTB * H;   // [TB][H] sum_j dtheta tanh pi
-  float* sBias = sDadt;                // [TB][H] d dt_raw for the dt_bias partial; each
+  float* sDadt = sLam + kPrepTB * H;   // [TB][HS] incoming cotangents (t-major)
+  float* sDgam = sDadt + kPrepTB * HS;
+  float* sDscl = sDgam + kPrepTB * HS;
+  float* sPhi = sDscl + kPrepTB * HS;  // [TB][H] sum_j dtheta tanh pi
+  float* sBias = sDadt;                // [TB][HS] d dt_raw for the dt_bias partial; each
                                        // thread overwrites only entries it has read
   float* sT = sPhi + kPrepTB * H;      // [TB][Nr] tanh(angles)
   float* sAng = sT + kPrepTB * Nr;     // [TB][Nr] sum_h dtheta dt
@@ -432,9 +441,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     for (int u = 0; u < KU; ++u) {
       const int i = i0 + u * kPrepThreads, h = i / nt, t = i % nt;
       if (i < nh) {
-        sDadt[t * H + h] = va[u];
-        sDgam[t * H + h] = vg[u];
-        sDscl[t * H + h] = vs[u];
+        sDadt[t * HS + h] = va[u];
+        sDgam[t * HS + h] = vg[u];
+        sDscl[t * HS + h] = vs[u];
       }
     }
   }
@@ -569,9 +578,10 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     const float xa = vxa[u];
     const float apre = -heavy_tail_(xa);
     const float a = fminf(apre, -p.a_floor);
-    const float dadt = sDadt[i];
-    const float dgt = sDgam[i] + sDscl[i];
-    const float dsp = tg > 0 ? (t > 0 ? sDscl[i - H] : sDsPrev[h]) : 0.f;
+    const int ip = t * HS + h;   // in the padded tables
+    const float dadt = sDadt[ip];
+    const float dgt = sDgam[ip] + sDscl[ip];
+    const float dsp = tg > 0 ? (t > 0 ? sDscl[ip - HS] : sDsPrev[h]) : 0.f;
     const float ddt = dadt * a + dgt * lam + dsp * (1.f - lam) + sPhi[i] + vdd[u];
     const float dlam = dgt * dt - dsp * dt + vdl[u];
     // softplus'(x) = sigmoid(x), 1 above the threshold (torch: exp(x) / (exp(x) + 1))
@@ -591,13 +601,13 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     ddtr[(int64_t)tg * p.ddtr.st + h] = (RT)dx;
     dar[(int64_t)tg * p.dar.st + h] = (RT)dxa;
     dtrr[(int64_t)tg * p.dtrr.st + h] = (RT)dtrap;
-    sBias[i] = dx;
+    sBias[ip] = dx;
    }
   }
   __syncthreads();
   for (int h = tid; h < H; h += kPrepThreads) {
     float s = 0.f;
-    for (int t = 0; t < nt; ++t) s += sBias[t * H + h];
+    for (int t = 0; t < nt; ++t) s += sBias[t * HS + h];
     p.bias_part[((int64_t)b * p.nblk + blk) * H + h] = s;
   }
 }
