@@ -233,90 +233,63 @@ prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
   }
 }
 
-// phi for one (batch element, block of 64 tokens): each wave takes one head at a time,
-// so a store instruction covers whole rows of one head's contiguous (t, Nr) slab. Lane
-// (row group rg, column quad q) owns RPL consecutive rows of that quad: a first pass
-// sums them, a shuffle scan over the row groups of the column gives each lane's
-// exclusive prefix, a second pass writes the running sum wrapped to [0, 2 pi) -- every
-// row into phi, and/or, into strips, the sum before each row whose index is a multiple
-// of 16 (the angle entering that 16-token strip). The block's tanh(angles) pi rows,
-// shared by the heads, are staged in LDS once.
+// phi for one (batch element, block of 64 tokens): one thread per (head, group of 4
+// angles) walks the block's rows in order with its running angle in registers, starting
+// from the block's carry. The tanh(angles) pi rows (shared by the heads) are LDS
+// broadcasts; every head's dt row is staged in LDS in one coalesced pass, with a padded
+// stride so that lanes of different heads read distinct banks. It writes each row
+// wrapped to [0, 2 pi) into phi, and/or, into strips, the angle before each row whose
+// index is a multiple of 16 (the angle entering that 16-token strip).
 __global__ void __launch_bounds__(kPrepThreads) prep_phi_kernel(const PrepFwdParams p) {
-  extern __shared__ float sT[];   // [kPrepTB][Nr]
+  extern __shared__ float sm[];
   const int H = p.H, Nr = p.Nr, L = p.L;
   const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * kPrepTB;
   const int nt = min(kPrepTB, L - t0);
+  constexpr int DS = kPrepTB + 1;
+  float* sT = sm;                   // [kPrepTB][Nr]
+  float* sD = sT + kPrepTB * Nr;    // [H][DS]
   const float* trow = p.tpi + ((int64_t)b * L + t0) * Nr;
   for (int i = tid; i < nt * Nr; i += kPrepThreads) sT[i] = trow[i];
+  for (int i = tid; i < H * kPrepTB; i += kPrepThreads) {
+    const int h = i / kPrepTB, t = i % kPrepTB;
+    sD[h * DS + t] = t < nt ? p.dt[((int64_t)b * H + h) * L + t0 + t] : 0.f;
+  }
   __syncthreads();
   const int J4 = (Nr + 3) / 4;
-  const int RG = 64 / J4;                      // row groups per wave (J4 <= 64)
-  const int RPL = (kPrepTB + RG - 1) / RG;     // consecutive rows per lane
-  const int lane = tid & 63, wave = tid >> 6;
-  const bool act = lane < RG * J4;
-  const int rg = act ? lane / J4 : 0, j0 = act ? 4 * (lane % J4) : 0;
-  const int r0 = rg * RPL;
-  for (int h = wave; h < H; h += kPrepThreads / 64) {
+  for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
+    const int h = pr / J4, j0 = 4 * (pr % J4);
     const int64_t bh = (int64_t)b * H + h;
-    const float* dtrow = p.dt + bh * L + t0;
-    f32x4 tot = {0.f, 0.f, 0.f, 0.f};
-    // this lane's rows in runs of 8, each run's dt loaded together before use
-    constexpr int RUN = 8;
-    for (int i0 = 0; i0 < RPL; i0 += RUN) {
-      float d8[RUN];
-#pragma unroll
-      for (int u = 0; u < RUN; ++u) d8[u] = dtrow[min(r0 + i0 + u, nt - 1)];
-#pragma unroll
-      for (int u = 0; u < RUN; ++u) {
-        const int t = r0 + i0 + u;
-        if (act && i0 + u < RPL && t < nt) {
-          const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) tot[c] += tp[c] * d8[u];
-        }
-      }
-    }
-    f32x4 incl = tot;
-    for (int off = 1; off < RG; off <<= 1) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float o = __shfl_up(incl[c], off * J4, 64);
-        if (rg >= off) incl[c] += o;
-      }
-    }
-    if (!act) continue;
     f32x4 run = ld_quad(p.tot + (((int64_t)b * p.nblk + blk) * H + h) * Nr, j0, Nr);
     f32x4 init = {0.f, 0.f, 0.f, 0.f};
     if (p.phi_init) init = ld_quad(p.phi_init + bh * Nr, j0, Nr);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) run[c] += incl[c] - tot[c];
     float* prow = p.phi ? p.phi + (bh * L + t0) * Nr : nullptr;
-    for (int i0 = 0; i0 < RPL; i0 += RUN) {
-      float d8[RUN];
+    float* srow = p.strips ? p.strips + (bh * (L >> 4) + (t0 >> 4)) * Nr : nullptr;
+    const float* drow = sD + h * DS;
+    auto row = [&](int t) {
+      if (srow && (t & 15) == 0) {   // t0 is a multiple of 16
+        f32x4 enter;
 #pragma unroll
-      for (int u = 0; u < RUN; ++u) d8[u] = dtrow[min(r0 + i0 + u, nt - 1)];
-#pragma unroll
-      for (int u = 0; u < RUN; ++u) {
-        const int t = r0 + i0 + u;
-        if (i0 + u < RPL && t < nt) {
-          const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
-          if (p.strips && ((t0 + t) & 15) == 0) {
-            f32x4 enter;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) enter[c] = wrap_(run[c] + init[c]);
-            st_quad(p.strips + (bh * (L >> 4) + ((t0 + t) >> 4)) * Nr, j0, Nr, enter);
-          }
-          f32x4 out;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            run[c] += tp[c] * d8[u];
-            out[c] = wrap_(run[c] + init[c]);
-          }
-          if (prow) st_quad(prow + t * Nr, j0, Nr, out);
-          if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
-        }
+        for (int c = 0; c < 4; ++c) enter[c] = wrap_(run[c] + init[c]);
+        st_quad(srow + (t >> 4) * Nr, j0, Nr, enter);
       }
+      const f32x4 tp = ld_quad(sT + t * Nr, j0, Nr);
+      const float d = drow[t];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) run[c] += tp[c] * d;
+      if (prow || t0 + t == L - 1) {
+        f32x4 out;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) out[c] = wrap_(run[c] + init[c]);
+        if (prow) st_quad(prow + t * Nr, j0, Nr, out);
+        if (t0 + t == L - 1) st_quad(p.phi_final + bh * Nr, j0, Nr, out);
+      }
+    };
+    if (nt == kPrepTB) {   // whole blocks: a fixed trip count
+#pragma unroll 8
+      for (int t = 0; t < kPrepTB; ++t) row(t);
+    } else {
+      for (int t = 0; t < nt; ++t) row(t);
     }
   }
 }
@@ -711,7 +684,8 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
   hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
                      dim3(kPrepThreads), 0, s, p.tot, nullptr, nullptr, B, hn, nblk, 0);
   if ((rc = launch_status("m3s_prep_fwd"))) return rc;
-  hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads), (size_t)kPrepTB * Nr * 4, s, p);
+  hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads),
+                     (size_t)(kPrepTB * Nr + H * (kPrepTB + 1)) * 4, s, p);
   return launch_status("m3s_prep_fwd");
 }
 
