@@ -213,24 +213,26 @@ prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
   if (idx >= (int64_t)B * HN) return;
   const int64_t b = idx / HN, r = idx % HN;
   float* base = tot + b * nblk * HN + r;
-  if (!reverse) {
-    float run = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < nblk; ++k) {
-      const float q = base[(int64_t)k * HN];
-      base[(int64_t)k * HN] = run;
-      run += q;
+  // blocks in groups of G: a group's loads are all issued before its stores, so the walk
+  // pays one memory latency per group instead of one per block (each store could alias
+  // the next load as far as the compiler knows)
+  constexpr int G = 16;
+  float run = reverse ? (init ? init[idx] : 0.f) : 0.f;
+  for (int k0 = 0; k0 < nblk; k0 += G) {
+    float q[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int k = reverse ? nblk - 1 - (k0 + u) : k0 + u;
+      q[u] = (k0 + u < nblk) ? base[(int64_t)k * HN] : 0.f;
     }
-  } else {
-    float run = init ? init[idx] : 0.f;
-#pragma unroll 8
-    for (int k = nblk - 1; k >= 0; --k) {
-      const float q = base[(int64_t)k * HN];
-      base[(int64_t)k * HN] = run;
-      run += q;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int k = reverse ? nblk - 1 - (k0 + u) : k0 + u;
+      if (k0 + u < nblk) base[(int64_t)k * HN] = run;
+      run += q[u];
     }
-    if (total) total[idx] = run;
   }
+  if (reverse && total) total[idx] = run;
 }
 
 // phi for one (batch element, block of 64 tokens): one thread per (head, group of 4
