@@ -38,6 +38,26 @@ constexpr int kPrepTB = 64;  // tokens per block of prep_bwd_kernel
 template <typename RT>
 __device__ __forceinline__ float ldr(const RT* base, int64_t i) { return (float)base[i]; }
 
+// n / d and n % d for 0 <= n < 2^20 by a divisor d known only at run time, without an
+// integer division (a software routine on the GPU): a float estimate of the quotient
+// (relative error below 2^-21, so off by at most one in this range), then one correction.
+struct DivMod {
+  int d;
+  float inv;
+  __device__ explicit DivMod(int d_) : d(d_), inv(__builtin_amdgcn_rcpf((float)d_)) {}
+  __device__ __forceinline__ void operator()(int n, int& q, int& r) const {
+    q = (int)((float)n * inv);
+    r = n - q * d;
+    if (r < 0) {
+      --q;
+      r += d;
+    } else if (r >= d) {
+      ++q;
+      r -= d;
+    }
+  }
+};
+
 __device__ __forceinline__ float softplus_(float x) {
   return x > 20.f ? x : log1pf(expf(x));
 }
@@ -126,13 +146,17 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   // KU items per thread per round, every load of a round issued before any use: one
   // memory latency per round instead of one per item
   constexpr int KU = 4;
+  const DivMod byH(H), byNr(Nr > 0 ? Nr : 1), byNt(nt);
   const int n1 = nt1 * H;
   for (int i0 = tid; i0 < n1; i0 += KU * kPrepThreads) {
     float vd[KU], vl[KU], va[KU], vb[KU];
+    int kk[KU];
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int i = min(i0 + u * kPrepThreads, n1 - 1);
-      const int t = i / H, h = i % H;
+      int t, h;
+      byH(i, t, h);
+      kk[u] = t * HS + h;
       const int64_t tg = t0 + t;
       vd[u] = ldr(dtr, tg * p.dtr.st + h);
       vl[u] = ldr(tr, tg * p.tr.st + h);
@@ -143,7 +167,7 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
     for (int u = 0; u < KU; ++u) {
       const int i = i0 + u * kPrepThreads;
       if (i < n1) {
-        const int k = (i / H) * HS + i % H;
+        const int k = kk[u];
         sDt[k] = softplus_(vd[u] + vb[u]);
         sLam[k] = sigmoid_(vl[u]);
         sA[k] = fminf(-heavy_tail_(va[u]), -p.a_floor);
@@ -156,7 +180,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int i = min(i0 + u * kPrepThreads, n2 - 1);
-      vg[u] = ldr(ang, (int64_t)(t0 + i / Nr) * p.ang.st + i % Nr);
+      int t, j;
+      byNr(i, t, j);
+      vg[u] = ldr(ang, (int64_t)(t0 + t) * p.ang.st + j);
     }
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
@@ -170,7 +196,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
   }
   __syncthreads();
   for (int i = tid; i < H * nt; i += kPrepThreads) {  // (h, t) order: (b, h) rows
-    const int h = i / nt, t = i % nt;
+    int h, t;
+    byNt(i, h, t);
     const int k = t * HS + h;
     const float dt = sDt[k], lam = sLam[k];
     const float nxt = (t0 + t + 1 < L) ? sDt[k + HS] * (1.f - sLam[k + HS]) : 0.f;
@@ -382,12 +409,15 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   // ---- stage: recomputed dt / lambda, incoming cotangents, tanh table -------------
   // (KU items per thread per round, every load of a round issued before any use)
   constexpr int KU = 4;
+  const DivMod byH(H), byNr(Nr > 0 ? Nr : 1), byNt(nt);
   const int nh = nt * H;
   for (int i0 = tid; i0 < nh; i0 += KU * kPrepThreads) {
     float vd[KU], vl[KU], vb[KU];
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      const int i = min(i0 + u * kPrepThreads, nh - 1), t = i / H, h = i % H;
+      const int i = min(i0 + u * kPrepThreads, nh - 1);
+      int t, h;
+      byH(i, t, h);
       vd[u] = ldr(dtr, (int64_t)(t0 + t) * p.dtr.st + h);
       vl[u] = ldr(tr, (int64_t)(t0 + t) * p.tr.st + h);
       vb[u] = p.dt_bias[h];
@@ -404,9 +434,13 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   }
   for (int i0 = tid; i0 < nh; i0 += KU * kPrepThreads) {  // (h, t) order: coalesced reads
     float va[KU], vg[KU], vs[KU];
+    int kk[KU];
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      const int i = min(i0 + u * kPrepThreads, nh - 1), h = i / nt, t = i % nt;
+      const int i = min(i0 + u * kPrepThreads, nh - 1);
+      int h, t;
+      byNt(i, h, t);
+      kk[u] = t * HS + h;
       const int64_t g = ((int64_t)b * H + h) * L + t0 + t;
       va[u] = p.dadt ? p.dadt[g] : 0.f;
       vg[u] = p.dgamma ? p.dgamma[g] : 0.f;
@@ -414,11 +448,11 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
     }
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      const int i = i0 + u * kPrepThreads, h = i / nt, t = i % nt;
+      const int i = i0 + u * kPrepThreads;
       if (i < nh) {
-        sDadt[t * HS + h] = va[u];
-        sDgam[t * HS + h] = vg[u];
-        sDscl[t * HS + h] = vs[u];
+        sDadt[kk[u]] = va[u];
+        sDgam[kk[u]] = vg[u];
+        sDscl[kk[u]] = vs[u];
       }
     }
   }
@@ -430,7 +464,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int i = min(i0 + u * kPrepThreads, nj - 1);
-      vg[u] = ldr(ang, (int64_t)(t0 + i / Nr) * p.ang.st + i % Nr);
+      int t, j;
+      byNr(i, t, j);
+      vg[u] = ldr(ang, (int64_t)(t0 + t) * p.ang.st + j);
     }
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
@@ -505,7 +541,9 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
         }
         __syncthreads();
         for (int e = tid; e < kPrepRun * Nr; e += kPrepThreads) {
-          const int u = e / Nr, j = e % Nr, t = tr - u;
+          int u, j;
+          byNr(e, u, j);
+          const int t = tr - u;
           if (t >= 0) {
             float acc = sAng[t * Nr + j];
 #pragma unroll
@@ -521,7 +559,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   if (Nr > 0) {
     RT* dang = static_cast<RT*>(p.dang.p) + b * p.dang.sb;
     for (int i = tid; i < nt * Nr; i += kPrepThreads) {
-      const int t = i / Nr, j = i % Nr;
+      int t, j;
+      byNr(i, t, j);
       const float tq = sT[i];
       dang[(int64_t)(t0 + t) * p.dang.st + j] = (RT)(sAng[i] * kPiF * (1.f - tq * tq));
     }
@@ -535,7 +574,10 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
    float vx[KU], vxa[KU], vdd[KU], vdl[KU];
 #pragma unroll
    for (int u = 0; u < KU; ++u) {
-    const int i = min(i0 + u * kPrepThreads, nh - 1), t = i / H, h = i % H, tg = t0 + t;
+    const int i = min(i0 + u * kPrepThreads, nh - 1);
+    int t, h;
+    byH(i, t, h);
+    const int tg = t0 + t;
     const int64_t g = ((int64_t)b * H + h) * L + tg;
     vx[u] = ldr(dtr, (int64_t)tg * p.dtr.st + h) + p.dt_bias[h];
     vxa[u] = ldr(ar, (int64_t)tg * p.ar.st + h);
@@ -546,7 +588,8 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
    for (int u = 0; u < KU; ++u) {
     const int i = i0 + u * kPrepThreads;
     if (i >= nh) break;
-    const int t = i / H, h = i % H;
+    int t, h;
+    byH(i, t, h);
     const int tg = t0 + t;
     const float dt = sDt[i], lam = sLam[i];
     const float x = vx[u];
