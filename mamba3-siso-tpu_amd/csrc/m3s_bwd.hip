@@ -1772,24 +1772,28 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   }
 }
 
-// dq[b, t, :] = sum_h du[b, h, t, :] (and dk from dw): one thread per 4 consecutive
-// elements of a (b, t) row, summing over heads in f32. Bandwidth-bound.
+// dq[b, t, :] = sum_h du[b, h, t, :] (and dk from dw): one thread per 8 consecutive
+// elements of a (b, t) row (LN is a multiple of 8), summing over heads in f32, heads in
+// order. Bandwidth-bound; the rows are read once, so the loads are non-temporal.
 template <typename MT>
 __global__ void __launch_bounds__(256) headsum_kernel(const MT* __restrict__ part,
                                                       float* __restrict__ dq,
                                                       float* __restrict__ dk, int B, int H,
                                                       int64_t LN) {
-  const int64_t i4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  const int64_t i8 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   const int which = blockIdx.y;           // 0: dq from du, 1: dk from dw
   const int b = blockIdx.z;
-  if (i4 >= LN) return;
-  const MT* src = part + ((int64_t)which * B + b) * H * LN + i4;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (i8 >= LN) return;
+  const MT* src = part + ((int64_t)which * B + b) * H * LN + i8;
+  f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
   for (int h = 0; h < H; ++h) {
-    const sub_t<MT> v = *reinterpret_cast<const sub_t<MT>*>(src + h * LN);
-    acc += sub_to_f32<MT>(v);
+    const sub_t<MT>* row = reinterpret_cast<const sub_t<MT>*>(src + h * LN);
+    lo += sub_to_f32<MT>(__builtin_nontemporal_load(row));
+    hi += sub_to_f32<MT>(__builtin_nontemporal_load(row + 1));
   }
-  *reinterpret_cast<f32x4*>((which ? dk : dq) + (int64_t)b * LN + i4) = acc;
+  float* dst = (which ? dk : dq) + (int64_t)b * LN + i8;
+  *reinterpret_cast<f32x4*>(dst) = lo;
+  *reinterpret_cast<f32x4*>(dst + 4) = hi;
 }
 
 // Every per-(b, h) stream of bwd_bf16_kernel must be addressable with 31-bit byte
@@ -1827,7 +1831,8 @@ static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   int32_t rc = launch_status("m3s_bwd");
   if (rc != M3S_OK) return rc;
   const int64_t LN = (int64_t)prm.L * N;
-  const dim3 hgrid((unsigned)((LN / 4 + 255) / 256), 2, prm.B);
+  static_assert(N % 8 == 0, "head sum threads take 8 elements");
+  const dim3 hgrid((unsigned)((LN / 8 + 255) / 256), 2, prm.B);
   hipLaunchKernelGGL((headsum_kernel<MT>), hgrid, dim3(256), 0, stream,
                      static_cast<const MT*>(prm.part), prm.dq, prm.dk, prm.B, prm.H, LN);
   return launch_status("m3s_bwd (head sum)");
