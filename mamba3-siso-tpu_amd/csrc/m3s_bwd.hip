@@ -932,6 +932,9 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   constexpr int LDQ = F::LDQ, LDP = F::LDP, LDF = F::LDF;
   constexpr int PB = F::PB, NB = F::NB, CB = F::CB, SPW = F::SPW;
 
+  // half of each XCD's workgroups start ~28 K cycles (about half of phase R plus the
+  // staging) late: at B=8 L=8192 H=32 that took the backward from 1.667 to 1.614 ms
+  if (p.nc >= 16) stagger_start(blockIdx.x, 2, 14);
   __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
   auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
   bf16* sQ = reinterpret_cast<bf16*>(smem);                                        // q~ [t][n]

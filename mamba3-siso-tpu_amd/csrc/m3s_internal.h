@@ -48,6 +48,18 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return (nwg % 8 == 0) ? (bid % 8) * (nwg / 8) + bid / 8 : bid;
 }
 
+// Staggered start for the sequential scans. Their workgroups start together and run the
+// same per-chunk phase sequence at the same pace, so the memory-heavy phases of all of
+// them coincide and queue on HBM while the other phases leave it idle. Delaying a share
+// of each XCD's workgroups (block i runs on XCD i % 8, so i / 8 counts within one XCD)
+// by a fraction of a chunk's time spreads that traffic over the chunk: group
+// g = (i / 8) % groups (groups a power of two) first sleeps g * units * ~2048 cycles
+// (s_sleep 32 is 32 * 64 cycles). The cost is that delay, once.
+__device__ __forceinline__ void stagger_start(int bid, int groups, int units) {
+  const int g = (bid >> 3) & (groups - 1);
+  for (int i = 0; i < g * units; ++i) __builtin_amdgcn_s_sleep(32);
+}
+
 }  // namespace m3s
 
 namespace m3s {
