@@ -213,14 +213,17 @@ def main():
                 "traffic_source": TRAFFIC_SOURCE, "algorithmic_bytes": scan_bytes,
                 "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5)}
         if args.leg in ("all", "bwd"):
+            # the training path's pair: with gradients the layer materialises phi and both
+            # scans read it (phi_in_kernel=None)
+            kr = dict(ka, phi=phi_full)
             with torch.no_grad():
-                y, fs, fk, fv, res = K.siso_forward(**ka, chunk=128, save_residuals=True)
+                y, fs, fk, fv, res = K.siso_forward(**kr, chunk=128, save_residuals=True)
                 dyk = torch.randn(y.shape, generator=gen.manual_seed(2), device=dev
                                   ).to(torch.bfloat16)
                 bw = lambda: K.siso_backward_kernel(  # noqa: E731
-                    dyk, res.ybar, ka["z"], ka["q"], ka["k"], ka["v"], ka["adt"], ka["gamma"],
-                    ka["scale"], ka["phi"], ka["q_bias"], ka["k_bias"], res.chunk_states,
-                    d_skip=ka["d_skip"], chunk=128)
+                    dyk, res.ybar, kr["z"], kr["q"], kr["k"], kr["v"], kr["adt"], kr["gamma"],
+                    kr["scale"], kr["phi"], kr["q_bias"], kr["k_bias"], res.chunk_states,
+                    d_skip=kr["d_skip"], chunk=128)
                 for _ in range(max(3, args.warmup)):
                     bw()
                 bwd_ms = gpu_time_ms(bw, max(10, args.steps // 2), torch)
@@ -237,12 +240,13 @@ def main():
             line.update(bwd_kernel_ms=round(bwd_ms, 4),
                         bwd_kernel_tflops=round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2))
             line["bwd_roofline"] = {
-                "kernel": "bwd_bf16_kernel<128,128,64> + headsum_kernel (m3s_bwd)",
+                "kernel": "bwd_bf16_kernel<128,128,64,false> + headsum_kernel (m3s_bwd, phi "
+                          "read: the training path's backward)",
                 "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
                 "algorithmic_bytes": bwd_bytes,
                 "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 5)}
-            del y, res, dyk
+            del y, res, dyk, kr
         del ka, kc, phi_full
         torch.cuda.empty_cache()
         if args.leg != "all":
@@ -295,8 +299,10 @@ def main():
     dy = torch.randn(B, L, DM, generator=gen.manual_seed(2), device=dev).to(torch.bfloat16)
 
     def fwdbwd_step():
+        # the gradients of u and of every parameter, returned (as jax.grad does) rather
+        # than accumulated into .grad, which would add one add kernel per tensor
         y, _ = m3.mamba3_siso_layer(pg, ug, cfg)
-        y.backward(dy)
+        return torch.autograd.grad(y, (ug, *pg), dy)
 
     for _ in range(2):
         fwdbwd_step()
