@@ -336,6 +336,31 @@ typedef struct m3s_rms_args {
   void* workspace;      /* backward scratch, m3s_rms_bwd_workspace_bytes() bytes */
 } m3s_rms_args;
 
+/* The optimizer update of the LM training step. Replaces optax
+ * chain(clip_by_global_norm, adamw) of the reference's training step (train.py:799-805)
+ * once the global gradient norm is known: for each of `count` float32 tensors, in place,
+ * one pass, per element (s = *grad_scale, the clip factor, or 1 when grad_scale is NULL):
+ *   g = grad s;  m = m + one_minus_beta1 (g - m);  v = beta2 v + one_minus_beta2 g^2;
+ *   p = p param_decay - step_size m / (sqrt(v) / bias_correction2_sqrt + eps)
+ * For update t >= 1 with learning rate lr: param_decay = 1 - lr weight_decay, step_size =
+ * lr / (1 - beta1^t), bias_correction2_sqrt = sqrt(1 - beta2^t); the caller forms these
+ * scalars (and the complements of the betas) in double precision, as a framework's
+ * scalar arguments are, so that none of them loses digits to a float32 subtraction. The
+ * five arrays are host arrays of `count` entries; each tensor is dense and 4-byte
+ * aligned (16-byte aligned buffers take 16-byte vectors). */
+typedef struct m3s_adamw_args {
+  int32_t struct_size;        /* sizeof(m3s_adamw_args) */
+  int32_t count;              /* tensors */
+  float* const* params;       /* [count] parameter buffers, updated */
+  const float* const* grads;  /* [count] gradients */
+  float* const* exp_avg;      /* [count] first moments m, updated */
+  float* const* exp_avg_sq;   /* [count] second moments v, updated */
+  const int64_t* numel;       /* [count] elements of each tensor */
+  const float* grad_scale;    /* device scalar multiplying every gradient, or NULL */
+  float one_minus_beta1, beta2, one_minus_beta2, eps;
+  float param_decay, step_size, bias_correction2_sqrt;
+} m3s_adamw_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -390,6 +415,7 @@ int32_t m3s_swiglu_fwd(const m3s_swiglu_args* args, void* stream);
 int32_t m3s_swiglu_bwd(const m3s_swiglu_args* args, void* stream);
 int32_t m3s_rms_fwd(const m3s_rms_args* args, void* stream);
 int32_t m3s_rms_bwd(const m3s_rms_args* args, void* stream);
+int32_t m3s_adamw(const m3s_adamw_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -167,13 +167,23 @@ class RmsArgs(C.Structure):
     ]
 
 
+class AdamwArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32), ("count", i32), ("params", vp), ("grads", vp),
+        ("exp_avg", vp), ("exp_avg_sq", vp), ("numel", vp), ("grad_scale", vp),
+        ("one_minus_beta1", C.c_float), ("beta2", C.c_float), ("one_minus_beta2", C.c_float),
+        ("eps", C.c_float), ("param_decay", C.c_float), ("step_size", C.c_float),
+        ("bias_correction2_sqrt", C.c_float),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
            "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes",
-           "m3s_norm_bwd_noalloc")
+           "m3s_norm_bwd_noalloc", "m3s_adamw")
 
 _lib = None
 
@@ -230,6 +240,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     for fn in (lib.m3s_swiglu_fwd, lib.m3s_swiglu_bwd):
         fn.restype = i32
         fn.argtypes = [C.POINTER(SwigluArgs), vp]
+    lib.m3s_adamw.restype = i32
+    lib.m3s_adamw.argtypes = [C.POINTER(AdamwArgs), vp]
     ver = lib.m3s_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")

@@ -786,6 +786,54 @@ def bcnorm_backward(xs, weights, rstds, dys, dxs):
     return dws
 
 
+def adamw_update(params, grads, exp_avg, exp_avg_sq, lr: float, beta1: float, beta2: float,
+                 eps: float, weight_decay: float, count: int,
+                 grad_scale: Optional[Tensor] = None) -> None:
+    """Update number ``count`` (>= 1) of clip-then-AdamW over lists of dense float32
+    device tensors, in place, one ``m3s_adamw`` pass (optax ``chain(clip_by_global_norm,
+    adamw)``, ``train.py:799-805``, after the global norm). ``grad_scale``: a float32
+    device scalar multiplying every gradient (the clip factor), or None."""
+    n = len(params)
+    if not (len(grads) == len(exp_avg) == len(exp_avg_sq) == n):
+        raise ValueError("adamw_update: the four tensor lists must have equal length")
+    if count < 1:
+        raise ValueError("adamw_update: the update count starts at 1")
+    dev = None
+    for group in (params, grads, exp_avg, exp_avg_sq):
+        for t in group:
+            if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("adamw_update: every tensor must be a dense float32 device tensor")
+            if dev is None:
+                dev = t.device
+            if t.device != dev:
+                raise ValueError("adamw_update: tensors on different devices")
+    for p, g, m, v in zip(params, grads, exp_avg, exp_avg_sq):
+        if not (p.shape == g.shape == m.shape == v.shape):
+            raise ValueError("adamw_update: a parameter, its gradient and moments differ in shape")
+    if grad_scale is not None and (not grad_scale.is_cuda or grad_scale.dtype != torch.float32
+                                   or grad_scale.numel() != 1 or grad_scale.device != dev):
+        raise ValueError("adamw_update: grad_scale must be a float32 device scalar")
+    if n == 0:
+        return
+    ptrs = ctypes.c_void_p * n
+    a = _lib.AdamwArgs()
+    a.struct_size = ctypes.sizeof(_lib.AdamwArgs)
+    a.count = n
+    arrays = [ptrs(*[t.data_ptr() for t in group])
+              for group in (params, grads, exp_avg, exp_avg_sq)]
+    numel = (ctypes.c_int64 * n)(*[t.numel() for t in params])
+    a.params, a.grads, a.exp_avg, a.exp_avg_sq = [ctypes.cast(x, ctypes.c_void_p) for x in arrays]
+    a.numel = ctypes.cast(numel, ctypes.c_void_p)
+    a.grad_scale = grad_scale.data_ptr() if grad_scale is not None else None
+    # every scalar formed in double precision (as a framework passes Python scalars)
+    a.one_minus_beta1, a.beta2, a.one_minus_beta2 = 1.0 - beta1, beta2, 1.0 - beta2
+    a.eps, a.param_decay = eps, 1.0 - lr * weight_decay
+    a.step_size = lr / (1.0 - beta1 ** count)
+    a.bias_correction2_sqrt = math.sqrt(1.0 - beta2 ** count)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_adamw(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_adamw")
+
+
 def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
     """LM block norm: ``x`` (..., D) in f32 or bf16 -> ``(y (..., D) in out_dtype, rstd
     (...,) f32)`` with ``y = x rstd w``, ``rstd = 1/sqrt(mean(x^2) + eps)`` in f32 (one

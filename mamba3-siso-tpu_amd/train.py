@@ -28,6 +28,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from . import kernels as K
 from . import model as M
 
 Tensor = torch.Tensor
@@ -144,11 +145,23 @@ class AdamW:
         if any(g is None for g in grads):
             raise ValueError("a parameter has no gradient")
         grads = [g if g.dtype == p.dtype else g.to(p.dtype) for g, p in zip(grads, self.params)]
-        if self.clip is not None:
-            self.last_norm = clip_by_global_norm_(grads, self.clip)
         lr = float(self.schedule(self.count))
         self.count += 1
         t = self.count
+        if all(p.is_cuda and p.dtype == torch.float32 for p in self.params):
+            # device float32 (the master weights): the clip factor stays on the device and
+            # the update is one m3s_adamw pass over every tensor
+            scale = None
+            if self.clip is not None:
+                norm = global_norm(grads)
+                self.last_norm = norm
+                scale = torch.where(norm < self.clip, torch.ones_like(norm),
+                                    self.clip / norm).float()
+            K.adamw_update(self.params, [g.contiguous() for g in grads], self.mu, self.nu,
+                           lr, self.b1, self.b2, self.eps, self.weight_decay, t, scale)
+            return
+        if self.clip is not None:
+            self.last_norm = clip_by_global_norm_(grads, self.clip)
         torch._foreach_lerp_(self.mu, grads, 1.0 - self.b1)
         torch._foreach_mul_(self.nu, self.b2)
         torch._foreach_addcmul_(self.nu, grads, grads, value=1.0 - self.b2)

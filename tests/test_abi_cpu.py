@@ -61,6 +61,8 @@ int main(void) {
          offsetof(m3s_swiglu_args, dh));
   printf("%zu %zu %zu\n", sizeof(m3s_rms_args), offsetof(m3s_rms_args, x),
          offsetof(m3s_rms_args, workspace));
+  printf("%zu %zu %zu\n", sizeof(m3s_adamw_args), offsetof(m3s_adamw_args, grad_scale),
+         offsetof(m3s_adamw_args, bias_correction2_sqrt));
   return 0;
 }
 """
@@ -88,8 +90,10 @@ int main(void) {
                             lib.TransposeArgs.out.offset]
     assert sizes[25:28] == [ctypes.sizeof(lib.SwigluArgs), lib.SwigluArgs.rows.offset,
                             lib.SwigluArgs.dh.offset]
-    assert sizes[28:] == [ctypes.sizeof(lib.RmsArgs), lib.RmsArgs.x.offset,
-                          lib.RmsArgs.workspace.offset]
+    assert sizes[28:31] == [ctypes.sizeof(lib.RmsArgs), lib.RmsArgs.x.offset,
+                            lib.RmsArgs.workspace.offset]
+    assert sizes[31:] == [ctypes.sizeof(lib.AdamwArgs), lib.AdamwArgs.grad_scale.offset,
+                          lib.AdamwArgs.bias_correction2_sqrt.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -277,3 +281,31 @@ def test_rms_arguments_are_checked_without_a_launch(lib):
     assert b"aligned" in h.m3s_last_error()
     a.rows = 0
     assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.OK
+
+
+def test_adamw_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_adamw(None, None) == lib.ERR_INVALID
+    a = lib.AdamwArgs()
+    a.struct_size = 12
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"struct_size" in h.m3s_last_error()
+    a.struct_size = ctypes.sizeof(lib.AdamwArgs)
+    a.count = -1
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.ERR_INVALID
+    a.count = 0
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.OK   # nothing to update
+    a.count = 2
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.ERR_INVALID   # NULL arrays
+    assert b"NULL" in h.m3s_last_error()
+    ptrs = (ctypes.c_void_p * 2)(0x1000, 0x2000)
+    numel = (ctypes.c_int64 * 2)(4, -1)
+    for f in ("params", "grads", "exp_avg", "exp_avg_sq"):
+        setattr(a, f, ctypes.cast(ptrs, ctypes.c_void_p))
+    a.numel = ctypes.cast(numel, ctypes.c_void_p)
+    a.bias_correction2_sqrt = 0.0
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.ERR_INVALID   # update count 0
+    assert b"bias" in h.m3s_last_error()
+    a.bias_correction2_sqrt = 0.1
+    assert h.m3s_adamw(ctypes.byref(a), None) == lib.ERR_INVALID   # negative numel
+    assert b"numel" in h.m3s_last_error()
