@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 5
+#define M3S_ABI_VERSION 6
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -81,7 +81,8 @@ typedef struct m3s_fwd_args {
   const float* seed_v;                 /* (B, H, P), if has_seed                      */
   const float* seed_coef;              /* (B, H) = dt_0 (1 - lam_0), if has_seed      */
   m3s_bhlp y;                          /* out (B, H, L, P)                            */
-  float* ybar;                         /* out (B, H, L, P) pre-gate, if save_residuals */
+  void* ybar;                          /* out (B, H, L, P) pre-gate in `dtype`, if
+                                          save_residuals (the reference keeps it f32) */
   void* chunk_states;                  /* out (B, H, nc, N, P) state at each chunk start,
                                           stored N-major, if save_residuals           */
   float* final_ssm;                    /* out (B, H, P, N)                            */
@@ -99,7 +100,7 @@ typedef struct m3s_bwd_args {
   int32_t dtype;       /* dtype of dy, z, q, k, v, chunk_states, dv, dz */
   int32_t has_d, has_z;
   m3s_bhlp dy;                 /* (B, H, L, P) cotangent of the gated output           */
-  const float* ybar;           /* (B, H, L, P) from the forward                        */
+  const void* ybar;            /* (B, H, L, P) from the forward, in `dtype`            */
   m3s_bhlp z;                  /* (B, H, L, P), if has_z                               */
   const void* q;               /* (B, L, N)                                            */
   const void* k;               /* (B, L, N)                                            */

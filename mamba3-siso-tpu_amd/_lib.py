@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1

@@ -36,7 +36,7 @@ struct BwdParams {
   int has_d, has_z;
   const void* dy;
   int64_t dy_sb, dy_sh, dy_st;
-  const float* ybar;
+  const void* ybar;   // (B, H, L, P) in the matmul dtype
   const void* z;
   int64_t z_sb, z_sh, z_st;
   const void* q;
@@ -195,7 +195,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   const MT* zg = p.has_z ? static_cast<const MT*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
   MT* dzg = p.has_z ? static_cast<MT*>(p.dz) + b * p.dz_sb + h * p.dz_sh : nullptr;
   MT* dvg = static_cast<MT*>(p.dv) + b * p.dv_sb + h * p.dv_sh;
-  const float* ybg = p.ybar + bh * (int64_t)L * P;
+  const MT* ybg = static_cast<const MT*>(p.ybar) + bh * (int64_t)L * P;
   const float* adtg = p.adt + bh * L;
   const float* gamg = p.gamma + bh * L;
   const float* sclg = p.scale + bh * L;
@@ -256,8 +256,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
   vec rq[F::QKR][2][2], rk[F::QKR][2][2];
   f32x4 rphi[F::QKR][2][VEC / 4];
   float rscale[F::QKR][2];
-  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2];
-  f32x4 ryb[F::VR][2][VEC / 4];
+  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2], ryb[F::VR][2];
   vec rs[F::SR];
   float radt[F::E], rgam_s, rscl_s;
 
@@ -314,9 +313,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
           rdy[r][e] = *reinterpret_cast<const vec*>(dyg + t * p.dy_st + p0);
           if (zg) {
             rz[r][e] = *reinterpret_cast<const vec*>(zg + t * p.z_st + p0);
-#pragma unroll
-            for (int i = 0; i < VEC; i += 4)
-              ryb[r][e][i / 4] = *reinterpret_cast<const f32x4*>(ybg + t * P + p0 + i);
+            ryb[r][e] = *reinterpret_cast<const vec*>(ybg + t * P + p0);
           }
         }
       }
@@ -448,7 +445,7 @@ __global__ void __launch_bounds__(NW * 64) bwd_kernel(const BwdParams p) {
               const float zf = (float)rz[r][e][i];
               const float sg = sigmoidf_(zf);
               gv = dy * (zf * sg);
-              odz[i] = (MT)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
+              odz[i] = (MT)(dy * (float)ryb[r][e][i] * sg * (1.f + zf * (1.f - sg)));
             }
             dqk[e] += gv * (float)rv[r][e][i];
             og[i] = (MT)gv;
@@ -989,7 +986,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   const bf16* zg = p.has_z ? static_cast<const bf16*>(p.z) + b * p.z_sb + h * p.z_sh : nullptr;
   bf16* dzg = p.has_z ? static_cast<bf16*>(p.dz) + b * p.dz_sb + h * p.dz_sh : nullptr;
   bf16* dvg = static_cast<bf16*>(p.dv) + b * p.dv_sb + h * p.dv_sh;
-  const float* ybg = p.ybar + bh * (int64_t)L * P;
+  const bf16* ybg = static_cast<const bf16*>(p.ybar) + bh * (int64_t)L * P;
   // phi rows of this (b, h), or (phi_strips mode) the head-shared tanh(angles) pi rows of
   // batch element b with the same addressing, plus dt and the strips' entering angles
   const float* phig = STRIPS ? p.tht + (int64_t)b * L * Nr : p.phi + bh * (int64_t)L * Nr;
@@ -1006,7 +1003,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   const auto rZ = make_rsrc(zg, zg ? span(p.z_st) : 0u);
   // without z, ybar is not read: a zero-size descriptor makes its (unconditional) loads
   // return zeros, as it does for z
-  const auto rYb = make_rsrc(zg ? ybg : nullptr, zg ? (uint32_t)L * P * 4 : 0u);
+  const auto rYb = make_rsrc(zg ? ybg : nullptr, zg ? (uint32_t)L * P * 2 : 0u);
   // phi[t][j .. j+3] for j < Nr. With Nr % 4 == 0 (wave-uniform) every lane issues one
   // 16-byte load: a per-lane choice of load width would make the compiler drain the load
   // queue at the join.
@@ -1065,8 +1062,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
   float rpdt[F::QKR][2];             // phi_strips mode: dt of the two rows
   f32x4 rstr[STRIPS ? F::QKR : 1][VEC / 4];   // phi_strips mode: the strip's entering angles
   float rscale[F::QKR][2];
-  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2];
-  f32x4 ryb[F::VR][2][VEC / 4];
+  vec rv[F::VR][2], rdy[F::VR][2], rz[F::VR][2], ryb[F::VR][2];
   vec rs[F::SR];
   float radt[F::E], rgam_s, rscl_s;
 
@@ -1167,11 +1163,8 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
             rdy[r][e] = gld<vec>(dyg, (uint32_t)(c * C * p.dy_st * 2) + (uint32_t)(t * p.dy_st + p0) * 2);
             rz[r][e] = buf_load<vec>(rZ, (uint32_t)(t * p.z_st + p0) * 2, (uint32_t)(c * C * p.z_st * 2));
           }
-          if (part & 2) {
-#pragma unroll
-            for (int i = 0; i < VEC; i += 4)
-              ryb[r][e][i / 4] = buf_load<f32x4>(rYb, (uint32_t)(t * P + p0 + i) * 4, (uint32_t)c * C * P * 4);
-          }
+          if (part & 2)
+            ryb[r][e] = buf_load<vec>(rYb, (uint32_t)(t * P + p0) * 2, (uint32_t)c * C * P * 2);
         }
       }
     }
@@ -1254,7 +1247,7 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
                 const float zf = (float)rz[r][e][i];
                 const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zf * kLog2e));
                 gv = dy * (zf * sg);
-                odz[i] = (bf16)(dy * ryb[r][e][i / 4][i % 4] * sg * (1.f + zf * (1.f - sg)));
+                odz[i] = (bf16)(dy * (float)ryb[r][e][i] * sg * (1.f + zf * (1.f - sg)));
               }
               dqk[e] += gv * (float)rv[r][e][i];
               og[i] = (bf16)gv;

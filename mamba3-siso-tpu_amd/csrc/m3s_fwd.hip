@@ -54,7 +54,7 @@ struct FwdParams {
   const float* seed_coef;
   void* y;
   int64_t y_sb, y_sh, y_st;
-  float* ybar;
+  void* ybar;     // (B, H, L, P) in the matmul dtype
   void* cstates;
   float* fssm;
   float* fk;
@@ -523,10 +523,10 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
             for (int u = 0; u < 4; ++u) yb[i + u] = o[u] + coef * (float)cv[r][e][i + u];
           }
           if (p.save) {
-            float* dst = p.ybar + (bh * L + t0 + t) * (int64_t)P + p0;
+            vec ybv;
 #pragma unroll
-            for (int i = 0; i < VEC; i += 4)
-              *reinterpret_cast<f32x4*>(dst + i) = f32x4{yb[i], yb[i + 1], yb[i + 2], yb[i + 3]};
+            for (int i = 0; i < VEC; ++i) ybv[i] = (MT)yb[i];
+            *reinterpret_cast<vec*>(static_cast<MT*>(p.ybar) + (bh * L + t0 + t) * (int64_t)P + p0) = ybv;
           }
           vec yo;
 #pragma unroll
@@ -719,7 +719,8 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   const auto rV = make_rsrc(vg, (uint32_t)(((int64_t)(L - 1) * p.v_st + P) * 2));
   const auto rZ = make_rsrc(zg, zg ? (uint32_t)(((int64_t)(L - 1) * p.z_st + P) * 2) : 0u);
   const auto rY = make_rsrc(yg, (uint32_t)(((int64_t)(L - 1) * p.y_st + P) * 2));
-  const auto rYb = make_rsrc(p.save ? p.ybar + bh * L * (int64_t)P : nullptr, p.save ? (uint32_t)L * P * 4 : 0u);
+  const auto rYb = make_rsrc(p.save ? static_cast<bf16*>(p.ybar) + bh * L * (int64_t)P : nullptr,
+                             p.save ? (uint32_t)L * P * 2 : 0u);
   const auto rCs = make_rsrc(csg, p.save ? (uint32_t)nc * N * P * 2 : 0u);
 
   // ---- carried state: registers; wave owns tiles (pb_w, nb0 + NSTEP m) ------------
@@ -1284,10 +1285,10 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
             for (int u = 0; u < 4; ++u) yb[i + u] = o[u];
           }
           if (p.save) {
+            bf16x8 ybv;
 #pragma unroll
-            for (int i = 0; i < 8; i += 4)
-              buf_store(f32x4{yb[i], yb[i + 1], yb[i + 2], yb[i + 3]}, rYb,
-                        (uint32_t)(t * P + p0 + i) * 4, (uint32_t)t0 * P * 4);
+            for (int i = 0; i < 8; ++i) ybv[i] = (bf16)yb[i];
+            buf_store(ybv, rYb, (uint32_t)(t * P + p0) * 2, (uint32_t)t0 * P * 2);
           }
           bf16x8 zz;
           if (zg) zz = *reinterpret_cast<const bf16x8*>(sZ + vz_off(t, p0));

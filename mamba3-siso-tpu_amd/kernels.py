@@ -65,7 +65,10 @@ def _phi_fields(a, phi, dev) -> list:
 
 class ForwardResiduals(NamedTuple):
     """``kernel_fwd.py:41-52``. ``chunk_states`` is the logical ``(B, H, nc, P, N)``
-    view of an N-major ``(B, H, nc, N, P)`` buffer (the layout the backward reads)."""
+    view of an N-major ``(B, H, nc, N, P)`` buffer (the layout the backward reads).
+    ``ybar`` is in the policy's matmul dtype (bf16 under the bf16 policy; the reference
+    keeps it float32): the backward only uses it in ``dz``, where its bf16 rounding is far
+    inside the gradient tolerance, and it halves the residual's bytes."""
 
     ybar: Tensor
     chunk_states: Tensor
@@ -255,7 +258,7 @@ def siso_forward(
     final_k = torch.empty(batch, nheads, state_dim, **f32)
     final_v = torch.empty(batch, nheads, headdim, **f32)
     if save_residuals:
-        ybar = torch.empty(batch, nheads, seqlen, headdim, **f32)
+        ybar = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
         cstates = torch.empty(batch, nheads, nc, state_dim, headdim, device=dev, dtype=mt)
     else:
         ybar = cstates = None
@@ -545,7 +548,7 @@ def siso_backward_kernel(
             f"headdim={headdim}")
     dyc, zc, vc = _bhlp_operand(dy, mt), _bhlp_operand(z, mt), _bhlp_operand(v, mt)
     qc, kc = _mt(q, mt), _mt(k, mt)
-    ybc = _f32c(ybar)
+    ybc = _mt(ybar, mt)
     adt_c, gam_c, scl_c = _f32c(adt), _f32c(gamma), _f32c(scale)
     qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
     cs = _nmajor_states(chunk_states, mt)

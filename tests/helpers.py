@@ -6,8 +6,9 @@ Tolerances (stated once, used by every GPU test):
     (``tests.py:60-88``) <= 2e-5 for forward/decode outputs and <= 2e-4 for gradients
     (the reference's own bars, ``tests.py:533, 612``).
   * bf16 policy against the oracle's bf16 rounding model (the same rounding points as the
-    reference kernel): p95 <= 2e-3 for f32 outputs (ybar, state) and <= 5e-3 for outputs
-    stored in bf16 (one bf16 rounding is up to 2^-8 relative); elementwise, a bf16
+    reference kernel): p95 <= 2e-3 for f32 outputs (the state) and <= 5e-3 for outputs
+    stored in bf16 (y, and ybar, which the bf16 policy stores in bf16; one bf16 rounding
+    is up to 2^-8 relative); elementwise, a bf16
     output is within one bf16 ulp of |ref| plus 4e-3 max|ref| (the operand roundings of
     the products, which the model reproduces only up to accumulation order).
   * bf16 policy against the float64 maths:

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 5
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 6
 
 
 def test_struct_layouts_match_the_header(lib):

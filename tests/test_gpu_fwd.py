@@ -62,7 +62,7 @@ def test_forward_bf16_matches_rounding_model_and_maths(m3, chunk):
                                          save_residuals=True)
     assert y.dtype == BF16 and res.chunk_states.dtype == BF16
     # the kernel's own rounding model (reference kernel_fwd.py:133-187)
-    assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+    assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
     assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
     # the float64 maths
     assert_p95(y, yr, BF16_P95, "y")
@@ -82,7 +82,7 @@ def test_forward_bf16_other_shapes_and_no_gate(m3, n, chunk, gate):
     ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
     y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy="bf16",
                                          save_residuals=True)
-    assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+    assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
     assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
     # chunk states are stored in bf16: one more rounding of up to 2^-8 relative
     assert_p95(res.chunk_states, dbgm["chunk_states"], BF16_OUT_MODEL_P95, "chunk states vs bf16 model")
@@ -107,7 +107,7 @@ def test_forward_every_table_shape(m3, policy, n, p, chunk):
         assert_p95(res.chunk_states, dbg["chunk_states"], FWD_F32_P95, "chunk_states")
     else:
         ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
-        assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+        assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
         assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
         assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
         assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
@@ -137,11 +137,11 @@ def test_forward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
         assert_p95(y, cpu(base[0]), FWD_F32_P95, "y vs phi read")
     else:
         ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
-        assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model")
+        assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
         assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
         assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
         assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
-        assert_p95(res.ybar, cpu(base[4].ybar), BF16_MODEL_P95, "ybar vs phi read")
+        assert_p95(res.ybar, cpu(base[4].ybar), BF16_OUT_MODEL_P95, "ybar vs phi read")
     assert_p95(fk, sr.k, FWD_F32_P95, "final k")
     assert O.max_rel(cpu(fv), cpu(base[3])) == 0.0
 
@@ -152,7 +152,7 @@ def test_forward_bf16_with_carried_state(m3):
     ym, sm, dbgm = oracle_fwd(c, 128, with_seed=True, mm=BF16)
     y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=128, dtype_policy="bf16",
                                          save_residuals=True)
-    assert_p95(res.ybar, dbgm["ybar"], BF16_MODEL_P95, "ybar vs bf16 model (seeded)")
+    assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model (seeded)")
     assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model (seeded)")
     assert_maxrel(y, yr, BF16_MAXREL, "y (seeded)")
 
