@@ -229,10 +229,10 @@ def main():
                 bwd_ms = gpu_time_ms(bw, max(10, args.steps // 2), torch)
             bwd_flops = B * H * L * (2 * cfg.chunk * (3 * N + 2 * P) + 8 * P * N)
             # The backward's necessary bytes (no per-head rows): reads q, k (head-shared),
-            # v, z, dy bf16, ybar f32, adt/gamma/scale f32, phi f32, the chunk states
+            # v, z, dy, ybar bf16, adt/gamma/scale f32, phi f32, the chunk states
             # bf16; writes dv, dz bf16, dadt/dqk/dscale/uw f32, dphi f32, dq/dk f32.
             nc = L // cfg.chunk
-            bwd_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + B * H * L * P * 4
+            bwd_bytes = (2 * B * L * N * 2 + 4 * B * H * L * P * 2
                          + 3 * B * H * L * 4 + phi_read + B * H * nc * N * P * 2
                          + 2 * B * H * L * P * 2 + 4 * B * H * L * 4 + B * H * L * Nr * 4
                          + 2 * B * L * N * 4)
