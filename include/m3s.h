@@ -319,7 +319,12 @@ typedef struct m3s_swiglu_args {
  * rstd = 1 / sqrt(mean(x^2) + eps), y = (x rstd w) cast to y_dtype;
  * s = sum(dy w x), dx = rstd (dy w - x rstd^2 s / width) in x_dtype,
  * dw = sum over rows of dy x rstd, summed in a fixed order. Rows are dense and aligned to
- * 4 elements; width a multiple of 4, at most 4096. */
+ * 4 elements; width a multiple of 4, at most 4096.
+ * Residual form (the LM's residual add before each norm, model.py:222-228): with `add`
+ * (y_dtype) the forward normalises s = x + add, which it writes to `sum` (x_dtype), and
+ * `x` stays the stream row before the add; the backward's `x` is then that `sum`, and
+ * with `dsum` (x_dtype, the cotangent of s from the rest of the network) dx becomes
+ * dsum + the norm's pullback, also written to `dadd` (y_dtype) when given. */
 typedef struct m3s_rms_args {
   int32_t struct_size;  /* sizeof(m3s_rms_args) */
   int32_t x_dtype;      /* M3S_DTYPE_* of x and dx (the stream) */
@@ -335,6 +340,10 @@ typedef struct m3s_rms_args {
   void* dx;             /* backward out (rows, width) */
   float* dweight;       /* backward out (width) */
   void* workspace;      /* backward scratch, m3s_rms_bwd_workspace_bytes() bytes */
+  const void* add;      /* forward: residual added to x first (rows, width), or NULL */
+  void* sum;            /* forward out: x + add (rows, width), iff add */
+  const void* dsum;     /* backward: cotangent of the sum (rows, width), or NULL */
+  void* dadd;           /* backward out: dx again in y_dtype (rows, width), or NULL */
 } m3s_rms_args;
 
 /* The optimizer update of the LM training step. Replaces optax

@@ -163,7 +163,8 @@ class RmsArgs(C.Structure):
         ("struct_size", i32), ("x_dtype", i32), ("y_dtype", i32), ("width", i32),
         ("rows", i64), ("eps", C.c_float),
         ("x", vp), ("weight", vp), ("y", vp), ("rstd", vp), ("dy", vp), ("dx", vp),
-        ("dweight", vp), ("workspace", vp),
+        ("dweight", vp), ("workspace", vp), ("add", vp), ("sum", vp), ("dsum", vp),
+        ("dadd", vp),
     ]
 
 

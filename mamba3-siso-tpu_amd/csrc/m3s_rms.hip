@@ -13,6 +13,13 @@
 // the waves of a block in LDS, and leaves one partial row per block; a second launch sums
 // those in a fixed order, so dw does not depend on the order in which blocks finish.
 // HBM-bound.
+//
+// With a residual (`add`), the forward first forms the stream's next row s = x + add (in
+// f32, stored in x's dtype: the residual add of model.py:222-228 before the next norm)
+// and normalises s; the backward takes the cotangent the rest of the network gives s
+// (`dsum`) and returns dsum + the norm's pullback, once in the stream's dtype and once in
+// add's (the cotangents of x and of the block output). Each direction is then one pass
+// where the residual add, its backward and the gradient cast were three more.
 #include <algorithm>
 
 #include "m3s_common.h"
@@ -49,14 +56,29 @@ __global__ void __launch_bounds__(kRmsThreads) rms_fwd_kernel(const TX* __restri
                                                               const float* __restrict__ w,
                                                               TY* __restrict__ y,
                                                               float* __restrict__ rstd,
+                                                              const TY* __restrict__ add,
+                                                              TX* __restrict__ sum,
                                                               int64_t M, int D, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * kRmsWaves + (threadIdx.x >> 6);
   if (r >= M) return;   // whole waves leave together
   const TX* xr = x + r * D;
+  const TY* ar = add ? add + r * D : nullptr;
+  // the row the norm sees: x, or s = x + add rounded to the stream's dtype (both passes
+  // form it from x and add; the second pass's reads hit the cache)
+  auto row = [&](int c) {
+    f32x4 v = ld4(xr + c);
+    if (ar) {
+      const f32x4 d = ld4(ar + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (float)(TX)(v[i] + d[i]);
+    }
+    return v;
+  };
   float ss = 0.f;
   for (int c = 4 * lane; c < D; c += 256) {
-    const f32x4 v = ld4(xr + c);
+    const f32x4 v = row(c);
+    if (ar) st4(sum + r * D + c, v);
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss += v[i] * v[i];
   }
@@ -64,7 +86,7 @@ __global__ void __launch_bounds__(kRmsThreads) rms_fwd_kernel(const TX* __restri
   const float rs = 1.f / sqrtf(ss / (float)D + eps);
   TY* yr = y + r * D;
   for (int c = 4 * lane; c < D; c += 256) {
-    const f32x4 v = ld4(xr + c);
+    const f32x4 v = row(c);
     const f32x4 g = *reinterpret_cast<const f32x4*>(w + c);
     f32x4 o;
 #pragma unroll
@@ -84,6 +106,8 @@ __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restri
                                                               const TY* __restrict__ dy,
                                                               TX* __restrict__ dx,
                                                               float* __restrict__ part,
+                                                              const TX* __restrict__ dsum,
+                                                              TY* __restrict__ dadd,
                                                               int64_t M, int D) {
   extern __shared__ float sAcc[];   // [kRmsWaves][D]: sized at launch, for occupancy
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -129,7 +153,13 @@ __global__ void __launch_bounds__(kRmsThreads) rms_bwd_kernel(const TX* __restri
         f32x4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = rs * (d[i] * g[i] - v[i] * cr);
+        if (dsum) {
+          const f32x4 e = ld4(dsum + r * D + c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = (float)(TX)o[i] + e[i];
+        }
         st4(xo + c, o);
+        if (dadd) st4(dadd + r * D + c, o);
       }
     }
   }
@@ -189,6 +219,15 @@ static int32_t check_rms(const m3s_rms_args* a, const char* who, bool bwd) {
                   (bwd ? ((uintptr_t)a->dy % (4 * ys) == 0 && (uintptr_t)a->dx % (4 * xs) == 0)
                        : (uintptr_t)a->y % (4 * ys) == 0),
               "%s: rows must be aligned to 4 elements", who);
+  if (bwd) {
+    M3S_REQUIRE((uintptr_t)a->dsum % (4 * xs) == 0 && (uintptr_t)a->dadd % (4 * ys) == 0,
+                "%s: dsum / dadd rows must be aligned to 4 elements", who);
+  } else {
+    M3S_REQUIRE((a->add == nullptr) == (a->sum == nullptr),
+                "%s: give both add and sum, or neither", who);
+    M3S_REQUIRE((uintptr_t)a->add % (4 * ys) == 0 && (uintptr_t)a->sum % (4 * xs) == 0,
+                "%s: add / sum rows must be aligned to 4 elements", who);
+  }
   return 0;
 }
 
@@ -197,7 +236,8 @@ static void launch_rms_fwd(const m3s_rms_args* a, hipStream_t s) {
   const int64_t blocks = (a->rows + kRmsWaves - 1) / kRmsWaves;
   hipLaunchKernelGGL((rms_fwd_kernel<TX, TY>), dim3((unsigned)blocks), dim3(kRmsThreads), 0, s,
                      static_cast<const TX*>(a->x), a->weight, static_cast<TY*>(a->y), a->rstd,
-                     a->rows, a->width, a->eps);
+                     static_cast<const TY*>(a->add), static_cast<TX*>(a->sum), a->rows, a->width,
+                     a->eps);
 }
 
 template <typename TX, typename TY>
@@ -208,7 +248,8 @@ static void launch_rms_bwd(const m3s_rms_args* a, hipStream_t s) {
   const auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(nblk), dim3(kRmsThreads), lds, s, static_cast<const TX*>(a->x),
                        a->weight, a->rstd, static_cast<const TY*>(a->dy), static_cast<TX*>(a->dx),
-                       part, a->rows, a->width);
+                       part, static_cast<const TX*>(a->dsum), static_cast<TY*>(a->dadd), a->rows,
+                       a->width);
   };
   if (a->width <= 1024) go(rms_bwd_kernel<TX, TY, 4>);
   else if (a->width <= 2048) go(rms_bwd_kernel<TX, TY, 8>);

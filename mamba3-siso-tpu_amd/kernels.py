@@ -837,10 +837,15 @@ def adamw_update(params, grads, exp_avg, exp_avg_sq, lr: float, beta1: float, be
         _lib.check(_lib.load().m3s_adamw(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_adamw")
 
 
-def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
+def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype,
+                add: Optional[Tensor] = None):
     """LM block norm: ``x`` (..., D) in f32 or bf16 -> ``(y (..., D) in out_dtype, rstd
     (...,) f32)`` with ``y = x rstd w``, ``rstd = 1/sqrt(mean(x^2) + eps)`` in f32 (one
-    ``m3s_rms_fwd`` launch; ``layer.py:190-198`` as ``model.py:194-232`` applies it)."""
+    ``m3s_rms_fwd`` launch; ``layer.py:190-198`` as ``model.py:194-232`` applies it).
+
+    With ``add`` (same shape, in ``out_dtype``: a block's output) the launch first forms
+    the residual sum ``s = x + add`` in x's dtype and normalises ``s``; it then returns
+    ``(y, rstd, s)``."""
     if not x.is_cuda:
         raise ValueError("rms_forward: x must be a ROCm device tensor")
     x = x.contiguous()
@@ -853,15 +858,29 @@ def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype):
     a.x_dtype, a.y_dtype = _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype)
     a.width, a.rows, a.eps = d, x.numel() // d, float(eps)
     a.x, a.weight, a.y, a.rstd = x.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr()
+    s = None
+    if add is not None:
+        if add.shape != x.shape or add.dtype != out_dtype or add.device != x.device:
+            raise ValueError("rms_forward: add must match x's shape, in out_dtype, on x's device")
+        add = add.contiguous()
+        s = torch.empty_like(x)
+        a.add, a.sum = add.data_ptr(), s.data_ptr()
     with torch.cuda.device(x.device):
         _lib.check(_lib.load().m3s_rms_fwd(ctypes.byref(a), _lib.stream_handle(x.device)),
                    "m3s_rms_fwd")
-    return y, rstd
+    return (y, rstd) if add is None else (y, rstd, s)
 
 
-def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor):
+def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor,
+                 dsum: Optional[Tensor] = None, add_dtype: Optional[torch.dtype] = None):
     """Cotangents of `rms_forward`: ``dy`` (..., D) in y's dtype -> ``(dx in x's dtype,
-    dweight (D,) f32)``, dweight summed in a fixed order (one ``m3s_rms_bwd`` call)."""
+    dweight (D,) f32)``, dweight summed in a fixed order (one ``m3s_rms_bwd`` call).
+
+    Residual form: ``x`` is the sum the forward normalised; ``dsum`` (x's dtype, or None
+    for zero) is the cotangent the rest of the network gives that sum, and ``dx`` becomes
+    ``dsum`` plus the norm's pullback. With ``add_dtype`` the same ``dx`` comes back a
+    second time in that dtype (the cotangent of the added block output):
+    ``(dx, dweight, dadd)``."""
     x = x.contiguous()
     dy = dy.contiguous()
     w = weight.float().contiguous()
@@ -876,10 +895,21 @@ def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor):
     a.width, a.rows = d, x.numel() // d
     a.x, a.weight, a.rstd, a.dy = x.data_ptr(), w.data_ptr(), rstd.data_ptr(), dy.data_ptr()
     a.dx, a.dweight, a.workspace = dx.data_ptr(), dw.data_ptr(), ws.data_ptr()
+    if dsum is not None:
+        if dsum.shape != x.shape or dsum.device != x.device:
+            raise ValueError("rms_backward: dsum must match x's shape and device")
+        dsum = dsum.to(x.dtype).contiguous()
+        a.dsum = dsum.data_ptr()
+    dadd = None
+    if add_dtype is not None:
+        if add_dtype != dy.dtype:
+            raise ValueError("rms_backward: the added tensor's dtype must be dy's")
+        dadd = torch.empty(x.shape, device=x.device, dtype=add_dtype)
+        a.dadd = dadd.data_ptr()
     with torch.cuda.device(x.device):
         _lib.check(_lib.load().m3s_rms_bwd(ctypes.byref(a), _lib.stream_handle(x.device)),
                    "m3s_rms_bwd")
-    return dx, dw
+    return (dx, dw) if add_dtype is None else (dx, dw, dadd)
 
 
 def _swiglu_args(h: Tensor, width: int) -> "_lib.SwigluArgs":

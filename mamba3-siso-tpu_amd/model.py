@@ -224,8 +224,12 @@ def _logits(x: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
     rounded to bf16 and accumulated in float32 (the head is about 0.3% of the model's
     flops, so a float32 product of the rounded operands costs nothing measurable)."""
     dt = _mm_dtype(cfg)
-    xn = _norm(x, params.final_norm, cfg.siso.norm_eps, dt)
-    return xn.float() @ _head(params, cfg).to(dt).float()
+    return _head_logits(_norm(x, params.final_norm, cfg.siso.norm_eps, dt), params, cfg)
+
+
+def _head_logits(xn: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
+    """The head product of `_logits` on the already normalised rows."""
+    return xn.float() @ _head(params, cfg).to(_mm_dtype(cfg)).float()
 
 
 class _NormFn(torch.autograd.Function):
@@ -244,6 +248,44 @@ class _NormFn(torch.autograd.Function):
         x, gain, rstd = ctx.saved_tensors
         dx, dw = K.rms_backward(x, gain, rstd, dy)
         return dx, dw.to(gain.dtype), None, None
+
+
+class _AddNormFn(torch.autograd.Function):
+    """The residual add and the next norm as one autograd node: ``s = x + y`` (the stream
+    after a block, in x's dtype) and ``rms_norm(s)`` in ``dt``, one ``m3s_rms_fwd`` pass;
+    backward, the cotangent of ``s`` from the rest of the network plus the norm's
+    pullback, returned for x and (in y's dtype) for y, one ``m3s_rms_bwd`` pass. The
+    same values as `_add_residual` followed by `_norm`, without the add, its backward
+    and the cast of its cotangent."""
+
+    @staticmethod
+    def forward(ctx, x, y, gain, eps, dt):
+        n, rstd, s = K.rms_forward(x, gain, eps, dt, add=y)
+        ctx.save_for_backward(s, gain, rstd)
+        ctx.y_dtype = y.dtype
+        ctx.set_materialize_grads(False)
+        return s, n
+
+    @staticmethod
+    def backward(ctx, ds, dn):
+        s, gain, rstd = ctx.saved_tensors
+        if dn is None:
+            dn = torch.zeros(s.shape, device=s.device, dtype=ctx.y_dtype)
+        dx, dw, dy = K.rms_backward(s, gain, rstd, dn, dsum=ds, add_dtype=ctx.y_dtype)
+        return dx, dy, dw.to(gain.dtype), None, None
+
+
+def _add_norm(x: Tensor, y: Tensor, gain: Tensor, eps: float, dt: torch.dtype):
+    """``(x + y, rms_norm(x + y, gain, eps) in dt)`` for the residual stream ``x`` and a
+    block output ``y``: one HIP pass each way (`_AddNormFn`) when the sum keeps x's dtype
+    and y is already in ``dt``, else the add and `_norm`."""
+    d = x.shape[-1]
+    if (x.is_cuda and y.is_cuda and x.shape == y.shape and y.dtype == dt
+            and torch.promote_types(x.dtype, y.dtype) == x.dtype and d % 4 == 0 and d <= 4096
+            and x.dtype in (torch.float32, torch.bfloat16)):
+        return _AddNormFn.apply(x, y, gain, eps, dt)
+    s = x + y
+    return s, _norm(s, gain, eps, dt)
 
 
 def _norm(x: Tensor, gain: Tensor, eps: float, dt: torch.dtype) -> Tensor:
@@ -274,14 +316,20 @@ def lm_forward(params: LMParams, tokens: Tensor, cfg: LMConfig, interpret: Any =
     x = _embed(params.embed, tokens)
     new_states = []
     eps = cfg.siso.norm_eps
-    for i, b in enumerate(params.blocks):
-        y, st = LY.mamba3_siso_layer(b.siso, _norm(x, b.norm_gain, eps, dt), cfg.siso,
+    blocks = params.blocks
+    # each residual add is fused with the norm that reads the sum next (the next sublayer's,
+    # or the head's); the first block's norm reads the embedding alone
+    h = _norm(x, blocks[0].norm_gain, eps, dt) if blocks else None
+    for i, b in enumerate(blocks):
+        y, st = LY.mamba3_siso_layer(b.siso, h, cfg.siso,
                                      state=None if states is None else states[i])
         new_states.append(st)
-        x = x + y
+        nxt = blocks[i + 1].norm_gain if i + 1 < len(blocks) else params.final_norm
         if b.mlp is not None:
-            x = x + gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, eps, dt), dt)
-    logits = _logits(x, params, cfg)
+            x, h = _add_norm(x, y, b.mlp_norm_gain, eps, dt)
+            y = gated_mlp(b.mlp, h, dt)
+        x, h = _add_norm(x, y, nxt, eps, dt)
+    logits = _head_logits(h, params, cfg) if blocks else _logits(x, params, cfg)
     return (logits, new_states) if states is not None else logits
 
 

@@ -65,3 +65,63 @@ def test_norm_node_in_the_model_and_empty_rows(m3, dev):
     e = torch.empty(0, 64, device=dev)
     y0, r0 = K.rms_forward(e, torch.ones(64, device=dev), 1e-5, torch.bfloat16)
     assert y0.shape == (0, 64) and r0.shape == (0,)
+
+
+@pytest.mark.parametrize("rows,d", [(4096, 768), (333, 1024), (5, 12), (64, 4096)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16)])
+def test_residual_form_equals_add_then_norm(m3, dev, rows, d, xdt, ydt):
+    """`m3s_rms_fwd` / `m3s_rms_bwd` with a residual: the sum and the normalised rows are
+    bit-identical to the add followed by the plain kernel (the same roundings), and the
+    cotangents of x, of the added block output and of the gain match autograd of
+    ``x + y`` into the plain norm node with the sum's outside cotangent (dx, dy
+    within one rounding of the add: 1e-6 max-normalised in f32, 2^-7 in bf16)."""
+    K = m3.kernels
+    g = torch.Generator().manual_seed(3 * rows + d)
+    x = (2 * torch.randn(rows, d, generator=g)).to(xdt).to(dev)
+    y = torch.randn(rows, d, generator=g).to(ydt).to(dev)
+    w = (1 + 0.3 * torch.randn(d, generator=g)).to(dev)
+    n, rstd, s = K.rms_forward(x, w, 1e-5, ydt, add=y)
+    s_ref = x + y
+    assert s.dtype == xdt and torch.equal(s, s_ref)
+    n_ref, rstd_ref = K.rms_forward(s_ref, w, 1e-5, ydt)
+    assert torch.equal(n, n_ref) and torch.equal(rstd, rstd_ref)
+    dn = torch.randn(rows, d, generator=g).to(ydt).to(dev)
+    ds = torch.randn(rows, d, generator=g).to(xdt).to(dev)
+    for dsum in (ds, None):
+        dx, dw, dadd = K.rms_backward(s, w, rstd, dn, dsum=dsum, add_dtype=ydt)
+        xr = x.detach().clone().requires_grad_(True)
+        yr = y.detach().clone().requires_grad_(True)
+        wr = w.detach().clone().requires_grad_(True)
+        sr = xr + yr
+        nr = m3.model._NormFn.apply(sr, wr, 1e-5, ydt)
+        outs, grads = [nr], [dn]
+        if dsum is not None:
+            outs.append(sr)
+            grads.append(dsum)
+        gx, gy, gw = torch.autograd.grad(outs, (xr, yr, wr), grads)
+        tol = 1e-6 if xdt == torch.float32 else 2.0 ** -7
+        assert dx.dtype == xdt and dadd.dtype == ydt
+        assert maxrel(dx, gx) <= tol
+        assert maxrel(dadd, gy) <= (tol if ydt == torch.float32 else 2.0 ** -7)
+        assert torch.equal(dw, gw)
+
+
+def test_add_norm_in_the_model_matches_the_composed_ops(m3, dev):
+    """`model._add_norm` (one node) against ``x + y`` into `model._norm`: same outputs
+    bit for bit, gradients of x, y and the gain within float rounding."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 96, 512, generator=g).to(dev).requires_grad_(True)
+    y = torch.randn(2, 96, 512, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(512, generator=g)).to(dev).requires_grad_(True)
+    s, h = m3.model._add_norm(x, y, w, 1e-5, torch.bfloat16)
+    s2 = x + y
+    h2 = m3.model._norm(s2, w, 1e-5, torch.bfloat16)
+    assert torch.equal(s, s2) and torch.equal(h, h2)
+    ds = torch.randn(s.shape, generator=g).to(dev)
+    dh = torch.randn(h.shape, generator=g).to(torch.bfloat16).to(dev)
+    got = torch.autograd.grad((s, h), (x, y, w), (ds, dh))
+    want = torch.autograd.grad((s2, h2), (x, y, w), (ds, dh))
+    assert maxrel(got[0], want[0]) <= 1e-6
+    assert got[1].dtype == torch.bfloat16 and maxrel(got[1], want[1]) <= 2.0 ** -7
+    assert maxrel(got[2], want[2]) <= 1e-6
