@@ -188,6 +188,24 @@ def _fused_ok(u: Tensor, cfg: SISOConfig, state) -> bool:
             and n // vec <= 64)
 
 
+def weight_grad(a: Tensor, b: Tensor) -> Tensor:
+    """``a^T b`` in float32 for ``(M, P)`` and ``(M, Q)`` operands over the M tokens: the
+    weight gradient of a projection. Its output is small (P x Q) and its reduction long
+    (M = B*L), so one library GEMM has too few output tiles to fill the GPU; with M a
+    multiple of 8 and at least 16384 the tokens are cut into 8 slices, one batched GEMM
+    forms the 8 partial products (float32 out) and they are summed in slice order. The
+    right operand is never a transposed view (a column slice is a strided row view)."""
+    m = a.shape[0]
+    if a.dtype != b.dtype or a.dim() != 2 or b.dim() != 2 or b.shape[0] != m:
+        raise ValueError("weight_grad: a (M, P) and b (M, Q) of one dtype")
+    if m % 8 or m < 16384 or not a.is_cuda:
+        return (a.t() @ b).float()
+    a3, b3 = a.unflatten(0, (8, m // 8)), b.unflatten(0, (8, m // 8))
+    if a.dtype == torch.float32:
+        return torch.bmm(a3.transpose(1, 2), b3).sum(0)
+    return torch.bmm(a3.transpose(1, 2), b3, out_dtype=torch.float32).sum(0)
+
+
 class _LayerFn(torch.autograd.Function):
     """``layer.py:201-262`` with state=None as one autograd node (see the module notes).
     Outputs: out (B, L, d_model), final ssm, final k, final v, final phi."""
@@ -254,7 +272,7 @@ class _LayerFn(torch.autograd.Function):
             dout2 = dout.reshape(m, dm).to(dt)
             dy2 = dout2 @ out_proj.to(dt).t()
             if needs[2]:
-                d_out_proj = (y2.t() @ dout2).to(out_proj.dtype)
+                d_out_proj = weight_grad(y2, dout2).to(out_proj.dtype)
             dys = dy2.view(batch, seqlen, H, P).permute(0, 2, 1, 3)
         else:
             dys = torch.zeros_like(y)
@@ -276,7 +294,7 @@ class _LayerFn(torch.autograd.Function):
         if needs[0]:
             du = (dp2 @ in_proj.to(dt).t()).view(batch, seqlen, dm)
         if needs[1]:
-            d_in_proj = (dp2.t() @ u.reshape(m, dm)).t().to(in_proj.dtype)
+            d_in_proj = weight_grad(u.reshape(m, dm), dp2).to(in_proj.dtype)
 
         def like(t, p_):
             return None if (t is None or p_ is None) else t.to(p_.dtype)

@@ -93,9 +93,33 @@ def _mm_dtype(cfg: LMConfig) -> torch.dtype:
     return L.policy(cfg.siso.policy_name).matmul
 
 
+class _MatmulFn(torch.autograd.Function):
+    """``x.to(dt) @ w.to(dt)`` as one autograd node whose weight gradient is
+    `layer.weight_grad` (split over the tokens, float32 out) instead of one library GEMM
+    with too few output tiles for the GPU; the input gradient is the usual product."""
+
+    @staticmethod
+    def forward(ctx, x, w, dt):
+        xd, wd = x.to(dt), w.to(dt)
+        ctx.save_for_backward(xd, wd)
+        ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
+        return xd @ wd
+
+    @staticmethod
+    def backward(ctx, dy):
+        xd, wd = ctx.saved_tensors
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = (dy @ wd.t()).to(ctx.x_dtype)
+        if ctx.needs_input_grad[1]:
+            dw = LY.weight_grad(xd.reshape(-1, xd.shape[-1]),
+                                dy.reshape(-1, dy.shape[-1]).to(xd.dtype)).to(ctx.w_dtype)
+        return dx, dw, None
+
+
 def _mm(x: Tensor, w: Tensor, dt: torch.dtype) -> Tensor:
-    """A matrix product with both operands in the policy's operand dtype."""
-    return x.to(dt) @ w.to(dt)
+    """A matrix product with both operands in the policy's operand dtype (`_MatmulFn`)."""
+    return _MatmulFn.apply(x, w, dt)
 
 
 class _GateFn(torch.autograd.Function):
@@ -229,7 +253,7 @@ def _logits(x: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
 
 def _head_logits(xn: Tensor, params: LMParams, cfg: LMConfig) -> Tensor:
     """The head product of `_logits` on the already normalised rows."""
-    return xn.float() @ _head(params, cfg).to(_mm_dtype(cfg)).float()
+    return _mm(xn.float(), _head(params, cfg).to(_mm_dtype(cfg)), torch.float32)
 
 
 class _NormFn(torch.autograd.Function):
