@@ -140,8 +140,11 @@ def test_fused_layer_without_grad_saves_nothing(m3, dev):
 
 
 @pytest.mark.parametrize("src,dst,rows,cols,out_rows,stride_pad", [
-    (BF16, BF16, 1024, 4480, 4608, 0),     # the configs[1] in_proj layout
-    (F32, BF16, 200, 133, 256, 5),         # ragged tiles, strided input, f32 parameters
+    (BF16, BF16, 1024, 4480, 4608, 0),     # the configs[1] in_proj layout (8-element runs)
+    (BF16, BF16, 2048, 1024, 1024, 0),     # out_proj
+    (F32, BF16, 1536, 768, 768, 0),        # an LM out_proj from float32 parameters
+    (F32, BF16, 200, 136, 256, 8),         # 8-element runs over ragged tiles, strided input
+    (F32, BF16, 200, 133, 256, 5),         # element-wise: ragged tiles, strided input
     (F32, F32, 64, 64, 64, 0),
     (BF16, F32, 70, 1, 8, 3),
 ])
