@@ -391,8 +391,8 @@ int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen, in
  * -1 on bad dimensions. */
 int64_t m3s_prep_fwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                      int32_t n_angles);
-/* Bytes of m3s_prep_bwd_args.workspace: the per-block dphi carries (B, ceil(L/64), H,
- * Nr) and dt_bias partials (B, ceil(L/64), H), f32. No counterpart in the reference.
+/* Bytes of m3s_prep_bwd_args.workspace: the per-block dphi carries (B, ceil(L/32), H,
+ * Nr) and dt_bias partials (B, ceil(L/32), H), f32. No counterpart in the reference.
  * -1 on bad dimensions. */
 int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                      int32_t n_angles);

@@ -33,7 +33,11 @@ namespace m3s {
 constexpr float kPiF = 3.14159265358979323846f;
 constexpr float kTwoPiF = 6.28318530717958647692f;
 constexpr int kPrepThreads = 256;
-constexpr int kPrepTB = 64;  // tokens per block of prep_bwd_kernel
+constexpr int kPrepTB = 64;     // tokens per block of the forward kernels
+// tokens per block of the backward kernels: 32 halves prep_bwd_kernel's LDS tables, so four
+// blocks fit a CU instead of two (0.218 -> 0.175 ms at cfg3); the forward kernels are
+// faster at 64
+constexpr int kPrepBwdTB = 32;
 
 template <typename RT>
 __device__ __forceinline__ float ldr(const RT* base, int64_t i) { return (float)base[i]; }
@@ -333,8 +337,8 @@ __global__ void __launch_bounds__(kPrepThreads)
 prep_dphi_totals_kernel(const float* __restrict__ dphi, float* __restrict__ tot, int L, int H,
                         int Nr, int nblk) {
   const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
-  const int t0 = blk * kPrepTB;
-  const int nt = min(kPrepTB, L - t0);
+  const int t0 = blk * kPrepBwdTB;
+  const int nt = min(kPrepBwdTB, L - t0);
   const int J4 = (Nr + 3) / 4;
   for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
     const int h = pr / J4, j0 = 4 * (pr % J4);
@@ -372,7 +376,7 @@ constexpr int kPrepRun = 8;
 // angle-cotangent accumulator, dscale just before the block for each head, and each
 // wave's angle-cotangent partials of one run.
 __host__ __device__ inline int prep_bwd_lds_floats(int H, int Nr) {
-  return 3 * kPrepTB * H + 3 * kPrepTB * (H + 1) + 2 * kPrepTB * Nr + H +
+  return 3 * kPrepBwdTB * H + 3 * kPrepBwdTB * (H + 1) + 2 * kPrepBwdTB * Nr + H +
          (kPrepThreads / 64) * kPrepRun * Nr;
 }
 
@@ -385,22 +389,22 @@ __global__ void __launch_bounds__(kPrepThreads) prep_bwd_kernel(const PrepBwdPar
   // one head fall in distinct LDS banks
   const int HS = H + 1;
   float* sDt = lds;                    // [TB][H] dt
-  float* sLam = sDt + kPrepTB * H;     // [TB][H] lambda
-  float* sDadt = sLam + kPrepTB * H;   // [TB][HS] incoming cotangents (t-major)
-  float* sDgam = sDadt + kPrepTB * HS;
-  float* sDscl = sDgam + kPrepTB * HS;
-  float* sPhi = sDscl + kPrepTB * HS;  // [TB][H] sum_j dtheta tanh pi
+  float* sLam = sDt + kPrepBwdTB * H;     // [TB][H] lambda
+  float* sDadt = sLam + kPrepBwdTB * H;   // [TB][HS] incoming cotangents (t-major)
+  float* sDgam = sDadt + kPrepBwdTB * HS;
+  float* sDscl = sDgam + kPrepBwdTB * HS;
+  float* sPhi = sDscl + kPrepBwdTB * HS;  // [TB][H] sum_j dtheta tanh pi
   float* sBias = sDadt;                // [TB][HS] d dt_raw for the dt_bias partial; each
                                        // thread overwrites only entries it has read
-  float* sT = sPhi + kPrepTB * H;      // [TB][Nr] tanh(angles)
-  float* sAng = sT + kPrepTB * Nr;     // [TB][Nr] sum_h dtheta dt
-  float* sDsPrev = sAng + kPrepTB * Nr;  // [H] dscale at t0 - 1
+  float* sT = sPhi + kPrepBwdTB * H;      // [TB][Nr] tanh(angles)
+  float* sAng = sT + kPrepBwdTB * Nr;     // [TB][Nr] sum_h dtheta dt
+  float* sDsPrev = sAng + kPrepBwdTB * Nr;  // [H] dscale at t0 - 1
   float* sStage = sDsPrev + H;           // [wave][kPrepRun][Nr] this run's partials
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int blk = blockIdx.x, b = blockIdx.y;
-  const int t0 = blk * kPrepTB;
-  const int nt = min(kPrepTB, L - t0);
+  const int t0 = blk * kPrepBwdTB;
+  const int nt = min(kPrepBwdTB, L - t0);
   const RT* dtr = static_cast<const RT*>(p.dtr.p) + b * p.dtr.sb;
   const RT* ar = static_cast<const RT*>(p.ar.p) + b * p.ar.sb;
   const RT* tr = static_cast<const RT*>(p.tr.p) + b * p.tr.sb;
@@ -737,7 +741,7 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
 extern "C" int64_t m3s_prep_bwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                                  int32_t n_angles) {
   if (batch <= 0 || seqlen <= 0 || nheads <= 0 || n_angles < 0) return -1;
-  const int64_t nblk = (seqlen + kPrepTB - 1) / kPrepTB;
+  const int64_t nblk = (seqlen + kPrepBwdTB - 1) / kPrepBwdTB;
   return align256((int64_t)batch * nblk * nheads * n_angles * 4) +
          (int64_t)batch * nblk * nheads * 4;
 }
@@ -767,7 +771,7 @@ extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
   const size_t lds = (size_t)prep_bwd_lds_floats(H, Nr) * 4;
   M3S_REQUIRE(lds <= 160 * 1024, "m3s_prep_bwd: nheads=%d, n_angles=%d exceed the LDS budget", H, Nr);
   M3S_REQUIRE((int64_t)B * H < (1ll << 31), "m3s_prep_bwd: B*H too large");
-  const int nblk = (L + kPrepTB - 1) / kPrepTB;
+  const int nblk = (L + kPrepBwdTB - 1) / kPrepBwdTB;
   float* carry = static_cast<float*>(a->workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
                                          align256((int64_t)B * nblk * H * Nr * 4));
