@@ -12,8 +12,9 @@ the default. The file is keyed by the library versions it was made with (its
     gemm_tuning.enable()                                      # use the committed file
 
 `tune` runs, once each, the workloads whose GEMM shapes the benchmark measures: the
-configs[1]/[2] layer forward and backward (B=8, L=8192, d_model=1024) and the configs[4]
-LM training step (B=16, L=2048, d_model=768). Results are numerically the GEMMs' own:
+configs[1]/[2] layer forward and backward (B=8, L=8192, d_model=1024), the configs[3]
+decode step (B=256), the configs[4] LM training step (B=16, L=2048, d_model=768) and the
+LM's decode step at batch 1 and 256. Results are numerically the GEMMs' own:
 only the choice of library kernel changes.
 """
 
@@ -51,6 +52,11 @@ def _workloads(m3, dev):
     u = torch.randn(8, 8192, 1024, device=dev).to(torch.bfloat16)
     with torch.no_grad():
         m3.mamba3_siso_layer(p16, u, cfg)
+        # the layer's decode step at B=256 (its two projections are small GEMMs)
+        state = m3.zero_state(256, cfg.nheads, cfg.headdim, cfg.d_state, cfg.n_angles)
+        state = m3.SISOState(*(t.to(dev) for t in state))
+        m3.mamba3_siso_decode_step(p16, torch.randn(256, 1024, device=dev).to(torch.bfloat16),
+                                   cfg, state)
     pg = m3.SISOParams(*(t.detach().clone().requires_grad_(True) for t in p32))
     ug = u.detach().clone().requires_grad_(True)
     y, _ = m3.mamba3_siso_layer(pg, ug, cfg)
@@ -65,6 +71,13 @@ def _workloads(m3, dev):
     step = T.make_step(lcfg, opt)
     xs = torch.randint(0, 256, (16, 2048), device=dev)
     step(params, opt, xs, xs)
+    # the LM's decode step at batch 1 and 256 (its products are matrix-vector shapes)
+    dparams = m3.model.decode_params(params, lcfg)
+    with torch.no_grad():
+        for bsz in (1, 256):
+            states = m3.model.zero_states(lcfg, bsz, device=dev)
+            m3.model.lm_decode_step(dparams, torch.zeros(bsz, dtype=torch.int64, device=dev),
+                                    states, lcfg)
     torch.cuda.synchronize()
 
 
