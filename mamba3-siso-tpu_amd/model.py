@@ -308,7 +308,7 @@ def _add_norm(x: Tensor, y: Tensor, gain: Tensor, eps: float, dt: torch.dtype):
             and torch.promote_types(x.dtype, y.dtype) == x.dtype and d % 4 == 0 and d <= 4096
             and x.dtype in (torch.float32, torch.bfloat16)):
         return _AddNormFn.apply(x, y, gain, eps, dt)
-    s = x + y
+    s = _add_residual(x, y)
     return s, _norm(s, gain, eps, dt)
 
 
@@ -395,13 +395,19 @@ def lm_decode_step(params: LMParams, token: Tensor, states: list, cfg: LMConfig,
     reference donates it); the returned list holds the same state tensors."""
     dt = _mm_dtype(cfg)
     c = cfg.siso
+    eps = c.norm_eps
     x = _embed(params.embed, token)
     out_states = []
-    for i, b in enumerate(params.blocks):
-        y, st = LY.mamba3_siso_decode_step(b.siso, _norm(x, b.norm_gain, c.norm_eps, dt), c,
-                                           states[i])
+    blocks = params.blocks
+    # as in lm_forward: each residual add fused with the norm that reads the sum next
+    h = _norm(x, blocks[0].norm_gain, eps, dt) if blocks else None
+    for i, b in enumerate(blocks):
+        y, st = LY.mamba3_siso_decode_step(b.siso, h, c, states[i])
         out_states.append(st)
-        x = _add_residual(x, y)
+        nxt = blocks[i + 1].norm_gain if i + 1 < len(blocks) else params.final_norm
         if b.mlp is not None:
-            x = _add_residual(x, gated_mlp(b.mlp, _norm(x, b.mlp_norm_gain, c.norm_eps, dt), dt))
-    return _logits(x, params, cfg), out_states
+            x, h = _add_norm(x, y, b.mlp_norm_gain, eps, dt)
+            y = gated_mlp(b.mlp, h, dt)
+        x, h = _add_norm(x, y, nxt, eps, dt)
+    logits = _head_logits(h, params, cfg) if blocks else _logits(x, params, cfg)
+    return logits, out_states

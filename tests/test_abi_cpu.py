@@ -151,7 +151,8 @@ def test_prep_arguments_are_checked_without_a_launch(lib):
     b.struct_size = ctypes.sizeof(lib.PrepBwdArgs) - 8
     assert h.m3s_prep_bwd(ctypes.byref(b), None) == lib.ERR_INVALID
     assert b"ABI mismatch" in h.m3s_last_error()
-    assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 128 * 32 * 32 * 4 + 8 * 128 * 32 * 4
+    # the backward's blocks are 32 tokens: 256 per sequence at L=8192
+    assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 256 * 32 * 32 * 4 + 8 * 256 * 32 * 4
     assert h.m3s_prep_bwd_workspace_bytes(0, 8, 1, 1) == -1
     assert h.m3s_prep_fwd_workspace_bytes(8, 8192, 32, 32) == 8 * 8192 * 32 * 4 + 8 * 128 * 32 * 32 * 4
     assert h.m3s_prep_fwd_workspace_bytes(1, 8, 1, -1) == -1
