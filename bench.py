@@ -211,7 +211,10 @@ def main():
                 "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
                 "traffic": traffic_figure("fwd_bf16_kernel_strips"),
                 "traffic_source": TRAFFIC_SOURCE, "algorithmic_bytes": scan_bytes,
-                "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5)}
+                "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5),
+                # the same scan reading the materialised phi (the training forward's form):
+                # more bytes in about the same time
+                "phi_read_frac": round(scan_read_bytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if args.leg in ("all", "bwd"):
             # the training path's pair: with gradients the layer materialises phi and both
             # scans read it (phi_in_kernel=None)

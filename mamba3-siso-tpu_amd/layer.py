@@ -199,7 +199,9 @@ def weight_grad(a: Tensor, b: Tensor) -> Tensor:
     if a.dtype != b.dtype or a.dim() != 2 or b.dim() != 2 or b.shape[0] != m:
         raise ValueError("weight_grad: a (M, P) and b (M, Q) of one dtype")
     if m % 8 or m < 16384 or not a.is_cuda:
-        return (a.t() @ b).float()
+        if a.dtype == torch.float32 or not a.is_cuda:
+            return (a.t() @ b).float()
+        return torch.mm(a.t(), b, out_dtype=torch.float32)
     a3, b3 = a.unflatten(0, (8, m // 8)), b.unflatten(0, (8, m // 8))
     if a.dtype == torch.float32:
         return torch.bmm(a3.transpose(1, 2), b3).sum(0)

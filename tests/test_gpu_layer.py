@@ -362,3 +362,25 @@ def test_recorded_gemm_solutions_change_only_gemm_rounding(m3):
             gemm_tuning.disable()
     assert_maxrel(outs[1][0], cpu(outs[0][0]), 1e-2, "y")
     assert_maxrel(outs[1][1], cpu(outs[0][1]), 2e-2, "du")
+
+
+@pytest.mark.parametrize("m,p,q,dtype", [
+    (65536, 2048, 1024, torch.bfloat16),   # configs[2] out_proj: 8 token slices
+    (32768, 768, 520, torch.bfloat16),     # a strided column slice (in the layer: dproj[..., :d])
+    (16384, 256, 96, torch.float32),       # float32 operands (the LM head)
+    (1000, 64, 32, torch.bfloat16),        # too few tokens to split: one product
+])
+def test_weight_grad_matches_float64(m3, dev, m, p, q, dtype):
+    """`layer.weight_grad` (``a^T b`` over the tokens, float32 out) against float64: the
+    split sums 8 float32 partial products in slice order; 1e-5 of max |ref| (f32
+    accumulation over up to 65536 terms), bit-identical on a second call."""
+    g = torch.Generator().manual_seed(m + p)
+    a = torch.randn(m, p, generator=g).to(dtype)
+    bfull = torch.randn(m, q + 8, generator=g).to(dtype)
+    ad, bd = a.to(dev), bfull.to(dev)[:, :q]
+    got = m3.layer.weight_grad(ad, bd)
+    ref = a.double().t() @ bfull[:, :q].double()
+    assert got.dtype == torch.float32 and got.shape == (p, q)
+    err = ((got.cpu().double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 1e-5, err
+    assert torch.equal(got, m3.layer.weight_grad(ad, bd))
