@@ -293,8 +293,12 @@ def main():
             _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
         torch.cuda.synchronize()
         dec_ms = (time.perf_counter() - t0) * 1e3 / T
+    # The legs from here to the headline run back to back, without emptying the allocator
+    # cache in between: the GPU lowers its clocks within a millisecond or two of idling
+    # (measured: a 20 ms pause before 5 warmup steps costs the next 20 forwards 7%, an
+    # empty_cache() after the fwd+bwd leg 3.5%), so a pause would put the timed steps on
+    # the ramp back up instead of the steady state a busy device runs at.
     del toks, state
-    torch.cuda.empty_cache()
 
     # ---------------- forward + backward ---------------------------------
     pg = m3.SISOParams(*(t.detach().clone().requires_grad_(True) for t in params32))
@@ -307,7 +311,7 @@ def main():
         y, _ = m3.mamba3_siso_layer(pg, ug, cfg)
         return torch.autograd.grad(y, (ug, *pg), dy)
 
-    for _ in range(2):
+    for _ in range(max(3, args.warmup)):
         fwdbwd_step()
     fb_iters = max(3, args.steps // 4)
     torch.cuda.synchronize()
@@ -317,7 +321,6 @@ def main():
     torch.cuda.synchronize()
     fb_ms = (time.perf_counter() - t0) * 1e3 / fb_iters
     del pg, ug, dy
-    torch.cuda.empty_cache()
 
     # ---------------- headline: layer forward, the K timed steps ----------
     def fwd_step():
