@@ -246,33 +246,54 @@ __global__ void __launch_bounds__(kPrepThreads) prep_scalars_kernel(const PrepFw
 // Over the blocks of one (b, h, angle): replace each block total by the exclusive
 // running sum -- in time order (reverse = 0), or from the end, seeded with `init`,
 // with the full sum written to `total` (reverse = 1).
+// A workgroup takes kCarryR consecutive (h, angle) columns of one batch element and cuts
+// the walk over the blocks into kCarrySeg segments, one thread per (column, segment):
+// each thread sums its segment, the segment sums are combined in segment order through
+// LDS, and each thread walks its segment again from that offset (the second reads hit
+// L2). That is kCarrySeg walks of nblk / kCarrySeg blocks side by side instead of one
+// of nblk; each walk issues a group's loads before its stores, one memory latency per
+// group (a store could alias the next load as far as the compiler knows).
+constexpr int kCarryR = 16;
+constexpr int kCarrySeg = kPrepThreads / kCarryR;
 __global__ void __launch_bounds__(kPrepThreads)
 prep_carry_kernel(float* __restrict__ tot, const float* __restrict__ init,
-                  float* __restrict__ total, int B, int HN, int nblk, int reverse) {
-  const int64_t idx = (int64_t)blockIdx.x * kPrepThreads + threadIdx.x;
-  if (idx >= (int64_t)B * HN) return;
-  const int64_t b = idx / HN, r = idx % HN;
-  float* base = tot + b * nblk * HN + r;
-  // blocks in groups of G: a group's loads are all issued before its stores, so the walk
-  // pays one memory latency per group instead of one per block (each store could alias
-  // the next load as far as the compiler knows)
-  constexpr int G = 16;
-  float run = reverse ? (init ? init[idx] : 0.f) : 0.f;
-  for (int k0 = 0; k0 < nblk; k0 += G) {
-    float q[G];
+                  float* __restrict__ total, int HN, int nblk, int reverse) {
+  __shared__ float part[kCarrySeg][kCarryR];
+  const int rl = threadIdx.x % kCarryR, seg = threadIdx.x / kCarryR;
+  const int r = blockIdx.x * kCarryR + rl, b = blockIdx.y;
+  const bool valid = r < HN;
+  float* base = tot + (int64_t)b * nblk * HN + r;
+  const int len = (nblk + kCarrySeg - 1) / kCarrySeg;
+  const int s0 = min(seg * len, nblk), s1 = min(s0 + len, nblk);
+  // the u-th block of the walk (from the end when reverse)
+  auto at = [&](int u) -> int64_t { return (int64_t)(reverse ? nblk - 1 - u : u) * HN; };
+  constexpr int G = 8;
+  float sum = 0.f;
+  if (valid) {
+    for (int u0 = s0; u0 < s1; u0 += G) {
+      float q[G];
 #pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const int k = reverse ? nblk - 1 - (k0 + u) : k0 + u;
-      q[u] = (k0 + u < nblk) ? base[(int64_t)k * HN] : 0.f;
-    }
+      for (int g = 0; g < G; ++g) q[g] = (u0 + g < s1) ? base[at(u0 + g)] : 0.f;
 #pragma unroll
-    for (int u = 0; u < G; ++u) {
-      const int k = reverse ? nblk - 1 - (k0 + u) : k0 + u;
-      if (k0 + u < nblk) base[(int64_t)k * HN] = run;
-      run += q[u];
+      for (int g = 0; g < G; ++g) sum += q[g];
     }
   }
-  if (reverse && total) total[idx] = run;
+  part[seg][rl] = sum;
+  __syncthreads();
+  float run = (reverse && init && valid) ? init[(int64_t)b * HN + r] : 0.f;
+  for (int k = 0; k < seg; ++k) run += part[k][rl];
+  if (reverse && total && valid && seg == kCarrySeg - 1) total[(int64_t)b * HN + r] = run + sum;
+  if (!valid) return;
+  for (int u0 = s0; u0 < s1; u0 += G) {
+    float q[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) q[g] = (u0 + g < s1) ? base[at(u0 + g)] : 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (u0 + g < s1) base[at(u0 + g)] = run;
+      run += q[g];
+    }
+  }
 }
 
 // phi for one (batch element, block of 64 tokens): one thread per (head, group of 4
@@ -348,6 +369,33 @@ prep_dphi_totals_kernel(const float* __restrict__ dphi, float* __restrict__ tot,
   const int tid = threadIdx.x, blk = blockIdx.x, b = blockIdx.y;
   const int t0 = blk * kPrepBwdTB;
   const int nt = min(kPrepBwdTB, L - t0);
+  const int Q = Nr >> 2;   // 16-byte quads per row
+  if ((Nr & 3) == 0 && Q > 0 && Q <= 64 && (Q & (Q - 1)) == 0) {
+    // A wave per head: the block's rows are nt * Nr contiguous floats, read as 16-byte
+    // pieces by consecutive lanes (1 KB per load), not a 128-byte row piece from each of
+    // the wave's heads. Q divides 64, so lane l always holds quad l % Q of some row, and
+    // the row sum is an xor-shuffle sum over the lanes of equal l % Q (a fixed order).
+    const int wave = tid >> 6, lane = tid & 63;
+    const int E4 = nt * Q;
+    for (int h = wave; h < H; h += kPrepThreads / 64) {
+      const f32x4* src =
+          reinterpret_cast<const f32x4*>(dphi + (((int64_t)b * H + h) * L + t0) * Nr);
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int e = lane; e < E4; e += 64) {
+        const f32x4 d = src[e];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] += d[i];
+      }
+      for (int off = Q; off < 64; off <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] += __shfl_xor(s[i], off, 64);
+      }
+      if (lane < Q)
+        *reinterpret_cast<f32x4*>(tot + (((int64_t)b * nblk + blk) * H + h) * Nr + 4 * lane) = s;
+    }
+    return;
+  }
   const int J4 = (Nr + 3) / 4;
   for (int pr = tid; pr < H * J4; pr += kPrepThreads) {
     const int h = pr / J4, j0 = 4 * (pr % J4);
@@ -743,8 +791,8 @@ extern "C" int32_t m3s_prep_fwd(const m3s_prep_fwd_args* a, void* stream) {
                    : launch_lds(prep_scalars_kernel<float>, grid, lds, s, p, "m3s_prep_fwd");
   if (rc || Nr == 0) return rc;
   const int hn = H * Nr;
-  hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
-                     dim3(kPrepThreads), 0, s, p.tot, nullptr, nullptr, B, hn, nblk, 0);
+  hipLaunchKernelGGL(prep_carry_kernel, dim3((hn + kCarryR - 1) / kCarryR, B),
+                     dim3(kPrepThreads), 0, s, p.tot, nullptr, nullptr, hn, nblk, 0);
   if ((rc = launch_status("m3s_prep_fwd"))) return rc;
   hipLaunchKernelGGL(prep_phi_kernel, grid, dim3(kPrepThreads),
                      (size_t)(kPrepTB * Nr + H * (kPrepTB + 1)) * 4, s, p);
@@ -802,8 +850,8 @@ extern "C" int32_t m3s_prep_bwd(const m3s_prep_bwd_args* a, void* stream) {
                          dim3(kPrepThreads), 0, s, carry, (int64_t)B * nblk * hn);
     }
     if ((rc = launch_status("m3s_prep_bwd"))) return rc;
-    hipLaunchKernelGGL(prep_carry_kernel, dim3((B * hn + kPrepThreads - 1) / kPrepThreads),
-                       dim3(kPrepThreads), 0, s, carry, a->dphi_final, a->dphi_init, B, hn, nblk, 1);
+    hipLaunchKernelGGL(prep_carry_kernel, dim3((hn + kCarryR - 1) / kCarryR, B),
+                       dim3(kPrepThreads), 0, s, carry, a->dphi_final, a->dphi_init, hn, nblk, 1);
     if ((rc = launch_status("m3s_prep_bwd"))) return rc;
   }
   PrepBwdParams p{};
