@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 6
+#define M3S_ABI_VERSION 7
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -371,6 +371,28 @@ typedef struct m3s_adamw_args {
   float param_decay, step_size, bias_correction2_sqrt;
 } m3s_adamw_args;
 
+/* The weight gradient of a projection: c (rows, cols) float32 = a^T b, reduced over the
+ * tokens, for token-major bf16 operands a (tokens, rows) and b (tokens, cols) with row
+ * strides lda and ldb (elements). Replaces the weight half of the transposed products
+ * jax.grad forms for the projection einsums (layer.py:233, 256; model.py:231, 268, 288),
+ * which the reference leaves to XLA. tokens must be a multiple of 32; a and b 16-byte
+ * aligned with lda, ldb multiples of 8; each operand spans under 2 GiB. The tokens are cut
+ * into a shape-dependent number of splits whose float32 partials are added in split order
+ * (deterministic); with more than one split, workspace holds
+ * m3s_wgrad_workspace_bytes() bytes (16-byte aligned) and c must be 16-byte aligned when
+ * ldc % 4 == 0. */
+typedef struct m3s_wgrad_args {
+  int32_t struct_size;  /* sizeof(m3s_wgrad_args) */
+  int32_t tokens, rows, cols;
+  const void* a;        /* (tokens, rows) bf16 */
+  int64_t lda;
+  const void* b;        /* (tokens, cols) bf16 */
+  int64_t ldb;
+  float* c;             /* out (rows, cols) f32 */
+  int64_t ldc;
+  void* workspace;      /* the split partials, or NULL when one split */
+} m3s_wgrad_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -426,6 +448,10 @@ int32_t m3s_swiglu_bwd(const m3s_swiglu_args* args, void* stream);
 int32_t m3s_rms_fwd(const m3s_rms_args* args, void* stream);
 int32_t m3s_rms_bwd(const m3s_rms_args* args, void* stream);
 int32_t m3s_adamw(const m3s_adamw_args* args, void* stream);
+/* Bytes of m3s_wgrad_args.workspace for this shape (0 when one split suffices), -1 on bad
+ * dimensions. No counterpart in the reference. */
+int64_t m3s_wgrad_workspace_bytes(int32_t tokens, int32_t rows, int32_t cols);
+int32_t m3s_wgrad(const m3s_wgrad_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -838,6 +838,50 @@ def adamw_update(params, grads, exp_avg, exp_avg_sq, lr: float, beta1: float, be
         _lib.check(_lib.load().m3s_adamw(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_adamw")
 
 
+def wgrad_supported(a: Tensor, b: Tensor) -> bool:
+    """Whether `wgrad` takes these operands: bf16 device matrices of one device with unit
+    column stride, 16-byte aligned rows, a token count that is a multiple of 32 and
+    operands under 2 GiB."""
+    if not (a.is_cuda and b.is_cuda and a.dtype == b.dtype == torch.bfloat16
+            and a.dim() == b.dim() == 2 and a.device == b.device and a.shape[0] == b.shape[0]):
+        return False
+    m = a.shape[0]
+    if m == 0 or m % 32 or a.shape[1] == 0 or b.shape[1] == 0:
+        return False
+    for t in (a, b):
+        if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16 or t.stride(0) < t.shape[1]:
+            return False
+        if ((m - 1) * t.stride(0) + t.shape[1]) * 2 >= 1 << 31:
+            return False
+    return True
+
+
+def wgrad(a: Tensor, b: Tensor) -> Tensor:
+    """``a^T b`` in float32 for token-major bf16 ``a (M, P)`` and ``b (M, Q)``: a
+    projection's weight gradient (one ``m3s_wgrad`` call: MFMA tiles over token splits,
+    the split partials added in a fixed order). Operands must pass `wgrad_supported`."""
+    if not wgrad_supported(a, b):
+        raise ValueError("wgrad: a (M, P) and b (M, Q) must be bf16 device matrices with unit "
+                         "column stride, 16-byte aligned rows and M a multiple of 32")
+    lib = _lib.load()
+    m, p, q = a.shape[0], a.shape[1], b.shape[1]
+    c = torch.empty(p, q, device=a.device, dtype=torch.float32)
+    nbytes = lib.m3s_wgrad_workspace_bytes(m, p, q)
+    if nbytes < 0:
+        raise ValueError(f"wgrad: bad shape {(m, p, q)}")
+    ws = torch.empty(max(nbytes // 4, 1), device=a.device, dtype=torch.float32)
+    w = _lib.WgradArgs()
+    w.struct_size = ctypes.sizeof(_lib.WgradArgs)
+    w.tokens, w.rows, w.cols = m, p, q
+    w.a, w.lda = a.data_ptr(), a.stride(0)
+    w.b, w.ldb = b.data_ptr(), b.stride(0)
+    w.c, w.ldc = c.data_ptr(), q
+    w.workspace = ws.data_ptr() if nbytes > 0 else None
+    with torch.cuda.device(a.device):
+        _lib.check(lib.m3s_wgrad(ctypes.byref(w), _lib.stream_handle(a.device)), "m3s_wgrad")
+    return c
+
+
 def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype,
                 add: Optional[Tensor] = None):
     """LM block norm: ``x`` (..., D) in f32 or bf16 -> ``(y (..., D) in out_dtype, rstd

@@ -191,13 +191,19 @@ def _fused_ok(u: Tensor, cfg: SISOConfig, state) -> bool:
 def weight_grad(a: Tensor, b: Tensor) -> Tensor:
     """``a^T b`` in float32 for ``(M, P)`` and ``(M, Q)`` operands over the M tokens: the
     weight gradient of a projection. Its output is small (P x Q) and its reduction long
-    (M = B*L), so one library GEMM has too few output tiles to fill the GPU; with M a
-    multiple of 8 and at least 16384 the tokens are cut into 8 slices, one batched GEMM
-    forms the 8 partial products (float32 out) and they are summed in slice order. The
-    right operand is never a transposed view (a column slice is a strided row view)."""
+    (M = B*L), so one library GEMM has too few output tiles to fill the GPU.
+
+    bf16 device operands that `kernels.wgrad_supported` takes go to ``m3s_wgrad`` (MFMA
+    tiles over token splits sized to fill the CUs, partials added in a fixed order). Else,
+    with M a multiple of 8 and at least 16384, the tokens are cut into 8 slices, one
+    batched GEMM forms the 8 partial products (float32 out) and they are summed in slice
+    order. The right operand is never a transposed view (a column slice is a strided row
+    view)."""
     m = a.shape[0]
     if a.dtype != b.dtype or a.dim() != 2 or b.dim() != 2 or b.shape[0] != m:
         raise ValueError("weight_grad: a (M, P) and b (M, Q) of one dtype")
+    if K.wgrad_supported(a, b):
+        return K.wgrad(a, b)
     if m % 8 or m < 16384 or not a.is_cuda:
         if a.dtype == torch.float32 or not a.is_cuda:
             return (a.t() @ b).float()

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 6
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 7
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -63,6 +63,8 @@ int main(void) {
          offsetof(m3s_rms_args, workspace));
   printf("%zu %zu %zu\n", sizeof(m3s_adamw_args), offsetof(m3s_adamw_args, grad_scale),
          offsetof(m3s_adamw_args, bias_correction2_sqrt));
+  printf("%zu %zu %zu\n", sizeof(m3s_wgrad_args), offsetof(m3s_wgrad_args, ldb),
+         offsetof(m3s_wgrad_args, workspace));
   return 0;
 }
 """
@@ -92,8 +94,10 @@ int main(void) {
                             lib.SwigluArgs.dh.offset]
     assert sizes[28:31] == [ctypes.sizeof(lib.RmsArgs), lib.RmsArgs.x.offset,
                             lib.RmsArgs.workspace.offset]
-    assert sizes[31:] == [ctypes.sizeof(lib.AdamwArgs), lib.AdamwArgs.grad_scale.offset,
-                          lib.AdamwArgs.bias_correction2_sqrt.offset]
+    assert sizes[31:34] == [ctypes.sizeof(lib.AdamwArgs), lib.AdamwArgs.grad_scale.offset,
+                            lib.AdamwArgs.bias_correction2_sqrt.offset]
+    assert sizes[34:] == [ctypes.sizeof(lib.WgradArgs), lib.WgradArgs.ldb.offset,
+                          lib.WgradArgs.workspace.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -282,6 +286,37 @@ def test_rms_arguments_are_checked_without_a_launch(lib):
     assert b"aligned" in h.m3s_last_error()
     a.rows = 0
     assert h.m3s_rms_fwd(ctypes.byref(a), None) == lib.OK
+
+
+def test_wgrad_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_wgrad(None, None) == lib.ERR_INVALID
+    w = lib.WgradArgs()
+    w.struct_size = 8
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID
+    assert b"struct_size" in h.m3s_last_error()
+    w.struct_size = ctypes.sizeof(lib.WgradArgs)
+    w.tokens, w.rows, w.cols = 100, 64, 64
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID   # tokens % 32
+    assert b"multiple of 32" in h.m3s_last_error()
+    w.tokens = 4096
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID   # NULL operands
+    w.a, w.b, w.c = 0x1000, 0x2008, 0x3000
+    w.lda, w.ldb, w.ldc = 64, 64, 64
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID   # b not 16-byte aligned
+    assert b"aligned" in h.m3s_last_error()
+    w.b = 0x2000
+    w.ldb = 60
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID   # ldb too short
+    w.ldb = 64
+    # 4096 tokens over one 64 x 64 tile: split over the tokens, so a workspace is needed
+    assert h.m3s_wgrad_workspace_bytes(4096, 64, 64) > 0
+    assert h.m3s_wgrad(ctypes.byref(w), None) == lib.ERR_INVALID
+    assert b"workspace" in h.m3s_last_error()
+    assert h.m3s_wgrad_workspace_bytes(4096, 64, 0) == -1
+    assert h.m3s_wgrad_workspace_bytes(100, 64, 64) == -1
+    # one step of 32 tokens cannot be split
+    assert h.m3s_wgrad_workspace_bytes(32, 64, 64) == 0
 
 
 def test_adamw_arguments_are_checked_without_a_launch(lib):

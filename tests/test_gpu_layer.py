@@ -368,12 +368,15 @@ def test_recorded_gemm_solutions_change_only_gemm_rounding(m3):
     (65536, 2048, 1024, torch.bfloat16),   # configs[2] out_proj: 8 token slices
     (32768, 768, 520, torch.bfloat16),     # a strided column slice (in the layer: dproj[..., :d])
     (16384, 256, 96, torch.float32),       # float32 operands (the LM head)
-    (1000, 64, 32, torch.bfloat16),        # too few tokens to split: one product
+    (1000, 64, 32, torch.bfloat16),        # tokens not a multiple of 32: one library product
+    (64, 300, 40, torch.bfloat16),         # m3s_wgrad with one split, ragged 256-tiles
+    (4096, 520, 1000, torch.bfloat16),     # m3s_wgrad, several splits, ragged tiles
 ])
 def test_weight_grad_matches_float64(m3, dev, m, p, q, dtype):
-    """`layer.weight_grad` (``a^T b`` over the tokens, float32 out) against float64: the
-    split sums 8 float32 partial products in slice order; 1e-5 of max |ref| (f32
-    accumulation over up to 65536 terms), bit-identical on a second call."""
+    """`layer.weight_grad` (``a^T b`` over the tokens, float32 out) against float64: bf16
+    operands go to ``m3s_wgrad`` (token splits whose float32 partials are added in split
+    order), the others to the library split; 1e-5 of max |ref| (f32 accumulation over up
+    to 65536 terms), bit-identical on a second call."""
     g = torch.Generator().manual_seed(m + p)
     a = torch.randn(m, p, generator=g).to(dtype)
     bfull = torch.randn(m, q + 8, generator=g).to(dtype)
