@@ -25,12 +25,10 @@
 namespace m3s {
 
 constexpr int kWgT = 256;              // output tile edge (rows of P, columns of Q)
-constexpr int kWgK = 32;               // tokens per step
-#ifndef M3S_WG_WP
-#define M3S_WG_WP 4
-#define M3S_WG_WQ 2
-#endif
-constexpr int kWgWP = M3S_WG_WP, kWgWQ = M3S_WG_WQ;   // waves over rows x columns
+constexpr int kWgK = 32;               // tokens per step (a multiple of 32)
+// waves over rows x columns: 4 x 2 waves of 64 x 128 (four waves of 128 x 128, with 256
+// accumulator registers each, were no faster)
+constexpr int kWgWP = 4, kWgWQ = 2;
 constexpr int kWgThreads = 64 * kWgWP * kWgWQ;
 constexpr int kWgRT = kWgT / kWgWP / 16, kWgCT = kWgT / kWgWQ / 16;   // 16 x 16 tiles per wave
 constexpr int kWgPieces = kWgK * kWgT / 8 / kWgThreads;   // 16-byte pieces per thread per operand
@@ -117,21 +115,24 @@ __global__ void __launch_bounds__(kWgThreads) wgrad_kernel(const WgParams p) {
   auto compute = [&](int st) {
     const bf16* sa = lds + st * kWgStage;
     const bf16* sb = sa + kWgK * kWgLd;
-    bf16x4 a0[kWgRT], a1[kWgRT], b0[kWgCT], b1[kWgCT];
 #pragma unroll
-    for (int i = 0; i < kWgRT; ++i) {
-      a0[i] = ld_tr4(sa, kWgLd, kh0, wp * 16 * kWgRT + 16 * i, lane);
-      a1[i] = ld_tr4(sa, kWgLd, kh1, wp * 16 * kWgRT + 16 * i, lane);
-    }
+    for (int k = 0; k < kWgK; k += 32) {
+      bf16x4 a0[kWgRT], a1[kWgRT], b0[kWgCT], b1[kWgCT];
 #pragma unroll
-    for (int j = 0; j < kWgCT; ++j) {
-      b0[j] = ld_tr4(sb, kWgLd, kh0, wq * 16 * kWgCT + 16 * j, lane);
-      b1[j] = ld_tr4(sb, kWgLd, kh1, wq * 16 * kWgCT + 16 * j, lane);
-    }
+      for (int i = 0; i < kWgRT; ++i) {
+        a0[i] = ld_tr4(sa, kWgLd, k + kh0, wp * 16 * kWgRT + 16 * i, lane);
+        a1[i] = ld_tr4(sa, kWgLd, k + kh1, wp * 16 * kWgRT + 16 * i, lane);
+      }
 #pragma unroll
-    for (int i = 0; i < kWgRT; ++i) {
+      for (int j = 0; j < kWgCT; ++j) {
+        b0[j] = ld_tr4(sb, kWgLd, k + kh0, wq * 16 * kWgCT + 16 * j, lane);
+        b1[j] = ld_tr4(sb, kWgLd, k + kh1, wq * 16 * kWgCT + 16 * j, lane);
+      }
 #pragma unroll
-      for (int j = 0; j < kWgCT; ++j) mma32(acc[i][j], a0[i], a1[i], b0[j], b1[j]);
+      for (int i = 0; i < kWgRT; ++i) {
+#pragma unroll
+        for (int j = 0; j < kWgCT; ++j) mma32(acc[i][j], a0[i], a1[i], b0[j], b1[j]);
+      }
     }
   };
 
@@ -145,10 +146,13 @@ __global__ void __launch_bounds__(kWgThreads) wgrad_kernel(const WgParams p) {
     swrite(0);
     if (n > 1) gload(k0 + 1);
     for (int it = 0; it < n; ++it) {
-      __syncthreads();   // stage it & 1 is written; stage (it + 1) & 1 is no longer read
+      // after this barrier stage it & 1 holds step it, and every wave is done reading
+      // stage (it + 1) & 1 (step it - 1), which is refilled after this step's products:
+      // the fragment reads start right after the barrier, not behind a burst of writes
+      __syncthreads();
+      compute(it & 1);
       if (it + 1 < n) swrite((it + 1) & 1);
       if (it + 2 < n) gload(k0 + it + 2);
-      compute(it & 1);
     }
   }
 
