@@ -136,10 +136,9 @@ __global__ void __launch_bounds__(kWgThreads) wgrad_kernel(const WgParams p) {
     }
   };
 
-  // Step k is read from LDS stage k & 1. At the top of step k (after the barrier) the
-  // other stage is free, step k + 1 is written there from its register set, and that set
-  // is refilled with step k + 3; step k + 2 is in flight in the other set. Unrolled by two
-  // so that each register set is a fixed set of registers.
+  // Step k is read from LDS stage k & 1; step k + 1 waits in registers (loaded during
+  // step k - 1) and goes to the other stage after step k's products, then step k + 2's
+  // loads are issued into the same registers.
   const int n = k1 - k0;
   if (n > 0) {
     gload(k0);
