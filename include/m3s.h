@@ -409,7 +409,8 @@ int64_t m3s_bwd_workspace_bytes(int32_t dtype, int32_t batch, int32_t seqlen, in
                                 int32_t state_dim);
 
 /* Bytes of m3s_prep_fwd_args.workspace: the tanh(angles) pi table (B, L, Nr) and the
- * per-block theta totals (B, ceil(L/64), H, Nr), f32. No counterpart in the reference.
+ * theta totals per 16-token strip (B, ceil(L/16), H, Nr), f32 (per 64-token block when phi
+ * itself is written). No counterpart in the reference.
  * -1 on bad dimensions. */
 int64_t m3s_prep_fwd_workspace_bytes(int32_t batch, int32_t seqlen, int32_t nheads,
                                      int32_t n_angles);

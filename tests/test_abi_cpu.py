@@ -158,7 +158,7 @@ def test_prep_arguments_are_checked_without_a_launch(lib):
     # the backward's blocks are 32 tokens: 256 per sequence at L=8192
     assert h.m3s_prep_bwd_workspace_bytes(8, 8192, 32, 32) == 8 * 256 * 32 * 32 * 4 + 8 * 256 * 32 * 4
     assert h.m3s_prep_bwd_workspace_bytes(0, 8, 1, 1) == -1
-    assert h.m3s_prep_fwd_workspace_bytes(8, 8192, 32, 32) == 8 * 8192 * 32 * 4 + 8 * 128 * 32 * 32 * 4
+    assert h.m3s_prep_fwd_workspace_bytes(8, 8192, 32, 32) == 8 * 8192 * 32 * 4 + 8 * 512 * 32 * 32 * 4
     assert h.m3s_prep_fwd_workspace_bytes(1, 8, 1, -1) == -1
 
 
