@@ -54,8 +54,13 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
 // of each XCD's workgroups (block i runs on XCD i % 8, so i / 8 counts within one XCD)
 // by a fraction of a chunk's time spreads that traffic over the chunk: group
 // g = (i / 8) % groups (groups a power of two) first sleeps g * units * ~2048 cycles
-// (s_sleep 32 is 32 * 64 cycles). The cost is that delay, once.
+// (s_sleep 32 is 32 * 64 cycles). The cost is that delay, once. Only the first round of
+// a launch starts in step (one scan workgroup per CU, 256 CUs on MI355X); a workgroup of
+// a later round starts when one of the first ends, already out of phase, so it does not
+// sleep (cfg5's backward, 384 workgroups: 0.794 -> 0.786 ms).
+constexpr int kFirstRound = 256;
 __device__ __forceinline__ void stagger_start(int bid, int groups, int units) {
+  if (bid >= kFirstRound) return;
   const int g = (bid >> 3) & (groups - 1);
   for (int i = 0; i < g * units; ++i) __builtin_amdgcn_s_sleep(32);
 }
