@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 7
+#define M3S_ABI_VERSION 8
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -393,6 +393,22 @@ typedef struct m3s_wgrad_args {
   void* workspace;      /* the split partials, or NULL when one split */
 } m3s_wgrad_args;
 
+/* A projection of a one-token decode step: y (rows, n) = x (rows, k) w (k, n), bf16 in and
+ * out, float32 accumulation, for 1 <= rows <= 4. Replaces, in the decode step, the per-token
+ * projections of the reference's layer and LM step (model.py:266-296: in_proj, out_proj,
+ * fc1, fc2), left to XLA there. n a multiple of 8; k <= 4096; w 16-byte aligned with ldw a
+ * multiple of 8. Row strides are in elements. Deterministic (fixed summation order). */
+typedef struct m3s_gemv_args {
+  int32_t struct_size;  /* sizeof(m3s_gemv_args) */
+  int32_t rows, k, n;
+  const void* x;        /* (rows, k) bf16 */
+  int64_t ldx;
+  const void* w;        /* (k, n) bf16 */
+  int64_t ldw;
+  void* y;              /* out (rows, n) bf16 */
+  int64_t ldy;
+} m3s_gemv_args;
+
 /* Library identity; no counterpart in the reference. */
 int32_t m3s_abi_version(void);
 /* Message for the last non-zero return on this thread ("" if none). */
@@ -453,6 +469,7 @@ int32_t m3s_adamw(const m3s_adamw_args* args, void* stream);
  * dimensions. No counterpart in the reference. */
 int64_t m3s_wgrad_workspace_bytes(int32_t tokens, int32_t rows, int32_t cols);
 int32_t m3s_wgrad(const m3s_wgrad_args* args, void* stream);
+int32_t m3s_gemv(const m3s_gemv_args* args, void* stream);
 
 #ifdef __cplusplus
 }

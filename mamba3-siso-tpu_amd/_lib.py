@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -186,13 +186,20 @@ class WgradArgs(C.Structure):
     ]
 
 
+class GemvArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32), ("rows", i32), ("k", i32), ("n", i32),
+        ("x", vp), ("ldx", i64), ("w", vp), ("ldw", i64), ("y", vp), ("ldy", i64),
+    ]
+
+
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
            "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes",
-           "m3s_norm_bwd_noalloc", "m3s_adamw", "m3s_wgrad", "m3s_wgrad_workspace_bytes")
+           "m3s_norm_bwd_noalloc", "m3s_adamw", "m3s_wgrad", "m3s_wgrad_workspace_bytes", "m3s_gemv")
 
 _lib = None
 
@@ -255,6 +262,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_wgrad.argtypes = [C.POINTER(WgradArgs), vp]
     lib.m3s_wgrad_workspace_bytes.restype = i64
     lib.m3s_wgrad_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.m3s_gemv.restype = i32
+    lib.m3s_gemv.argtypes = [C.POINTER(GemvArgs), vp]
     ver = lib.m3s_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")

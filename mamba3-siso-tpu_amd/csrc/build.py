@@ -17,7 +17,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 SOURCES = ["m3s_abi.hip", "m3s_fwd.hip", "m3s_bwd.hip", "m3s_decode.hip", "m3s_prep.hip",
            "m3s_norm.hip", "m3s_layout.hip", "m3s_mlp.hip",
-           "m3s_rms.hip", "m3s_optim.hip", "m3s_wgrad.hip"]
+           "m3s_rms.hip", "m3s_optim.hip", "m3s_wgrad.hip", "m3s_gemv.hip"]
 LIB = os.path.join(HERE, "libm3s.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

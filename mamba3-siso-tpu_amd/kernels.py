@@ -882,6 +882,51 @@ def wgrad(a: Tensor, b: Tensor) -> Tensor:
     return c
 
 
+def gemv_supported(x: Tensor, w: Tensor) -> bool:
+    """Whether `gemv` takes ``x @ w``: bf16 device operands on one device, 1 to 4 rows
+    with unit column stride, ``w`` ``(K, N)`` row-major with N a multiple of 8, 16-byte
+    aligned rows and K at most 4096."""
+    if not (x.is_cuda and w.is_cuda and x.dtype == w.dtype == torch.bfloat16
+            and x.dim() == 2 and w.dim() == 2 and x.device == w.device):
+        return False
+    m, k = x.shape
+    kw, n = w.shape
+    return (1 <= m <= 4 and k == kw and 0 < k <= 4096 and n > 0 and n % 8 == 0
+            and x.stride(1) == 1 and w.stride(1) == 1 and w.stride(0) % 8 == 0
+            and w.data_ptr() % 16 == 0)
+
+
+def gemv(x: Tensor, w: Tensor) -> Tensor:
+    """``x @ w`` for a decode step's few rows (one ``m3s_gemv`` launch: a single streaming
+    pass over the weight, float32 accumulation, bf16 out). Operands must pass
+    `gemv_supported`."""
+    if not gemv_supported(x, w):
+        raise ValueError("gemv: x (1..4, K) and w (K, N) must be bf16 device matrices with "
+                         "unit column stride, N % 8 == 0, 16-byte aligned w rows, K <= 4096")
+    m, k = x.shape
+    n = w.shape[1]
+    y = torch.empty(m, n, device=x.device, dtype=torch.bfloat16)
+    a = _lib.GemvArgs()
+    a.struct_size = ctypes.sizeof(_lib.GemvArgs)
+    a.rows, a.k, a.n = m, k, n
+    a.x, a.ldx = x.data_ptr(), x.stride(0) if m > 1 else k
+    a.w, a.ldw = w.data_ptr(), w.stride(0)
+    a.y, a.ldy = y.data_ptr(), n
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().m3s_gemv(ctypes.byref(a), _lib.stream_handle(x.device)),
+                   "m3s_gemv")
+    return y
+
+
+def matmul(x: Tensor, w: Tensor) -> Tensor:
+    """``x @ w``: through `gemv` for one or two rows that it takes (a decode step's
+    projections: inside a recorded decode step 3.6-4 us against the library's 5.8-8.5 us
+    at the LM's widths), else the library product. Four rows are faster in the library."""
+    if x.dim() == 2 and x.shape[0] <= 2 and gemv_supported(x, w):
+        return gemv(x, w)
+    return x @ w
+
+
 def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype,
                 add: Optional[Tensor] = None):
     """LM block norm: ``x`` (..., D) in f32 or bf16 -> ``(y (..., D) in out_dtype, rstd

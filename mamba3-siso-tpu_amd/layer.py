@@ -361,7 +361,7 @@ def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,
     place by the decode kernel (the reference donates it). When ``u`` is in the policy's
     operand dtype, everything between the two projections (BCNorm, dt / lambda / a, the
     state update and readout) is one ``m3s_decode_layer`` launch on the projection rows."""
-    proj = u @ params.in_proj.to(u.dtype)
+    proj = K.matmul(u, params.in_proj.to(u.dtype))
     if _decode_fused_ok(u, cfg):
         y, st = K.decode_layer_step(
             proj, state, nheads=cfg.nheads, headdim=cfg.headdim, state_dim=cfg.d_state,
@@ -379,5 +379,5 @@ def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,
         y, st = K.decode_step(c, b, x[:, 0], a * dt, dt, lam, angles[:, 0], params.c_bias,
                               params.b_bias, state, d_skip=params.d_skip, z=z[:, 0],
                               dtype_policy=cfg.policy_name)
-    out = y.reshape(u.shape[0], cfg.d_inner).to(u.dtype) @ params.out_proj.to(u.dtype)
+    out = K.matmul(y.reshape(u.shape[0], cfg.d_inner).to(u.dtype), params.out_proj.to(u.dtype))
     return out, st

@@ -103,7 +103,7 @@ class _MatmulFn(torch.autograd.Function):
         xd, wd = x.to(dt), w.to(dt)
         ctx.save_for_backward(xd, wd)
         ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
-        return xd @ wd
+        return K.matmul(xd, wd)
 
     @staticmethod
     def backward(ctx, dy):

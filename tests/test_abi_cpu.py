@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 7
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 8
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -65,6 +65,8 @@ int main(void) {
          offsetof(m3s_adamw_args, bias_correction2_sqrt));
   printf("%zu %zu %zu\n", sizeof(m3s_wgrad_args), offsetof(m3s_wgrad_args, ldb),
          offsetof(m3s_wgrad_args, workspace));
+  printf("%zu %zu %zu\n", sizeof(m3s_gemv_args), offsetof(m3s_gemv_args, ldw),
+         offsetof(m3s_gemv_args, ldy));
   return 0;
 }
 """
@@ -96,8 +98,10 @@ int main(void) {
                             lib.RmsArgs.workspace.offset]
     assert sizes[31:34] == [ctypes.sizeof(lib.AdamwArgs), lib.AdamwArgs.grad_scale.offset,
                             lib.AdamwArgs.bias_correction2_sqrt.offset]
-    assert sizes[34:] == [ctypes.sizeof(lib.WgradArgs), lib.WgradArgs.ldb.offset,
-                          lib.WgradArgs.workspace.offset]
+    assert sizes[34:37] == [ctypes.sizeof(lib.WgradArgs), lib.WgradArgs.ldb.offset,
+                            lib.WgradArgs.workspace.offset]
+    assert sizes[37:] == [ctypes.sizeof(lib.GemvArgs), lib.GemvArgs.ldw.offset,
+                          lib.GemvArgs.ldy.offset]
 
 
 def test_null_and_stale_args_are_rejected_without_a_launch(lib):
@@ -317,6 +321,30 @@ def test_wgrad_arguments_are_checked_without_a_launch(lib):
     assert h.m3s_wgrad_workspace_bytes(100, 64, 64) == -1
     # one step of 32 tokens cannot be split
     assert h.m3s_wgrad_workspace_bytes(32, 64, 64) == 0
+
+
+def test_gemv_arguments_are_checked_without_a_launch(lib):
+    h = lib.load()
+    assert h.m3s_gemv(None, None) == lib.ERR_INVALID
+    a = lib.GemvArgs()
+    a.struct_size = 4
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID
+    assert b"struct_size" in h.m3s_last_error()
+    a.struct_size = ctypes.sizeof(lib.GemvArgs)
+    a.rows, a.k, a.n = 5, 64, 64
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # rows > 4
+    a.rows = 1
+    a.n = 60
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # n % 8
+    a.n = 64
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # NULL operands
+    a.x, a.w, a.y = 0x1000, 0x2008, 0x3000
+    a.ldx, a.ldw, a.ldy = 64, 64, 64
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # w misaligned
+    assert b"aligned" in h.m3s_last_error()
+    a.w = 0x2000
+    a.k, a.ldx = 5000, 5000
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # k > 4096
 
 
 def test_adamw_arguments_are_checked_without_a_launch(lib):

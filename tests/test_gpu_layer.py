@@ -387,3 +387,25 @@ def test_weight_grad_matches_float64(m3, dev, m, p, q, dtype):
     err = ((got.cpu().double() - ref).abs().max() / ref.abs().max()).item()
     assert err <= 1e-5, err
     assert torch.equal(got, m3.layer.weight_grad(ad, bd))
+
+
+@pytest.mark.parametrize("m,k,n,ldw", [
+    (1, 768, 3432, 3432),    # the LM's in_proj at one row
+    (2, 1536, 768, 776),     # out_proj / fc2 widths, a padded weight row stride
+    (1, 4096, 8, 8),         # the longest reduction the kernel takes
+    (3, 40, 24, 24),         # three rows, fewer rows than the row lanes
+    (4, 1000, 1000, 1000),   # four rows, ragged column tiles
+])
+def test_gemv_matches_float64(m3, dev, m, k, n, ldw):
+    """``m3s_gemv`` (a decode step's projection) against float64: bf16 output, so within
+    one bf16 rounding of max |ref| (2^-8), bit-identical on a second call."""
+    g = torch.Generator().manual_seed(m + k + n)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    wfull = (torch.randn(k, ldw, generator=g) / k ** 0.5).to(torch.bfloat16)
+    xd, wd = x.to(dev), wfull.to(dev)[:, :n]
+    got = m3.kernels.gemv(xd, wd)
+    ref = x.double() @ wfull[:, :n].double()
+    assert got.dtype == torch.bfloat16 and got.shape == (m, n)
+    err = ((got.cpu().double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 2 ** -8, err
+    assert torch.equal(got, m3.kernels.gemv(xd, wd))
