@@ -118,8 +118,9 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); every GPU box in "
-              "this build has one GPU, and the scan shards over (batch, head) with no "
-              "communication -- see DESIGN.md for how it would shard.", file=sys.stderr)
+              "this build has one GPU. The scan shards over (batch, head) with no "
+              "communication: each GPU would run these kernels on its B/n share, and training "
+              "would add one data-parallel all-reduce of the layer gradients.", file=sys.stderr)
         sys.exit(2)
 
     import torch
