@@ -40,12 +40,14 @@ def parse():
     ap.add_argument("--default-gemms", action="store_true",
                     help="leave the library GEMMs on hipBLASLt's default heuristic instead of "
                          "the recorded solutions (gemm_tuning.enable)")
-    ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy", "lm"), default="all",
+    ap.add_argument("--leg", choices=("all", "scan", "bwd", "decode", "copy", "lm", "wgrad"),
+                    default="all",
                     help="run one leg alone (for rocprofv3 counter passes): 'scan' = the forward "
                          "scan kernel at the kernel boundary, 'bwd' = the backward scan kernel, "
                          "'decode' = the decode kernel, 'copy' = a plain 1 GiB device copy that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters, 'lm' = the configs[4] "
-                         "byte-LM training step and the LM decode stack")
+                         "byte-LM training step and the LM decode stack, 'wgrad' = the "
+                         "weight-gradient kernel at the configs[4] in_proj shape")
     return ap.parse_args()
 
 
@@ -147,6 +149,21 @@ def main():
         ms = gpu_time_ms(lambda: dst.copy_(src), 10, torch)
         print(json.dumps({"leg": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30,
                           "ms": round(ms, 4), "gbs": round(2 * (1 << 30) / (ms * 1e-3) / 1e9, 1)}))
+        return
+
+    if args.leg == "wgrad":
+        # m3s_wgrad at the configs[4] in_proj weight gradient: u (B*L, 768) bf16 against
+        # the projection gradient's 3432 used columns of a 3584-wide buffer
+        gw = torch.Generator(device=dev).manual_seed(0)
+        m, pw, qw, ldq = 16 * 2048, 768, 3432, 3584
+        a = torch.randn(m, pw, generator=gw, device=dev).to(torch.bfloat16)
+        b = torch.randn(m, ldq, generator=gw, device=dev).to(torch.bfloat16)[:, :qw]
+        for _ in range(args.warmup + args.steps):
+            K.wgrad(a, b)
+        torch.cuda.synchronize()
+        ms = min(gpu_time_ms(lambda: K.wgrad(a, b), max(args.steps, 10), torch) for _ in range(2))
+        print(json.dumps({"leg": "wgrad", "shape": [m, pw, qw], "ms": round(ms, 4),
+                          "tflops": round(2 * m * pw * qw / (ms * 1e-3) / 1e12, 1)}))
         return
 
     if args.leg == "lm":
