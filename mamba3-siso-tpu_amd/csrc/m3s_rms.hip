@@ -75,7 +75,41 @@ __global__ void __launch_bounds__(kRmsThreads) rms_fwd_kernel(const TX* __restri
     }
     return v;
   };
+  TY* yr = y + r * D;
   float ss = 0.f;
+  if (D <= 4 * 256) {
+    // rows up to 1024 wide stay in registers between the two passes (at most four
+    // 16-byte pieces per lane), and every load of the row is issued before the sum
+    // (with the residual at 32768 x 768: 0.065 -> 0.053 ms; one row 3.1 -> 2.8 us)
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = 4 * lane + 256 * k;
+      v[k] = c < D ? row(c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = 4 * lane + 256 * k;
+      if (c < D && ar) st4(sum + r * D + c, v[k]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss += v[k][i] * v[k][i];
+    }
+    ss = wave_total(ss);
+    const float rs = 1.f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = 4 * lane + 256 * k;
+      if (c < D) {
+        const f32x4 g = *reinterpret_cast<const f32x4*>(w + c);
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = v[k][i] * rs * g[i];
+        st4(yr + c, o);
+      }
+    }
+    if (lane == 0 && rstd) rstd[r] = rs;
+    return;
+  }
   for (int c = 4 * lane; c < D; c += 256) {
     const f32x4 v = row(c);
     if (ar) st4(sum + r * D + c, v);
@@ -84,7 +118,6 @@ __global__ void __launch_bounds__(kRmsThreads) rms_fwd_kernel(const TX* __restri
   }
   ss = wave_total(ss);
   const float rs = 1.f / sqrtf(ss / (float)D + eps);
-  TY* yr = y + r * D;
   for (int c = 4 * lane; c < D; c += 256) {
     const f32x4 v = row(c);
     const f32x4 g = *reinterpret_cast<const f32x4*>(w + c);
