@@ -457,7 +457,11 @@ int32_t m3s_norm_bwd(const m3s_norm_bwd_args* args, void* stream);
  * (enough for every width m3s_norm_bwd accepts, at most 512), held until the process
  * ends; args->workspace is ignored and nothing is allocated or freed. Calls that overlap
  * on one GPU (different streams, or threads) share that array and race: serialise them.
- * Widths the array cannot hold are rejected with M3S_ERR_INVALID. */
+ * Widths the array cannot hold are rejected with M3S_ERR_INVALID. The array's device
+ * address is looked up on a device's first call and kept for the life of the process: it
+ * stays valid until that device is reset (hipDeviceReset unloads the code object that
+ * holds the array), so a caller that resets a device must reload the library before
+ * calling this again. */
 int32_t m3s_norm_bwd_noalloc(const m3s_norm_bwd_args* args, void* stream);
 int32_t m3s_transpose(const m3s_transpose_args* args, void* stream);
 int32_t m3s_swiglu_fwd(const m3s_swiglu_args* args, void* stream);

@@ -59,17 +59,19 @@ def config_to_dict(cfg: M.LMConfig) -> dict:
 
 
 def config_from_dict(d: dict) -> M.LMConfig:
-    """Inverse of `config_to_dict` (``checkpoint.py:94-116``): unknown ``siso`` keys are
-    dropped, missing ones take `SISOConfig`'s defaults; a newer format version raises."""
-    got = d.get("format_version", 0)
-    if got > FORMAT_VERSION:
-        raise ValueError(f"checkpoint format version {got} is newer than this package "
-                         f"supports ({FORMAT_VERSION})")
-    fields = {f.name for f in dataclasses.fields(LY.SISOConfig)}
-    kw = {k: v for k, v in d["siso"].items() if k in fields}
-    return M.LMConfig(vocab_size=int(d["vocab_size"]), n_layers=int(d["n_layers"]),
-                      siso=LY.SISOConfig(**kw), tie_head=bool(d["tie_head"]),
-                      d_intermediate=int(d.get("d_intermediate", 0)))
+    """Inverse of `config_to_dict` (``checkpoint.py:94-116``). ``siso`` entries that
+    `SISOConfig` does not define are ignored and absent ones keep its defaults, so files
+    from a writer with more (or fewer) config fields still load. A file whose layout
+    version is above `FORMAT_VERSION` is refused."""
+    version = int(d.get("format_version", 0))
+    if version > FORMAT_VERSION:
+        raise ValueError(f"unsupported checkpoint layout v{version} (this reader handles "
+                         f"layouts up to v{FORMAT_VERSION})")
+    defined = LY.SISOConfig.__dataclass_fields__
+    siso = LY.SISOConfig(**{k: d["siso"][k] for k in defined if k in d["siso"]})
+    top = dict(vocab_size=int(d["vocab_size"]), n_layers=int(d["n_layers"]),
+               tie_head=bool(d["tie_head"]), d_intermediate=int(d.get("d_intermediate", 0)))
+    return M.LMConfig(siso=siso, **top)
 
 
 def _to_array(t: torch.Tensor, dtype) -> tuple[np.ndarray, str]:
@@ -106,31 +108,42 @@ def save(path: str, params: M.LMParams, cfg: M.LMConfig, dtype: Any = None) -> s
     return path if path.endswith(".npz") else path + ".npz"
 
 
+def _manifest_problems(files: set, expected: dict) -> list:
+    """What keeps an npz's arrays from matching the tree its config implies: expected
+    names it lacks, then names it has beyond those, as readable strings."""
+    lacking = [n for n in expected if n not in files]
+    surplus = sorted(files - set(expected) - {CONFIG_KEY})
+    out = [f"is missing array {n!r}" for n in lacking]
+    if surplus:
+        out.append(f"holds arrays the config does not define (unexpected arrays): {surplus}")
+    return out
+
+
 def load(path: str, dtype: Any = None, device=None) -> tuple:
     """Read a checkpoint written by `save` -> ``(params, cfg)`` (``checkpoint.py:166-204``).
-    The stored config rebuilds the tree; every array it implies must be present with the
-    implied shape, and no other array may be, else ``ValueError``. ``dtype`` casts on load
-    (``torch.float32`` widens a bf16 file)."""
+    The file's own config rebuilds the tree (`model.lm_template`); the arrays must be
+    exactly that tree's leaves, each of its leaf's shape, else ``ValueError``. ``dtype``
+    casts on load (``torch.float32`` widens a bf16 file)."""
     with np.load(path, allow_pickle=False) as z:
-        if CONFIG_KEY not in z.files:
-            raise ValueError(f"{path} has no {CONFIG_KEY} entry; not a Mamba-3 SISO checkpoint")
+        files = set(z.files)
+        if CONFIG_KEY not in files:
+            raise ValueError(f"{path}: no {CONFIG_KEY} record, so this npz is not a "
+                             f"Mamba-3 SISO checkpoint")
         meta = json.loads(bytes(z[CONFIG_KEY]).decode("utf-8"))
         cfg = config_from_dict(meta)
-        stored = meta.get("dtypes", {})
         template = M.lm_template(cfg)
-        named = _named_leaves(template)
-        got: dict[str, torch.Tensor] = {}
-        for name, ref in named:
-            if name not in z.files:
-                raise ValueError(f"{path} is missing array {name!r}")
-            a = z[name]
-            if tuple(a.shape) != tuple(ref.shape):
-                raise ValueError(f"{name}: checkpoint has shape {a.shape}, config implies "
-                                 f"{tuple(ref.shape)}")
-            t = _from_array(a, stored.get(name, str(a.dtype)))
-            got[name] = t.to(device=device, dtype=dtype) if (dtype or device) else t
-        extra = set(z.files) - {CONFIG_KEY} - set(got)
-        if extra:
-            raise ValueError(f"{path} has unexpected arrays: {sorted(extra)}")
-    name_of = {id(ref): name for name, ref in named}
-    return M.lm_map(lambda ref: got[name_of[id(ref)]], template), cfg
+        expected = dict(_named_leaves(template))
+        problems = _manifest_problems(files, expected)
+        if problems:
+            raise ValueError(f"{path} " + "; ".join(problems))
+        recorded = meta.get("dtypes", {})
+        tensors: dict[str, torch.Tensor] = {}
+        for name, leaf in expected.items():
+            arr = z[name]
+            if arr.shape != tuple(leaf.shape):
+                raise ValueError(f"array {name!r} is {arr.shape} on disk but {tuple(leaf.shape)} "
+                                 f"under the stored config (shape mismatch)")
+            t = _from_array(arr, recorded.get(name, str(arr.dtype)))
+            tensors[name] = t.to(device=device, dtype=dtype) if (dtype or device) else t
+    by_id = {id(leaf): name for name, leaf in expected.items()}
+    return M.lm_map(lambda leaf: tensors[by_id[id(leaf)]], template), cfg

@@ -924,6 +924,9 @@ struct Bwd2Cfg {
 template <int C, int N, int P, bool STRIPS>
 __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p) {
   using F = Bwd2Cfg<C, N, P>;
+  // the in-strip angle prefix (angles_to_turns) shuffles over the 8 row pairs of a strip,
+  // which must be lanes QKG apart in one wave
+  static_assert(!STRIPS || 8 * F::QKG <= 64, "a strip's row pairs span more than one wave");
   using vec = bf16x8;
   constexpr int NW = F::NW, NT = F::NT, VEC = F::VEC, H2 = F::H2;
   constexpr int LDQ = F::LDQ, LDP = F::LDP, LDF = F::LDF;
@@ -1808,7 +1811,8 @@ template <typename MT, int C, int N, int P>
 static int32_t launch_bwd(const BwdParams& prm, int grid, hipStream_t stream) {
   bool done = false;
   const bool strips = prm.pstr != nullptr;
-  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0 && C <= N) {
+  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0 && C <= N &&
+                N / 16 <= 8) {   // N <= 128: a strip's row pairs in one wave (phi strips)
     if (bwd_fits_rsrc(prm, N, P)) {
       if (strips)
         hipLaunchKernelGGL((bwd_bf16_kernel<C, N, P, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);

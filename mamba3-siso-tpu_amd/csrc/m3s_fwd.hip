@@ -1414,13 +1414,22 @@ static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   const bool strips = prm.pstr != nullptr;
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
     if (fits_rsrc(prm, N, P)) {
-      if (strips && (prm.Nr <= 32 || N / 64 < 2))
+      // phi strips: NRB 32-column blocks hold the rotary pairs (Nr <= 32 NRB); only
+      // NRB = 1 and 2 are compiled, so Nr > 64 takes the generic kernel below
+      if (strips && prm.Nr <= 32) {
         hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 1>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
-      else if (strips)
-        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, (N / 64 >= 2 ? 2 : 1)>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
-      else
+        return launch_status("m3s_fwd");
+      }
+      if constexpr (N / 64 >= 2) {
+        if (strips && prm.Nr <= 64) {
+          hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 2>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+          return launch_status("m3s_fwd");
+        }
+      }
+      if (!strips) {
         hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 0>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
-      return launch_status("m3s_fwd");
+        return launch_status("m3s_fwd");
+      }
     }
   }
   {

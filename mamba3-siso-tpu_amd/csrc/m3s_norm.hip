@@ -308,7 +308,9 @@ static int32_t norm_bwd_run(const m3s_norm_bwd_args* a, const NormBwdParams& p, 
 // (kNormBwdBlocks, 2, 512) f32 = 4 MiB. A __device__ array exists once per device and
 // lives until the process ends. In host code its name is only a stand-in for the symbol,
 // so the device address is looked up (hipGetSymbolAddress) once per device, with that
-// device current, and only that address is handed to kernels.
+// device current, and only that address is handed to kernels. The kept address is valid
+// until the device is reset (hipDeviceReset unloads the code object holding the array);
+// the header tells callers that reset a device to reload the library.
 constexpr int kNormScratchWidth = 512;
 constexpr int64_t kNormScratchBytes = (int64_t)kNormBwdBlocks * 2 * kNormScratchWidth * 4;
 static __device__ __align__(256) float scratch[kNormBwdBlocks * 2 * kNormScratchWidth];

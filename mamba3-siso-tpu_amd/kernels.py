@@ -24,6 +24,26 @@ from . import layout as LY
 
 Tensor = torch.Tensor
 
+#: Test-only switch (no counterpart in the reference): when True, `empty` and
+#: `empty_like` -- which allocate every kernel output and workspace in this package --
+#: fill the new memory with all-ones bytes (NaN for float32, bfloat16 and float16), so a
+#: region a kernel fails to write, or scratch it reads before writing, surfaces as a
+#: non-finite value in the parity checks. The product path never sets it.
+POISON_OUTPUTS = False
+
+
+def empty(*size, device=None, dtype=None) -> Tensor:
+    """``torch.empty`` for kernel outputs and workspaces (see `POISON_OUTPUTS`)."""
+    t = torch.empty(*size, device=device, dtype=dtype)
+    if POISON_OUTPUTS:
+        t.view(torch.uint8).fill_(255) if t.numel() else None
+    return t
+
+
+def empty_like(x: Tensor) -> Tensor:
+    """``torch.empty_like`` for kernel outputs (see `POISON_OUTPUTS`)."""
+    return empty(x.shape, device=x.device, dtype=x.dtype)
+
 
 class PhiStrips(NamedTuple):
     """phi in the compact form the scan kernels rebuild it from (the cumulative angle of
@@ -117,8 +137,8 @@ def _empty_like_layout(v: Tensor, dtype: torch.dtype) -> Tensor:
     reshape it to ``(B, L, H*P)`` for free."""
     b, h, l, p = v.shape
     if v.stride(2) > v.stride(1):
-        return torch.empty(b, l, h, p, device=v.device, dtype=dtype).permute(0, 2, 1, 3)
-    return torch.empty(b, h, l, p, device=v.device, dtype=dtype)
+        return empty(b, l, h, p, device=v.device, dtype=dtype).permute(0, 2, 1, 3)
+    return empty(b, h, l, p, device=v.device, dtype=dtype)
 
 
 def _tile(pol: LY.DtypePolicy, chunk: int, state_dim: int, headdim: int, role: str) -> int:
@@ -254,12 +274,12 @@ def siso_forward(
     y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
     y = _empty_like_layout(vc, mt)
     f32 = dict(device=dev, dtype=torch.float32)
-    final_ssm = torch.empty(batch, nheads, headdim, state_dim, **f32)
-    final_k = torch.empty(batch, nheads, state_dim, **f32)
-    final_v = torch.empty(batch, nheads, headdim, **f32)
+    final_ssm = empty(batch, nheads, headdim, state_dim, **f32)
+    final_k = empty(batch, nheads, state_dim, **f32)
+    final_v = empty(batch, nheads, headdim, **f32)
     if save_residuals:
-        ybar = torch.empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
-        cstates = torch.empty(batch, nheads, nc, state_dim, headdim, device=dev, dtype=mt)
+        ybar = empty(batch, nheads, seqlen, headdim, device=dev, dtype=mt)
+        cstates = empty(batch, nheads, nc, state_dim, headdim, device=dev, dtype=mt)
     else:
         ybar = cstates = None
 
@@ -358,7 +378,7 @@ def siso_decode(q: Tensor, k: Tensor, v: Tensor, adt: Tensor, dt: Tensor, lam: T
     qc, kc, vc, zc = _mt(q, mt), _mt(k, mt), _mt(v, mt), _mt(z, mt)
     adt_c, dt_c, lam_c, ang_c = _f32c(adt), _f32c(dt), _f32c(lam), _f32c(angles)
     qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
-    y = torch.empty(batch, nheads, headdim, device=dev, dtype=mt)
+    y = empty(batch, nheads, headdim, device=dev, dtype=mt)
 
     a = _lib.DecodeArgs()
     a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
@@ -403,7 +423,7 @@ def decode_layer_step(proj: Tensor, state, *, nheads: int, headdim: int, state_d
     phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
     wb, wc, bias = _f32c(b_norm_weight), _f32c(c_norm_weight), _f32c(dt_bias)
     qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
-    y = torch.empty(batch, nheads, headdim, device=dev, dtype=mt)
+    y = empty(batch, nheads, headdim, device=dev, dtype=mt)
     a = _lib.DecodeLayerArgs()
     a.struct_size = ctypes.sizeof(_lib.DecodeLayerArgs)
     a.batch, a.nheads, a.headdim, a.state_dim, a.n_angles = batch, nheads, headdim, state_dim, n_angles
@@ -555,21 +575,21 @@ def siso_backward_kernel(
     dfs, dfv = _f32c(dfinal_ssm), _f32c(dfinal_v)
 
     f32 = dict(device=dev, dtype=torch.float32)
-    dq = torch.empty(batch, seqlen, state_dim, **f32)
-    dk = torch.empty(batch, seqlen, state_dim, **f32)
+    dq = empty(batch, seqlen, state_dim, **f32)
+    dk = empty(batch, seqlen, state_dim, **f32)
     dv = _out_buffer(dv_out, vc, mt, "dv_out")
     dz = _out_buffer(dz_out, zc, mt, "dz_out") if zc is not None else None
-    dadt = torch.empty(batch, nheads, seqlen, **f32)
-    dqk = torch.empty(batch, nheads, seqlen, **f32)
-    dscale = torch.empty(batch, nheads, seqlen, **f32)
-    uw = torch.empty(batch, nheads, seqlen, **f32)
-    dphi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
-    dqb = torch.empty(batch, nheads, state_dim, **f32)
-    dkb = torch.empty(batch, nheads, state_dim, **f32)
-    kfin = torch.empty(batch, nheads, state_dim, **f32)
-    dseed = torch.empty(batch, nheads, headdim, state_dim, **f32)
+    dadt = empty(batch, nheads, seqlen, **f32)
+    dqk = empty(batch, nheads, seqlen, **f32)
+    dscale = empty(batch, nheads, seqlen, **f32)
+    uw = empty(batch, nheads, seqlen, **f32)
+    dphi = empty(batch, nheads, seqlen, n_angles, **f32)
+    dqb = empty(batch, nheads, state_dim, **f32)
+    dkb = empty(batch, nheads, state_dim, **f32)
+    kfin = empty(batch, nheads, state_dim, **f32)
+    dseed = empty(batch, nheads, headdim, state_dim, **f32)
     ws_bytes = _lib.load().m3s_bwd_workspace_bytes(dcode, batch, seqlen, nheads, state_dim)
-    workspace = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    workspace = empty(ws_bytes, device=dev, dtype=torch.uint8)
 
     a = _lib.BwdArgs()
     a.struct_size = ctypes.sizeof(_lib.BwdArgs)
@@ -744,8 +764,8 @@ def bcnorm_forward(xs, weights, eps: float):
     for x in xs:
         if tuple(x.shape) != tuple(x0.shape) or x.dtype != x0.dtype or not _norm_rows_ok(x):
             raise ValueError("bcnorm inputs must share shape and dtype, with 16-byte aligned rows")
-    ys = [torch.empty(batch, seqlen, width, device=dev, dtype=x0.dtype) for _ in xs]
-    rstds = [torch.empty(batch, seqlen, device=dev, dtype=torch.float32) for _ in xs]
+    ys = [empty(batch, seqlen, width, device=dev, dtype=x0.dtype) for _ in xs]
+    rstds = [empty(batch, seqlen, device=dev, dtype=torch.float32) for _ in xs]
     ws = [_f32c(w) for w in weights]
     a = _lib.NormFwdArgs()
     a.struct_size = ctypes.sizeof(_lib.NormFwdArgs)
@@ -773,9 +793,9 @@ def bcnorm_backward(xs, weights, rstds, dys, dxs):
             raise ValueError("bcnorm gradient buffers must match the inputs, with 16-byte aligned rows")
     ws = [_f32c(w) for w in weights]
     dyc = [_f32c(d) for d in dys]
-    dws = [torch.empty(width, device=dev, dtype=torch.float32) for _ in xs]
+    dws = [empty(width, device=dev, dtype=torch.float32) for _ in xs]
     lib = _lib.load()
-    work = torch.empty(lib.m3s_norm_bwd_workspace_bytes(width), device=dev, dtype=torch.uint8)
+    work = empty(lib.m3s_norm_bwd_workspace_bytes(width), device=dev, dtype=torch.uint8)
     a = _lib.NormBwdArgs()
     a.struct_size = ctypes.sizeof(_lib.NormBwdArgs)
     a.batch, a.seqlen, a.width = batch, seqlen, width
@@ -865,11 +885,11 @@ def wgrad(a: Tensor, b: Tensor) -> Tensor:
                          "column stride, 16-byte aligned rows and M a multiple of 32")
     lib = _lib.load()
     m, p, q = a.shape[0], a.shape[1], b.shape[1]
-    c = torch.empty(p, q, device=a.device, dtype=torch.float32)
+    c = empty(p, q, device=a.device, dtype=torch.float32)
     nbytes = lib.m3s_wgrad_workspace_bytes(m, p, q)
     if nbytes < 0:
         raise ValueError(f"wgrad: bad shape {(m, p, q)}")
-    ws = torch.empty(max(nbytes // 4, 1), device=a.device, dtype=torch.float32)
+    ws = empty(max(nbytes // 4, 1), device=a.device, dtype=torch.float32)
     w = _lib.WgradArgs()
     w.struct_size = ctypes.sizeof(_lib.WgradArgs)
     w.tokens, w.rows, w.cols = m, p, q
@@ -905,7 +925,7 @@ def gemv(x: Tensor, w: Tensor) -> Tensor:
                          "unit column stride, N % 8 == 0, 16-byte aligned w rows, K <= 4096")
     m, k = x.shape
     n = w.shape[1]
-    y = torch.empty(m, n, device=x.device, dtype=torch.bfloat16)
+    y = empty(m, n, device=x.device, dtype=torch.bfloat16)
     a = _lib.GemvArgs()
     a.struct_size = ctypes.sizeof(_lib.GemvArgs)
     a.rows, a.k, a.n = m, k, n
@@ -941,8 +961,8 @@ def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype,
     x = x.contiguous()
     w = weight.float().contiguous()
     d = x.shape[-1]
-    y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
-    rstd = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    y = empty(x.shape, device=x.device, dtype=out_dtype)
+    rstd = empty(x.shape[:-1], device=x.device, dtype=torch.float32)
     a = _lib.RmsArgs()
     a.struct_size = ctypes.sizeof(_lib.RmsArgs)
     a.x_dtype, a.y_dtype = _lib.dtype_code(x.dtype), _lib.dtype_code(out_dtype)
@@ -953,7 +973,7 @@ def rms_forward(x: Tensor, weight: Tensor, eps: float, out_dtype: torch.dtype,
         if add.shape != x.shape or add.dtype != out_dtype or add.device != x.device:
             raise ValueError("rms_forward: add must match x's shape, in out_dtype, on x's device")
         add = add.contiguous()
-        s = torch.empty_like(x)
+        s = empty_like(x)
         a.add, a.sum = add.data_ptr(), s.data_ptr()
     with torch.cuda.device(x.device):
         _lib.check(_lib.load().m3s_rms_fwd(ctypes.byref(a), _lib.stream_handle(x.device)),
@@ -975,9 +995,9 @@ def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor,
     dy = dy.contiguous()
     w = weight.float().contiguous()
     d = x.shape[-1]
-    dx = torch.empty_like(x)
-    dw = torch.empty(d, device=x.device, dtype=torch.float32)
-    ws = torch.empty(max(_lib.load().m3s_rms_bwd_workspace_bytes(d), 0) // 4 + 1,
+    dx = empty_like(x)
+    dw = empty(d, device=x.device, dtype=torch.float32)
+    ws = empty(max(_lib.load().m3s_rms_bwd_workspace_bytes(d), 0) // 4 + 1,
                      device=x.device, dtype=torch.float32)
     a = _lib.RmsArgs()
     a.struct_size = ctypes.sizeof(_lib.RmsArgs)
@@ -994,7 +1014,7 @@ def rms_backward(x: Tensor, weight: Tensor, rstd: Tensor, dy: Tensor,
     if add_dtype is not None:
         if add_dtype != dy.dtype:
             raise ValueError("rms_backward: the added tensor's dtype must be dy's")
-        dadd = torch.empty(x.shape, device=x.device, dtype=add_dtype)
+        dadd = empty(x.shape, device=x.device, dtype=add_dtype)
         a.dadd = dadd.data_ptr()
     with torch.cuda.device(x.device):
         _lib.check(_lib.load().m3s_rms_bwd(ctypes.byref(a), _lib.stream_handle(x.device)),
@@ -1019,7 +1039,7 @@ def swiglu_forward(h: Tensor, width: int) -> Tensor:
     """``h`` (..., 2 width) = value | gate -> ``value * silu(gate)`` (..., width) in h's
     dtype (one ``m3s_swiglu_fwd`` launch; ``model.py:125-140``'s elementwise middle)."""
     a = _swiglu_args(h, width)
-    out = torch.empty(*h.shape[:-1], width, device=h.device, dtype=h.dtype)
+    out = empty(*h.shape[:-1], width, device=h.device, dtype=h.dtype)
     a.a = out.data_ptr()
     with torch.cuda.device(h.device):
         _lib.check(_lib.load().m3s_swiglu_fwd(ctypes.byref(a), _lib.stream_handle(h.device)),
@@ -1034,7 +1054,7 @@ def swiglu_backward(h: Tensor, da: Tensor, width: int) -> Tensor:
     da = da.to(h.dtype).contiguous()
     if tuple(da.shape) != (*h.shape[:-1], width):
         raise ValueError("swiglu: da must be (..., width)")
-    dh = torch.empty_like(h)
+    dh = empty_like(h)
     a.da, a.dh = da.data_ptr(), dh.data_ptr()
     with torch.cuda.device(h.device):
         _lib.check(_lib.load().m3s_swiglu_bwd(ctypes.byref(a), _lib.stream_handle(h.device)),
@@ -1050,7 +1070,7 @@ def transpose_pad(w: Tensor, dtype: torch.dtype, out_rows: int) -> Tensor:
     if w.dim() != 2 or w.stride(1) != 1:
         w = w.contiguous()
     rows, cols = w.shape
-    out = torch.empty(out_rows, rows, device=dev, dtype=dtype)
+    out = empty(out_rows, rows, device=dev, dtype=dtype)
     a = _lib.TransposeArgs()
     a.struct_size = ctypes.sizeof(_lib.TransposeArgs)
     a.rows, a.cols, a.out_rows = rows, cols, out_rows

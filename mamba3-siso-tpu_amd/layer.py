@@ -52,10 +52,11 @@ class SISOConfig:
     ``chunk`` follows the reference's rule (a positive multiple of 128) widened to the
     shorter kernel tiles 32 and 64 (`layout.validate_chunk`); a chunk with no kernel of
     its own is scanned in tiles of the largest compiled chunk dividing it
-    (`layout.kernel_chunk`: the chunked form is exact for any chunk length). The config is
-    rejected at construction, as the reference rejects a bad chunk (``layer.py:97-99``),
-    unless forward, backward and decode kernels are compiled to run its (policy, chunk,
-    d_state, headdim) (`layout.validate_kernel_shape`).
+    (`layout.kernel_chunk`: the chunked form is exact for any chunk length). Construction
+    makes the reference's checks only (``layer.py:74-99``), so host-only work -- checkpoint
+    conversion, the CPU oracle -- takes any shape. Whether forward, backward and decode
+    kernels are compiled for its (policy, chunk, d_state, headdim) is checked by
+    `require_kernels`, which the layer's entry points call before their first launch.
     """
 
     d_model: int
@@ -103,6 +104,11 @@ class SISOConfig:
         LY.validate_chunk(self.chunk)
         LY.policy(self.policy_name)
         _ = self.nheads, self.n_angles
+
+    def require_kernels(self) -> None:
+        """``ValueError`` naming the missing kernels (and the chunks that are compiled)
+        unless this (policy, chunk, d_state, headdim) can run on the device
+        (`layout.validate_kernel_shape`)."""
         LY.validate_kernel_shape(self.policy_name, self.chunk, self.d_state, self.headdim)
 
 
@@ -285,7 +291,7 @@ class _LayerFn(torch.autograd.Function):
         else:
             dys = torch.zeros_like(y)
         # every slice of the projection gradient is written by exactly one kernel below
-        dproj = torch.empty(batch, seqlen, dp, device=u.device, dtype=dt)
+        dproj = K.empty(batch, seqlen, dp, device=u.device, dtype=dt)
         dz_v, dx_v, db_v, dc_v, ddt_v, da_v, dtr_v, dang_v = split_in_proj(dproj[..., :d], cfg)
         g = K.siso_backward(
             dys, q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias, b_bias, ybar,
@@ -293,7 +299,7 @@ class _LayerFn(torch.autograd.Function):
             dfinal_v=dfv, chunk=cfg.chunk, dtype_policy=cfg.policy_name,
             dv_out=dx_v.permute(0, 2, 1, 3), dz_out=dz_v.permute(0, 2, 1, 3))
         dwb, dwc = K.bcnorm_backward([b, c], [wb, wc], [rk, rq], [g.dk, g.dq], [db_v, dc_v])
-        d_bias = torch.empty(H, device=u.device, dtype=torch.float32)
+        d_bias = K.empty(H, device=u.device, dtype=torch.float32)
         SP.prep_backward_launch(dt_raw, a_raw, trap_raw, angles, bias, cfg.a_floor,
                                 (g.dadt, g.dgamma, g.dscale, None, None, g.dphi, dphi_final),
                                 ddt_v, da_v, dtr_v, dang_v, d_bias, None)
@@ -326,6 +332,7 @@ def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
     faster as a whole (the preprocess writes no phi), the backward scan slower (its
     in-kernel prefix sits on its critical path). ``None`` (the default) picks the compact
     form exactly when no gradient will be taken; True / False force either form."""
+    cfg.require_kernels()
     if _fused_ok(u, cfg, state):
         out, fs, fk, fv, phi_final = _LayerFn.apply(
             u, params.in_proj, params.out_proj, params.dt_bias, params.b_norm_weight,
@@ -361,6 +368,7 @@ def mamba3_siso_decode_step(params: SISOParams, u: Tensor, cfg: SISOConfig,
     place by the decode kernel (the reference donates it). When ``u`` is in the policy's
     operand dtype, everything between the two projections (BCNorm, dt / lambda / a, the
     state update and readout) is one ``m3s_decode_layer`` launch on the projection rows."""
+    cfg.require_kernels()
     proj = K.matmul(u, params.in_proj.to(u.dtype))
     if _decode_fused_ok(u, cfg):
         y, st = K.decode_layer_step(

@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
+from . import kernels as K
 
 TWO_PI = 2.0 * math.pi
 Tensor = torch.Tensor
@@ -145,10 +146,10 @@ def prep_forward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
     n_angles = r_ang.shape[-1]
     dev = r_dt.device
     f32 = dict(device=dev, dtype=torch.float32)
-    adt, gamma, scale, lam, dt = (torch.empty(batch, nheads, seqlen, **f32) for _ in range(5))
-    phi_final = torch.empty(batch, nheads, n_angles, **f32)
+    adt, gamma, scale, lam, dt = (K.empty(batch, nheads, seqlen, **f32) for _ in range(5))
+    phi_final = K.empty(batch, nheads, n_angles, **f32)
     lib = _lib.load()
-    ws = torch.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+    ws = K.empty(lib.m3s_prep_fwd_workspace_bytes(batch, seqlen, nheads, n_angles),
                      device=dev, dtype=torch.uint8)
     a = _lib.PrepFwdArgs()
     a.struct_size = ctypes.sizeof(_lib.PrepFwdArgs)
@@ -160,12 +161,12 @@ def prep_forward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
     a.dt_bias, a.phi_init = bias.data_ptr(), _lib.ptr(init)
     a.adt, a.gamma, a.scale, a.lam, a.dt = (t.data_ptr() for t in (adt, gamma, scale, lam, dt))
     if compact:
-        table = torch.empty(batch, seqlen, n_angles, **f32)
-        strips = torch.empty(batch, nheads, seqlen // 16, n_angles, **f32)
+        table = K.empty(batch, seqlen, n_angles, **f32)
+        strips = K.empty(batch, nheads, seqlen // 16, n_angles, **f32)
         a.theta_table, a.phi_strips = table.data_ptr(), strips.data_ptr()
         phi = PhiStrips(table, dt, strips)
     else:
-        phi = torch.empty(batch, nheads, seqlen, n_angles, **f32)
+        phi = K.empty(batch, nheads, seqlen, n_angles, **f32)
         a.phi = phi.data_ptr()
     a.phi_final = phi_final.data_ptr()
     a.workspace = ws.data_ptr()
@@ -186,7 +187,7 @@ def prep_backward_launch(r_dt: Tensor, r_a: Tensor, r_tr: Tensor, r_ang: Tensor,
     dev = r_dt.device
     ins = [_f32c(t) for t in cots]
     lib = _lib.load()
-    ws = torch.empty(lib.m3s_prep_bwd_workspace_bytes(batch, seqlen, nheads, n_angles),
+    ws = K.empty(lib.m3s_prep_bwd_workspace_bytes(batch, seqlen, nheads, n_angles),
                      device=dev, dtype=torch.uint8)
     a = _lib.PrepBwdArgs()
     a.struct_size = ctypes.sizeof(_lib.PrepBwdArgs)
@@ -243,13 +244,13 @@ class _PrepFn(torch.autograd.Function):
         n_angles = r_ang.shape[-1]
         dev = r_dt.device
         rdt = r_dt.dtype
-        d_dt = torch.empty(batch, seqlen, nheads, device=dev, dtype=rdt)
-        d_a = torch.empty_like(d_dt)
-        d_tr = torch.empty_like(d_dt)
-        d_ang = torch.empty(batch, seqlen, n_angles, device=dev, dtype=rdt)
-        d_bias = torch.empty(nheads, device=dev, dtype=torch.float32)
+        d_dt = K.empty(batch, seqlen, nheads, device=dev, dtype=rdt)
+        d_a = K.empty_like(d_dt)
+        d_tr = K.empty_like(d_dt)
+        d_ang = K.empty(batch, seqlen, n_angles, device=dev, dtype=rdt)
+        d_bias = K.empty(nheads, device=dev, dtype=torch.float32)
         want_init = ctx.in_dtypes[5] is not None and ctx.needs_input_grad[5]
-        d_init = (torch.empty(batch, nheads, n_angles, device=dev, dtype=torch.float32)
+        d_init = (K.empty(batch, nheads, n_angles, device=dev, dtype=torch.float32)
                   if want_init else None)
         prep_backward_launch(r_dt, r_a, r_tr, r_ang, bias, ctx.a_floor,
                              (dadt, dgamma, dscale, dlam, ddt, dphi, dphi_final),

@@ -36,3 +36,22 @@ def dev():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but no ROCm device is visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _poisoned_kernel_outputs(request):
+    """Every GPU test runs with `kernels.POISON_OUTPUTS` on: each kernel output and
+    workspace starts as all-ones bytes (NaN in every float type), so a region a kernel
+    leaves unwritten, or scratch it reads before writing, fails the parity bounds instead of
+    passing on whatever the caching allocator left there."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    import mamba3_siso_tpu_amd.kernels as K
+
+    old = K.POISON_OUTPUTS
+    K.POISON_OUTPUTS = True
+    try:
+        yield
+    finally:
+        K.POISON_OUTPUTS = old

@@ -4,7 +4,10 @@
 Tolerances (stated once, used by every GPU test):
   * f32 policy vs the float64 oracle: p95 relative error over |ref| >= 1e-2
     (``tests.py:60-88``) <= 2e-5 for forward/decode outputs and <= 2e-4 for gradients
-    (the reference's own bars, ``tests.py:533, 612``).
+    (the reference's own bars, ``tests.py:533, 612``), AND max |got - ref| / max |ref|
+    <= 1e-4 on outputs and <= 1e-3 on gradients (`assert_f32`). The p95 figure alone
+    ignores the worst 5% of entries and every entry below 1e-2, so a wrong row per chunk
+    or an unwritten tile could pass it; the max-normalised bound catches those.
   * bf16 policy against the oracle's bf16 rounding model (the same rounding points as the
     reference kernel): p95 <= 2e-3 for f32 outputs (the state) and <= 5e-3 for outputs
     stored in bf16 (y, and ybar, which the bf16 policy stores in bf16; one bf16 rounding
@@ -31,6 +34,8 @@ BF16 = torch.bfloat16
 
 FWD_F32_P95 = 2e-5
 GRAD_F32_P95 = 2e-4
+F32_OUT_MAXREL = 1e-4
+F32_GRAD_MAXREL = 1e-3
 BF16_MODEL_P95 = 2e-3
 BF16_OUT_MODEL_P95 = 5e-3
 BF16_LAYER_MODEL_P95 = 1e-2
@@ -99,6 +104,22 @@ def assert_p95(got, ref, tol, what=""):
 def assert_maxrel(got, ref, tol, what=""):
     e = O.max_rel(cpu(got), ref)
     assert e <= tol, f"{what}: max-normalised error {e:.3e} > {tol:.1e}"
+
+
+def assert_f32(got, ref, kind, what=""):
+    """The f32 policy's two bars against the float64 oracle: the reference's p95 metric
+    and a max-normalised bound over every entry (``kind`` "out": 2e-5 / 1e-4; "grad":
+    2e-4 / 1e-3). A reference that is zero throughout needs |got| <= 1e-6."""
+    p95, mx = (FWD_F32_P95, F32_OUT_MAXREL) if kind == "out" else (GRAD_F32_P95, F32_GRAD_MAXREL)
+    g, r = cpu(got), ref.detach().double().cpu()
+    assert bool(torch.isfinite(g).all()), f"{what}: non-finite entries"
+    assert_p95(g, r, p95, what)
+    top = float(r.abs().max()) if r.numel() else 0.0
+    err = float((g - r).abs().max()) if r.numel() else 0.0
+    if top < 1e-6:
+        assert err <= 1e-6, f"{what}: reference ~0 but max |got| {err:.3e}"
+    else:
+        assert err <= mx * top, f"{what}: max-normalised error {err / top:.3e} > {mx:.1e}"
 
 
 def assert_maxabs(got, ref, tol, what=""):

@@ -45,11 +45,21 @@ def test_config_fields_defaults_and_rules(m3):
     (dict(d_model=192, d_state=32, headdim=24), "forward/backward/decode"),
 ])
 def test_config_rejects_shapes_without_compiled_kernels(m3, kw, match):
-    """The reference rejects a bad chunk when the config is built (layer.py:97-99); here
-    the whole (policy, chunk, d_state, headdim) must have forward, backward and decode
-    kernels, and the error names the chunks that do exist."""
+    """The reference rejects a bad chunk when the config is built (layer.py:97-99), and so
+    does this one. A (policy, chunk, d_state, headdim) without forward, backward and decode
+    kernels still builds (host-only work such as checkpoint conversion takes any shape),
+    and `require_kernels` -- called by the layer entry points before a launch -- refuses it
+    with an error naming the chunks that do exist."""
+    if match == "multiple of 128":
+        with pytest.raises(ValueError, match=match):
+            m3.SISOConfig(**kw)
+        return
+    cfg = m3.SISOConfig(**kw)
     with pytest.raises(ValueError, match=match):
-        m3.SISOConfig(**kw)
+        cfg.require_kernels()
+    u = torch.zeros(1, cfg.chunk, cfg.d_model)
+    with pytest.raises(ValueError, match=match):   # refused before any device work
+        m3.mamba3_siso_layer(m3.init_params(cfg, 0), u, cfg)
 
 
 def test_config_accepts_every_compiled_shape(m3):
@@ -58,6 +68,7 @@ def test_config_accepts_every_compiled_shape(m3):
     for pol, c, n, p in sorted(both):
         if (pol, 0, n, p) in LY.KERNELS["decode"]:
             cfg = m3.SISOConfig(d_model=4 * p, d_state=n, headdim=p, chunk=c, policy_name=pol)
+            cfg.require_kernels()
             assert (cfg.chunk, cfg.d_state, cfg.headdim) == (c, n, p)
     assert LY.compiled_chunks("f32", 128, 64) == (32,)
     assert LY.compiled_chunks("bf16", 128, 64) == (32, 64, 128)

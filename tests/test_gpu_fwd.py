@@ -5,7 +5,7 @@ import math
 import pytest
 import torch
 
-from helpers import (BF16, BF16_MAXREL, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_P95,
+from helpers import (assert_f32, BF16, BF16_MAXREL, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_P95,
                      BF16_Y_MAXREL, F32, FWD_F32_P95, STATE_MAXABS, assert_bf16_bound,
                      assert_maxabs, assert_maxrel, assert_p95, boundary_inputs, cpu, fwd_args,
                      phi_strips_of, report)
@@ -40,17 +40,17 @@ def test_forward_f32_matches_oracle(m3, b, h, L, n, p, nr, chunk):
     yr, sr, dbg = oracle_fwd(c, chunk)
     y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy="f32",
                                          save_residuals=True)
-    assert_p95(y, yr, FWD_F32_P95, "y")
-    assert_p95(fs, sr.ssm, FWD_F32_P95, "final ssm")
-    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+    assert_f32(y, yr, "out", "y")
+    assert_f32(fs, sr.ssm, "out", "final ssm")
+    assert_f32(fk, sr.k, "out", "final k")
     assert O.max_rel(cpu(fv), sr.v) == 0.0
-    assert_p95(res.ybar, dbg["ybar"], FWD_F32_P95, "ybar")
+    assert_f32(res.ybar, dbg["ybar"], "out", "ybar")
     assert tuple(res.chunk_states.shape) == (b, h, L // tile, p, n)
-    assert_p95(res.chunk_states[:, :, ::chunk // tile], dbg["chunk_states"], FWD_F32_P95,
+    assert_f32(res.chunk_states[:, :, ::chunk // tile], dbg["chunk_states"], "out",
                "chunk_states")
     if tile != chunk:
         _, _, dbg_t = oracle_fwd(c, tile)
-        assert_p95(res.chunk_states, dbg_t["chunk_states"], FWD_F32_P95, "tile states")
+        assert_f32(res.chunk_states, dbg_t["chunk_states"], "out", "tile states")
 
 
 @pytest.mark.parametrize("chunk", [128, 64, 32])
@@ -68,7 +68,7 @@ def test_forward_bf16_matches_rounding_model_and_maths(m3, chunk):
     assert_p95(y, yr, BF16_P95, "y")
     assert_maxrel(y, yr, BF16_MAXREL, "y")
     assert_maxrel(fs, sr.ssm, BF16_MAXREL, "final ssm")
-    assert_p95(fk, sr.k, FWD_F32_P95, "final k (computed in f32)")
+    assert_f32(fk, sr.k, "out", "final k (computed in f32)")
 
 
 @pytest.mark.parametrize("n,chunk,gate", [(64, 64, True), (128, 128, False), (128, 64, False)])
@@ -87,8 +87,8 @@ def test_forward_bf16_other_shapes_and_no_gate(m3, n, chunk, gate):
     # chunk states are stored in bf16: one more rounding of up to 2^-8 relative
     assert_p95(res.chunk_states, dbgm["chunk_states"], BF16_OUT_MODEL_P95, "chunk states vs bf16 model")
     assert_maxrel(y, yr, BF16_MAXREL, "y")
-    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
-    assert_p95(fv, sr.v, FWD_F32_P95, "final v")
+    assert_f32(fk, sr.k, "out", "final k")
+    assert_f32(fv, sr.v, "out", "final v")
 
 
 @pytest.mark.parametrize("policy,n,p,chunk", [
@@ -102,16 +102,16 @@ def test_forward_every_table_shape(m3, policy, n, p, chunk):
     y, fs, fk, fv, res = m3.siso_forward(*fwd_args(d), chunk=chunk, dtype_policy=policy,
                                          save_residuals=True)
     if policy == "f32":
-        assert_p95(y, yr, FWD_F32_P95, "y")
-        assert_p95(fs, sr.ssm, FWD_F32_P95, "final ssm")
-        assert_p95(res.chunk_states, dbg["chunk_states"], FWD_F32_P95, "chunk_states")
+        assert_f32(y, yr, "out", "y")
+        assert_f32(fs, sr.ssm, "out", "final ssm")
+        assert_f32(res.chunk_states, dbg["chunk_states"], "out", "chunk_states")
     else:
         ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
         assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
         assert_p95(fs, sm.ssm, BF16_MODEL_P95, "ssm vs bf16 model")
         assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
         assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
-    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+    assert_f32(fk, sr.k, "out", "final k")
 
 
 @pytest.mark.parametrize("policy,n,p,chunk", [
@@ -131,10 +131,10 @@ def test_forward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
     y, fs, fk, fv, res = m3.siso_forward(*args, chunk=chunk, dtype_policy=policy,
                                          save_residuals=True)
     if policy == "f32":
-        assert_p95(y, yr, FWD_F32_P95, "y")
-        assert_p95(fs, sr.ssm, FWD_F32_P95, "final ssm")
-        assert_p95(res.chunk_states, dbg["chunk_states"], FWD_F32_P95, "chunk_states")
-        assert_p95(y, cpu(base[0]), FWD_F32_P95, "y vs phi read")
+        assert_f32(y, yr, "out", "y")
+        assert_f32(fs, sr.ssm, "out", "final ssm")
+        assert_f32(res.chunk_states, dbg["chunk_states"], "out", "chunk_states")
+        assert_f32(y, cpu(base[0]), "out", "y vs phi read")
     else:
         ym, sm, dbgm = oracle_fwd(c, chunk, mm=BF16)
         assert_p95(res.ybar, dbgm["ybar"], BF16_OUT_MODEL_P95, "ybar vs bf16 model")
@@ -142,7 +142,7 @@ def test_forward_with_phi_built_in_the_kernel(m3, policy, n, p, chunk):
         assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
         assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
         assert_p95(res.ybar, cpu(base[4].ybar), BF16_OUT_MODEL_P95, "ybar vs phi read")
-    assert_p95(fk, sr.k, FWD_F32_P95, "final k")
+    assert_f32(fk, sr.k, "out", "final k")
     assert O.max_rel(cpu(fv), cpu(base[3])) == 0.0
 
 
@@ -161,8 +161,8 @@ def test_forward_with_carried_state(m3):
     c, d = boundary_inputs(2, 2, 128, 128, 64, 32, "f32", seed=3, seeds=True)
     yr, sr, _ = oracle_fwd(c, 64, with_seed=True)
     y, fs, fk, fv = m3.siso_forward(*fwd_args(d), chunk=64, dtype_policy="f32")
-    assert_p95(y, yr, FWD_F32_P95, "y (seeded)")
-    assert_p95(fs, sr.ssm, FWD_F32_P95, "ssm (seeded)")
+    assert_f32(y, yr, "out", "y (seeded)")
+    assert_f32(fs, sr.ssm, "out", "ssm (seeded)")
 
 
 def test_forward_no_gate_no_skip(m3):
@@ -170,7 +170,7 @@ def test_forward_no_gate_no_skip(m3):
     c.pop("d_skip"), c.pop("z"), d.pop("d_skip"), d.pop("z")
     yr, sr, _ = oracle_fwd(c, 32)
     y, fs, _, _ = m3.siso_forward(*fwd_args(d), chunk=32, dtype_policy="f32")
-    assert_p95(y, yr, FWD_F32_P95, "y plain")
+    assert_f32(y, yr, "out", "y plain")
 
 
 def test_forward_reads_strided_views_in_place(m3):

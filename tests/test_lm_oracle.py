@@ -68,6 +68,90 @@ def test_lm_forward_collapses_without_residual_branches(m3, tie):
     torch.testing.assert_close(got, want, rtol=1e-13, atol=1e-13)
 
 
+def _per_token_lm(p, tokens, lay, variant="reference"):
+    """Known answer for `lm_forward` on a model whose state decays at once (every a_raw is
+    thousands, so 2^{A_i - A_j} underflows to 0 for i > j and the carried state vanishes):
+    the layer then maps each token on its own, ``y_t = [(D_h + gamma_t (u_t . w_t)) x_t
+    silu(z_t)]_h @ out_proj`` (the scan's diagonal term, kernel_fwd.py:146-187; the rotation
+    leaves u . w unchanged), and the whole stack is a per-token closed form.
+    ``variant`` builds the stack in the block order of model.py:194-232 ("reference") or
+    with one plausible mistake, to show that the known answer tells them apart."""
+    eps = lay["norm_eps"]
+    b = p["blocks"][0]
+    sp = b["siso"]
+    n, hd = lay["d_state"], lay["headdim"]
+
+    def norm(x, g):
+        return x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * g
+
+    def mixer(h):
+        d_model = h.shape[-1]
+        d_inner, nh, nr, _ = O.layer_dims(d_model, n, hd, lay["expand"], lay["rope_fraction"])
+        proj = h @ sp["in_proj"]
+        z, x, bb, cc, dt_raw, _, trap, _ = torch.split(
+            proj, (d_inner, d_inner, n, n, nh, nh, nh, nr), dim=-1)
+        u = norm(cc, sp["c_norm_weight"])[..., None, :] + sp["c_bias"]
+        w = norm(bb, sp["b_norm_weight"])[..., None, :] + sp["b_bias"]
+        dt = torch.nn.functional.softplus(dt_raw + sp["dt_bias"])
+        gamma = dt * torch.sigmoid(trap)
+        coef = sp["d_skip"] + gamma * (u * w).sum(-1)
+        zz = z.unflatten(-1, (nh, hd))
+        y = coef[..., None] * x.unflatten(-1, (nh, hd)) * zz * torch.sigmoid(zz)
+        return y.flatten(-2) @ sp["out_proj"]
+
+    def mlp(x):
+        value, gate = (x @ b["fc1"]).chunk(2, dim=-1)
+        return (value * gate * torch.sigmoid(gate)) @ b["fc2"]
+
+    x = p["embed"][tokens]
+    h = norm(x, b["norm_gain"])
+    if variant == "post_norm":
+        x1 = norm(x + mixer(x), b["norm_gain"])
+    elif variant == "residual_from_normed":
+        x1 = h + mixer(h)
+    else:
+        x1 = x + mixer(h)
+    if variant == "mlp_reads_mixer_gain":
+        x2 = x1 + mlp(norm(x1, b["norm_gain"]))
+    elif variant == "mlp_before_residual":
+        x2 = x1 + mlp(norm(x, b["mlp_norm_gain"]))
+    else:
+        x2 = x1 + mlp(norm(x1, b["mlp_norm_gain"]))
+    head = p["embed"].t() if p["head"] is None else p["head"]
+    return norm(x2, p["final_norm"]) @ head
+
+
+def test_lm_forward_block_order_known_answer(m3):
+    """`lm_forward`'s block order (model.py:194-232: pre-norm with the block's gain, residual
+    add of the raw stream, then the MLP on its own norm of the updated stream, the final
+    norm, the tied head) against `_per_token_lm`'s closed form on a one-layer model whose
+    mixer and MLP branches are both nonzero; each swapped order lands far from it."""
+    cfg, params, lay = small_lm(m3, n_layers=1)
+    p = LO.from_lm_params(params)
+    g = torch.Generator().manual_seed(41)
+    blk = p["blocks"][0]
+    p["embed"] = 0.5 + torch.rand(p["embed"].shape, generator=g, dtype=f64)   # positive rows
+    for key in ("norm_gain", "mlp_norm_gain"):
+        blk[key] = 0.5 + torch.rand(blk[key].shape, generator=g, dtype=f64)
+    p["final_norm"] = 0.5 + torch.rand(p["final_norm"].shape, generator=g, dtype=f64)
+    # a_raw = 1e4 * sum(h) with h > 0: adt ~ -1e2 per token, the decay 2^(A_i - A_j) is 0
+    d_inner, nh, _, _ = O.layer_dims(32, 16, 16, 2, 0.5)
+    a0 = 2 * d_inner + 2 * 16 + nh
+    blk["siso"]["in_proj"][:, a0:a0 + nh] = 1e4
+    tokens = torch.tensor([[1, 5, 7, 2] * 8, [0, 10, 3, 3] * 8])
+    got = LO.lm_forward(p, tokens, lay)
+    want = _per_token_lm(p, tokens, lay)
+    mixer_scale = float((want - _per_token_lm({**p, "blocks": [
+        {**blk, "siso": {**blk["siso"], "out_proj": torch.zeros_like(blk["siso"]["out_proj"])}}]},
+        tokens, lay)).abs().max())
+    assert mixer_scale > 1e-2, "the mixer branch must be nonzero for the check to mean anything"
+    torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10)
+    for variant in ("post_norm", "residual_from_normed", "mlp_reads_mixer_gain",
+                    "mlp_before_residual"):
+        wrong = _per_token_lm(p, tokens, lay, variant)
+        assert O.max_rel(wrong, got) > 1e-3, variant
+
+
 def test_lm_decode_chain_reproduces_forward(m3):
     """Token-by-token decode through the stack equals the chunked prefill's logits at
     every position, and the carried states agree (both in float64)."""
