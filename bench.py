@@ -67,25 +67,32 @@ def gpu_time_ms(fn, iters, torch):
 
 def scan_inputs(m3, params16, cfg, u, torch):
     """Kernel-boundary operands of the configs[1] layer: the projections of ``u`` through
-    split_in_proj, BCNorm and preprocess, as the layer hands them to the scan -- phi in
-    the compact form the layer uses (``kernels.PhiStrips``), and the same phi
-    materialised (``phi_full``) for the phi-reading mode."""
+    split_in_proj and BCNorm, as the layer hands them to the scan. Three forms: raw mode
+    (what the inference forward runs: the raw dt / a / trap slices of the projection and
+    the rotary table and strip totals the BCNorm launch writes), the preprocess-fed scan
+    with phi compact (``kernels.PhiStrips``), and the same phi materialised
+    (``phi_full``, the training forward's form)."""
+    from mamba3_siso_tpu_amd import kernels as K
     from mamba3_siso_tpu_amd import scan_prep as SP
 
     with torch.no_grad():
-        proj = u @ params16.in_proj
+        proj = torch.nn.functional.pad(u @ params16.in_proj, (0, 128))   # the layer's padded row
+        proj = proj[..., :cfg.d_in_proj]
         z, x, bb, cc, dt_raw, a_raw, trap_raw, angles = m3.split_in_proj(proj, cfg)
-        kq = m3.rms_norm(cc, params16.c_norm_weight, cfg.norm_eps)
-        kk = m3.rms_norm(bb, params16.b_norm_weight, cfg.norm_eps)
         bias = params16.dt_bias.float().contiguous()
+        (kk, kq), _, angs = K.bcnorm_forward(
+            [bb, cc], [params16.b_norm_weight, params16.c_norm_weight], cfg.norm_eps,
+            theta=(angles, dt_raw, bias, cfg.chunk))
         adt, gamma, scale, _, _, strips, _ = SP.prep_forward_launch(
             dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=True)
         phi_full = SP.prep_forward_launch(dt_raw, a_raw, trap_raw, angles, bias, None,
                                           cfg.a_floor)[5]
         kv, kz = x.permute(0, 2, 1, 3), z.permute(0, 2, 1, 3)
-    return dict(q=kq, k=kk, v=kv, adt=adt, gamma=gamma, scale=scale, phi=strips,
-                q_bias=params16.c_bias.float(), k_bias=params16.b_bias.float(),
-                d_skip=params16.d_skip.float(), z=kz), phi_full
+    common = dict(q=kq, k=kk, v=kv, q_bias=params16.c_bias.float(),
+                  k_bias=params16.b_bias.float(), d_skip=params16.d_skip.float(), z=kz)
+    raw = dict(common, dt_raw=dt_raw, a_raw=a_raw, trap_raw=trap_raw, angles=angs,
+               dt_bias=bias, a_floor=cfg.a_floor)
+    return raw, dict(common, adt=adt, gamma=gamma, scale=scale, phi=strips), phi_full
 
 
 def layer_roofline(B, L, DM, cfg, scan_bytes, scan_flops, measured_ms):
@@ -100,11 +107,10 @@ def layer_roofline(B, L, DM, cfg, scan_bytes, scan_flops, measured_ms):
 
     parts = {
         "in_proj": floor_ms(2 * M * DM * d_in, M * DM * 2 + DM * dpad * 2 + M * dpad * 2),
-        "bcnorm": floor_ms(0, 4 * M * N * 2),
-        # reads dt/a/trap/angles rows; writes adt, gamma, scale, dt and the compact phi
-        # (the tanh(angles) pi table and one angle row per 16 tokens)
-        "preprocess": floor_ms(0, M * (3 * H + Nr) * 2 + 4 * M * H * 4 + M * Nr * 4
-                               + M * H * Nr * 4 // 16),
+        # the B and C rows in and out; the angle and dt rows in, the rotary table and the
+        # per-strip theta totals out (raw mode's share of the preprocess)
+        "bcnorm": floor_ms(0, 4 * M * N * 2 + M * (H + Nr) * 2 + M * Nr * 4
+                           + M * H * Nr * 4 // 16),
         "scan": floor_ms(scan_flops, scan_bytes),
         "out_proj": floor_ms(2 * M * cfg.d_inner * DM, M * cfg.d_inner * 2 + cfg.d_inner * DM * 2
                              + M * DM * 2),
@@ -185,34 +191,41 @@ def main():
 
     # ---------------- the scan kernels alone, kernel boundary -------------------------
     # Algorithmic bytes of one forward launch as the layer's inference forward runs it
-    # (phi built in the kernel): q, k once (head-shared), v, z, y bf16; adt/gamma/scale
-    # f32; the tanh(angles) pi table (head-shared), dt and one phi row per 16 tokens; the
-    # final ssm f32 (+ k, v rows). The training forward reads phi (B, H, L, Nr) f32
-    # instead of the compact form (the phi_read fields).
+    # (raw mode): q, k once (head-shared), v, z, y bf16; the raw dt / a / trap slices bf16;
+    # the tanh(angles) pi table (head-shared) and the theta strip totals f32; the final
+    # ssm f32 (+ k, v, phi rows). The preprocess-fed scan reads adt / gamma / scale f32 and
+    # phi compact (dt and one phi row per 16 tokens) or materialised (B, H, L, Nr) f32
+    # (the training forward's form).
     phi_compact = B * L * Nr * 4 + B * H * L * 4 + B * H * (L // 16) * Nr * 4
     phi_read = B * H * L * Nr * 4
     scan_fixed = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * H * L * 4
                   + B * H * P * N * 4 + B * H * (N + P) * 4)
-    scan_bytes = scan_fixed + phi_compact
+    scan_compact_bytes = scan_fixed + phi_compact
     scan_read_bytes = scan_fixed + phi_read
+    scan_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * L * H * 2
+                  + B * L * Nr * 4 + B * H * (L // 16) * Nr * 4
+                  + B * H * P * N * 4 + B * H * (N + P + Nr) * 4)
     scan_flops = B * H * L * 2 * (2 * N * P + cfg.chunk * N + cfg.chunk * P)
     if args.leg in ("all", "scan", "bwd"):
-        ka, phi_full = scan_inputs(m3, params16, cfg, u, torch)
-        kc = ka
+        kraw, kc, phi_full = scan_inputs(m3, params16, cfg, u, torch)
         ka = dict(kc, phi=phi_full)
         if args.leg in ("all", "scan"):
-            scan = lambda: K.siso_forward(**kc, chunk=128)  # noqa: E731
+            scan = lambda: K.siso_forward_raw(**kraw, chunk=128)  # noqa: E731
+            scan_c = lambda: K.siso_forward(**kc, chunk=128)  # noqa: E731
             scan_r = lambda: K.siso_forward(**ka, chunk=128)  # noqa: E731
             # a kernel-boundary micro-measurement: enough launches that the clocks have
-            # settled (a few ms of warmup), whatever --steps says for the headline; the two
-            # phi forms alternate, and each keeps the better of its two averages
+            # settled (a few ms of warmup), whatever --steps says for the headline; the
+            # three forms alternate, and each keeps the better of its two averages
             for _ in range(max(args.warmup, 10)):
                 scan()
+                scan_c()
                 scan_r()
             n = max(args.steps, 50)
-            times = [(gpu_time_ms(scan, n, torch), gpu_time_ms(scan_r, n, torch)) for _ in range(2)]
+            times = [(gpu_time_ms(scan, n, torch), gpu_time_ms(scan_c, n, torch),
+                      gpu_time_ms(scan_r, n, torch)) for _ in range(2)]
             scan_ms = min(t[0] for t in times)
-            read_ms = min(t[1] for t in times)
+            comp_ms = min(t[1] for t in times)
+            read_ms = min(t[2] for t in times)
             scan_gbs = scan_bytes / (scan_ms * 1e-3) / 1e9
             scan_tflops = scan_flops / (scan_ms * 1e-3) / 1e12
             line.update(scan_kernel_ms=round(scan_ms, 4),
@@ -220,18 +233,20 @@ def main():
                         scan_kernel_gbs=round(scan_gbs, 1),
                         scan_kernel_tflops=round(scan_tflops, 2),
                         scan_kernel_mfma_frac=round(scan_tflops / BF16_PEAK_TFLOPS, 5),
+                        scan_kernel_phi_compact_ms=round(comp_ms, 4),
+                        scan_kernel_phi_compact_gbs=round(scan_compact_bytes / (comp_ms * 1e-3) / 1e9, 1),
                         scan_kernel_phi_read_ms=round(read_ms, 4),
                         scan_kernel_phi_read_gbs=round(scan_read_bytes / (read_ms * 1e-3) / 1e9, 1))
             line["roofline"] = {
-                "kernel": "fwd_bf16_kernel<128,128,64,1> (m3s_fwd, kernel boundary, phi built "
-                          "in the kernel)",
+                "kernel": "fwd_bf16_kernel<128,128,64,1,true> (m3s_fwd in raw mode, kernel "
+                          "boundary: the preprocess and the phi carry inside the scan)",
                 "bound": "hbm", "achieved": round(scan_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(scan_gbs / HBM_PEAK_GBS, 4),
-                "traffic": traffic_figure("fwd_bf16_kernel_strips"),
+                "traffic": traffic_figure("fwd_bf16_kernel_raw"),
                 "traffic_source": TRAFFIC_SOURCE, "algorithmic_bytes": scan_bytes,
                 "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5),
-                # the same scan reading the materialised phi (the training forward's form):
-                # more bytes in about the same time
+                # the same scan fed by the preprocess launches, phi compact or materialised
+                "phi_compact_frac": round(scan_compact_bytes / (comp_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "phi_read_frac": round(scan_read_bytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         if args.leg in ("all", "bwd"):
             # the training path's pair: with gradients the layer materialises phi and both
@@ -268,7 +283,7 @@ def main():
                 "algorithmic_bytes": bwd_bytes,
                 "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 5)}
             del y, res, dyk, kr
-        del ka, kc, phi_full
+        del ka, kc, kraw, phi_full
         torch.cuda.empty_cache()
         if args.leg != "all":
             print(json.dumps({"leg": args.leg, **line}))
@@ -374,8 +389,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) inputs, init_params(seed=0) weights)",
-        "config": {"workload": "configs[1]: one Mamba-3 SISO layer forward (in_proj, BCNorm, "
-                               "preprocess, HIP chunked scan, out_proj)",
+        "config": {"workload": "configs[1]: one Mamba-3 SISO layer forward (in_proj; BCNorm "
+                               "with the rotary table; the HIP chunked scan reading the raw "
+                               "dt / a / trap slices; out_proj)",
                    "batch": B, "seq_len": L, "nheads": H, "headdim": P, "d_state": N,
                    "d_model": DM, "chunk": 128, "n_angles": Nr},
         "gemm_solutions": "recorded (mamba3-siso-tpu_amd/tuned_gemms.csv)" if tuned

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 8
+#define M3S_ABI_VERSION 9
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -88,6 +88,29 @@ typedef struct m3s_fwd_args {
   float* final_ssm;                    /* out (B, H, P, N)                            */
   float* final_k;                      /* out (B, H, N) rotated, unscaled             */
   float* final_v;                      /* out (B, H, P)                               */
+  /* Raw mode (raw = 1; no counterpart in the reference, whose callers run `preprocess`
+   * before its kernel, reference.py:160-199, siso.py:176-181): the kernel reads the raw
+   * dt / a / trap slices of the projection in place and computes dt = softplus(dt_raw +
+   * dt_bias), a = min(-heavy_tail(a_raw), -a_floor), lam = sigmoid(trap_raw), adt, gamma
+   * and the t+1 scale shift on the way in; it carries phi across its chunks from the
+   * chunk totals and builds each row's angle from that carry, its strip's prefix and
+   * theta_table times its own dt (the three written by m3s_norm_fwd at theta_chunk =
+   * chunk), starting from phi_init, and writes phi at the last position to phi_final. adt, gamma, scale, phi,
+   * phi_dt and phi_strips are then NULL, theta_table is given, save_residuals is 0 (the
+   * backward reads the materialised scalars), n_angles % 4 == 0 and L % 16 == 0. The
+   * three raw slices share their strides, and a_raw / trap_raw start a fixed number of
+   * elements (>= 0, below stride_t) after dt_raw, as slices of one projection row do.
+   * M3S_ERR_UNSUPPORTED where no raw-mode kernel exists (m3s_fwd_raw_supported). */
+  int32_t raw;
+  float a_floor;
+  m3s_blx dt_raw;                      /* (B, L, H) in dtype                          */
+  m3s_blx a_raw;                       /* (B, L, H) in dtype                          */
+  m3s_blx trap_raw;                    /* (B, L, H) in dtype                          */
+  const float* dt_bias;                /* (H)                                         */
+  const float* theta_prefix;           /* (B, H, L / 16, Nr) from m3s_norm_fwd        */
+  const float* theta_chunk_totals;     /* (B, H, L / chunk, Nr) from m3s_norm_fwd     */
+  const float* phi_init;               /* (B, H, Nr), or NULL for zero                */
+  float* phi_final;                    /* out (B, H, Nr) in [0, 2 pi)                 */
 } m3s_fwd_args;
 
 /* Reverse-scan backward. Replaces `kernel_bwd.siso_backward_kernel`
@@ -261,6 +284,21 @@ typedef struct m3s_norm_fwd_args {
   const float* weight[2];/* (width) gains */
   void* y[2];            /* out (B, L, width), dense, 16-byte aligned */
   float* rstd[2];        /* out (B, L) for the backward, or NULL */
+  /* Optional, in the same launch: the rotary angles' per-token work that m3s_fwd's raw
+   * mode reads (reference.py:134-157, split between this pass and the scan's carry). With
+   * theta_t = theta_table[t] softplus(dt_raw[t, h] + dt_bias[h]) summed over each 16-token
+   * strip in t order: theta_prefix holds, for every strip, the sum of the strips before
+   * it in its chunk of theta_chunk tokens (0 for a chunk's first strip), and
+   * theta_chunk_totals each chunk's sum. theta_chunk is the chunk m3s_fwd runs at (a
+   * multiple of 16 dividing L); n_angles % 4 == 0. Give angles, dt_raw, dt_bias and the
+   * three outputs together, or leave all NULL. */
+  int32_t nheads, n_angles, theta_chunk;
+  m3s_blx angles;        /* (B, L, Nr) raw angle slice, in dtype */
+  m3s_blx dt_raw;        /* (B, L, H) raw dt slice, in dtype */
+  const float* dt_bias;  /* (H) */
+  float* theta_table;    /* out (B, L, Nr): tanh(angles) pi */
+  float* theta_prefix;   /* out (B, H, L / 16, Nr), 16-byte aligned */
+  float* theta_chunk_totals; /* out (B, H, L / theta_chunk, Nr), 16-byte aligned */
 } m3s_norm_fwd_args;
 
 /* Backward of m3s_norm_fwd (autograd of layer.py:190-198). dy arrives in f32 and is
@@ -417,6 +455,10 @@ const char* m3s_last_error(void);
  * chunk = 0. `which` is 0 = forward, 1 = backward, 2 = decode. */
 int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, int32_t state_dim,
                       int32_t headdim);
+/* 1 if m3s_fwd takes this (dtype, chunk, N, P, Nr) in raw mode, else 0. No counterpart in
+ * the reference. */
+int32_t m3s_fwd_raw_supported(int32_t dtype, int32_t chunk, int32_t state_dim, int32_t headdim,
+                              int32_t n_angles);
 
 /* Bytes of m3s_bwd_args.workspace: the per-head dq/dk rows, 2*B*H*L*N elements of
  * the dtype. No counterpart in the reference (its head sum is an in-kernel

@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -44,6 +44,10 @@ class FwdArgs(C.Structure):
         ("seed_ssm", vp), ("seed_k", vp), ("seed_v", vp), ("seed_coef", vp),
         ("y", Bhlp), ("ybar", vp), ("chunk_states", vp),
         ("final_ssm", vp), ("final_k", vp), ("final_v", vp),
+        ("raw", i32), ("a_floor", C.c_float),
+        ("dt_raw", Blx), ("a_raw", Blx), ("trap_raw", Blx),
+        ("dt_bias", vp), ("theta_prefix", vp), ("theta_chunk_totals", vp),
+        ("phi_init", vp), ("phi_final", vp),
     ]
 
 
@@ -129,6 +133,9 @@ class NormFwdArgs(C.Structure):
         ("batch", i32), ("seqlen", i32), ("width", i32),
         ("dtype", i32), ("count", i32), ("eps", C.c_float),
         ("x", Blx * 2), ("weight", vp * 2), ("y", vp * 2), ("rstd", vp * 2),
+        ("nheads", i32), ("n_angles", i32), ("theta_chunk", i32), ("angles", Blx),
+        ("dt_raw", Blx), ("dt_bias", vp), ("theta_table", vp), ("theta_prefix", vp),
+        ("theta_chunk_totals", vp),
     ]
 
 
@@ -194,7 +201,8 @@ class GemvArgs(C.Structure):
 
 
 #: Every symbol ``include/m3s.h`` declares.
-EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_bwd_workspace_bytes",
+EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_fwd_raw_supported",
+           "m3s_bwd_workspace_bytes",
            "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
@@ -220,6 +228,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_last_error.restype = C.c_char_p
     lib.m3s_supported.restype = i32
     lib.m3s_supported.argtypes = [i32, i32, i32, i32, i32]
+    lib.m3s_fwd_raw_supported.restype = i32
+    lib.m3s_fwd_raw_supported.argtypes = [i32, i32, i32, i32, i32]
     lib.m3s_bwd_workspace_bytes.restype = i64
     lib.m3s_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.m3s_fwd.restype = i32
@@ -283,6 +293,11 @@ def check(rc: int, what: str) -> None:
 
 def supported(which: int, dtype: int, chunk: int, state_dim: int, headdim: int) -> bool:
     return bool(load().m3s_supported(which, dtype, chunk, state_dim, headdim))
+
+
+def raw_supported(dtype: int, chunk: int, state_dim: int, headdim: int, n_angles: int) -> bool:
+    """Whether ``m3s_fwd`` takes this shape in raw mode (`m3s_fwd_raw_supported`)."""
+    return bool(load().m3s_fwd_raw_supported(dtype, chunk, state_dim, headdim, n_angles))
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -32,3 +32,8 @@ extern "C" int32_t m3s_supported(int32_t which, int32_t dtype, int32_t chunk, in
     default: return 0;
   }
 }
+
+extern "C" int32_t m3s_fwd_raw_supported(int32_t dtype, int32_t chunk, int32_t state_dim,
+                                         int32_t headdim, int32_t n_angles) {
+  return m3s::fwd_raw_supported_impl(dtype, chunk, state_dim, headdim, n_angles);
+}

@@ -160,6 +160,9 @@ template <> __device__ __forceinline__ f32x4 buf_load<f32x4>(__amdgpu_buffer_rsr
 template <> __device__ __forceinline__ float buf_load<float>(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));
 }
+template <> __device__ __forceinline__ bf16 buf_load<bf16>(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_bit_cast(bf16, __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0));
+}
 __device__ __forceinline__ void buf_store(bf16x8 x, __amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, x), r, v, s, 0);
 }
@@ -265,8 +268,61 @@ __device__ __forceinline__ float wave_total(float v) {
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48)));
 }
 
+// n / d and n % d for 0 <= n < 2^20 by a divisor d known only at run time, without an
+// integer division (a software routine on the GPU): a float estimate of the quotient
+// (relative error below 2^-21, so off by at most one in this range), then one correction.
+struct DivMod {
+  int d;
+  float inv;
+  __device__ explicit DivMod(int d_) : d(d_), inv(__builtin_amdgcn_rcpf((float)d_)) {}
+  __device__ __forceinline__ void operator()(int n, int& q, int& r) const {
+    q = (int)((float)n * inv);
+    r = n - q * d;
+    if (r < 0) {
+      --q;
+      r += d;
+    } else if (r >= d) {
+      ++q;
+      r -= d;
+    }
+  }
+};
+
 // ---- elementwise maths ----------------------------------------------------------
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The preprocess nonlinearities of reference.py:160-209, one definition for every kernel
+// that applies them (the per-token pass, the scans' raw loads, the decode step, the
+// preprocess kernels), so they agree bit for bit: softplus with torch's threshold 20,
+// heavy_tail(x) = max(x, 0) + 1 / (1 - min(x, 0)), the logistic sigmoid.
+__device__ __forceinline__ float softplus_(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float heavy_tail_(float x) {
+  return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
+}
+__device__ __forceinline__ float sigmoid_(float x) { return 1.f / (1.f + expf(-x)); }
+// The same three from the hardware exp2 / log2 / reciprocal (about 2e-6 relative at |x| <=
+// 20, from rounding x log2(e)): for the scans' raw loads, whose results feed bf16 products.
+// log1p(e) by Goldberg's correction, log(u) e / (u - 1) with u = 1 + e, which stays accurate
+// where 1 + e rounds (small dt), and is e itself where u rounds to 1.
+constexpr float kLn2 = 0.69314718055994531f;
+__device__ __forceinline__ float softplus_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(x * kLog2e);
+  const float u = 1.f + e, d = u - 1.f;
+  const float r = d == 0.f ? e : (__builtin_amdgcn_logf(u) * kLn2) * (e * __builtin_amdgcn_rcpf(d));
+  return x > 20.f ? x : r;
+}
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+// tanh from the hardware exp2 / reciprocal: sign(x) (1 - e) / (1 + e), e = 2^{-2 |x| log2 e}.
+// Near 0 the subtraction leaves an absolute error of a few 1e-8 (a relative one of
+// ~1e-7 / |x|): for angles that are summed into a phase, where the absolute error counts.
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float e = __builtin_amdgcn_exp2f(-2.f * kLog2e * fabsf(x));
+  return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), x);
+}
+__device__ __forceinline__ float heavy_tail_fast(float x) {
+  return fmaxf(x, 0.f) + __builtin_amdgcn_rcpf(1.f - fminf(x, 0.f));
+}
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 // silu from the hardware exp2 / reciprocal (~2 ulp): for gates whose product is rounded
 // to bf16 right after.
@@ -275,6 +331,13 @@ __device__ __forceinline__ float silu_fast(float x) {
 }
 __device__ __forceinline__ float wrap_2pi(float phi) {
   return phi - kTwoPi * floorf(phi / kTwoPi);
+}
+// wrap_2pi without the division: the quotient from a multiply by 1 / (2 pi), one fma for
+// the remainder, then a step back into [0, 2 pi) where the quotient was off by one.
+__device__ __forceinline__ float wrap_2pi_fast(float phi) {
+  float r = fmaf(-kTwoPi, floorf(phi * 0.15915494309189535f), phi);
+  r = r < 0.f ? r + kTwoPi : r;
+  return r >= kTwoPi ? r - kTwoPi : r;
 }
 
 // ---- two adjacent elements as one LDS store ---------------------------------------

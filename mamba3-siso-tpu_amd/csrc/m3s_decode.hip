@@ -56,10 +56,6 @@ struct DecParams {
 
 constexpr int kDecThreads = 256;
 
-__device__ __forceinline__ float dec_softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-__device__ __forceinline__ float dec_heavy_tail(float x) {
-  return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
-}
 
 template <typename MT, int N, int P, bool LAYER>
 __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) {
@@ -97,9 +93,9 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
   float adt, dt, lam;
   if constexpr (LAYER) {
     const MT* sc = prow + 2 * HP + 2 * N;
-    dt = dec_softplus((float)sc[h] + p.dt_bias[h]);
+    dt = softplus_((float)sc[h] + p.dt_bias[h]);
     lam = 1.f / (1.f + expf(-(float)sc[2 * p.H + h]));
-    adt = fminf(-dec_heavy_tail((float)sc[p.H + h]), -p.a_floor) * dt;
+    adt = fminf(-heavy_tail_((float)sc[p.H + h]), -p.a_floor) * dt;
   } else {
     adt = p.adt[bh];
     dt = p.dt[bh];

@@ -22,6 +22,7 @@
 //    gate, stores) runs on contiguous rows with 16-byte global accesses.
 //  * XCD-aware block numbering keeps the H heads of one batch element (which share
 //    q/k) on one XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "m3s_common.h"
@@ -59,6 +60,19 @@ struct FwdParams {
   float* fssm;
   float* fk;
   float* fv;
+  // raw mode: the dt slice of the projection (the a and trap slices a_off / t_off
+  // elements after it in each row; sc_span = max(a_off, t_off) + 1), its b / t strides,
+  // the head biases, each strip's theta prefix within its chunk (B, H, L / 16, Nr) and
+  // the chunk totals (B, H, nc, Nr), phi_init (or NULL) and the phi_final output
+  const void* sc;
+  int64_t sc_sb, sc_st;
+  int a_off, t_off, sc_span;
+  float a_floor;
+  const float* dt_bias;
+  const float* tpre;
+  const float* ctot;
+  const float* phi_init;
+  float* phi_final;
 };
 
 template <typename MT> struct V16;
@@ -641,20 +655,38 @@ __device__ __forceinline__ bf16x4 ld_tr4_at(const bf16* ptr) {
   return __builtin_bit_cast(bf16x4, r);
 }
 
+// LDS of raw mode's strip angles: the angle entering each 16-token strip of a chunk, for
+// the NRB 32-column blocks of rotary pairs, double-buffered by chunk parity.
+template <int C, int NRB>
+constexpr int raw_strip_floats() { return 2 * (C / 16) * 32 * NRB; }
+template <int C, int N, int P, int NRB>
+constexpr bool raw_fits() {
+  return NRB > 0 && Fwd2Cfg<C, N, P>::LDS_BYTES + 4 * raw_strip_floats<C, NRB>() <= 163840;
+}
+
 // NRB = 0: phi is read. NRB > 0 (phi_strips mode): phi is built from the compact form,
 // and NRB is the number of 32-column blocks that hold rotary pairs (Nr <= 32 NRB).
-template <int C, int N, int P, int NRB>
+// RAW (raw mode, NRB > 0): the row scalars come from the projection's raw dt / a / trap
+// slices, and the angle entering each strip from a carry across chunks this kernel keeps
+// itself plus the strip's prefix within its chunk (see `carry` below), instead of phi_dt /
+// phi_strips.
+template <int C, int N, int P, int NRB, bool RAW = false>
 __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p) {
   using F = Fwd2Cfg<C, N, P>;
   constexpr bool STRIPS = NRB > 0;
   static_assert(NRB <= F::LOB, "rotary blocks lie in the rotated half");
+  static_assert(!RAW || raw_fits<C, N, P, NRB>(), "raw mode needs phi built and its LDS");
+  constexpr int SPC = C / 16;                  // 16-token strips per chunk
+  constexpr int ELD = 32 * NRB;                // row stride of the strip-angle table
+  constexpr int TQ = 64 / SPC;                 // angle quads per lane load of the carry
+  constexpr int TL = RAW ? (ELD + 4 * TQ - 1) / (4 * TQ) : 1;   // such loads
   constexpr int NT = F::NT, LDK = F::LDK, LDO = F::LDO;
   constexpr int H2 = N / 2, PB = F::PB, SPW = F::SPW, NSTEP = F::NSTEP;
 
   // four groups of each XCD's workgroups start 0, 4, 8 and 12 K cycles late (a chunk takes
   // about 16 K): at B=8 L=8192 H=32 the scan took 2% less
   if (p.nc >= 16) stagger_start(blockIdx.x, 4, 2);
-  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES];
+  __shared__ __align__(16) unsigned char smem[F::LDS_BYTES + 4 * (RAW ? raw_strip_floats<C, NRB>() : 0)];
   auto opq = [](int x) { asm volatile("" : "+s"(x)); return x; };
   bf16* sK2 = reinterpret_cast<bf16*>(smem);                                // [2] k-hat tiles
   bf16* sV = reinterpret_cast<bf16*>(smem + opq(2 * F::SZ_K));              // v tile
@@ -664,6 +696,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   float* sQb = reinterpret_cast<float*>(smem + opq(2 * F::SZ_K + 2 * F::SZ_V + F::SZ_S + F::SZ_O));
   float* sKb = sQb + N;
   float* sSc2 = sKb + N;   // [2] row scalar blocks, laid out as in `scalars` below
+  float* sE = sSc2 + 10 * C;   // raw mode: [2][SPC][ELD] angle entering each strip
   // buffer b's k-hat tile, and its row scalars: A_t, 2^{A_t}, 2^{A_last - A_t},
   // D + gamma_t (u_t . w_t), and 2^{A_{16 s + 15} - A_j} (s = j's strip: a key row's
   // decay to its strip end)
@@ -712,7 +745,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // dt and the strip angles through SGPR-base global loads (two SGPRs per base where a
   // buffer descriptor takes four): past the last chunk they read chunk 0 again, unused
   const float* pdtg = STRIPS ? p.pdt + bh * L : nullptr;
-  const float* pstrg = STRIPS ? p.pstr + bh * (int64_t)(L / 16) * Nr : nullptr;
+  const float* pstrg = (STRIPS && !RAW) ? p.pstr + bh * (int64_t)(L / 16) * Nr : nullptr;
   const auto rScl = make_rsrc(sclg, (uint32_t)L * 4);
   const auto rGam = make_rsrc(gamg, (uint32_t)L * 4);
   const auto rAdt = make_rsrc(adtg, (uint32_t)L * 4);
@@ -722,6 +755,17 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   const auto rYb = make_rsrc(p.save ? static_cast<bf16*>(p.ybar) + bh * L * (int64_t)P : nullptr,
                              p.save ? (uint32_t)L * P * 2 : 0u);
   const auto rCs = make_rsrc(csg, p.save ? (uint32_t)nc * N * P * 2 : 0u);
+  // raw mode: this (b, h)'s raw scalars through one descriptor (dt at element t sc_st,
+  // a and trap a_off / t_off further; past the sequence it reads zeros), its chunk theta
+  // totals, and its dt bias
+  const int64_t sc_st = RAW ? p.sc_st : 0;
+  const bf16* scg = RAW ? static_cast<const bf16*>(p.sc) + b * p.sc_sb + h : nullptr;
+  const auto rSc = make_rsrc(scg, RAW ? (uint32_t)(((int64_t)(L - 1) * sc_st + p.sc_span) * 2) : 0u);
+  const auto rCt = make_rsrc(RAW ? p.ctot + bh * (int64_t)nc * Nr : nullptr,
+                             RAW ? (uint32_t)nc * Nr * 4 : 0u);
+  const auto rPre = make_rsrc(RAW ? p.tpre + bh * (int64_t)(L / 16) * Nr : nullptr,
+                              RAW ? (uint32_t)(L / 16) * Nr * 4 : 0u);
+  const float dtb = RAW ? p.dt_bias[h] : 0.f;
 
   // ---- carried state: registers; wave owns tiles (pb_w, nb0 + NSTEP m) ------------
   const int pb_w = wave % PB, nb0 = wave / PB;
@@ -814,6 +858,14 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   float rscale, rgam;
   float radt[F::E];
   const bool phi_vec = (Nr % 4) == 0;
+  // raw mode: this lane's raw scalar of the next chunk (lane group g = lane >> 4 holds
+  // dt_raw (g = 0) or trap_raw (g = 1) of its row t, the same of row t + 1 (g = 2, 3)),
+  // the A-scan rows' dt_raw and a_raw, and, used by the carry wave only (lane: strip
+  // lane % SPC, angle quads lane / SPC + TQ i), the strip prefixes and the total of the
+  // chunk after next and the angle entering it
+  float rraw = 0.f;
+  float rdr[RAW ? F::E : 1], rar[RAW ? F::E : 1];
+  f32x4 rX[TL], rC[TL], Pc[TL];
 
   auto prefetch_qk = [&](int c) {   // c >= nc: a chunk that does not exist, read as zeros
     const bool live = c < nc;
@@ -868,13 +920,69 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
         }
       }
     }
-    rscale = buf_load<float>(dScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
-    rgam = buf_load<float>(dGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
     // every wave loads the A-scan inputs (only wave 0 uses them): no wave-dependent
     // branch around loads (it would cost exact wait counts)
+    if constexpr (RAW) {   // the raw dt and a of the A-scan rows (gamma, scale: build_turns)
+      // wave 0 alone reads them: 128 rows of the projection are 128 cache lines, so the
+      // other waves' copies of the same loads go through the zero-size descriptor (a
+      // wave-uniform choice of descriptor, not a branch around the loads)
+      const auto dSc = (live && wave == 0) ? rSc : rNul;
+      const uint32_t sc0 = (uint32_t)(c * C * sc_st * 2);
 #pragma unroll
-    for (int e = 0; e < F::E; ++e)
-      radt[e] = buf_load<float>(dAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+      for (int e = 0; e < F::E; ++e) {
+        const uint32_t o = (uint32_t)((lane * F::E + e) * sc_st) * 2;
+        rdr[e] = (float)buf_load<bf16>(dSc, o, sc0);
+        rar[e] = (float)buf_load<bf16>(dSc, o + 2 * p.a_off, sc0);
+      }
+    } else {
+      rscale = buf_load<float>(dScl, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+      rgam = buf_load<float>(dGam, (uint32_t)trow * 4, (uint32_t)c * C * 4);
+#pragma unroll
+      for (int e = 0; e < F::E; ++e)
+        radt[e] = buf_load<float>(dAdt, (uint32_t)(lane * F::E + e) * 4, (uint32_t)c * C * 4);
+    }
+  };
+
+  // raw mode: chunk cc's strip prefixes and total (zeros past the last chunk: the carry
+  // adds the total); the other waves issue the same loads through the zero-size descriptor
+  auto load_ctot = [&](int cc) {
+    if constexpr (RAW) {
+      const bool live = cc < nc && wave == 1;
+      const auto dX = live ? rPre : rNul, dT = live ? rCt : rNul;
+      if (cc >= nc) cc = 0;
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63;
+      const int st = lane % SPC, q = lane / SPC;
+#pragma unroll
+      for (int i = 0; i < TL; ++i) {
+        const uint32_t j0 = 4 * (q + i * TQ);
+        rX[i] = buf_load<f32x4>(dX, (uint32_t)(st * Nr + j0) * 4, (uint32_t)cc * SPC * Nr * 4);
+        rC[i] = buf_load<f32x4>(dT, j0 * 4, (uint32_t)cc * Nr * 4);
+      }
+    }
+  };
+  // raw mode, the carry wave: the angle entering each strip of chunk cc, P + the strip's
+  // prefix, into sE[cc & 1]; then P (Pc, the angle entering chunk cc) moves past the chunk.
+  // The other waves read their strip's entry when they build the chunk's turns, two
+  // barriers later.
+  auto carry = [&](int cc) {
+    if constexpr (RAW) {
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63;
+      const int st = lane % SPC, q = lane / SPC;
+#pragma unroll
+      for (int i = 0; i < TL; ++i) {
+        const int j0 = 4 * (q + i * TQ);
+        f32x4 ent;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ent[e] = Pc[i][e] + rX[i][e];
+        if (j0 < ELD) *reinterpret_cast<f32x4*>(sE + ((cc & 1) * SPC + st) * ELD + j0) = ent;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Pc[i][e] = wrap_2pi_fast(Pc[i][e] + rC[i][e]);
+      }
+    }
   };
 
   // phi_strips mode: chunk c's table rows, strip angles and dt (issued at the start of the
@@ -883,6 +991,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // instead of lengthening the end of the long strips' phase
   auto prefetch_angles = [&](int c) {
     if constexpr (STRIPS) {
+      load_ctot(c + 1);     // raw mode: the carry's inputs for the chunk after this one
       if (c >= nc) c = 0;   // past the end: chunk 0 again, never used
       int ln = threadIdx.x;
       asm volatile("" : "+v"(ln));
@@ -897,7 +1006,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
 #pragma unroll
           for (int qd = 0; qd < 2; ++qd) {
             rtab[lb][qd] = buf_load<f32x4>(rPhi, (uint32_t)(trow * Nr + 32 * lb + g8 + 4 * qd) * 4, sphi);
-            rstr[lb][qd] = gld<f32x4>(pstrg, sstr + (uint32_t)(32 * lb + g8 + 4 * qd) * 4);
+            if constexpr (!RAW) rstr[lb][qd] = gld<f32x4>(pstrg, sstr + (uint32_t)(32 * lb + g8 + 4 * qd) * 4);
           }
         } else {
 #pragma unroll
@@ -907,15 +1016,51 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
             for (int i = 0; i < 4; ++i) {
               const bool in = j + i < Nr;
               rtab[lb][qd][i] = in ? buf_load<float>(rPhi, (uint32_t)(trow * Nr + j + i) * 4, sphi) : 0.f;
-              rstr[lb][qd][i] = in ? gld<float>(pstrg, sstr + (uint32_t)(j + i) * 4) : 0.f;
+              if constexpr (!RAW) rstr[lb][qd][i] = in ? gld<float>(pstrg, sstr + (uint32_t)(j + i) * 4) : 0.f;
             }
           }
         }
       }
-      rpdt = gld<float>(pdtg, (uint32_t)(c * C + trow) * 4);
+      if constexpr (RAW) {   // one raw scalar per lane: dt or trap of row trow or trow + 1
+        const int g = lane >> 4;
+        const uint32_t o = (uint32_t)((trow + (g >> 1)) * sc_st + ((g & 1) ? p.t_off : 0)) * 2;
+        rraw = (float)buf_load<bf16>(rSc, o, (uint32_t)(c * C * sc_st * 2));
+      } else {
+        rpdt = gld<float>(pdtg, (uint32_t)(c * C + trow) * 4);
+      }
     }
   };
-  auto build_turns = [&]() {
+  auto build_turns = [&](int c) {   // chunk c's rows
+    if constexpr (RAW) {
+      // the row scalars (reference.py:160-199) from the raw slices, the four per row
+      // spread over the four lane groups so one softplus-or-sigmoid sequence makes them
+      // all: dt_t (g = 0), lam_t (g = 1), dt_{t+1} (g = 2), lam_{t+1} (g = 3), zero past
+      // the sequence (the trapezoid's dt_L = lam_L = 0). Hardware exp2 / log2 / rcp on
+      // u = 1 + e^{+-x}: softplus = log(u), sigmoid = 1 / u, three transcendentals for both.
+      // log(u) loses the bits of e that 1 + e rounds off: 6e-5 relative at dt = 1e-3,
+      // far below the bf16 operands dt feeds here (gamma, scale, this strip's angle
+      // offsets; the carry across strips comes from the BCNorm pass's exact totals).
+      int ln = threadIdx.x;
+      asm volatile("" : "+v"(ln));
+      const int lane = ln & 63, g = lane >> 4, r = lane & 15;
+      const bool isdt = (g & 1) == 0;
+      const float x = rraw + (isdt ? dtb : 0.f);
+      const float u = 1.f + __builtin_amdgcn_exp2f((isdt ? x : -x) * kLog2e);
+      float v = isdt ? (x > 20.f ? x : __builtin_amdgcn_logf(u) * kLn2) : __builtin_amdgcn_rcpf(u);
+      if (g >= 2 && c * C + 16 * strip + r + 1 >= L) v = 0.f;
+      const float dtt = __shfl(v, r, 64), lamt = __shfl(v, 16 + r, 64);
+      const float dtn = __shfl(v, 32 + r, 64), lamn = __shfl(v, 48 + r, 64);
+      rgam = dtt * lamt;
+      rscale = rgam + dtn * (1.f - lamn);
+      rpdt = dtt;
+      // the angle entering this wave's strip, from the carry wave
+      const float* er = sE + ((c & 1) * SPC + strip) * ELD + 8 * g;
+#pragma unroll
+      for (int lb = 0; lb < NRB; ++lb) {
+#pragma unroll
+        for (int qd = 0; qd < 2; ++qd) rstr[lb][qd] = *reinterpret_cast<const f32x4*>(er + 32 * lb + 4 * qd);
+      }
+    }
     if constexpr (STRIPS) {
 #pragma unroll
       for (int lb = 0; lb < NRB; ++lb) {
@@ -974,7 +1119,13 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
       float run = 0.f;
 #pragma unroll
       for (int e = 0; e < F::E; ++e) {
-        run += radt[e] * kLog2e;
+        float adt;
+        if constexpr (RAW) {   // reference.py:160-199: a = min(-heavy_tail(a_raw), -a_floor)
+          adt = fminf(-heavy_tail_fast(rar[e]), -p.a_floor) * softplus_fast(rdr[e] + dtb);
+        } else {
+          adt = radt[e];
+        }
+        run += adt * kLog2e;
         a[e] = run;
       }
       float incl = run;
@@ -1199,7 +1350,7 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     prefetch_rest(c + 1);
     prefetch_vz(c + 1 < nc ? rV : rNul, c + 1 < nc ? c + 1 : 0, rZ, c);
     __builtin_amdgcn_sched_barrier(0);
-    build_turns();   // chunk c+1's angles (phi_strips mode)
+    build_turns(c + 1);   // chunk c+1's angles (phi_strips mode)
     // inter-chunk: out^T[p][t] += 2^{A_t} sum_n S[p][n] q~[t][n]
     // (every fragment of S, the diagonal v values and the scalars are read first, then
     // PB independent MFMA chains: one LDS round trip)
@@ -1317,13 +1468,29 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     }
   };
 
+  if constexpr (RAW) {   // the carry starts from phi_init; the strip entries of chunk 0 first
+    const int q = lane / SPC;
+#pragma unroll
+    for (int i = 0; i < TL; ++i) {
+      const int j0 = 4 * (q + i * TQ);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        Pc[i][e] = (p.phi_init && j0 + e < Nr) ? p.phi_init[bh * Nr + j0 + e] : 0.f;
+    }
+    load_ctot(0);
+    vm_wait_all();
+    if (wave == 1) carry(0);
+  }
   prefetch_vz(rV, 0, rNul, 0);
   prefetch_qk(0);
   prefetch_rest(0);
-  prefetch_angles(0);
+  prefetch_angles(0);   // (raw mode: the carry's inputs for chunk 1)
   vm_wait_all();
-  build_turns();
-  __syncthreads();  // sQb / sKb
+  if constexpr (RAW) {
+    if (wave == 1) carry(1);
+  }
+  __syncthreads();  // sQb / sKb (raw mode: the strip entries of chunks 0 and 1)
+  build_turns(0);
   stage_regs();     // chunk 0
   stage_write(0);
   prefetch_qk(1);
@@ -1350,6 +1517,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     if (c > 0 && light) epilogue(c - 1);
     products(c);
     store_state(c);
+    if constexpr (RAW) {   // the strip entries of chunk c+2 (its inputs came with c+1's angles)
+      if (wave == 1) carry(c + 2);
+    }
     stage_regs();
     stage_write((c + 1) & 1);   // chunk c+1's k-hat rows and scalars, into the other buffer
     __builtin_amdgcn_sched_barrier(0);
@@ -1360,6 +1530,19 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
   // tail: out and z of the last chunk, its epilogue
   phase_a(nc);
   write_vz(false);
+  if constexpr (RAW) {   // the carry past the last chunk is phi at L-1: phi_final, and LDS
+    if (wave == 1) {     // row 0 of the strip table (no longer read) for final_k
+      const int st = lane % SPC, q = lane / SPC;
+#pragma unroll
+      for (int i = 0; i < TL; ++i) {
+        const int j0 = 4 * (q + i * TQ);
+        if (st == 0 && j0 < ELD) {
+          *reinterpret_cast<f32x4*>(sE + j0) = Pc[i];
+          if (j0 < Nr) *reinterpret_cast<f32x4*>(p.phi_final + bh * Nr + j0) = Pc[i];
+        }
+      }
+    }
+  }
   __syncthreads();
   if (light) epilogue(nc - 1);
 
@@ -1381,7 +1564,9 @@ __global__ void __launch_bounds__(C / 16 * 64) fwd_bf16_kernel(const FwdParams p
     float kl = (float)kg[row + j] + sKb[j], kh = (float)kg[row + H2 + j] + sKb[H2 + j];
     if (j < Nr) {
       float turns;
-      if constexpr (STRIPS) {   // the last strip's entering angle plus its 16 thetas
+      if constexpr (RAW) {
+        turns = __builtin_amdgcn_fractf(sE[j] * 0.15915494309189535f);
+      } else if constexpr (STRIPS) {   // the last strip's entering angle plus its 16 thetas
         float ph = p.pstr[(bh * (L / 16) + L / 16 - 1) * Nr + j];
         for (int t = L - 16; t < L; ++t) ph += phig[(int64_t)t * Nr + j] * p.pdt[bh * L + t];
         turns = __builtin_amdgcn_fractf(ph * 0.15915494309189535f);
@@ -1409,9 +1594,36 @@ static bool fits_rsrc(const FwdParams& p, int N, int P) {
          (int64_t)p.nc * N * P * 2 <= lim;
 }
 
+// Raw mode's kernel for this (dtype, C, N, P, Nr): the bf16 kernel with phi built, where
+// its strip-angle table fits the LDS. -1 where there is none.
+template <typename MT, int C, int N, int P>
+constexpr int raw_nrb_max() {
+  if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
+    if constexpr (N / 64 >= 2 && raw_fits<C, N, P, 2>()) return 2;
+    if constexpr (raw_fits<C, N, P, 1>()) return 1;
+  }
+  return 0;
+}
+
 template <typename MT, int C, int N, int P>
 static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   const bool strips = prm.pstr != nullptr;
+  if (prm.sc != nullptr) {   // raw mode (the caller checked raw_nrb_max and fits_rsrc)
+    if constexpr (raw_nrb_max<MT, C, N, P>() >= 1) {
+      if (prm.Nr <= 32) {
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 1, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+        return launch_status("m3s_fwd");
+      }
+    }
+    if constexpr (raw_nrb_max<MT, C, N, P>() >= 2) {
+      if (prm.Nr <= 64) {
+        hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 2, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
+        return launch_status("m3s_fwd");
+      }
+    }
+    set_error("m3s_fwd: no raw-mode kernel for n_angles %d", prm.Nr);
+    return M3S_ERR_UNSUPPORTED;
+  }
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
     if (fits_rsrc(prm, N, P)) {
       // phi strips: NRB 32-column blocks hold the rotary pairs (Nr <= 32 NRB); only
@@ -1481,6 +1693,16 @@ int32_t fwd_supported(int dtype, int chunk, int n, int pdim) {
   return 0;
 }
 
+int32_t fwd_raw_supported_impl(int dtype, int chunk, int n, int pdim, int nr) {
+  if (nr <= 0 || nr % 4 != 0) return 0;
+#define X(MT, C, N, P)                                                        \
+  if (dtype == dtype_code<MT>() && chunk == C && n == N && pdim == P)         \
+    return 32 * raw_nrb_max<MT, C, N, P>() >= nr ? 1 : 0;
+  M3S_FWD_CONFIGS(X)
+#undef X
+  return 0;
+}
+
 }  // namespace m3s
 
 extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
@@ -1508,13 +1730,51 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
   M3S_REQUIRE(bhlp_ok(a->v, vec), "m3s_fwd: v null, misaligned or strides not multiples of %d", vec);
   M3S_REQUIRE(!a->has_z || bhlp_ok(a->z, vec), "m3s_fwd: z null, misaligned or bad strides");
   M3S_REQUIRE(bhlp_ok(a->y, vec), "m3s_fwd: y null, misaligned or bad strides");
-  const bool strips = a->theta_table || a->phi_dt || a->phi_strips;
+  const bool raw = a->raw != 0;
+  const bool strips = !raw && (a->theta_table || a->phi_dt || a->phi_strips);
+  int a_off = 0, t_off = 0;
+  if (raw) {
+    M3S_REQUIRE(!a->adt && !a->gamma && !a->scale && !a->phi && !a->phi_dt && !a->phi_strips,
+                "m3s_fwd: raw mode takes the raw slices, not adt / gamma / scale / phi");
+    M3S_REQUIRE(a->theta_table && a->theta_prefix && a->theta_chunk_totals &&
+                    aligned16(a->theta_table) && aligned16(a->theta_prefix) &&
+                    aligned16(a->theta_chunk_totals),
+                "m3s_fwd: raw mode needs theta_table, theta_prefix and theta_chunk_totals, "
+                "16-byte aligned");
+    M3S_REQUIRE(!a->save_residuals, "m3s_fwd: raw mode does not save residuals (the backward "
+                "reads the materialised scalars)");
+    M3S_REQUIRE(Nr > 0 && Nr % 4 == 0 && L % 16 == 0,
+                "m3s_fwd: raw mode needs n_angles %% 4 == 0 (got %d) and seqlen %% 16 == 0", Nr);
+    M3S_REQUIRE(a->dt_raw.ptr && a->a_raw.ptr && a->trap_raw.ptr && a->dt_bias && a->phi_final &&
+                    aligned16(a->phi_final),
+                "m3s_fwd: raw mode needs dt_raw, a_raw, trap_raw, dt_bias and phi_final");
+    M3S_REQUIRE(a->a_raw.stride_b == a->dt_raw.stride_b && a->trap_raw.stride_b == a->dt_raw.stride_b &&
+                    a->a_raw.stride_t == a->dt_raw.stride_t && a->trap_raw.stride_t == a->dt_raw.stride_t,
+                "m3s_fwd: the raw slices must share their strides");
+    const int esz = a->dtype == M3S_DTYPE_BF16 ? 2 : 4;
+    const int64_t da = (const char*)a->a_raw.ptr - (const char*)a->dt_raw.ptr;
+    const int64_t dtr = (const char*)a->trap_raw.ptr - (const char*)a->dt_raw.ptr;
+    M3S_REQUIRE(da >= 0 && dtr >= 0 && da % esz == 0 && dtr % esz == 0 &&
+                    da / esz + H <= a->dt_raw.stride_t && dtr / esz + H <= a->dt_raw.stride_t,
+                "m3s_fwd: a_raw / trap_raw must start a fixed number of elements after dt_raw "
+                "within each row");
+    a_off = (int)(da / esz);
+    t_off = (int)(dtr / esz);
+    M3S_REQUIRE(((int64_t)(L - 1) * a->dt_raw.stride_t + std::max(a_off, t_off) + 1) * esz < (1ll << 31),
+                "m3s_fwd: the raw slices of one batch element span 2 GiB or more");
+    if (!fwd_raw_supported_impl(a->dtype, C, N, P, Nr)) {
+      set_error("m3s_fwd: no raw-mode kernel for dtype=%s chunk=%d state_dim=%d headdim=%d "
+                "n_angles=%d", a->dtype == M3S_DTYPE_BF16 ? "bf16" : "f32", C, N, P, Nr);
+      return M3S_ERR_UNSUPPORTED;
+    }
+  }
   M3S_REQUIRE(!strips || (a->theta_table && a->phi_dt && a->phi_strips && !a->phi),
               "m3s_fwd: give phi, or theta_table, phi_dt and phi_strips (not both)");
   M3S_REQUIRE(!strips || L % 16 == 0, "m3s_fwd: phi_strips needs seqlen %% 16 == 0");
-  M3S_REQUIRE(a->adt && a->gamma && a->scale && (a->phi || strips) && a->q_bias && a->k_bias,
+  M3S_REQUIRE((raw || (a->adt && a->gamma && a->scale && (a->phi || strips))) && a->q_bias &&
+                  a->k_bias,
               "m3s_fwd: a required input pointer is NULL");
-  M3S_REQUIRE(Nr == 0 || Nr % 4 != 0 ||
+  M3S_REQUIRE(raw || Nr == 0 || Nr % 4 != 0 ||
                   (strips ? aligned16(a->theta_table) && aligned16(a->phi_strips) : aligned16(a->phi)),
               "m3s_fwd: phi (or theta_table / phi_strips) misaligned");
   M3S_REQUIRE(!a->has_d || a->d_skip, "m3s_fwd: has_d but d_skip is NULL");
@@ -1535,7 +1795,7 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
   prm.z = a->has_z ? a->z.ptr : nullptr;
   prm.z_sb = a->z.stride_b; prm.z_sh = a->z.stride_h; prm.z_st = a->z.stride_t;
   prm.adt = a->adt; prm.gamma = a->gamma; prm.scale = a->scale; prm.phi = a->phi;
-  prm.tht = strips ? a->theta_table : nullptr;
+  prm.tht = (strips || raw) ? a->theta_table : nullptr;
   prm.pdt = strips ? a->phi_dt : nullptr;
   prm.pstr = strips ? a->phi_strips : nullptr;
   prm.qb = a->q_bias; prm.kb = a->k_bias; prm.dsk = a->d_skip;
@@ -1544,6 +1804,18 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
   prm.y = a->y.ptr; prm.y_sb = a->y.stride_b; prm.y_sh = a->y.stride_h; prm.y_st = a->y.stride_t;
   prm.ybar = a->ybar; prm.cstates = a->chunk_states;
   prm.fssm = a->final_ssm; prm.fk = a->final_k; prm.fv = a->final_v;
+  if (raw) {
+    prm.sc = a->dt_raw.ptr; prm.sc_sb = a->dt_raw.stride_b; prm.sc_st = a->dt_raw.stride_t;
+    prm.a_off = a_off; prm.t_off = t_off; prm.sc_span = std::max(a_off, t_off) + 1;
+    prm.a_floor = a->a_floor;
+    prm.dt_bias = a->dt_bias;
+    prm.tpre = a->theta_prefix;
+    prm.ctot = a->theta_chunk_totals;
+    prm.phi_init = a->phi_init;
+    prm.phi_final = a->phi_final;
+    M3S_REQUIRE(fits_rsrc(prm, N, P), "m3s_fwd: raw mode needs every per-(b, h) stream under "
+                "2 GiB");
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int grid = B * H;
 #define X(MT, CC, NN, PP)                                                     \

@@ -69,6 +69,7 @@ __device__ __forceinline__ void stagger_start(int bid, int groups, int units) {
 
 namespace m3s {
 int32_t fwd_supported(int dtype, int chunk, int n, int pdim);
+int32_t fwd_raw_supported_impl(int dtype, int chunk, int n, int pdim, int nr);
 int32_t bwd_supported(int dtype, int chunk, int n, int pdim);
 int32_t decode_supported(int dtype, int n, int pdim);
 }  // namespace m3s

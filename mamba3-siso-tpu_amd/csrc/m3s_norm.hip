@@ -32,12 +32,32 @@ struct NormRows {
   const float* w[2];
 };
 
+// The rotary angles' per-token work, done in the same launch as the norms (a third
+// role after the `count` norm roles), for the forward scan's raw mode (reference.py:134-157
+// split between this pass and the scan): the head-shared table theta_table = tanh(angles)
+// pi; for every head, theta_t = theta_table[t] softplus(dt_raw[t] + dt_bias) summed over
+// each 16-token strip, and the strip sums' exclusive prefix within each chunk of `chunk`
+// tokens (the angle a strip starts at, relative to its chunk's start); and each chunk's
+// total. The scan carries the chunk totals across its chunks and adds the rest per row.
+struct NormThetaParams {
+  const void* ang;
+  int64_t asb, ast;
+  const void* dtr;
+  int64_t dsb, dst;
+  const float* dt_bias;
+  float* tab;    // (B, L, Nr)
+  float* pre;    // (B, H, L / 16, Nr) strip starts within their chunk
+  float* ctot;   // (B, H, L / chunk, Nr) chunk totals
+  int H, Nr, chunk, nblk;
+};
+
 struct NormFwdParams {
   NormRows in;
-  int B, L, N, G;
+  int B, L, N, G, count;
   float eps;
   void* y[2];
   float* rstd[2];
+  NormThetaParams th;
 };
 
 struct NormBwdParams {
@@ -74,16 +94,149 @@ __device__ __forceinline__ float group_sum_dyn(float v, int G) {
   return v;
 }
 
+// The norms together with the angle role: one 512-thread block per chunk of one batch
+// element does the chunk's B and C rows and, in three parallel steps, its angle work: the
+// chunk's table rows and every head's dt into LDS; every (strip, head, angle quad) sum of
+// 16 rows in time order into LDS; a thread per (head, quad) walks the strips for their
+// prefixes and the chunk total. The angle role's loads are issued first, so the norm rows
+// stream while they are in flight. LDS: chunk (Nr + H) + chunk / 16 * H * Nr floats.
+constexpr int kThetaThreads = 512;
+// The chunk's B and C rows, kRowBatch rows per group of G lanes at a time: every row's
+// load is issued before the first row's statistic (one memory latency per batch).
+constexpr int kRowBatch = 8;
 template <typename T>
-__global__ void __launch_bounds__(kNormThreads) norm_fwd_kernel(const NormFwdParams p) {
+__device__ __forceinline__ void norm_rows_of_chunk(const NormFwdParams& p, int b, int t0) {
   constexpr int VEC = NVec<T>::n;
-  const int which = blockIdx.y;
-  const int G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
-  const int rows_per_block = kNormThreads / G;
-  const int64_t M = (int64_t)p.B * p.L;
-  const int64_t r = (int64_t)blockIdx.x * rows_per_block + gid;
-  if (r >= M) return;   // whole groups leave together: the shuffles below stay in-group
-  const int b = (int)(r / p.L), t = (int)(r % p.L);
+  using VT = typename NVec<T>::type;
+  const int C = p.th.chunk, G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
+  const int rows = p.count * C, per_pass = kThetaThreads / G;
+  const int n0 = gl * VEC;
+  const bool act = n0 < p.N;
+  for (int base = 0; base < rows; base += kRowBatch * per_pass) {
+    VT xv[kRowBatch];
+#pragma unroll
+    for (int k = 0; k < kRowBatch; ++k) {   // uniform over each group of G lanes
+      const int rr = base + gid + k * per_pass;
+      const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
+      if (rr < rows && act)
+        xv[k] = *reinterpret_cast<const VT*>(static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] +
+                                             t * p.in.xst[which] + n0);
+    }
+#pragma unroll
+    for (int k = 0; k < kRowBatch; ++k) {
+      const int rr = base + gid + k * per_pass;
+      if (rr >= rows) break;
+      const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
+      const int64_t r = (int64_t)b * p.L + t;
+      float ss = 0.f;
+      if (act) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) ss += (float)xv[k][i] * (float)xv[k][i];
+      }
+      ss = group_sum_dyn(ss, G);
+      const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
+      if (act) {
+        const float* w = p.in.w[which] + n0;
+        VT yv;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) yv[i] = (T)((float)xv[k][i] * rstd * w[i]);
+        *reinterpret_cast<VT*>(static_cast<T*>(p.y[which]) + r * p.N + n0) = yv;
+      }
+      if (gl == 0 && p.rstd[which]) p.rstd[which][r] = rstd;
+    }
+  }
+}
+template <typename T>
+__global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwdParams p) {
+  extern __shared__ float dyn[];
+  const NormThetaParams& q = p.th;
+  const int L = p.L;
+  const int Nr = q.Nr, H = q.H, C = q.chunk, nc = L / C, ns = L / 16, spc = C / 16;
+  const int nq = Nr / 4;
+  const int b = blockIdx.x / nc, c = blockIdx.x - b * nc, t0 = c * C;
+  float* sTab = dyn;              // [C][Nr]
+  float* sDt = dyn + C * Nr;      // [C][H]
+  float* sSum = sDt + C * H;      // [spc][H][Nr]
+  const T* ang = static_cast<const T*>(q.ang) + b * q.asb;
+  const T* dtr = static_cast<const T*>(q.dtr) + b * q.dsb;
+  // rounds of kThetaRound items per thread, every load of a round issued before any use
+  // (one memory latency per round, not per item); quotients by the run-time Nr, H and
+  // pair counts through DivMod (a float estimate), not integer division; tanh and softplus
+  // from the hardware exp2 / log2 / rcp (tanh_fast, softplus_fast)
+  constexpr int kThetaRound = 8;
+  const DivMod byNr(Nr), byH(H), byPairs(H * nq), byNq(nq);
+  for (int base = 0; base < C * Nr; base += kThetaRound * kThetaThreads) {
+    float v[kThetaRound];
+#pragma unroll
+    for (int u = 0; u < kThetaRound; ++u) {
+      const int i = base + threadIdx.x + u * kThetaThreads;
+      int t, j;
+      byNr(i, t, j);
+      v[u] = i < C * Nr ? (float)ang[(int64_t)(t0 + t) * q.ast + j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kThetaRound; ++u) {
+      const int i = base + threadIdx.x + u * kThetaThreads;
+      if (i < C * Nr) {
+        const float tp = tanh_fast(v[u]) * kPi;
+        q.tab[((int64_t)b * L + t0) * Nr + i] = tp;   // the chunk's rows are contiguous
+        sTab[i] = tp;
+      }
+    }
+  }
+  for (int base = 0; base < C * H; base += kThetaRound * kThetaThreads) {
+    float v[kThetaRound];
+#pragma unroll
+    for (int u = 0; u < kThetaRound; ++u) {
+      const int i = base + threadIdx.x + u * kThetaThreads;
+      int t, h;
+      byH(i, t, h);
+      v[u] = i < C * H ? (float)dtr[(int64_t)(t0 + t) * q.dst + h] + q.dt_bias[h] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kThetaRound; ++u) {
+      const int i = base + threadIdx.x + u * kThetaThreads;
+      if (i < C * H) sDt[i] = softplus_fast(v[u]);
+    }
+  }
+  norm_rows_of_chunk<T>(p, b, t0);
+  __syncthreads();
+  for (int i = threadIdx.x; i < spc * H * nq; i += kThetaThreads) {   // (strip, head, quad)
+    int st, r, h, jq;
+    byPairs(i, st, r);
+    byNq(r, h, jq);
+    const int j0 = 4 * jq;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const f32x4 tb = *reinterpret_cast<const f32x4*>(sTab + (16 * st + t) * Nr + j0);
+      const float dt = sDt[(16 * st + t) * H + h];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += tb[e] * dt;
+    }
+    *reinterpret_cast<f32x4*>(sSum + (st * H + h) * Nr + j0) = acc;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < H * nq; i += kThetaThreads) {
+    int h, jq;
+    byNq(i, h, jq);
+    const int j0 = 4 * jq;
+    float* pre = q.pre + (((int64_t)b * H + h) * ns + t0 / 16) * Nr + j0;
+    f32x4 run = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < spc; ++s) {
+      *reinterpret_cast<f32x4*>(pre + s * Nr) = run;
+      run += *reinterpret_cast<const f32x4*>(sSum + (s * H + h) * Nr + j0);
+    }
+    *reinterpret_cast<f32x4*>(q.ctot + (((int64_t)b * H + h) * nc + c) * Nr + j0) = run;
+  }
+}
+
+// One (B or C) row of one token: G lanes, 16 bytes each; the row statistic is a shuffle
+// reduction inside the group, so all G lanes of a group call this together.
+template <typename T>
+__device__ __forceinline__ void norm_row(const NormFwdParams& p, int which, int b, int t,
+                                         int64_t r, int gl) {
+  constexpr int VEC = NVec<T>::n;
   const int n0 = gl * VEC;
   const bool act = n0 < p.N;
   const T* xrow = static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] + t * p.in.xst[which];
@@ -94,7 +247,7 @@ __global__ void __launch_bounds__(kNormThreads) norm_fwd_kernel(const NormFwdPar
 #pragma unroll
     for (int i = 0; i < VEC; ++i) ss += x[i] * x[i];
   }
-  ss = group_sum_dyn(ss, G);
+  ss = group_sum_dyn(ss, p.G);
   const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
   if (act) {
     const float* w = p.in.w[which] + n0;
@@ -104,6 +257,17 @@ __global__ void __launch_bounds__(kNormThreads) norm_fwd_kernel(const NormFwdPar
     store_row<T>(static_cast<T*>(p.y[which]) + r * p.N + n0, y);
   }
   if (gl == 0 && p.rstd[which]) p.rstd[which][r] = rstd;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kNormThreads) norm_fwd_kernel(const NormFwdParams p) {
+  const int which = blockIdx.y;
+  const int G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
+  const int rows_per_block = kNormThreads / G;
+  const int64_t M = (int64_t)p.B * p.L;
+  const int64_t r = (int64_t)blockIdx.x * rows_per_block + gid;
+  if (r >= M) return;   // whole groups leave together: the shuffles stay in-group
+  norm_row<T>(p, which, (int)(r / p.L), (int)(r % p.L), r, gl);
 }
 
 template <typename T>
@@ -235,10 +399,45 @@ extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
     p.y[i] = a->y[i];
     p.rstd[i] = a->rstd[i];
   }
-  p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec); p.eps = a->eps;
+  p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec); p.eps = a->eps; p.count = cnt;
+  const bool theta = a->theta_table || a->theta_prefix || a->theta_chunk_totals ||
+                     a->angles.ptr || a->dt_raw.ptr;
+  size_t dyn = 0;
+  if (theta) {
+    const int H = a->nheads, Nr = a->n_angles, C = a->theta_chunk;
+    M3S_REQUIRE(a->theta_table && a->theta_prefix && a->theta_chunk_totals && a->angles.ptr &&
+                    a->dt_raw.ptr && a->dt_bias,
+                "m3s_norm_fwd: give angles, dt_raw, dt_bias, theta_table, theta_prefix and "
+                "theta_chunk_totals together (or none)");
+    M3S_REQUIRE(H > 0 && Nr > 0 && Nr % 4 == 0 && H <= 1024 && Nr <= 1024,
+                "m3s_norm_fwd: nheads %d / n_angles %d out of range (n_angles %% 4 == 0)", H, Nr);
+    M3S_REQUIRE(C >= 16 && C % 16 == 0 && L % C == 0,
+                "m3s_norm_fwd: theta_chunk %d must be a multiple of 16 dividing seqlen %d", C, L);
+    M3S_REQUIRE((int64_t)C * (H + Nr + H * Nr / 16) * 4 <= 65536,
+                "m3s_norm_fwd: theta_chunk %d, nheads %d and n_angles %d too large for the angle "
+                "kernel's LDS (chunk (H + Nr + H Nr / 16) floats <= 64 KiB)", C, H, Nr);
+    M3S_REQUIRE(aligned16(a->theta_prefix) && aligned16(a->theta_chunk_totals),
+                "m3s_norm_fwd: theta_prefix / theta_chunk_totals must be 16-byte aligned");
+    p.th.ang = a->angles.ptr; p.th.asb = a->angles.stride_b; p.th.ast = a->angles.stride_t;
+    p.th.dtr = a->dt_raw.ptr; p.th.dsb = a->dt_raw.stride_b; p.th.dst = a->dt_raw.stride_t;
+    p.th.dt_bias = a->dt_bias;
+    p.th.tab = a->theta_table;
+    p.th.pre = a->theta_prefix;
+    p.th.ctot = a->theta_chunk_totals;
+    p.th.H = H; p.th.Nr = Nr; p.th.chunk = C; p.th.nblk = B * (L / C);
+    dyn = (size_t)C * (H + Nr + H * Nr / 16) * sizeof(float);
+  }
   const int64_t rows_per_block = kNormThreads / p.G;
-  const dim3 grid((unsigned)(((int64_t)B * L + rows_per_block - 1) / rows_per_block), cnt);
+  const int64_t nblk = ((int64_t)B * L + rows_per_block - 1) / rows_per_block;
+  const dim3 grid((unsigned)nblk, cnt);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (theta) {   // one launch: each block does a chunk's norms and its angle work
+    if (a->dtype == M3S_DTYPE_BF16)
+      hipLaunchKernelGGL(norm_theta_kernel<bf16>, dim3(p.th.nblk), dim3(kThetaThreads), dyn, s, p);
+    else
+      hipLaunchKernelGGL(norm_theta_kernel<float>, dim3(p.th.nblk), dim3(kThetaThreads), dyn, s, p);
+    return launch_status("m3s_norm_fwd");
+  }
   if (a->dtype == M3S_DTYPE_BF16)
     hipLaunchKernelGGL(norm_fwd_kernel<bf16>, grid, dim3(kNormThreads), 0, s, p);
   else

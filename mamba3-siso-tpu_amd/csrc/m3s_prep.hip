@@ -42,33 +42,7 @@ constexpr int kPrepBwdTB = 32;
 template <typename RT>
 __device__ __forceinline__ float ldr(const RT* base, int64_t i) { return (float)base[i]; }
 
-// n / d and n % d for 0 <= n < 2^20 by a divisor d known only at run time, without an
-// integer division (a software routine on the GPU): a float estimate of the quotient
-// (relative error below 2^-21, so off by at most one in this range), then one correction.
-struct DivMod {
-  int d;
-  float inv;
-  __device__ explicit DivMod(int d_) : d(d_), inv(__builtin_amdgcn_rcpf((float)d_)) {}
-  __device__ __forceinline__ void operator()(int n, int& q, int& r) const {
-    q = (int)((float)n * inv);
-    r = n - q * d;
-    if (r < 0) {
-      --q;
-      r += d;
-    } else if (r >= d) {
-      ++q;
-      r -= d;
-    }
-  }
-};
 
-__device__ __forceinline__ float softplus_(float x) {
-  return x > 20.f ? x : log1pf(expf(x));
-}
-__device__ __forceinline__ float heavy_tail_(float x) {
-  return fmaxf(x, 0.f) + 1.f / (1.f - fminf(x, 0.f));
-}
-__device__ __forceinline__ float sigmoid_(float x) { return 1.f / (1.f + expf(-x)); }
 // x mod 2 pi in [0, 2 pi): the quotient from a multiply by 1 / (2 pi), the remainder by
 // one fma, then one correction step. Where x / (2 pi) lies within an ulp of an integer the
 // quotient can differ by one from floor(x / (2 pi)); the correction keeps the result in

@@ -310,6 +310,120 @@ def siso_forward(
     return outs
 
 
+class RawAngles(NamedTuple):
+    """The rotary angles' per-token work that `siso_forward_raw` reads, written by
+    `bcnorm_forward` (``theta=``) in the BCNorm launch for scans at ``chunk``: ``table`` =
+    ``tanh(angles) pi`` ``(B, L, Nr)`` (shared by the heads); with ``theta[t, h] = table[t]
+    dt[t, h]`` summed over each 16-token strip, ``prefix`` ``(B, H, L / 16, Nr)`` the sum of
+    the strips before each one within its chunk and ``chunk_totals`` ``(B, H, L / chunk,
+    Nr)`` each chunk's sum."""
+
+    table: Tensor
+    prefix: Tensor
+    chunk_totals: Tensor
+    chunk: int
+
+
+def raw_forward_ok(pol: LY.DtypePolicy | str, chunk: int, state_dim: int, headdim: int,
+                   n_angles: int, seqlen: int, nheads: int = 1) -> bool:
+    """Whether `siso_forward_raw` runs this shape: a raw-mode kernel of the head's own
+    width at the chunk's tile, ``n_angles % 4 == 0``, ``seqlen % 16 == 0``, and the BCNorm
+    call's angle kernel's per-chunk tables within its 64 KiB of LDS."""
+    pol = LY.policy(pol)
+    if n_angles <= 0 or n_angles % 4 or seqlen % 16:
+        return False
+    try:
+        tile = LY.kernel_chunk(pol.name, chunk, state_dim, headdim)
+    except ValueError:
+        return False
+    if seqlen % tile or tile * (nheads + n_angles + nheads * n_angles // 16) * 4 > 65536:
+        return False
+    return _lib.raw_supported(_lib.dtype_code(pol.matmul), tile, state_dim, headdim, n_angles)
+
+
+def siso_forward_raw(
+    q: Tensor, k: Tensor, v: Tensor, dt_raw: Tensor, a_raw: Tensor, trap_raw: Tensor,
+    angles: RawAngles, dt_bias: Tensor, q_bias: Tensor, k_bias: Tensor,
+    d_skip: Optional[Tensor] = None, z: Optional[Tensor] = None,
+    phi_init: Optional[Tensor] = None, a_floor: float = 1e-4, chunk: int = 128,
+    dtype_policy: LY.DtypePolicy | str = LY.BF16,
+):
+    """`reference.preprocess` (``reference.py:160-199``) and ``kernel_fwd.siso_forward``
+    (``kernel_fwd.py:204-248``) in one scan launch, without residuals (inference): the
+    kernel reads the projection's raw ``dt_raw``, ``a_raw``, ``trap_raw`` ``(B, L, H)``
+    slices in place and computes dt, a, lambda, adt, gamma and the trapezoid's t+1 scale
+    shift as it loads each chunk, and carries the cumulative angle phi across its strips
+    and chunks from ``angles`` (`RawAngles`, from `bcnorm_forward`), starting at
+    ``phi_init`` (zero when None). Returns ``(y, final_ssm, final_k, final_v, phi_final)``;
+    ``y`` has ``v``'s layout. The three raw slices must be views of one projection
+    buffer (shared strides, a and trap after dt in each row)."""
+    pol = LY.policy(dtype_policy)
+    LY.validate_chunk(chunk)
+    batch, seqlen, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[3]
+    n_angles = angles.table.shape[-1]
+    LY.num_chunks(seqlen, chunk)
+    if not raw_forward_ok(pol, chunk, state_dim, headdim, n_angles, seqlen, nheads):
+        raise ValueError(
+            f"no raw-mode forward for policy={pol.name} chunk={chunk} d_state={state_dim} "
+            f"headdim={headdim} n_angles={n_angles} seqlen={seqlen}")
+    chunk = _tile(pol, chunk, state_dim, headdim, "forward")
+    if q.shape != k.shape:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} must match")
+    if tuple(v.shape) != (batch, nheads, seqlen, headdim):
+        raise ValueError(f"unexpected v shape {tuple(v.shape)}")
+    for name, t in (("dt_raw", dt_raw), ("a_raw", a_raw), ("trap_raw", trap_raw)):
+        if tuple(t.shape) != (batch, seqlen, nheads):
+            raise ValueError(f"{name} must be (B, L, H) = {(batch, seqlen, nheads)}, got {tuple(t.shape)}")
+    if (tuple(angles.table.shape) != (batch, seqlen, n_angles)
+            or tuple(angles.prefix.shape) != (batch, nheads, seqlen // 16, n_angles)
+            or tuple(angles.chunk_totals.shape) != (batch, nheads, seqlen // chunk, n_angles)
+            or angles.chunk != chunk):
+        raise ValueError(
+            f"angles must come from bcnorm_forward for this shape at the scan's chunk {chunk}: "
+            "table (B, L, Nr), prefix (B, H, L / 16, Nr), chunk_totals (B, H, L / chunk, Nr)")
+    if z is not None and tuple(z.shape) != tuple(v.shape):
+        raise ValueError(f"z shape {tuple(z.shape)} must match v {tuple(v.shape)}")
+    mt = pol.matmul
+    dev = _device_of(q, k, v, dt_raw, a_raw, trap_raw, angles.table, angles.prefix, angles.chunk_totals, dt_bias,
+                     q_bias, k_bias, d_skip, z, phi_init)
+    if dt_raw.dtype != mt or a_raw.dtype != mt or trap_raw.dtype != mt:
+        raise ValueError(f"the raw slices must be in the policy's operand dtype {mt}")
+    qc, kc = _mt(q, mt), _mt(k, mt)
+    vc, zc = _bhlp_operand(v, mt), _bhlp_operand(z, mt)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    tab, pre, ctot, bias = (_f32c(t) for t in (angles.table, angles.prefix, angles.chunk_totals,
+                                                dt_bias))
+    pinit = _f32c(phi_init)
+    y = _empty_like_layout(vc, mt)
+    f32 = dict(device=dev, dtype=torch.float32)
+    final_ssm = empty(batch, nheads, headdim, state_dim, **f32)
+    final_k = empty(batch, nheads, state_dim, **f32)
+    final_v = empty(batch, nheads, headdim, **f32)
+    phi_final = empty(batch, nheads, n_angles, **f32)
+
+    a = _lib.FwdArgs()
+    a.struct_size = ctypes.sizeof(_lib.FwdArgs)
+    a.batch, a.seqlen, a.nheads, a.headdim = batch, seqlen, nheads, headdim
+    a.state_dim, a.n_angles, a.chunk = state_dim, n_angles, chunk
+    a.dtype = _lib.dtype_code(mt)
+    a.has_d, a.has_z, a.has_seed = int(d_c is not None), int(zc is not None), 0
+    a.save_residuals = 0
+    a.q, a.k = qc.data_ptr(), kc.data_ptr()
+    a.v, a.z = _lib.bhlp(vc), _lib.bhlp(zc)
+    a.theta_table = tab.data_ptr()
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.y = _lib.bhlp(y)
+    a.final_ssm, a.final_k, a.final_v = final_ssm.data_ptr(), final_k.data_ptr(), final_v.data_ptr()
+    a.raw, a.a_floor = 1, float(a_floor)
+    a.dt_raw, a.a_raw, a.trap_raw = _lib.blx(dt_raw), _lib.blx(a_raw), _lib.blx(trap_raw)
+    a.dt_bias, a.theta_prefix, a.theta_chunk_totals = bias.data_ptr(), pre.data_ptr(), ctot.data_ptr()
+    a.phi_init, a.phi_final = _lib.ptr(pinit), phi_final.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_fwd(ctypes.byref(a), _lib.stream_handle(dev)), "m3s_fwd")
+    return y, final_ssm, final_k, final_v, phi_final
+
+
 # ======================================================================================
 # Decode (kernel_decode.py:252-573)
 # ======================================================================================
@@ -754,10 +868,15 @@ def bcnorm_supported(x: Tensor) -> bool:
     return n % vec == 0 and n // vec <= 64 and _norm_rows_ok(x)
 
 
-def bcnorm_forward(xs, weights, eps: float):
+def bcnorm_forward(xs, weights, eps: float, theta=None):
     """RMSNorm of each (B, L, N) view in ``xs`` (one or two, same shape and dtype) with its
     gain; one ``m3s_norm_fwd`` launch. Returns ``(ys, rstds)``: dense (B, L, N) outputs in
-    the input dtype and the (B, L) f32 reciprocal RMS values the backward reuses."""
+    the input dtype and the (B, L) f32 reciprocal RMS values the backward reuses.
+
+    ``theta = (angles (B, L, Nr), dt_raw (B, L, H), dt_bias (H,), chunk)`` (raw projection
+    slices in the inputs' dtype; ``chunk`` the tile the scan runs at, `layout.kernel_chunk`)
+    also computes, in the same launch, the `RawAngles` that `siso_forward_raw` reads; the
+    result is then ``(ys, rstds, RawAngles)``."""
     x0 = xs[0]
     dev = _device_of(*xs, *weights)
     batch, seqlen, width = x0.shape
@@ -774,9 +893,30 @@ def bcnorm_forward(xs, weights, eps: float):
     for i, x in enumerate(xs):
         a.x[i] = _lib.blx(x)
         a.weight[i], a.y[i], a.rstd[i] = ws[i].data_ptr(), ys[i].data_ptr(), rstds[i].data_ptr()
+    keep = None
+    if theta is not None:
+        angles, dt_raw, dt_bias, chunk = theta
+        nr, nh = angles.shape[-1], dt_raw.shape[-1]
+        if (tuple(angles.shape[:2]) != (batch, seqlen) or tuple(dt_raw.shape[:2]) != (batch, seqlen)
+                or angles.dtype != x0.dtype or dt_raw.dtype != x0.dtype or chunk % 16
+                or seqlen % chunk or nr % 4):
+            raise ValueError("bcnorm theta: angles (B, L, Nr) and dt_raw (B, L, H) in the inputs' "
+                             "dtype, a chunk that is a multiple of 16 dividing L, Nr % 4 == 0")
+        _device_of(angles, dt_raw, dt_bias)
+        bias = _f32c(dt_bias)
+        table = empty(batch, seqlen, nr, device=dev, dtype=torch.float32)
+        prefix = empty(batch, nh, seqlen // 16, nr, device=dev, dtype=torch.float32)
+        ctot = empty(batch, nh, seqlen // chunk, nr, device=dev, dtype=torch.float32)
+        a.nheads, a.n_angles, a.theta_chunk = nh, nr, chunk
+        a.angles, a.dt_raw = _lib.blx(angles), _lib.blx(dt_raw)
+        a.dt_bias, a.theta_table = bias.data_ptr(), table.data_ptr()
+        a.theta_prefix, a.theta_chunk_totals = prefix.data_ptr(), ctot.data_ptr()
+        keep = (bias, RawAngles(table, prefix, ctot, chunk))
     with torch.cuda.device(dev):
         _lib.check(_lib.load().m3s_norm_fwd(ctypes.byref(a), _lib.stream_handle(dev)),
                    "m3s_norm_fwd")
+    if keep is not None:
+        return ys, rstds, keep[1]
     return ys, rstds
 
 

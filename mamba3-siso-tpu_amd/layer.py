@@ -238,18 +238,36 @@ class _LayerFn(torch.autograd.Function):
         u2 = u.reshape(m, dm)
         proj = (u2 @ w_t.t()).view(batch, seqlen, dp)
         z, x, b, c, dt_raw, a_raw, trap_raw, angles = split_in_proj(proj[..., :d], cfg)
-        (k, q), (rk, rq) = K.bcnorm_forward([b, c], [b_norm_weight, c_norm_weight], cfg.norm_eps)
         bias = dt_bias.float().contiguous()
         need = any(ctx.needs_input_grad[:9])   # all False under no_grad
-        # compact: phi stays compact (kernels.PhiStrips) and the scans rebuild it per row;
-        # otherwise the preprocess materialises it (B, H, L, Nr). By default compact exactly
-        # when no gradient is taken (the forward is faster that way, the backward slower).
-        compact = (not need) if phi_in_kernel is None else bool(phi_in_kernel)
-        adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
-            dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=compact)
-        outs = K.siso_forward(q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias,
-                              b_bias, d_skip=d_skip, z=z.permute(0, 2, 1, 3), chunk=cfg.chunk,
-                              dtype_policy=cfg.policy_name, save_residuals=need)
+        # Without gradients the preprocess runs inside the other launches (raw mode): the
+        # BCNorm launch also writes the rotary table and per-strip theta totals, and the scan
+        # reads the raw dt / a / trap slices in place and carries phi itself. With gradients
+        # the preprocess materialises the row scalars the backward reads, and phi either as
+        # (B, H, L, Nr) or compact (kernels.PhiStrips: the scans rebuild it per row).
+        raw = (not need and phi_in_kernel is not False
+               and K.raw_forward_ok(cfg.policy_name, cfg.chunk, cfg.d_state, cfg.headdim,
+                                    cfg.n_angles, seqlen, cfg.nheads))
+        if raw:
+            tile = LY.kernel_chunk(cfg.policy_name, cfg.chunk, cfg.d_state, cfg.headdim)
+            (k, q), (rk, rq), angs = K.bcnorm_forward(
+                [b, c], [b_norm_weight, c_norm_weight], cfg.norm_eps,
+                theta=(angles, dt_raw, bias, tile))
+            outs = K.siso_forward_raw(q, k, x.permute(0, 2, 1, 3), dt_raw, a_raw, trap_raw, angs,
+                                      bias, c_bias, b_bias, d_skip=d_skip,
+                                      z=z.permute(0, 2, 1, 3), a_floor=cfg.a_floor,
+                                      chunk=cfg.chunk, dtype_policy=cfg.policy_name)
+            phi_final = outs[4]
+        else:
+            (k, q), (rk, rq) = K.bcnorm_forward([b, c], [b_norm_weight, c_norm_weight],
+                                                cfg.norm_eps)
+            compact = (not need) if phi_in_kernel is None else bool(phi_in_kernel)
+            adt, gamma, scale, _, _, phi, phi_final = SP.prep_forward_launch(
+                dt_raw, a_raw, trap_raw, angles, bias, None, cfg.a_floor, compact=compact)
+            outs = K.siso_forward(q, k, x.permute(0, 2, 1, 3), adt, gamma, scale, phi, c_bias,
+                                  b_bias, d_skip=d_skip, z=z.permute(0, 2, 1, 3),
+                                  chunk=cfg.chunk, dtype_policy=cfg.policy_name,
+                                  save_residuals=need)
         y, fs, fk, fv = outs[:4]
         y2 = y.permute(0, 2, 1, 3).reshape(m, cfg.d_inner)
         wo_t = K.transpose_pad(out_proj, dt, dm)
@@ -328,10 +346,11 @@ def mamba3_siso_layer(params: SISOParams, u: Tensor, cfg: SISOConfig,
     ``phi_in_kernel`` (no counterpart in the reference; same results to float rounding):
     when True the cumulative rotary angle is not materialised as ``(B, H, L, Nr)``; the
     scan kernels rebuild it per token from the head-shared ``tanh(angles) pi`` table, dt
-    and one angle per 16 tokens, which moves 1/16 of phi's bytes. The forward scan is then
-    faster as a whole (the preprocess writes no phi), the backward scan slower (its
-    in-kernel prefix sits on its critical path). ``None`` (the default) picks the compact
-    form exactly when no gradient will be taken; True / False force either form."""
+    and one angle per 16 tokens, which moves 1/16 of phi's bytes. Without gradients
+    (``None`` or True) the whole preprocess then runs inside the BCNorm and scan launches
+    (`kernels.siso_forward_raw`) where a raw-mode kernel exists for the shape. With
+    gradients ``None`` (the default) materialises phi, whose backward scan is faster, and
+    True keeps it compact. False always materialises phi and the row scalars first."""
     cfg.require_kernels()
     if _fused_ok(u, cfg, state):
         out, fs, fk, fv, phi_final = _LayerFn.apply(

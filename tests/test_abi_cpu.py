@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 8
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 9
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -67,6 +67,8 @@ int main(void) {
          offsetof(m3s_wgrad_args, workspace));
   printf("%zu %zu %zu\n", sizeof(m3s_gemv_args), offsetof(m3s_gemv_args, ldw),
          offsetof(m3s_gemv_args, ldy));
+  printf("%zu %zu %zu %zu\n", offsetof(m3s_fwd_args, raw), offsetof(m3s_fwd_args, phi_final),
+         offsetof(m3s_norm_fwd_args, angles), offsetof(m3s_norm_fwd_args, theta_chunk_totals));
   return 0;
 }
 """
@@ -100,7 +102,9 @@ int main(void) {
                             lib.AdamwArgs.bias_correction2_sqrt.offset]
     assert sizes[34:37] == [ctypes.sizeof(lib.WgradArgs), lib.WgradArgs.ldb.offset,
                             lib.WgradArgs.workspace.offset]
-    assert sizes[37:] == [ctypes.sizeof(lib.GemvArgs), lib.GemvArgs.ldw.offset,
+    assert sizes[40:] == [lib.FwdArgs.raw.offset, lib.FwdArgs.phi_final.offset,
+                          lib.NormFwdArgs.angles.offset, lib.NormFwdArgs.theta_chunk_totals.offset]
+    assert sizes[37:40] == [ctypes.sizeof(lib.GemvArgs), lib.GemvArgs.ldw.offset,
                           lib.GemvArgs.ldy.offset]
 
 

@@ -130,6 +130,51 @@ def test_layer_bf16_forward_and_grads(m3, d_model, batch, seqlen, seed):
         assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
 
 
+@pytest.mark.parametrize("d_model,chunk,seqlen", [(1024, 128, 512), (256, 512, 1024),
+                                                  (512, 64, 256)])
+def test_layer_forward_without_gradients_runs_the_preprocess_in_the_scan(m3, monkeypatch,
+                                                                         d_model, chunk, seqlen):
+    """Under no_grad the bf16 layer runs raw mode (the BCNorm launch writes the rotary
+    table and strip totals, the scan reads the raw dt / a / trap slices and carries phi):
+    the preprocess launch is never called, and the output and final state agree with the
+    path that materialises phi and the row scalars first (phi_in_kernel=False) and with the
+    float64 layer and its bf16 rounding model."""
+    cfg = m3.SISOConfig(d_model=d_model, d_state=128, headdim=64, expand=2, chunk=chunk)
+    p_cpu = m3.init_params(cfg, 41)
+    params = m3.SISOParams(*(t.cuda() for t in p_cpu))
+    u = torch.randn(2, seqlen, d_model, generator=torch.Generator().manual_seed(42)).to(BF16)
+    with torch.no_grad():
+        y0, st0 = m3.mamba3_siso_layer(params, u.cuda(), cfg, phi_in_kernel=False)
+        with monkeypatch.context() as mp:
+            def refuse(*a, **k):
+                raise AssertionError("the preprocess launch ran in raw mode")
+            mp.setattr(m3.scan_prep, "prep_forward_launch", refuse)
+            y, st = m3.mamba3_siso_layer(params, u.cuda(), cfg)
+        # the rounding model at the chunk the kernel runs (a longer chunk runs as tiles)
+        from mamba3_siso_tpu_amd import layout as LY
+        tile = LY.kernel_chunk("bf16", chunk, 128, 64)
+        ym, sm = O.layer_forward(params_dict(p_cpu), u.double(), d_state=128, headdim=64,
+                                 expand=2, chunk=tile, mm_dtype=BF16, act_dtype=BF16)
+        yr, sr = O.layer_forward(params_dict(p_cpu), u.double(), d_state=128, headdim=64,
+                                 expand=2, chunk=chunk)
+    report("raw-mode layer y vs phi materialised", y, cpu(y0))
+    report("raw-mode layer final ssm vs phi materialised", st.ssm, cpu(st0.ssm))
+    # the raw path's dt, gamma and scale come from hardware exp2 / log2 / rcp (a few 1e-5
+    # relative), which moves some bf16 roundings of the operands
+    assert O.rel_error(cpu(y), cpu(y0)) <= 1e-2
+    assert O.max_rel(cpu(st.ssm), cpu(st0.ssm)) <= 5e-3
+    assert torch.equal(st.v, st0.v)
+    assert O.rel_error(cpu(st.phi), cpu(st0.phi), angle=True, pct=100.0) <= 1e-5
+    report("raw-mode layer y vs bf16 layer model", y, ym)
+    assert_p95(y, ym, BF16_LAYER_MODEL_P95, "y vs bf16 layer model")
+    assert_bf16_bound(y, ym, what="y vs bf16 layer model")
+    assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
+    assert_maxabs(st.ssm, sr.ssm, STATE_MAXABS, "final ssm")
+    # the angles and dt come from the bf16 projection, whose entries the GEMM rounds
+    # differently from the model in places (measured 1.2e-3 rad at L = 512)
+    assert O.rel_error(cpu(st.phi), sm.phi, angle=True, pct=100.0) <= 5e-3
+
+
 @pytest.mark.parametrize("policy,chunk", [("bf16", 256), ("bf16", 512), ("f32", 128),
                                           ("f32", 64)])
 def test_layer_at_chunks_without_a_kernel_of_their_own(m3, policy, chunk):
