@@ -112,9 +112,15 @@ struct FwdCfg {
   static_assert(LDS_BYTES <= 163840, "LDS budget of one gfx950 CU");
 };
 
-template <typename MT, int C, int N, int P, int NW, bool STRIPS>
+// STRIPS: phi built from the compact form (phi_strips mode). RAW (raw mode, with STRIPS):
+// the row scalars from the raw dt / a / trap slices (the library functions the preprocess
+// kernels use, so the same values), and each row's angle from a carry across chunks that
+// every thread keeps for its angle group, the strip's prefix within its chunk and the
+// strip's table rows times their dt.
+template <typename MT, int C, int N, int P, int NW, bool STRIPS, bool RAW = false>
 __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   using F = FwdCfg<MT, C, N, P, NW>;
+  static_assert(!RAW || STRIPS, "raw mode builds phi");
   using vec = typename V16<MT>::type;
   constexpr int NT = F::NT, VEC = F::VEC, H2 = F::H2;
   constexpr int LDQ = F::LDQ, LDT = F::LDT, LDO = F::LDO;
@@ -161,6 +167,13 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   const float* sclg = p.scale + bh * L;
   const float* phig = STRIPS ? nullptr : p.phi + bh * (int64_t)L * Nr;
   MT* csg = p.save ? static_cast<MT*>(p.cstates) + bh * (int64_t)nc * N * P : nullptr;
+  // raw mode: this (b, h)'s raw scalars (dt at element t sc_st, a and trap a_off / t_off
+  // further) and dt bias
+  const MT* scg = RAW ? static_cast<const MT*>(p.sc) + b * p.sc_sb + h : nullptr;
+  const int64_t sc_st = RAW ? p.sc_st : 0;
+  const float dtb = RAW ? p.dt_bias[h] : 0.f;
+  auto raw_dt = [&](int64_t t) { return softplus_((float)scg[t * sc_st] + dtb); };
+  auto raw_lam = [&](int64_t t) { return sigmoid_((float)scg[t * sc_st + p.t_off]); };
 
   // ---- carried state: registers, MFMA layout ------------------------------------
   f32x4 Sacc[F::SPW];
@@ -205,6 +218,17 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
   float rscale[F::QKR][2], rgam[F::QKR][2];
   vec rv[F::VR][2], rz[F::VR][2];
   float radt[F::E];
+  // raw mode: the angle entering the chunk being prefetched, for this thread's angle groups
+  float pin[RAW ? F::QKR : 1][VEC];
+  if constexpr (RAW) {
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int j0 = ((tid + r * NT) % F::QKG) * VEC;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        pin[r][i] = (p.phi_init && j0 + i < Nr) ? p.phi_init[bh * Nr + j0 + i] : 0.f;
+    }
+  }
 
   const bool phi_vec = (Nr % 4) == 0;
   auto prefetch = [&](int c) {
@@ -223,21 +247,24 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
           rk[r][e][1] = *reinterpret_cast<const vec*>(kg + t * N + H2 + j0);
           if constexpr (STRIPS) {
             // the strip's entering angle plus theta = tanh(angles) pi dt over the strip's
-            // rows up to t (at most 16)
+            // rows up to t (at most 16); raw mode: the entering angle is the chunk's carry
+            // plus the strip's prefix within the chunk, and dt comes from the raw slice
             const int64_t s16 = t >> 4;
-            const float* ps = p.pstr + (bh * (L / 16) + s16) * Nr;
+            const float* ps = (RAW ? p.tpre : p.pstr) + (bh * (L / 16) + s16) * Nr;
             const float* tb = p.tht + (int64_t)b * L * Nr;
-            const float* db = p.pdt + bh * L;
+            const float* db = RAW ? nullptr : p.pdt + bh * L;
 #pragma unroll
             for (int qd = 0; qd < VEC / 4; ++qd) {
 #pragma unroll
               for (int i = 0; i < 4; ++i) {
                 const int j = j0 + 4 * qd + i;
-                rphi[r][e][qd][i] = j < Nr ? ps[j] : 0.f;
+                float e0 = j < Nr ? ps[j] : 0.f;
+                if constexpr (RAW) e0 += pin[r][4 * qd + i];
+                rphi[r][e][qd][i] = e0;
               }
             }
             for (int64_t u = s16 * 16; u <= t; ++u) {
-              const float du = db[u];
+              const float du = RAW ? raw_dt(u) : db[u];
 #pragma unroll
               for (int qd = 0; qd < VEC / 4; ++qd) {
 #pragma unroll
@@ -260,9 +287,26 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
               }
             }
           }
-          rscale[r][e] = sclg[t];
-          rgam[r][e] = gamg[t];
+          if constexpr (RAW) {   // reference.py:104-131: gamma, and the t+1 scale shift
+            const float dtt = raw_dt(t), lamt = raw_lam(t);
+            const float nxt = t + 1 < L ? raw_dt(t + 1) * (1.f - raw_lam(t + 1)) : 0.f;
+            rgam[r][e] = dtt * lamt;
+            rscale[r][e] = rgam[r][e] + nxt;
+          } else {
+            rscale[r][e] = sclg[t];
+            rgam[r][e] = gamg[t];
+          }
         }
+      }
+    }
+    if constexpr (RAW) {   // the carry moves past this chunk
+#pragma unroll
+      for (int r = 0; r < F::QKR; ++r) {
+        const int j0 = ((tid + r * NT) % F::QKG) * VEC;
+        const float* ct = p.ctot + (bh * nc + c) * Nr;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          if (j0 + i < Nr) pin[r][i] = wrap_2pi(pin[r][i] + ct[j0 + i]);
       }
     }
 #pragma unroll
@@ -282,7 +326,13 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
 #pragma unroll
       for (int e = 0; e < F::E; ++e) {
         const int tt = lane * F::E + e;
-        radt[e] = tt < C ? adtg[t0 + tt] : 0.f;
+        if constexpr (RAW) {   // a = min(-heavy_tail(a_raw), -a_floor)
+          radt[e] = tt < C ? fminf(-heavy_tail_((float)scg[(t0 + tt) * sc_st + p.a_off]), -p.a_floor) *
+                                 raw_dt(t0 + tt)
+                           : 0.f;
+        } else {
+          radt[e] = tt < C ? adtg[t0 + tt] : 0.f;
+        }
       }
     }
   };
@@ -566,6 +616,18 @@ __global__ void __launch_bounds__(NW * 64) fwd_kernel(const FwdParams p) {
       for (int i = 0; i < 4; ++i) {
         const int prow = pb * 16 + 4 * (lane >> 4) + i;
         p.fssm[(bh * P + prow) * N + ncol] = Sacc[m][i];
+      }
+    }
+  }
+  if constexpr (RAW) {   // the carry past the last chunk: phi at L-1
+#pragma unroll
+    for (int r = 0; r < F::QKR; ++r) {
+      const int task = tid + r * NT;
+      const int j0 = (task % F::QKG) * VEC;
+      if (task < F::QKG) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i)
+          if (j0 + i < Nr) p.phi_final[bh * Nr + j0 + i] = pin[r][i];
       }
     }
   }
@@ -1608,21 +1670,25 @@ constexpr int raw_nrb_max() {
 template <typename MT, int C, int N, int P>
 static int32_t launch_fwd(const FwdParams& prm, int grid, hipStream_t stream) {
   const bool strips = prm.pstr != nullptr;
-  if (prm.sc != nullptr) {   // raw mode (the caller checked raw_nrb_max and fits_rsrc)
+  if (prm.sc != nullptr) {   // raw mode: the bf16 kernel where it applies, else the generic one
+    // the bf16 kernel addresses the raw slices and every stream through buffer descriptors
+    const bool fast = fits_rsrc(prm, N, P) &&
+                      ((int64_t)(prm.L - 1) * prm.sc_st + prm.sc_span) * (int64_t)sizeof(MT) < (1ll << 31);
     if constexpr (raw_nrb_max<MT, C, N, P>() >= 1) {
-      if (prm.Nr <= 32) {
+      if (fast && prm.Nr <= 32) {
         hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 1, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
         return launch_status("m3s_fwd");
       }
     }
     if constexpr (raw_nrb_max<MT, C, N, P>() >= 2) {
-      if (prm.Nr <= 64) {
+      if (fast && prm.Nr <= 64) {
         hipLaunchKernelGGL((fwd_bf16_kernel<C, N, P, 2, true>), dim3(grid), dim3(C / 16 * 64), 0, stream, prm);
         return launch_status("m3s_fwd");
       }
     }
-    set_error("m3s_fwd: no raw-mode kernel for n_angles %d", prm.Nr);
-    return M3S_ERR_UNSUPPORTED;
+    constexpr int NWr = (C / 16) > 4 ? (C / 16) : 4;
+    hipLaunchKernelGGL((fwd_kernel<MT, C, N, P, NWr, true, true>), dim3(grid), dim3(NWr * 64), 0, stream, prm);
+    return launch_status("m3s_fwd");
   }
   if constexpr (std::is_same<MT, bf16>::value && N % 64 == 0 && C % 64 == 0) {
     if (fits_rsrc(prm, N, P)) {
@@ -1693,14 +1759,11 @@ int32_t fwd_supported(int dtype, int chunk, int n, int pdim) {
   return 0;
 }
 
+// Every compiled configuration takes raw mode: the bf16 kernel where raw_nrb_max allows,
+// the generic kernel otherwise.
 int32_t fwd_raw_supported_impl(int dtype, int chunk, int n, int pdim, int nr) {
   if (nr <= 0 || nr % 4 != 0) return 0;
-#define X(MT, C, N, P)                                                        \
-  if (dtype == dtype_code<MT>() && chunk == C && n == N && pdim == P)         \
-    return 32 * raw_nrb_max<MT, C, N, P>() >= nr ? 1 : 0;
-  M3S_FWD_CONFIGS(X)
-#undef X
-  return 0;
+  return fwd_supported(dtype, chunk, n, pdim);
 }
 
 }  // namespace m3s
@@ -1760,8 +1823,6 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
                 "within each row");
     a_off = (int)(da / esz);
     t_off = (int)(dtr / esz);
-    M3S_REQUIRE(((int64_t)(L - 1) * a->dt_raw.stride_t + std::max(a_off, t_off) + 1) * esz < (1ll << 31),
-                "m3s_fwd: the raw slices of one batch element span 2 GiB or more");
     if (!fwd_raw_supported_impl(a->dtype, C, N, P, Nr)) {
       set_error("m3s_fwd: no raw-mode kernel for dtype=%s chunk=%d state_dim=%d headdim=%d "
                 "n_angles=%d", a->dtype == M3S_DTYPE_BF16 ? "bf16" : "f32", C, N, P, Nr);
@@ -1813,8 +1874,6 @@ extern "C" int32_t m3s_fwd(const m3s_fwd_args* a, void* stream) {
     prm.ctot = a->theta_chunk_totals;
     prm.phi_init = a->phi_init;
     prm.phi_final = a->phi_final;
-    M3S_REQUIRE(fits_rsrc(prm, N, P), "m3s_fwd: raw mode needs every per-(b, h) stream under "
-                "2 GiB");
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int grid = B * H;

@@ -16,6 +16,7 @@
 // gradient is summed per block in a fixed order, then over blocks by a second launch,
 // so it does not depend on the order in which blocks finish. HBM-bound.
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 #include "m3s_common.h"
@@ -99,7 +100,7 @@ __device__ __forceinline__ float group_sum_dyn(float v, int G) {
 // chunk's table rows and every head's dt into LDS; every (strip, head, angle quad) sum of
 // 16 rows in time order into LDS; a thread per (head, quad) walks the strips for their
 // prefixes and the chunk total. The angle role's loads are issued first, so the norm rows
-// stream while they are in flight. LDS: chunk (Nr + H) + chunk / 16 * H * Nr floats.
+// stream while they are in flight. LDS: chunk (Nr + H) + (chunk / 16) H Nr floats.
 constexpr int kThetaThreads = 512;
 // The chunk's B and C rows, kRowBatch rows per group of G lanes at a time: every row's
 // load is issued before the first row's statistic (one memory latency per batch).
@@ -178,7 +179,9 @@ __global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwd
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
       if (i < C * Nr) {
-        const float tp = tanh_fast(v[u]) * kPi;
+        // bf16 operands: the hardware exp2 / rcp; f32: the library functions, as the
+        // preprocess kernels use them
+        const float tp = (std::is_same<T, float>::value ? tanhf(v[u]) : tanh_fast(v[u])) * kPi;
         q.tab[((int64_t)b * L + t0) * Nr + i] = tp;   // the chunk's rows are contiguous
         sTab[i] = tp;
       }
@@ -196,7 +199,7 @@ __global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwd
 #pragma unroll
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
-      if (i < C * H) sDt[i] = softplus_fast(v[u]);
+      if (i < C * H) sDt[i] = std::is_same<T, float>::value ? softplus_(v[u]) : softplus_fast(v[u]);
     }
   }
   norm_rows_of_chunk<T>(p, b, t0);
@@ -413,9 +416,9 @@ extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
                 "m3s_norm_fwd: nheads %d / n_angles %d out of range (n_angles %% 4 == 0)", H, Nr);
     M3S_REQUIRE(C >= 16 && C % 16 == 0 && L % C == 0,
                 "m3s_norm_fwd: theta_chunk %d must be a multiple of 16 dividing seqlen %d", C, L);
-    M3S_REQUIRE((int64_t)C * (H + Nr + H * Nr / 16) * 4 <= 65536,
+    M3S_REQUIRE(((int64_t)C * (H + Nr) + (int64_t)(C / 16) * H * Nr) * 4 <= 65536,
                 "m3s_norm_fwd: theta_chunk %d, nheads %d and n_angles %d too large for the angle "
-                "kernel's LDS (chunk (H + Nr + H Nr / 16) floats <= 64 KiB)", C, H, Nr);
+                "kernel's LDS (chunk (H + Nr) + (chunk / 16) H Nr floats <= 64 KiB)", C, H, Nr);
     M3S_REQUIRE(aligned16(a->theta_prefix) && aligned16(a->theta_chunk_totals),
                 "m3s_norm_fwd: theta_prefix / theta_chunk_totals must be 16-byte aligned");
     p.th.ang = a->angles.ptr; p.th.asb = a->angles.stride_b; p.th.ast = a->angles.stride_t;
@@ -425,7 +428,7 @@ extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
     p.th.pre = a->theta_prefix;
     p.th.ctot = a->theta_chunk_totals;
     p.th.H = H; p.th.Nr = Nr; p.th.chunk = C; p.th.nblk = B * (L / C);
-    dyn = (size_t)C * (H + Nr + H * Nr / 16) * sizeof(float);
+    dyn = ((size_t)C * (H + Nr) + (size_t)(C / 16) * H * Nr) * sizeof(float);
   }
   const int64_t rows_per_block = kNormThreads / p.G;
   const int64_t nblk = ((int64_t)B * L + rows_per_block - 1) / rows_per_block;

@@ -336,7 +336,7 @@ def raw_forward_ok(pol: LY.DtypePolicy | str, chunk: int, state_dim: int, headdi
         tile = LY.kernel_chunk(pol.name, chunk, state_dim, headdim)
     except ValueError:
         return False
-    if seqlen % tile or tile * (nheads + n_angles + nheads * n_angles // 16) * 4 > 65536:
+    if seqlen % tile or (tile * (nheads + n_angles) + tile // 16 * nheads * n_angles) * 4 > 65536:
         return False
     return _lib.raw_supported(_lib.dtype_code(pol.matmul), tile, state_dim, headdim, n_angles)
 

@@ -130,6 +130,28 @@ def test_layer_bf16_forward_and_grads(m3, d_model, batch, seqlen, seed):
         assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
 
 
+def test_cfg1_layer_forward_without_gradients_in_raw_mode(m3, monkeypatch):
+    """BASELINE configs[0]'s layer (f32 policy) without gradients runs raw mode (the generic
+    kernel's): no preprocess launch; y and the final state within the f32 bars of the
+    float64 layer, and phi within 1e-5."""
+    cfg = cfg1(m3)
+    p_cpu = m3.init_params(cfg, 0)
+    params = m3.SISOParams(*(t.cuda() for t in p_cpu))
+    u = torch.randn(1, 512, 64, generator=torch.Generator().manual_seed(0))
+    with torch.no_grad(), monkeypatch.context() as mp:
+        def refuse(*a, **k):
+            raise AssertionError("the preprocess launch ran in raw mode")
+        mp.setattr(m3.scan_prep, "prep_forward_launch", refuse)
+        y, st = m3.mamba3_siso_layer(params, u.cuda(), cfg)
+    yr, sr = O.layer_forward(params_dict(p_cpu), u.double(), d_state=16, headdim=16, expand=1,
+                             chunk=64)
+    report("raw-mode cfg1 layer y vs float64", y, yr)
+    assert_f32(y, yr, "out", "y")
+    assert_f32(st.ssm, sr.ssm, "out", "final ssm")
+    assert_f32(st.k, sr.k, "out", "final k")
+    assert O.rel_error(cpu(st.phi), sr.phi, angle=True, pct=100.0) <= 1e-5
+
+
 @pytest.mark.parametrize("d_model,chunk,seqlen", [(1024, 128, 512), (256, 512, 1024),
                                                   (512, 64, 256)])
 def test_layer_forward_without_gradients_runs_the_preprocess_in_the_scan(m3, monkeypatch,

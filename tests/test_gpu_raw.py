@@ -9,19 +9,20 @@ import math
 import pytest
 import torch
 
-from helpers import (BF16, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_Y_MAXREL, F64,
-                     STATE_MAXABS, assert_bf16_bound, assert_maxabs, assert_maxrel, assert_p95,
-                     cpu, report)
+from helpers import (BF16, BF16_MODEL_P95, BF16_OUT_MODEL_P95, BF16_Y_MAXREL, F32, F64,
+                     STATE_MAXABS, assert_bf16_bound, assert_f32, assert_maxabs, assert_maxrel,
+                     assert_p95, cpu, report)
 from oracle import siso_oracle as O
 
 pytestmark = pytest.mark.gpu
 
 
-def raw_case(b, h, L, n, p, nr, seed, gate=True, phi_init=False, scale_dt=1.0):
-    """Seeded raw inputs, rounded to bf16 where the kernels read bf16: the dt / a / trap
-    slices live in one (B, L, 3H + 8) buffer (as in the projection), the angles in a
-    (B, L, Nr + 8) one; q and k are BCNorm outputs of random rows (the launch under test
-    writes them with the angle outputs). Returns (cpu float64 dict, device dict)."""
+def raw_case(b, h, L, n, p, nr, seed, gate=True, phi_init=False, scale_dt=1.0, mt=BF16):
+    """Seeded raw inputs, rounded to the operand dtype ``mt`` where the kernels read it:
+    the dt / a / trap slices live in one (B, L, 3H + 8) buffer (as in the projection), the
+    angles in a (B, L, Nr + 8) one; q and k are BCNorm outputs of random rows (the launch
+    under test writes them with the angle outputs). Returns (cpu float64 dict, device
+    dict)."""
     x = O.make_inputs(b, h, L, n, p, nr, seed=seed)
     g = torch.Generator().manual_seed(seed + 5)
     bias = torch.randn(h, generator=g, dtype=F64).float().double() * 0.5
@@ -29,25 +30,25 @@ def raw_case(b, h, L, n, p, nr, seed, gate=True, phi_init=False, scale_dt=1.0):
     sc[..., :h] = x["dt_raw"] + math.log(scale_dt) - bias
     sc[..., h:2 * h] = x["a_raw"]
     sc[..., 2 * h:3 * h] = x["trap_raw"]
-    sc = sc.to(BF16)
+    sc = sc.to(mt)
     ang = torch.zeros(b, L, nr + 8, dtype=F64)
     ang[..., :nr] = x["angles"] * 2.0
-    ang = ang.to(BF16)
+    ang = ang.to(mt)
     wb = (torch.rand(n, generator=g, dtype=F64) + 0.5).float()
     wc = (torch.rand(n, generator=g, dtype=F64) + 0.5).float()
-    kr = torch.randn(b, L, n, generator=g).to(BF16)
-    qr = torch.randn(b, L, n, generator=g).to(BF16)
+    kr = torch.randn(b, L, n, generator=g).to(mt)
+    qr = torch.randn(b, L, n, generator=g).to(mt)
     dev = dict(sc=sc.cuda(), ang=ang.cuda(), bias=bias.float().cuda(), wb=wb.cuda(),
                wc=wc.cuda(), kr=kr.cuda(), qr=qr.cuda(),
-               v=x["v"].to(BF16).cuda(), z=x["z"].to(BF16).cuda() if gate else None,
+               v=x["v"].to(mt).cuda(), z=x["z"].to(mt).cuda() if gate else None,
                qb=x["q_bias"].float().cuda(), kb=x["k_bias"].float().cuda(),
                d=x["d_skip"].float().cuda() if gate else None)
     if phi_init:
         dev["phi_init"] = (torch.rand(b, h, nr, generator=g) * 6.2).cuda()
     scd = sc.double()
     c = dict(dt_raw=scd[..., :h], a_raw=scd[..., h:2 * h], trap_raw=scd[..., 2 * h:3 * h],
-             angles=ang.double()[..., :nr], bias=bias, v=x["v"].to(BF16).double(),
-             z=x["z"].to(BF16).double() if gate else None, qb=x["q_bias"].float().double(),
+             angles=ang.double()[..., :nr], bias=bias, v=x["v"].to(mt).double(),
+             z=x["z"].to(mt).double() if gate else None, qb=x["q_bias"].float().double(),
              kb=x["k_bias"].float().double(), d=x["d_skip"].float().double() if gate else None,
              phi_init=dev["phi_init"].double().cpu() if phi_init else None)
     return c, dev
@@ -58,14 +59,15 @@ def views(dev, h, nr):
     return sc[..., :h], sc[..., h:2 * h], sc[..., 2 * h:3 * h], dev["ang"][..., :nr]
 
 
-def run_raw(m3, dev, h, nr, chunk, a_floor=1e-4):
+def run_raw(m3, dev, h, nr, chunk, a_floor=1e-4, policy="bf16"):
     K = m3.kernels
     dtr, ar, trr, ang = views(dev, h, nr)
     (k, q), _, angs = K.bcnorm_forward([dev["kr"], dev["qr"]], [dev["wb"], dev["wc"]], 1e-5,
                                        theta=(ang, dtr, dev["bias"], chunk))
     out = K.siso_forward_raw(q, k, dev["v"], dtr, ar, trr, angs, dev["bias"], dev["qb"],
                              dev["kb"], d_skip=dev["d"], z=dev["z"],
-                             phi_init=dev.get("phi_init"), a_floor=a_floor, chunk=chunk)
+                             phi_init=dev.get("phi_init"), a_floor=a_floor, chunk=chunk,
+                             dtype_policy=policy)
     return q, k, angs, out
 
 
@@ -135,6 +137,36 @@ def test_raw_forward_matches_oracle(m3, chunk, n, nr, gate, phi_init):
     assert_maxabs(fk, sr.k, 1e-4, "final k")
     assert torch.equal(fv.cpu(), sr.v.float())
     assert O.rel_error(cpu(phi_f), sr.phi, angle=True, pct=100.0) <= 2e-5
+
+
+@pytest.mark.parametrize("policy,chunk,n,p,nr,phi_init", [
+    ("f32", 64, 16, 16, 4, False),     # BASELINE configs[0]'s layer shapes
+    ("f32", 32, 128, 64, 32, True),    # f32 at the headline's state and head widths
+    ("bf16", 32, 32, 16, 8, True),     # bf16 shapes the generic kernel runs
+    ("bf16", 128, 16, 16, 4, False),
+])
+def test_raw_forward_generic_kernel_matches_oracle(m3, policy, chunk, n, p, nr, phi_init):
+    """Raw mode in the generic kernel (the f32 policy and the small bf16 shapes): the f32
+    policy to its two float64 bars (p95 2e-5 and 1e-4 of max |ref| on y and the final state;
+    phi within 1e-5), the bf16 shapes to the bf16 bars."""
+    b, h, L = 2, 3, 256
+    mt = F32 if policy == "f32" else BF16
+    c, dev = raw_case(b, h, L, n, p, nr, seed=43 + n + p, phi_init=phi_init, mt=mt)
+    assert m3.kernels.raw_forward_ok(policy, chunk, n, p, nr, L, h)
+    q, k, angs, (y, fs, fk, fv, phi_f) = run_raw(m3, dev, h, nr, chunk, policy=policy)
+    yr, sr = oracle(c, q, k, chunk)
+    report(f"raw y ({policy}, C {chunk}, N {n}, P {p}) vs float64", y, yr)
+    if policy == "f32":
+        assert_f32(y, yr, "out", "y")
+        assert_f32(fs, sr.ssm, "out", "final ssm")
+        assert_f32(fk, sr.k, "out", "final k")
+        assert O.rel_error(cpu(phi_f), sr.phi, angle=True, pct=100.0) <= 1e-5
+    else:
+        assert_maxrel(y, yr, BF16_Y_MAXREL, "y")
+        assert_maxabs(fs, sr.ssm, STATE_MAXABS, "final ssm")
+        assert_maxabs(fk, sr.k, 1e-4, "final k")
+        assert O.rel_error(cpu(phi_f), sr.phi, angle=True, pct=100.0) <= 2e-5
+    assert torch.equal(fv.cpu(), sr.v.float())
 
 
 def test_raw_forward_equals_the_preprocess_path(m3):
