@@ -313,6 +313,24 @@ def main():
     dec_gbs = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
     line.update(decode_kernel_ms=round(dec_kernel_ms, 4), decode_kernel_gbs=round(dec_gbs, 1),
                 decode_kernel_hbm_frac=round(dec_gbs / HBM_PEAK_GBS, 4))
+    # a known-length run (kernel_decode.py:474-533): T steps in one m3s_decode_scan launch
+    for bs in (BD, 1):
+        with torch.no_grad():
+            qs = torch.randn(bs, T, N, device=dev).to(torch.bfloat16)
+            vs = torch.randn(bs, H, T, P, device=dev).to(torch.bfloat16)
+            ss = torch.full((bs, H, T), 0.01, device=dev)
+            ns, ls = -ss, ss * 50
+            angs = torch.randn(bs, T, Nr, device=dev)
+            cb, bb, dk = (params16.c_bias.float(), params16.b_bias.float(),
+                          params16.d_skip.float())
+            st_s = m3.SISOState(*(t[:bs].clone() for t in state))
+            sscan = lambda: K.decode_scan(qs, qs, vs, ns, ss, ls, angs, cb, bb, st_s,  # noqa: E731
+                                          dk, vs)
+            sscan()
+            scan_ms = gpu_time_ms(sscan, 5 if bs == BD else 20, torch)
+        line[f"decode_scan_ms_per_token_b{bs}"] = round(scan_ms / T, 5)
+        del qs, vs, ss, ns, ls, angs, st_s
+    line["decode_scan_tokens"] = T
     if args.leg == "decode":
         print(json.dumps({"leg": "decode", **line}))
         return

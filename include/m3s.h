@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define M3S_ABI_VERSION 9
+#define M3S_ABI_VERSION 10
 
 #define M3S_DTYPE_F32 0  /* f32 operands, v_mfma_f32_16x16x4_f32 ("f32" policy)  */
 #define M3S_DTYPE_BF16 1 /* bf16 operands, v_mfma_f32_16x16x32_bf16 ("bf16" policy) */
@@ -183,6 +183,34 @@ typedef struct m3s_decode_args {
   float* phi_state;       /* in/out (B, H, Nr)             */
   void* y;                /* out (B, H, P)                 */
 } m3s_decode_args;
+
+/* T decode steps in one launch. Replaces `kernel_decode.decode_scan` (kernel_decode.py:
+ * 474-533: one lax.scan of decode_step over a known-length run, e.g. a fixed prompt suffix
+ * or teacher forcing). Each (b, h) state stays on chip for all T steps and is read and
+ * written once; every step's arithmetic is m3s_decode's, so the results equal T calls of
+ * m3s_decode. Inputs carry a time axis; the state is updated in place. */
+typedef struct m3s_decode_scan_args {
+  int32_t struct_size; /* sizeof(m3s_decode_scan_args) */
+  int32_t batch, steps, nheads, headdim, state_dim, n_angles;
+  int32_t dtype;       /* dtype of q, k, v, z, y and of the readout operands */
+  int32_t has_d, has_z;
+  const void* q;          /* (B, T, N)                     */
+  const void* k;          /* (B, T, N)                     */
+  const void* v;          /* (B, H, T, P)                  */
+  const void* z;          /* (B, H, T, P), if has_z        */
+  const float* adt;       /* (B, H, T)                     */
+  const float* dt;        /* (B, H, T)                     */
+  const float* lam;       /* (B, H, T)                     */
+  const float* angles;    /* (B, T, Nr) raw, pre-tanh      */
+  const float* q_bias;    /* (H, N)                        */
+  const float* k_bias;    /* (H, N)                        */
+  const float* d_skip;    /* (H), if has_d                 */
+  float* ssm;             /* in/out (B, H, P, N)           */
+  float* k_state;         /* in/out (B, H, N)              */
+  float* v_state;         /* in/out (B, H, P)              */
+  float* phi_state;       /* in/out (B, H, Nr)             */
+  void* y;                /* out (B, H, T, P)              */
+} m3s_decode_scan_args;
 
 /* The layer's per-token decode step (model.py:266-289 without the block norm, residual
  * and MLP; the layer step that BASELINE configs[3] times) from the in_proj output rows:
@@ -488,6 +516,7 @@ int64_t m3s_rms_bwd_workspace_bytes(int32_t width);
 int32_t m3s_fwd(const m3s_fwd_args* args, void* stream);
 int32_t m3s_bwd(const m3s_bwd_args* args, void* stream);
 int32_t m3s_decode(const m3s_decode_args* args, void* stream);
+int32_t m3s_decode_scan(const m3s_decode_scan_args* args, void* stream);
 int32_t m3s_decode_layer(const m3s_decode_layer_args* args, void* stream);
 int32_t m3s_prep_fwd(const m3s_prep_fwd_args* args, void* stream);
 int32_t m3s_prep_bwd(const m3s_prep_bwd_args* args, void* stream);

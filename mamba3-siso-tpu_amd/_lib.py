@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "csrc", "libm3s.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -74,6 +74,21 @@ class DecodeArgs(C.Structure):
     _fields_ = [
         ("struct_size", i32),
         ("batch", i32), ("nheads", i32), ("headdim", i32), ("state_dim", i32),
+        ("n_angles", i32),
+        ("dtype", i32),
+        ("has_d", i32), ("has_z", i32),
+        ("q", vp), ("k", vp), ("v", vp), ("z", vp),
+        ("adt", vp), ("dt", vp), ("lam", vp), ("angles", vp),
+        ("q_bias", vp), ("k_bias", vp), ("d_skip", vp),
+        ("ssm", vp), ("k_state", vp), ("v_state", vp), ("phi_state", vp),
+        ("y", vp),
+    ]
+
+
+class DecodeScanArgs(C.Structure):
+    _fields_ = [
+        ("struct_size", i32),
+        ("batch", i32), ("steps", i32), ("nheads", i32), ("headdim", i32), ("state_dim", i32),
         ("n_angles", i32),
         ("dtype", i32),
         ("has_d", i32), ("has_z", i32),
@@ -203,7 +218,7 @@ class GemvArgs(C.Structure):
 #: Every symbol ``include/m3s.h`` declares.
 EXPORTS = ("m3s_abi_version", "m3s_last_error", "m3s_supported", "m3s_fwd_raw_supported",
            "m3s_bwd_workspace_bytes",
-           "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode",
+           "m3s_prep_fwd_workspace_bytes", "m3s_prep_bwd_workspace_bytes", "m3s_fwd", "m3s_bwd", "m3s_decode", "m3s_decode_scan",
            "m3s_prep_fwd", "m3s_prep_bwd", "m3s_norm_bwd_workspace_bytes", "m3s_norm_fwd",
            "m3s_norm_bwd", "m3s_decode_layer", "m3s_transpose", "m3s_swiglu_fwd",
            "m3s_swiglu_bwd", "m3s_rms_fwd", "m3s_rms_bwd", "m3s_rms_bwd_workspace_bytes",
@@ -238,6 +253,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     lib.m3s_bwd.argtypes = [C.POINTER(BwdArgs), vp]
     lib.m3s_decode.restype = i32
     lib.m3s_decode.argtypes = [C.POINTER(DecodeArgs), vp]
+    lib.m3s_decode_scan.restype = i32
+    lib.m3s_decode_scan.argtypes = [C.POINTER(DecodeScanArgs), vp]
     lib.m3s_prep_fwd_workspace_bytes.restype = i64
     lib.m3s_prep_fwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.m3s_prep_bwd_workspace_bytes.restype = i64

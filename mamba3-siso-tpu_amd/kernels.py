@@ -583,11 +583,75 @@ def decode_loop(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip=Non
 def decode_scan(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip=None, z=None,
                 dtype_policy: LY.DtypePolicy | str = LY.BF16, interpret: Any = False,
                 folded: bool = True):
-    """``kernel_decode.py:474-533``: a known-length run of decode steps. The reference
-    uses one ``lax.scan``; here the steps are stream-ordered kernel launches with no
-    host synchronisation between them, which is the same device-only floor."""
-    return decode_loop(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip, z,
-                       dtype_policy=dtype_policy)
+    """``kernel_decode.py:474-533``: a known-length run of ``L`` decode steps (the
+    reference's ``lax.scan`` of ``decode_step``) as ONE ``m3s_decode_scan`` launch: each
+    (b, h) state is read once, stepped ``L`` times on chip and written once. Inputs as
+    `decode_loop` (q, k ``(B, L, N)``; v, z ``(B, H, L, P)``; adt/dt/lam ``(B, H, L)``;
+    angles ``(B, L, Nr)``); every step is `siso_decode`'s arithmetic, so the results are
+    `decode_loop`'s. Returns ``(y (B, H, L, P), state)``; the state is updated in place."""
+    from .scan_prep import SISOState
+
+    pol = LY.policy(dtype_policy)
+    batch, steps, state_dim = q.shape
+    nheads, headdim = v.shape[1], v.shape[3]
+    n_angles = angles.shape[-1]
+    if tuple(k.shape) != (batch, steps, state_dim):
+        raise ValueError(f"k shape {tuple(k.shape)} must match q {tuple(q.shape)}")
+    if tuple(v.shape[:3]) != (batch, nheads, steps):
+        raise ValueError(f"v must be (B, H, L, P) with B={batch}, L={steps}, got {tuple(v.shape)}")
+    for name, t in (("adt", adt), ("dt", dt), ("lam", lam)):
+        if tuple(t.shape) != (batch, nheads, steps):
+            raise ValueError(f"{name} must be (B, H, L) = {(batch, nheads, steps)}, "
+                             f"got {tuple(t.shape)}")
+    if tuple(angles.shape[:2]) != (batch, steps):
+        raise ValueError(f"angles must be (B, L, Nr), got {tuple(angles.shape)}")
+    if z is not None and tuple(z.shape) != tuple(v.shape):
+        raise ValueError("z must match v")
+    dev = _device_of(q, k, v, adt, dt, lam, angles, q_bias, k_bias, d_skip, z, *state)
+    mt = pol.matmul
+    width = LY.decode_headdim(pol.name, state_dim, headdim)
+    if width is None:
+        raise ValueError(f"no decode kernel for policy={pol.name} d_state={state_dim} headdim={headdim}")
+    ssm = _state_buf(state.ssm, (batch, nheads, headdim, state_dim), dev)
+    kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
+    vst = _state_buf(state.v, (batch, nheads, headdim), dev)
+    phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
+    r = headdim // width
+    if r > 1:   # sub-heads of `width` columns, as siso_decode
+        ssm_k, vst_k = ssm.view(batch, nheads * r, width, state_dim), vst.view(batch, nheads * r, width)
+        kst_k, phist_k = _rep(kst, r), _rep(phist, r)
+        v, z = _split_cols(v, r), _split_cols(z, r)
+        adt, dt, lam = _rep(adt, r), _rep(dt, r), _rep(lam, r)
+        q_bias, k_bias, d_skip = _rep(q_bias, r, 0), _rep(k_bias, r, 0), _rep(d_skip, r, 0)
+    else:
+        ssm_k, vst_k, kst_k, phist_k = ssm, vst, kst, phist
+    qc, kc, vc, zc = _mt(q, mt), _mt(k, mt), _mt(v, mt), _mt(z, mt)
+    adt_c, dt_c, lam_c, ang_c = _f32c(adt), _f32c(dt), _f32c(lam), _f32c(angles)
+    qb_c, kb_c, d_c = _f32c(q_bias), _f32c(k_bias), _f32c(d_skip)
+    y = empty(batch, nheads * r, steps, width, device=dev, dtype=mt)
+
+    a = _lib.DecodeScanArgs()
+    a.struct_size = ctypes.sizeof(_lib.DecodeScanArgs)
+    a.batch, a.steps, a.nheads, a.headdim = batch, steps, nheads * r, width
+    a.state_dim, a.n_angles = state_dim, n_angles
+    a.dtype = _lib.dtype_code(mt)
+    a.has_d, a.has_z = int(d_c is not None), int(zc is not None)
+    a.q, a.k, a.v, a.z = qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), _lib.ptr(zc)
+    a.adt, a.dt, a.lam, a.angles = adt_c.data_ptr(), dt_c.data_ptr(), lam_c.data_ptr(), ang_c.data_ptr()
+    a.q_bias, a.k_bias, a.d_skip = qb_c.data_ptr(), kb_c.data_ptr(), _lib.ptr(d_c)
+    a.ssm, a.k_state, a.v_state, a.phi_state = (t.data_ptr() for t in (ssm_k, kst_k, vst_k, phist_k))
+    a.y = y.data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().m3s_decode_scan(ctypes.byref(a), _lib.stream_handle(dev)),
+                   "m3s_decode_scan")
+    if r > 1:
+        kst.copy_(kst_k[:, ::r])
+        phist.copy_(phist_k[:, ::r])
+        y = _merge_cols(y, r)
+    y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
+    if y.dtype != y_dtype:
+        y = y.to(y_dtype)
+    return y, SISOState(ssm=ssm, k=kst, v=vst, phi=phist)
 
 
 # ======================================================================================

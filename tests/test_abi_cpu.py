@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol(lib):
     assert set(names) == set(lib.EXPORTS)
     for name in names:
         assert hasattr(handle, name), f"{name} declared in m3s.h but not exported"
-    assert handle.m3s_abi_version() == lib.ABI_VERSION == 9
+    assert handle.m3s_abi_version() == lib.ABI_VERSION == 10
 
 
 def test_struct_layouts_match_the_header(lib):
@@ -69,6 +69,8 @@ int main(void) {
          offsetof(m3s_gemv_args, ldy));
   printf("%zu %zu %zu %zu\n", offsetof(m3s_fwd_args, raw), offsetof(m3s_fwd_args, phi_final),
          offsetof(m3s_norm_fwd_args, angles), offsetof(m3s_norm_fwd_args, theta_chunk_totals));
+  printf("%zu %zu %zu\n", sizeof(m3s_decode_scan_args), offsetof(m3s_decode_scan_args, q),
+         offsetof(m3s_decode_scan_args, y));
   return 0;
 }
 """
@@ -102,8 +104,10 @@ int main(void) {
                             lib.AdamwArgs.bias_correction2_sqrt.offset]
     assert sizes[34:37] == [ctypes.sizeof(lib.WgradArgs), lib.WgradArgs.ldb.offset,
                             lib.WgradArgs.workspace.offset]
-    assert sizes[40:] == [lib.FwdArgs.raw.offset, lib.FwdArgs.phi_final.offset,
-                          lib.NormFwdArgs.angles.offset, lib.NormFwdArgs.theta_chunk_totals.offset]
+    assert sizes[40:44] == [lib.FwdArgs.raw.offset, lib.FwdArgs.phi_final.offset,
+                            lib.NormFwdArgs.angles.offset, lib.NormFwdArgs.theta_chunk_totals.offset]
+    assert sizes[44:] == [ctypes.sizeof(lib.DecodeScanArgs), lib.DecodeScanArgs.q.offset,
+                          lib.DecodeScanArgs.y.offset]
     assert sizes[37:40] == [ctypes.sizeof(lib.GemvArgs), lib.GemvArgs.ldw.offset,
                           lib.GemvArgs.ldy.offset]
 
@@ -122,6 +126,12 @@ def test_null_and_stale_args_are_rejected_without_a_launch(lib):
     d = lib.DecodeArgs()
     d.struct_size = ctypes.sizeof(lib.DecodeArgs)
     assert h.m3s_decode(ctypes.byref(d), None) == lib.ERR_INVALID
+    e = lib.DecodeScanArgs()
+    e.struct_size = ctypes.sizeof(lib.DecodeScanArgs)
+    assert h.m3s_decode_scan(ctypes.byref(e), None) == lib.ERR_INVALID   # zero dims
+    e.struct_size = 3
+    assert h.m3s_decode_scan(ctypes.byref(e), None) == lib.ERR_INVALID
+    assert b"ABI mismatch" in h.m3s_last_error()
 
 
 def test_unsupported_shapes_and_bad_dims_are_reported(lib):

@@ -126,3 +126,138 @@ def test_decode_reproduces_reference_torch_golden(m3):
     assert O.max_rel(cpu(torch.stack(ys, 1)), want) <= 2e-5
     assert O.max_rel(cpu(st.ssm), torch.from_numpy(fx["ssm_state"]).double()[..., perm.cpu()]) <= 2e-5
     assert O.rel_error(cpu(st.phi), torch.from_numpy(fx["angle_state"]).double(), angle=True) <= 1e-5
+
+
+# ---- decode_scan: T steps in one launch --------------------------------------------------
+
+def chain_inputs(b, h, T, n, p, nr, policy, seed):
+    """A T-step run (time axis on every input) and a random carried state."""
+    x = O.make_inputs(b, h, T, n, p, nr, seed=seed)
+    pre, _ = O.preprocess(x["dt_raw"], x["a_raw"], x["trap_raw"], x["angles"], x["dt_bias"])
+    mt = BF16 if policy == "bf16" else F32
+    g = torch.Generator().manual_seed(seed + 7)
+    st = O.SISOState(torch.randn(b, h, p, n, generator=g, dtype=torch.float64).float().double() * 0.1,
+                     torch.randn(b, h, n, generator=g, dtype=torch.float64).float().double(),
+                     torch.randn(b, h, p, generator=g, dtype=torch.float64).float().double(),
+                     (torch.rand(b, h, nr, generator=g, dtype=torch.float64) * 6).float().double())
+    c = dict(q=x["q"].to(mt).double(), k=x["k"].to(mt).double(), v=x["v"].to(mt).double(),
+             z=x["z"].to(mt).double(), adt=pre.adt.float().double(), dt=pre.dt.float().double(),
+             lam=pre.lam.float().double(), angles=x["angles"].float().double(),
+             q_bias=x["q_bias"].float().double(), k_bias=x["k_bias"].float().double(),
+             d_skip=x["d_skip"].float().double())
+    d = {k_: v_.to(mt if k_ in ("q", "k", "v", "z") else F32).cuda() for k_, v_ in c.items()}
+    return c, d, st
+
+
+def dev_state(st):
+    return O.SISOState(*(t.float().cuda() for t in st))
+
+
+def assert_same_run(a, b, what):
+    (ya, sa), (yb, sb) = a, b
+    assert torch.equal(ya, yb), f"{what}: y differs (max |d| {float((ya.float() - yb.float()).abs().max()):.3e})"
+    for name, ta, tb in zip(("ssm", "k", "v", "phi"), sa, sb):
+        assert torch.equal(ta, tb), f"{what}: {name} differs"
+
+
+@pytest.mark.parametrize("policy,b,h,T,n,p,nr,gated", [
+    ("bf16", 2, 3, 37, 128, 64, 32, True),
+    ("bf16", 1, 2, 1, 128, 64, 32, True),
+    ("bf16", 2, 2, 2, 128, 64, 32, False),
+    ("bf16", 3, 2, 29, 64, 64, 16, True),
+    ("bf16", 2, 3, 19, 16, 16, 4, False),
+    ("bf16", 1, 2, 23, 256, 64, 64, True),
+    ("bf16", 2, 2, 17, 128, 128, 32, True),    # headdim 128: two 64-wide sub-heads
+    ("f32", 2, 3, 37, 128, 64, 32, True),
+    ("f32", 2, 2, 21, 32, 16, 8, True),
+    ("f32", 1, 3, 13, 128, 64, 0, False),      # no rotary angles
+])
+def test_decode_scan_is_decode_loop_bit_for_bit(m3, policy, b, h, T, n, p, nr, gated):
+    """One launch for T steps gives exactly the T-launch chain's y and state."""
+    _, d, st = chain_inputs(b, h, T, n, p, nr, policy, seed=11 + T)
+    z = d["z"] if gated else None
+    dsk = d["d_skip"] if gated else None
+    args = (d["q"], d["k"], d["v"], d["adt"], d["dt"], d["lam"], d["angles"], d["q_bias"], d["k_bias"])
+    s_loop, s_scan = dev_state(st), dev_state(st)
+    ptrs = [t.data_ptr() for t in s_scan]
+    ref = m3.decode_loop(*args, s_loop, dsk, z, dtype_policy=policy)
+    got = m3.decode_scan(*args, s_scan, dsk, z, dtype_policy=policy)
+    assert [t.data_ptr() for t in got[1]] == ptrs     # updated in place
+    print(f"[decode_scan] {policy} b={b} h={h} T={T} n={n} p={p} nr={nr}", flush=True)
+    assert_same_run(got, ref, f"{policy} T={T}")
+
+
+@pytest.mark.parametrize("policy", ["f32", "bf16"])
+def test_decode_scan_matches_chained_oracle_steps(m3, policy):
+    """decode_scan vs T chained O.siso_step (float64; bf16 readout model for bf16)."""
+    b, h, T, n, p, nr = 2, 4, 48, 128, 64, 32
+    c, d, st = chain_inputs(b, h, T, n, p, nr, policy, seed=21)
+    mm = BF16 if policy == "bf16" else None
+    s, ys = st, []
+    for t in range(T):
+        y, s = O.siso_step(c["q"][:, t], c["k"][:, t], c["v"][:, :, t], c["adt"][:, :, t],
+                           c["dt"][:, :, t], c["lam"][:, :, t], c["angles"][:, t], c["q_bias"],
+                           c["k_bias"], s, c["d_skip"], c["z"][:, :, t], mm_dtype=mm)
+        ys.append(y)
+    yr = torch.stack(ys, dim=2)
+    y, s2 = m3.decode_scan(d["q"], d["k"], d["v"], d["adt"], d["dt"], d["lam"], d["angles"],
+                           d["q_bias"], d["k_bias"], dev_state(st), d["d_skip"], d["z"],
+                           dtype_policy=policy)
+    if policy == "f32":
+        assert_f32(y, yr, "out", "y")
+        assert_f32(s2.ssm, s.ssm, "out", "ssm")
+        assert_f32(s2.k, s.k, "out", "k")
+    else:
+        assert y.dtype == BF16
+        assert_p95(y, yr, BF16_OUT_MODEL_P95, "y vs bf16 readout model")
+        assert_maxrel(y, yr, 2e-2, "y vs bf16 readout model (max-normalised)")
+        assert_f32(s2.ssm, s.ssm, "out", "ssm (f32 update)")
+    assert O.max_rel(cpu(s2.v), s.v) == 0.0
+    assert O.rel_error(cpu(s2.phi), s.phi, angle=True) <= 1e-4
+
+
+def test_decode_scan_golden_chain(m3):
+    """The golden sequence (upstream's step reference, torch_ref.mamba3_siso_ref) as one
+    decode_scan from a zero state: bit-identical to the step-by-step chain and within the
+    f32 bar of the fixture."""
+    import numpy as np
+    from pathlib import Path
+    fx = dict(np.load(Path(__file__).resolve().parent / "golden" / "torch_ref_kernel_gated.npz",
+                      allow_pickle=False))
+    t = {k_: torch.from_numpy(v_).float().cuda() for k_, v_ in fx.items() if v_.dtype != bool and v_.ndim > 0}
+    b, L, n = t["q"].shape
+    h, p, nr = t["v"].shape[2], t["v"].shape[3], t["angles"].shape[-1]
+    perm = O.deinterleave_perm(n).cuda()
+    lam = torch.sigmoid(t["trap"])
+    args = (t["q"][..., perm], t["k"][..., perm], t["v"].transpose(1, 2), t["adt"], t["dt"], lam,
+            t["angles"], t["q_bias"][:, perm], t["k_bias"][:, perm])
+    loop = m3.decode_loop(*args, m3.zero_state(b, h, p, n, nr, device="cuda"), t["d"],
+                          t["z"].transpose(1, 2), dtype_policy="f32")
+    scan = m3.decode_scan(*args, m3.zero_state(b, h, p, n, nr, device="cuda"), t["d"],
+                          t["z"].transpose(1, 2), dtype_policy="f32")
+    assert_same_run(scan, loop, "golden chain")
+    y, st = scan
+    want = torch.from_numpy(fx["out"]).double()
+    assert O.max_rel(cpu(y.transpose(1, 2)), want) <= 2e-5
+    assert O.max_rel(cpu(st.ssm), torch.from_numpy(fx["ssm_state"]).double()[..., perm.cpu()]) <= 2e-5
+    assert O.rel_error(cpu(st.phi), torch.from_numpy(fx["angle_state"]).double(), angle=True) <= 1e-5
+
+
+def test_decode_scan_cfg4_size(m3):
+    """cfg4 sizes (B=256, H=32, P=64, N=128, Nr=32), 12 steps in one launch: the chain of
+    12 single-step launches, bit for bit."""
+    _, d, st = chain_inputs(256, 32, 12, 128, 64, 32, "bf16", seed=31)
+    args = (d["q"], d["k"], d["v"], d["adt"], d["dt"], d["lam"], d["angles"], d["q_bias"], d["k_bias"])
+    ref = m3.decode_loop(*args, dev_state(st), d["d_skip"], d["z"])
+    got = m3.decode_scan(*args, dev_state(st), d["d_skip"], d["z"])
+    assert_same_run(got, ref, "cfg4")
+
+
+def test_decode_scan_rejects_mismatched_shapes(m3):
+    _, d, st = chain_inputs(1, 2, 4, 128, 64, 32, "bf16", seed=41)
+    with pytest.raises(ValueError):
+        m3.decode_scan(d["q"], d["k"], d["v"][:, :, :3], d["adt"], d["dt"], d["lam"], d["angles"],
+                       d["q_bias"], d["k_bias"], dev_state(st))
+    with pytest.raises(ValueError):
+        m3.decode_scan(d["q"], d["k"], d["v"], d["adt"][:, :, :3], d["dt"], d["lam"], d["angles"],
+                       d["q_bias"], d["k_bias"], dev_state(st))
