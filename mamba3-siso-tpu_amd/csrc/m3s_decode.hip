@@ -85,19 +85,30 @@ __device__ __forceinline__ float state_step(float s, float alpha, float bvp, flo
 // One thread's share of a readout row: S'[p, n0 : n0 + 4] . q~[n0 : n0 + 4]. The bf16
 // policy rounds S' to bf16 (kernel_decode.py:216-222; q~ already is) and takes the two
 // two-term products on the bf16 dot instruction (exact bf16 products, f32 sums); f32
-// multiplies and adds in order.
+// multiplies and adds in order. q~ comes packed as the operand type (QPack).
+template <typename MT> struct QPack { f32x4 v; };
+template <> struct QPack<bf16> { bf16x2 lo, hi; };
+
 template <typename MT>
-__device__ __forceinline__ float readout4(const f32x4& s, const f32x4& q) {
+__device__ __forceinline__ QPack<MT> pack_q(const f32x4& q) {
   if constexpr (std::is_same<MT, float>::value) {
-    float acc = s[0] * q[0];
+    return QPack<MT>{q};
+  } else {
+    return QPack<MT>{bf16x2{(bf16)q[0], (bf16)q[1]}, bf16x2{(bf16)q[2], (bf16)q[3]}};
+  }
+}
+
+template <typename MT>
+__device__ __forceinline__ float readout4(const f32x4& s, const QPack<MT>& q) {
+  if constexpr (std::is_same<MT, float>::value) {
+    float acc = s[0] * q.v[0];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) acc = fmaf(s[i], q[i], acc);
+    for (int i = 1; i < 4; ++i) acc = fmaf(s[i], q.v[i], acc);
     return acc;
   } else {
     const bf16x2 s01 = {(bf16)s[0], (bf16)s[1]}, s23 = {(bf16)s[2], (bf16)s[3]};
-    const bf16x2 q01 = {(bf16)q[0], (bf16)q[1]}, q23 = {(bf16)q[2], (bf16)q[3]};
     return __builtin_amdgcn_fdot2_f32_bf16(
-        s23, q23, __builtin_amdgcn_fdot2_f32_bf16(s01, q01, 0.f, false), false);
+        s23, q.hi, __builtin_amdgcn_fdot2_f32_bf16(s01, q.lo, 0.f, false), false);
   }
 }
 
@@ -278,7 +289,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
   const int n0 = (tid % RV) * 4;       // fixed across iterations since NT % RV == 0
   const f32x4 kp = *reinterpret_cast<const f32x4*>(sKp + n0);
   const f32x4 kt = *reinterpret_cast<const f32x4*>(sKt + n0);
-  const f32x4 qt = *reinterpret_cast<const f32x4*>(sQt + n0);
+  const QPack<MT> qt = pack_q<MT>(*reinterpret_cast<const f32x4*>(sQt + n0));
   MT* yg = static_cast<MT*>(p.y) + bh * P;
   const MT* zg = LAYER ? prow + h * P : (p.has_z ? static_cast<const MT*>(p.z) + bh * P : nullptr);
   const float dsk = p.has_d ? p.dsk[h] : 0.f;
@@ -349,10 +360,14 @@ struct DecScanParams {
   void* y;              // (B, H, T, P)
 };
 
-// (the waves-per-EU hint only steers register allocation: without it the N = 128 kernels
-// take 189 VGPRs, two workgroups per CU; with it 129, and LDS then allows three)
+// (The waves-per-EU hint only steers register allocation. Without it the N = 128 kernels
+// take 189 VGPRs: two workgroups per CU. A hint of five waves makes the allocator stop at
+// 127 without spilling (a hint of four spills), and LDS then allows four workgroups; the
+// compiler warns that five is not met. N = 256 holds 64 state floats per thread and is
+// left at two waves per SIMD.)
 template <typename MT, int N, int P>
-__global__ void __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(5, 8)))
+__global__ void __launch_bounds__(kDecThreads)
+__attribute__((amdgpu_waves_per_eu(N >= 256 ? 2 : 5, 8)))
 decode_scan_kernel(const DecScanParams p) {
   constexpr int NT = kDecThreads;
   constexpr int H2 = N / 2;
@@ -370,8 +385,8 @@ decode_scan_kernel(const DecScanParams p) {
 
   __shared__ __align__(16) float sK[W2][N];   // k~ by step (slot t mod 2W)
   __shared__ __align__(16) float sV[W2][P];   // v by step (slot t mod 2W)
-  __shared__ __align__(16) float sQ[W][N];    // q~ rounded to MT, by window step
-  __shared__ __align__(16) float sZ[W][P];
+  __shared__ __align__(16) MT sQ[W][N];       // q~, by window step
+  __shared__ __align__(16) float sZ[W][P];    // silu(z)
   __shared__ __align__(16) float sC[W][4];    // alpha, beta, gamma, dt
   __shared__ float sPh[W][H2];                // angle increments, then phi
   __shared__ __align__(16) MT sY[W][P];       // gated y of the window
@@ -416,7 +431,7 @@ decode_scan_kernel(const DecScanParams p) {
     for (int i = tid; i < wn * P; i += NT) {
       const int w = i / P, pp = i % P;
       sV[(t0 + w) & (W2 - 1)][pp] = (float)vg[(int64_t)(t0 + w) * P + pp];
-      if (zg) sZ[w][pp] = (float)zg[(int64_t)(t0 + w) * P + pp];
+      if (zg) sZ[w][pp] = silu((float)zg[(int64_t)(t0 + w) * P + pp]);
     }
     if (tid < wn) {
       const float adt = adtg[t0 + tid], dt = dtg[t0 + tid], lam = lamg[t0 + tid];
@@ -448,8 +463,8 @@ decode_scan_kernel(const DecScanParams p) {
       const float whi = (float)kg[t * N + H2 + jr] + kbh;
       float sn = 0.f, cs = 1.f;
       if (jr < Nr) sincosf(sPh[w][jr], &sn, &cs);
-      sQ[w][jr] = (float)(MT)rot_lo(ulo, uhi, cs, sn);
-      sQ[w][H2 + jr] = (float)(MT)rot_hi(ulo, uhi, cs, sn);
+      sQ[w][jr] = (MT)rot_lo(ulo, uhi, cs, sn);
+      sQ[w][H2 + jr] = (MT)rot_hi(ulo, uhi, cs, sn);
       sK[t & (W2 - 1)][jr] = rot_lo(wlo, whi, cs, sn);
       sK[t & (W2 - 1)][H2 + jr] = rot_hi(wlo, whi, cs, sn);
     }
@@ -461,7 +476,7 @@ decode_scan_kernel(const DecScanParams p) {
       const f32x4 cf = *reinterpret_cast<const f32x4*>(&sC[w][0]);
       const f32x4 kp = *reinterpret_cast<const f32x4*>(&sK[sp][n0]);
       const f32x4 kt = *reinterpret_cast<const f32x4*>(&sK[sc][n0]);
-      const f32x4 qt = *reinterpret_cast<const f32x4*>(&sQ[w][n0]);
+      const QPack<MT> qt = *reinterpret_cast<const QPack<MT>*>(&sQ[w][n0]);
       // v of the group's rows at steps t - 1 and t (IT consecutive floats)
       float vp[IT], vc[IT];
       if constexpr (IT % 4 == 0) {
@@ -496,7 +511,7 @@ decode_scan_kernel(const DecScanParams p) {
       const int prow = g * IT + (lane >> LO);
       if ((lane & ((1 << LO) - 1)) == 0 && prow < P) {
         float yv = fmaf(dsk, sV[sc][prow], part[0]);
-        if (zg) yv *= silu(sZ[w][prow]);
+        if (zg) yv *= sZ[w][prow];
         sY[w][prow] = (MT)yv;
       }
     }
