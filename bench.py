@@ -203,7 +203,7 @@ def main():
     scan_compact_bytes = scan_fixed + phi_compact
     scan_read_bytes = scan_fixed + phi_read
     scan_bytes = (2 * B * L * N * 2 + 3 * B * H * L * P * 2 + 3 * B * L * H * 2
-                  + B * L * Nr * 4 + B * H * (L // 16) * Nr * 4
+                  + B * L * Nr * 4 + B * H * (L // 16) * Nr * 4 + B * H * (L // cfg.chunk) * Nr * 4
                   + B * H * P * N * 4 + B * H * (N + P + Nr) * 4)
     scan_flops = B * H * L * 2 * (2 * N * P + cfg.chunk * N + cfg.chunk * P)
     if args.leg in ("all", "scan", "bwd"):
@@ -245,6 +245,8 @@ def main():
                 "traffic": traffic_figure("fwd_bf16_kernel_raw"),
                 "traffic_source": TRAFFIC_SOURCE, "algorithmic_bytes": scan_bytes,
                 "mfma_frac": round(scan_tflops / BF16_PEAK_TFLOPS, 5),
+                "mfma_busy": counter_figure("fwd_bf16_kernel_raw", "mfma_busy_frac"),
+                "mfma_busy_source": COUNTER_SOURCE,
                 # the same scan fed by the preprocess launches, phi compact or materialised
                 "phi_compact_frac": round(scan_compact_bytes / (comp_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 "phi_read_frac": round(scan_read_bytes / (read_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -281,7 +283,12 @@ def main():
                 "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
                 "algorithmic_bytes": bwd_bytes,
-                "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 5)}
+                "traffic": _sum_or_none(traffic_figure("bwd_bf16_kernel"),
+                                        traffic_figure("headsum_kernel")),
+                "traffic_source": TRAFFIC_SOURCE.replace("--leg scan", "--leg bwd"),
+                "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 5),
+                "mfma_busy": counter_figure("bwd_bf16_kernel", "mfma_busy_frac"),
+                "mfma_busy_source": COUNTER_SOURCE.replace("--leg scan", "--leg bwd")}
             del y, res, dyk, kr
         del ka, kc, kraw, phi_full
         torch.cuda.empty_cache()
@@ -312,24 +319,28 @@ def main():
                  + BD * N * 2 * 2 + 3 * BD * H * P * 2 + 3 * BD * H * 4 + BD * Nr * 4)
     dec_gbs = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
     line.update(decode_kernel_ms=round(dec_kernel_ms, 4), decode_kernel_gbs=round(dec_gbs, 1),
-                decode_kernel_hbm_frac=round(dec_gbs / HBM_PEAK_GBS, 4))
+                decode_kernel_hbm_frac=round(dec_gbs / HBM_PEAK_GBS, 4),
+                decode_kernel_bytes=dec_bytes,
+                decode_kernel_traffic=traffic_figure("decode_kernel"))
     # a known-length run (kernel_decode.py:474-533): T steps in one m3s_decode_scan launch
     for bs in (BD, 1):
         with torch.no_grad():
             qs = torch.randn(bs, T, N, device=dev).to(torch.bfloat16)
+            ks = torch.randn(bs, T, N, device=dev).to(torch.bfloat16)
             vs = torch.randn(bs, H, T, P, device=dev).to(torch.bfloat16)
+            zs = torch.randn(bs, H, T, P, device=dev).to(torch.bfloat16)
             ss = torch.full((bs, H, T), 0.01, device=dev)
             ns, ls = -ss, ss * 50
             angs = torch.randn(bs, T, Nr, device=dev)
             cb, bb, dk = (params16.c_bias.float(), params16.b_bias.float(),
                           params16.d_skip.float())
             st_s = m3.SISOState(*(t[:bs].clone() for t in state))
-            sscan = lambda: K.decode_scan(qs, qs, vs, ns, ss, ls, angs, cb, bb, st_s,  # noqa: E731
-                                          dk, vs)
+            sscan = lambda: K.decode_scan(qs, ks, vs, ns, ss, ls, angs, cb, bb, st_s,  # noqa: E731
+                                          dk, zs)
             sscan()
             scan_ms = gpu_time_ms(sscan, 5 if bs == BD else 20, torch)
         line[f"decode_scan_ms_per_token_b{bs}"] = round(scan_ms / T, 5)
-        del qs, vs, ss, ns, ls, angs, st_s
+        del qs, ks, vs, zs, ss, ns, ls, angs, st_s
     line["decode_scan_tokens"] = T
     if args.leg == "decode":
         print(json.dumps({"leg": "decode", **line}))
@@ -344,6 +355,15 @@ def main():
             _, state = m3.mamba3_siso_decode_step(params16, toks[t], cfg, state)
         torch.cuda.synchronize()
         dec_ms = (time.perf_counter() - t0) * 1e3 / T
+    # the configs[3] layer step's necessary bytes: the token rows in and out, both
+    # projection weights, the in_proj row written and read, the state read and written,
+    # the gated y written and read
+    d_in = cfg.d_in_proj
+    dec_layer_bytes = (BD * DM * 2 * 2 + (DM * d_in + cfg.d_inner * DM) * 2 + BD * d_in * 2 * 2
+                       + 2 * BD * H * P * N * 4 + 2 * BD * H * (N + P + Nr) * 4
+                       + BD * cfg.d_inner * 2 * 2)
+    line.update(decode_layer_bytes=dec_layer_bytes,
+                decode_layer_gbs=round(dec_layer_bytes / (dec_ms * 1e-3) / 1e9, 1))
     # The legs from here to the headline run back to back, without emptying the allocator
     # cache in between: the GPU lowers its clocks within a millisecond or two of idling
     # (measured: a 20 ms pause before 5 warmup steps costs the next 20 forwards 7%, an
@@ -495,6 +515,27 @@ def _zipf_entropy(s):
 TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of "
                   "`bench.py --leg scan`, each scaled by its ratio on `bench.py --leg copy`; "
                   "measured in its own runs, not in this one")
+
+
+COUNTER_SOURCE = ("profiles/sq_counters.json: rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES "
+                  "GRBM_GUI_ACTIVE (with six other SQ counters) of `bench.py --leg scan`: MFMA "
+                  "busy cycles over 1024 SIMDs x GPU-active cycles per XCD; measured in its own "
+                  "runs, not in this one")
+
+
+def _sum_or_none(*xs):
+    return None if any(x is None for x in xs) else sum(xs)
+
+
+def counter_figure(kernel, field):
+    """One figure of ``kernel`` from the committed SQ counter summary
+    (profiles/sq_counters.json), or None if absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "sq_counters.json")) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return rec.get("kernels", {}).get(kernel, {}).get(field)
 
 
 def traffic_figure(kernel):
