@@ -103,48 +103,57 @@ __device__ __forceinline__ float group_sum_dyn(float v, int G) {
 // stream while they are in flight. LDS: chunk (Nr + H) + (chunk / 16) H Nr floats.
 constexpr int kThetaThreads = 512;
 // The chunk's B and C rows, kRowBatch rows per group of G lanes at a time: every row's
-// load is issued before the first row's statistic (one memory latency per batch).
+// load of a batch is issued before the first row's statistic (one memory latency per
+// batch). `norm_issue` loads batch `base`, `norm_finish` normalises and stores it.
 constexpr int kRowBatch = 8;
 template <typename T>
-__device__ __forceinline__ void norm_rows_of_chunk(const NormFwdParams& p, int b, int t0) {
+__device__ __forceinline__ void norm_issue(const NormFwdParams& p, int b, int t0, int base,
+                                           typename NVec<T>::type (&xv)[kRowBatch]) {
   constexpr int VEC = NVec<T>::n;
   using VT = typename NVec<T>::type;
   const int C = p.th.chunk, G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
   const int rows = p.count * C, per_pass = kThetaThreads / G;
   const int n0 = gl * VEC;
   const bool act = n0 < p.N;
-  for (int base = 0; base < rows; base += kRowBatch * per_pass) {
-    VT xv[kRowBatch];
 #pragma unroll
-    for (int k = 0; k < kRowBatch; ++k) {   // uniform over each group of G lanes
-      const int rr = base + gid + k * per_pass;
-      const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
-      if (rr < rows && act)
-        xv[k] = *reinterpret_cast<const VT*>(static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] +
-                                             t * p.in.xst[which] + n0);
+  for (int k = 0; k < kRowBatch; ++k) {   // uniform over each group of G lanes
+    const int rr = base + gid + k * per_pass;
+    const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
+    if (rr < rows && act)
+      xv[k] = *reinterpret_cast<const VT*>(static_cast<const T*>(p.in.x[which]) + b * p.in.xsb[which] +
+                                           t * p.in.xst[which] + n0);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void norm_finish(const NormFwdParams& p, int b, int t0, int base,
+                                            const typename NVec<T>::type (&xv)[kRowBatch]) {
+  constexpr int VEC = NVec<T>::n;
+  using VT = typename NVec<T>::type;
+  const int C = p.th.chunk, G = p.G, gid = threadIdx.x / G, gl = threadIdx.x % G;
+  const int rows = p.count * C, per_pass = kThetaThreads / G;
+  const int n0 = gl * VEC;
+  const bool act = n0 < p.N;
+#pragma unroll
+  for (int k = 0; k < kRowBatch; ++k) {
+    const int rr = base + gid + k * per_pass;
+    if (rr >= rows) break;
+    const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
+    const int64_t r = (int64_t)b * p.L + t;
+    float ss = 0.f;
+    if (act) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) ss += (float)xv[k][i] * (float)xv[k][i];
     }
+    ss = group_sum_dyn(ss, G);
+    const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
+    if (act) {
+      const float* w = p.in.w[which] + n0;
+      VT yv;
 #pragma unroll
-    for (int k = 0; k < kRowBatch; ++k) {
-      const int rr = base + gid + k * per_pass;
-      if (rr >= rows) break;
-      const int which = rr >= C ? 1 : 0, t = t0 + rr - which * C;
-      const int64_t r = (int64_t)b * p.L + t;
-      float ss = 0.f;
-      if (act) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) ss += (float)xv[k][i] * (float)xv[k][i];
-      }
-      ss = group_sum_dyn(ss, G);
-      const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
-      if (act) {
-        const float* w = p.in.w[which] + n0;
-        VT yv;
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) yv[i] = (T)((float)xv[k][i] * rstd * w[i]);
-        *reinterpret_cast<VT*>(static_cast<T*>(p.y[which]) + r * p.N + n0) = yv;
-      }
-      if (gl == 0 && p.rstd[which]) p.rstd[which][r] = rstd;
+      for (int i = 0; i < VEC; ++i) yv[i] = (T)((float)xv[k][i] * rstd * w[i]);
+      *reinterpret_cast<VT*>(static_cast<T*>(p.y[which]) + r * p.N + n0) = yv;
     }
+    if (gl == 0 && p.rstd[which]) p.rstd[which][r] = rstd;
   }
 }
 template <typename T>
@@ -161,13 +170,16 @@ __global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwd
   const T* ang = static_cast<const T*>(q.ang) + b * q.asb;
   const T* dtr = static_cast<const T*>(q.dtr) + b * q.dsb;
   // rounds of kThetaRound items per thread, every load of a round issued before any use
-  // (one memory latency per round, not per item); quotients by the run-time Nr, H and
-  // pair counts through DivMod (a float estimate), not integer division; tanh and softplus
-  // from the hardware exp2 / log2 / rcp (tanh_fast, softplus_fast)
+  // (one memory latency per round, not per item); the first round of all three kinds
+  // (angles, dt_raw, B / C rows) is issued before any of them is used. Quotients by the
+  // run-time Nr, H and pair counts through DivMod (a float estimate), not integer
+  // division; tanh and softplus from the hardware exp2 / log2 / rcp (tanh_fast,
+  // softplus_fast) for bf16 operands, the library functions for f32, as the preprocess
+  // kernels use them.
   constexpr int kThetaRound = 8;
+  constexpr int STEP = kThetaRound * kThetaThreads;
   const DivMod byNr(Nr), byH(H), byPairs(H * nq), byNq(nq);
-  for (int base = 0; base < C * Nr; base += kThetaRound * kThetaThreads) {
-    float v[kThetaRound];
+  auto issue_ang = [&](int base, float (&v)[kThetaRound]) {
 #pragma unroll
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
@@ -175,20 +187,19 @@ __global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwd
       byNr(i, t, j);
       v[u] = i < C * Nr ? (float)ang[(int64_t)(t0 + t) * q.ast + j] : 0.f;
     }
+  };
+  auto finish_ang = [&](int base, const float (&v)[kThetaRound]) {
 #pragma unroll
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
       if (i < C * Nr) {
-        // bf16 operands: the hardware exp2 / rcp; f32: the library functions, as the
-        // preprocess kernels use them
         const float tp = (std::is_same<T, float>::value ? tanhf(v[u]) : tanh_fast(v[u])) * kPi;
         q.tab[((int64_t)b * L + t0) * Nr + i] = tp;   // the chunk's rows are contiguous
         sTab[i] = tp;
       }
     }
-  }
-  for (int base = 0; base < C * H; base += kThetaRound * kThetaThreads) {
-    float v[kThetaRound];
+  };
+  auto issue_dt = [&](int base, float (&v)[kThetaRound]) {
 #pragma unroll
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
@@ -196,13 +207,40 @@ __global__ void __launch_bounds__(kThetaThreads) norm_theta_kernel(const NormFwd
       byH(i, t, h);
       v[u] = i < C * H ? (float)dtr[(int64_t)(t0 + t) * q.dst + h] + q.dt_bias[h] : 0.f;
     }
+  };
+  auto finish_dt = [&](int base, const float (&v)[kThetaRound]) {
 #pragma unroll
     for (int u = 0; u < kThetaRound; ++u) {
       const int i = base + threadIdx.x + u * kThetaThreads;
       if (i < C * H) sDt[i] = std::is_same<T, float>::value ? softplus_(v[u]) : softplus_fast(v[u]);
     }
+  };
+  {
+    float av[kThetaRound], dv[kThetaRound];
+    typename NVec<T>::type xv[kRowBatch];
+    issue_ang(0, av);
+    issue_dt(0, dv);
+    norm_issue<T>(p, b, t0, 0, xv);
+    finish_ang(0, av);
+    finish_dt(0, dv);
+    norm_finish<T>(p, b, t0, 0, xv);
   }
-  norm_rows_of_chunk<T>(p, b, t0);
+  for (int base = STEP; base < C * Nr; base += STEP) {
+    float v[kThetaRound];
+    issue_ang(base, v);
+    finish_ang(base, v);
+  }
+  for (int base = STEP; base < C * H; base += STEP) {
+    float v[kThetaRound];
+    issue_dt(base, v);
+    finish_dt(base, v);
+  }
+  const int rows_step = kRowBatch * (kThetaThreads / p.G);
+  for (int base = rows_step; base < p.count * C; base += rows_step) {
+    typename NVec<T>::type xv[kRowBatch];
+    norm_issue<T>(p, b, t0, base, xv);
+    norm_finish<T>(p, b, t0, base, xv);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < spc * H * nq; i += kThetaThreads) {   // (strip, head, quad)
     int st, r, h, jq;
