@@ -122,6 +122,140 @@ int32_t gemv_launch(const GvParams& p, hipStream_t s) {
   return M3S_ERR_UNSUPPORTED;
 }
 
+// ---- more rows: MFMA tiles ----------------------------------------------------------
+// From kGvMaxRows + 1 rows (a batch of decode tokens: 256 at the decode config) the
+// products run on v_mfma_f32_16x16x32_bf16. A workgroup of four waves takes a 64 x NC
+// output tile, wave w its rows 16 w .. 16 w + 15 and all NC columns, and walks K in steps
+// of kGmK = 64 (two MFMA K-blocks per step):
+//  * the x rows are each wave's own A operand: per step and K-block one 16-byte piece per
+//    lane (row lane & 15, K slots 8 (lane >> 4) ..), read straight into registers;
+//  * the weight's kGmK x NC block of a step is shared by the four waves: staged in LDS as
+//    it lies in memory (K rows, 16-byte pieces) and read as the B operand with
+//    ds_read_b64_tr_b16, which hands a lane four consecutive K of one column;
+//  * both are loaded kGmD steps ahead into a ring of registers (slot = step mod kGmD, so no
+//    register is copied: a copy of a register still being loaded would wait for it), and
+//    a step's weight block goes to the LDS stage it is read from one step early; two
+//    stages (stage = step mod 2; kGmD is even), one barrier per step.
+// The step count is padded to a multiple of kGmD: a step past the last reads zeros (its
+// loads go through an out-of-range offset), so every load and stage is unconditional and
+// the compiler's wait counts stay exact (a conditional load made it wait for every
+// outstanding load once per kGmD steps). Rows past M and columns past N read as zero
+// through the buffer descriptors' range and are not stored. The row tiles of one column
+// tile are consecutive blocks of one XCD, so the weight block is fetched from HBM once and
+// from L2 after that. Fixed summation order: deterministic.
+constexpr int kGmThreads = 256;
+constexpr int kGmMT = 64;    // rows per workgroup (16 per wave)
+constexpr int kGmK = 64;     // K per step (kGmKB MFMA K-blocks of 32)
+constexpr int kGmKB = kGmK / 32;
+constexpr int kGmD = 4;      // steps loaded ahead (even: the LDS stage of step s0 + d is d & 1)
+
+struct GmParams {
+  const bf16* x;
+  const bf16* w;
+  bf16* y;
+  int M, K, N, tiles_m, tiles_n;
+  int64_t ldx, ldw, ldy;
+  uint32_t ex, ew;   // the operands' extents in bytes
+};
+
+template <int NC>
+__global__ void __launch_bounds__(kGmThreads) gemm_rows_kernel(const GmParams p) {
+  constexpr int CT = NC / 16;                  // 16-column tiles per wave
+  constexpr int LD = NC + 8;                   // LDS row stride (bf16), 16 bytes of pad
+  constexpr int WPR = NC / 8;                  // 16-byte weight pieces per K row
+  constexpr int WP = kGmK * WPR / kGmThreads;  // weight pieces per thread and step
+  static_assert(WP >= 1 && kGmK * WPR % kGmThreads == 0, "whole weight pieces per thread");
+  __shared__ __attribute__((aligned(16))) bf16 sw[2][kGmK * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // block -> (row tile, column tile): the row tiles of one column tile on one XCD
+  const int nb = p.tiles_m * p.tiles_n, per = (nb + 7) >> 3, bid = blockIdx.x;
+  const int lin = (bid & 7) * per + (bid >> 3);
+  if (lin >= nb) return;   // the XCD groups are padded to equal size
+  const int tn = lin / p.tiles_m, tm = lin % p.tiles_m;
+  const int row = tm * kGmMT + 16 * wave + (lane & 15), n0 = tn * NC;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.ex), rw = make_rsrc(p.w, p.ew);
+  // this lane's x pieces: row `row`, K slots 8 (lane >> 4) .. of each K-block; past M: out
+  // of range
+  const uint32_t ox = row < p.M ? (uint32_t)(row * p.ldx + 8 * (lane >> 4)) * 2 : p.ex;
+  // this thread's weight pieces: row (tid + 256 r) / WPR of the step, columns
+  // 8 ((tid + 256 r) % WPR) ..
+  uint32_t ow[WP];
+  int lo[WP];
+#pragma unroll
+  for (int r = 0; r < WP; ++r) {
+    const int i = tid + r * kGmThreads, wr = i / WPR, wc = 8 * (i % WPR);
+    ow[r] = n0 + wc < p.N ? (uint32_t)(wr * p.ldw + n0 + wc) * 2 : p.ew;
+    lo[r] = wr * LD + wc;
+  }
+  const int ns = p.K / kGmK, nsp = (ns + kGmD - 1) / kGmD * kGmD;
+
+  bf16x8 ra[kGmD][kGmKB], rb[kGmD][WP];
+  auto load = [&](int st, int slot) {
+    const bool in = st < ns;
+#pragma unroll
+    for (int kb = 0; kb < kGmKB; ++kb)
+      ra[slot][kb] = buf_load<bf16x8>(rx, in ? ox : p.ex, in ? (uint32_t)(st * kGmK + 32 * kb) * 2 : 0u);
+#pragma unroll
+    for (int r = 0; r < WP; ++r)
+      rb[slot][r] = buf_load<bf16x8>(rw, in ? ow[r] : p.ew, in ? (uint32_t)(st * kGmK * p.ldw) * 2 : 0u);
+  };
+  auto stage = [&](int buf, int slot) {
+#pragma unroll
+    for (int r = 0; r < WP; ++r) *reinterpret_cast<bf16x8*>(&sw[buf][lo[r]]) = rb[slot][r];
+  };
+  f32x4 acc[CT];
+#pragma unroll
+  for (int j = 0; j < CT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int g = lane >> 4;
+  auto compute = [&](int buf, int slot) {
+    const bf16* sb = sw[buf];
+#pragma unroll
+    for (int kb = 0; kb < kGmKB; ++kb) {
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        const bf16x4 lo4 = ld_tr4(sb, LD, 32 * kb + 8 * g, 16 * j, lane);
+        const bf16x4 hi4 = ld_tr4(sb, LD, 32 * kb + 8 * g + 4, 16 * j, lane);
+        const bf16x8 b = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        mma32x(acc[j], ra[slot][kb], b);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int d = 0; d < kGmD; ++d) load(d, d);
+  stage(0, 0);
+  for (int s0 = 0; s0 < nsp; s0 += kGmD) {
+#pragma unroll
+    for (int d = 0; d < kGmD; ++d) {
+      __syncthreads();   // stage d & 1 holds step s0 + d; the other stage is free
+      compute(d & 1, d);
+      stage((d + 1) & 1, (d + 1) % kGmD);
+      load(s0 + d + kGmD, d);
+    }
+  }
+  // acc[j][e] = y[row0 + e][n0 + 16 j + (lane & 15)], row0 = the wave's row of 4 g
+  const int row0 = tm * kGmMT + 16 * wave + 4 * g;
+#pragma unroll
+  for (int j = 0; j < CT; ++j) {
+    const int col = n0 + 16 * j + (lane & 15);
+    if (col >= p.N) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (row0 + e < p.M) p.y[(int64_t)(row0 + e) * p.ldy + col] = (bf16)acc[j][e];
+  }
+}
+
+// Columns per workgroup: 64 when that still gives at least 128 workgroups, else 32.
+template <int NC>
+int32_t gemm_rows_launch(GmParams p, hipStream_t s) {
+  p.tiles_m = (p.M + kGmMT - 1) / kGmMT;
+  p.tiles_n = (p.N + NC - 1) / NC;
+  const int nb = p.tiles_m * p.tiles_n;
+  const unsigned grid = (unsigned)(((nb + 7) >> 3) * 8);
+  hipLaunchKernelGGL((gemm_rows_kernel<NC>), dim3(grid), dim3(kGmThreads), 0, s, p);
+  return launch_status("m3s_gemv");
+}
+
 }  // namespace m3s
 
 extern "C" int32_t m3s_gemv(const m3s_gemv_args* a, void* stream) {
@@ -131,17 +265,32 @@ extern "C" int32_t m3s_gemv(const m3s_gemv_args* a, void* stream) {
   M3S_REQUIRE(a->struct_size == (int32_t)sizeof(m3s_gemv_args),
               "m3s_gemv: struct_size %d != %d (ABI mismatch)", a->struct_size,
               (int)sizeof(m3s_gemv_args));
-  M3S_REQUIRE(a->rows >= 1 && a->rows <= kGvMaxRows, "m3s_gemv: rows %d not in [1, %d]",
-              a->rows, kGvMaxRows);
+  M3S_REQUIRE(a->rows >= 1, "m3s_gemv: rows %d < 1", a->rows);
   M3S_REQUIRE(a->k > 0 && a->n > 0, "m3s_gemv: non-positive k or n");
   M3S_REQUIRE(a->n % 8 == 0, "m3s_gemv: n %d is not a multiple of 8", a->n);
   M3S_REQUIRE(a->x && a->w && a->y, "m3s_gemv: a NULL operand");
   M3S_REQUIRE(aligned16(a->w) && a->ldw % 8 == 0 && a->ldw >= a->n,
               "m3s_gemv: w must be 16-byte aligned with a row stride >= n and a multiple of 8");
   M3S_REQUIRE(a->ldx >= a->k && a->ldy >= a->n, "m3s_gemv: a row stride is too short");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->rows > kGvMaxRows) {
+    M3S_REQUIRE(a->k % kGmK == 0, "m3s_gemv: k %d is not a multiple of %d (rows > %d)", a->k,
+                kGmK, kGvMaxRows);
+    M3S_REQUIRE(aligned16(a->x) && a->ldx % 8 == 0,
+                "m3s_gemv: x must be 16-byte aligned with a row stride a multiple of 8 (rows > %d)",
+                kGvMaxRows);
+    const int64_t ex = ((int64_t)(a->rows - 1) * a->ldx + a->k) * 2;
+    const int64_t ew = ((int64_t)(a->k - 1) * a->ldw + a->n) * 2;
+    M3S_REQUIRE(ex < (1ll << 31) && ew < (1ll << 31), "m3s_gemv: an operand spans 2 GiB or more");
+    GmParams g{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w),
+               static_cast<bf16*>(a->y), a->rows, a->k, a->n, 0, 0, a->ldx, a->ldw, a->ldy,
+               (uint32_t)ex, (uint32_t)ew};
+    const int tm = (a->rows + kGmMT - 1) / kGmMT;
+    if ((int64_t)tm * ((a->n + 63) / 64) >= 128) return gemm_rows_launch<64>(g, s);
+    return gemm_rows_launch<32>(g, s);
+  }
   GvParams p{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w),
              static_cast<bf16*>(a->y), a->rows, a->k, a->n, a->ldx, a->ldw, a->ldy};
-  hipStream_t s = static_cast<hipStream_t>(stream);
   M3S_REQUIRE(a->k <= kGvThreads * kGvMaxLoads, "m3s_gemv: k %d > %d", a->k,
               kGvThreads * kGvMaxLoads);
   switch (gemv_col_lanes(a->k, a->n)) {

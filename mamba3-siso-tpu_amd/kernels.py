@@ -1106,18 +1106,32 @@ def wgrad(a: Tensor, b: Tensor) -> Tensor:
     return c
 
 
+#: Rows that ``m3s_gemv``'s MFMA tiles take (5 to this many; 1-4 rows stream).
+GEMM_ROWS_MAX = 1024
+#: Row counts for which `matmul` prefers those tiles over the library product: measured
+#: on the LM's and the layer's projection widths (K 768-2048, N 768-4480), the tiles were
+#: faster from 32 to 256 rows (256 rows of the LM's in_proj 8.0 against 12.7 us, fc1 7.8
+#: against 12.2 us) and the library at 8 rows and from 512.
+MATMUL_TILE_ROWS = (32, 256)
+
+
 def gemv_supported(x: Tensor, w: Tensor) -> bool:
-    """Whether `gemv` takes ``x @ w``: bf16 device operands on one device, 1 to 4 rows
-    with unit column stride, ``w`` ``(K, N)`` row-major with N a multiple of 8, 16-byte
-    aligned rows and K at most 4096."""
+    """Whether `gemv` takes ``x @ w``: bf16 device operands on one device with unit
+    column strides, ``w`` ``(K, N)`` row-major with N a multiple of 8 and 16-byte aligned
+    rows; 1 to 4 rows with K at most 4096 (the streaming pass), or 5 to `GEMM_ROWS_MAX`
+    rows with K a multiple of 64 and 16-byte aligned x rows (the MFMA tiles)."""
     if not (x.is_cuda and w.is_cuda and x.dtype == w.dtype == torch.bfloat16
             and x.dim() == 2 and w.dim() == 2 and x.device == w.device):
         return False
     m, k = x.shape
     kw, n = w.shape
-    return (1 <= m <= 4 and k == kw and 0 < k <= 4096 and n > 0 and n % 8 == 0
-            and x.stride(1) == 1 and w.stride(1) == 1 and w.stride(0) % 8 == 0
-            and w.data_ptr() % 16 == 0)
+    if not (k == kw and k > 0 and n > 0 and n % 8 == 0 and x.stride(1) == 1
+            and w.stride(1) == 1 and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0):
+        return False
+    if 1 <= m <= 4:
+        return k <= 4096
+    return (m <= GEMM_ROWS_MAX and k % 64 == 0 and x.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0)
 
 
 def gemv(x: Tensor, w: Tensor) -> Tensor:
@@ -1125,8 +1139,9 @@ def gemv(x: Tensor, w: Tensor) -> Tensor:
     pass over the weight, float32 accumulation, bf16 out). Operands must pass
     `gemv_supported`."""
     if not gemv_supported(x, w):
-        raise ValueError("gemv: x (1..4, K) and w (K, N) must be bf16 device matrices with "
-                         "unit column stride, N % 8 == 0, 16-byte aligned w rows, K <= 4096")
+        raise ValueError("gemv: x (M, K) and w (K, N) must be bf16 device matrices with unit "
+                         "column stride, N % 8 == 0 and 16-byte aligned w rows; M <= 4 needs "
+                         f"K <= 4096, 5 <= M <= {GEMM_ROWS_MAX} K % 64 == 0 and aligned x rows")
     m, k = x.shape
     n = w.shape[1]
     y = empty(m, n, device=x.device, dtype=torch.bfloat16)
@@ -1143,11 +1158,14 @@ def gemv(x: Tensor, w: Tensor) -> Tensor:
 
 
 def matmul(x: Tensor, w: Tensor) -> Tensor:
-    """``x @ w``: through `gemv` for one or two rows that it takes (a decode step's
-    projections: inside a recorded decode step 3.6-4 us against the library's 5.8-8.5 us
-    at the LM's widths), else the library product. Four rows are faster in the library."""
-    if x.dim() == 2 and x.shape[0] <= 2 and gemv_supported(x, w):
-        return gemv(x, w)
+    """``x @ w``: through `gemv` for one or two rows (a decode step's projections: inside a
+    recorded decode step 3.6-4 us against the library's 5.8-8.5 us at the LM's widths) and
+    for `MATMUL_TILE_ROWS` rows (a batch of decode tokens) when it takes them, else the
+    library product (three and four rows are faster there)."""
+    if x.dim() == 2 and gemv_supported(x, w):
+        m = x.shape[0]
+        if m <= 2 or MATMUL_TILE_ROWS[0] <= m <= MATMUL_TILE_ROWS[1]:
+            return gemv(x, w)
     return x @ w
 
 

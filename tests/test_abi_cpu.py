@@ -345,8 +345,8 @@ def test_gemv_arguments_are_checked_without_a_launch(lib):
     assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID
     assert b"struct_size" in h.m3s_last_error()
     a.struct_size = ctypes.sizeof(lib.GemvArgs)
-    a.rows, a.k, a.n = 5, 64, 64
-    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # rows > 4
+    a.rows, a.k, a.n = 0, 64, 64
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # rows < 1
     a.rows = 1
     a.n = 60
     assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # n % 8
@@ -359,6 +359,11 @@ def test_gemv_arguments_are_checked_without_a_launch(lib):
     a.w = 0x2000
     a.k, a.ldx = 5000, 5000
     assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # k > 4096
+    a.rows, a.k, a.ldx = 64, 96, 96
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # the tiles: k % 64
+    assert b"multiple of 64" in h.m3s_last_error()
+    a.k, a.ldx, a.x = 128, 132, 0x1000
+    assert h.m3s_gemv(ctypes.byref(a), None) == lib.ERR_INVALID   # the tiles: x row stride
 
 
 def test_adamw_arguments_are_checked_without_a_launch(lib):

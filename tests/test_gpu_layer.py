@@ -515,3 +515,31 @@ def test_gemv_matches_float64(m3, dev, m, k, n, ldw):
     err = ((got.cpu().double() - ref).abs().max() / ref.abs().max()).item()
     assert err <= 2 ** -8, err
     assert torch.equal(got, m3.kernels.gemv(xd, wd))
+
+
+@pytest.mark.parametrize("m,k,n,ldx,ldw", [
+    (256, 1024, 4480, 1024, 4480),   # the layer's in_proj at the decode batch
+    (256, 2048, 1024, 2048, 1024),   # its out_proj
+    (64, 768, 3432, 768, 3432),      # the LM's in_proj, ragged 64-column tiles
+    (5, 1536, 768, 1544, 776),       # five rows (a partial row tile), padded row strides
+    (300, 128, 40, 128, 40),         # a ragged row tile and 32-column tiles, N % 32 != 0
+    (1024, 64, 256, 64, 256),        # the largest row count, one K step
+])
+def test_gemv_tiles_match_float64(m3, dev, m, k, n, ldx, ldw):
+    """``m3s_gemv`` with more than four rows (its MFMA tiles) against float64: within one
+    bf16 rounding of max |ref| (2^-8), rows and columns past the matrix untouched (the
+    output is NaN-filled first), bit-identical on a second call."""
+    g = torch.Generator().manual_seed(m + k + n)
+    xfull = torch.randn(m, ldx, generator=g).to(torch.bfloat16)
+    wfull = (torch.randn(k, ldw, generator=g) / k ** 0.5).to(torch.bfloat16)
+    xd, wd = xfull.to(dev)[:, :k], wfull.to(dev)[:, :n]
+    got = m3.kernels.gemv(xd, wd)
+    ref = xfull[:, :k].double() @ wfull[:, :n].double()
+    assert got.dtype == torch.bfloat16 and got.shape == (m, n)
+    assert bool(torch.isfinite(got).all())
+    err = ((got.cpu().double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 2 ** -8, err
+    assert torch.equal(got, m3.kernels.gemv(xd, wd))
+    # the layer routes its decode batch through the same tiles
+    if m3.kernels.MATMUL_TILE_ROWS[0] <= m <= m3.kernels.MATMUL_TILE_ROWS[1]:
+        assert torch.equal(m3.kernels.matmul(xd, wd), got)
