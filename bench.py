@@ -363,7 +363,9 @@ def main():
                        + 2 * BD * H * P * N * 4 + 2 * BD * H * (N + P + Nr) * 4
                        + BD * cfg.d_inner * 2 * 2)
     line.update(decode_layer_bytes=dec_layer_bytes,
-                decode_layer_gbs=round(dec_layer_bytes / (dec_ms * 1e-3) / 1e9, 1))
+                decode_layer_gbs=round(dec_layer_bytes / (dec_ms * 1e-3) / 1e9, 1),
+                decode_layer_hbm_frac=round(dec_layer_bytes / (dec_ms * 1e-3) / 1e9
+                                            / HBM_PEAK_GBS, 4))
     # The legs from here to the headline run back to back, without emptying the allocator
     # cache in between: the GPU lowers its clocks within a millisecond or two of idling
     # (measured: a 20 ms pause before 5 warmup steps costs the next 20 forwards 7%, an
