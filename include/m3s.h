@@ -459,11 +459,13 @@ typedef struct m3s_wgrad_args {
   void* workspace;      /* the split partials, or NULL when one split */
 } m3s_wgrad_args;
 
-/* A projection of a one-token decode step: y (rows, n) = x (rows, k) w (k, n), bf16 in and
- * out, float32 accumulation, for 1 <= rows <= 4. Replaces, in the decode step, the per-token
- * projections of the reference's layer and LM step (model.py:266-296: in_proj, out_proj,
- * fc1, fc2), left to XLA there. n a multiple of 8; k <= 4096; w 16-byte aligned with ldw a
- * multiple of 8. Row strides are in elements. Deterministic (fixed summation order). */
+/* A projection of a decode step: y (rows, n) = x (rows, k) w (k, n), bf16 in and out,
+ * float32 accumulation. Replaces, in the decode step, the per-token projections of the
+ * reference's layer and LM step (model.py:266-296: in_proj, out_proj, fc1, fc2), left to
+ * XLA there. n a multiple of 8; w 16-byte aligned with ldw a multiple of 8. 1 <= rows <= 4:
+ * a streaming pass over w, k <= 4096. rows > 4 (a batch of tokens): MFMA tiles, k a
+ * multiple of 64, x 16-byte aligned with ldx a multiple of 8, each operand under 2 GiB.
+ * Row strides are in elements. Deterministic (fixed summation order). */
 typedef struct m3s_gemv_args {
   int32_t struct_size;  /* sizeof(m3s_gemv_args) */
   int32_t rows, k, n;
