@@ -245,12 +245,21 @@ def test_decode_scan_golden_chain(m3):
 
 def test_decode_scan_cfg4_size(m3):
     """cfg4 sizes (B=256, H=32, P=64, N=128, Nr=32), 12 steps in one launch: the chain of
-    12 single-step launches, bit for bit."""
-    _, d, st = chain_inputs(256, 32, 12, 128, 64, 32, "bf16", seed=31)
+    12 single-step launches bit for bit, and chained float64 steps under the bf16 readout
+    model on the first two batch rows."""
+    c, d, st = chain_inputs(256, 32, 12, 128, 64, 32, "bf16", seed=31)
     args = (d["q"], d["k"], d["v"], d["adt"], d["dt"], d["lam"], d["angles"], d["q_bias"], d["k_bias"])
     ref = m3.decode_loop(*args, dev_state(st), d["d_skip"], d["z"])
     got = m3.decode_scan(*args, dev_state(st), d["d_skip"], d["z"])
     assert_same_run(got, ref, "cfg4")
+    s, ys = O.SISOState(*(t[:2] for t in st)), []
+    for t in range(12):
+        y, s = O.siso_step(c["q"][:2, t], c["k"][:2, t], c["v"][:2, :, t], c["adt"][:2, :, t],
+                           c["dt"][:2, :, t], c["lam"][:2, :, t], c["angles"][:2, t], c["q_bias"],
+                           c["k_bias"], s, c["d_skip"], c["z"][:2, :, t], mm_dtype=BF16)
+        ys.append(y)
+    assert_p95(got[0][:2], torch.stack(ys, dim=2), BF16_OUT_MODEL_P95, "y vs bf16 readout model")
+    assert_f32(got[1].ssm[:2], s.ssm, "out", "ssm (f32 update)")
 
 
 def test_decode_scan_rejects_mismatched_shapes(m3):
