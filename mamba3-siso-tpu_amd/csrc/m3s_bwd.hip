@@ -1657,11 +1657,16 @@ __global__ void __launch_bounds__(C / 16 * 64) bwd_bf16_kernel(const BwdParams p
                 }
               }
             }
-            // this head's du / dw row pieces; the head sum happens in headsum_kernel
-            gst<vec>(dug, sqk + o, du0);
-            gst<vec>(dug, sqk + o + 2 * H2, du1);
-            gst<vec>(dwg, sqk + o, dw0);
-            gst<vec>(dwg, sqk + o + 2 * H2, dw1);
+            // this head's du / dw row pieces; the head sum happens in headsum_kernel. Stored
+            // non-temporally: 1.07 GB at cfg3 that only the head sum reads back, streamed past
+            // the caches the scan's own operands use (0.5-1% faster than plain stores)
+            auto nts = [&](bf16* base, uint32_t off, vec x) {
+              __builtin_nontemporal_store(x, reinterpret_cast<vec*>(reinterpret_cast<char*>(base) + off));
+            };
+            nts(dug, sqk + o, du0);
+            nts(dug, sqk + o + 2 * H2, du1);
+            nts(dwg, sqk + o, dw0);
+            nts(dwg, sqk + o + 2 * H2, dw1);
           }
           dqq = group_sum<F::QKG>(dqq);
           dsc = group_sum<F::QKG>(dsc);
