@@ -236,6 +236,10 @@ def test_decode_scan_golden_chain(m3):
     scan = m3.decode_scan(*args, m3.zero_state(b, h, p, n, nr, device="cuda"), t["d"],
                           t["z"].transpose(1, 2), dtype_policy="f32")
     assert_same_run(scan, loop, "golden chain")
+    # the reference's `folded` switch (tests.py:814-824 checks both) selects the same step here
+    unfolded = m3.decode_scan(*args, m3.zero_state(b, h, p, n, nr, device="cuda"), t["d"],
+                              t["z"].transpose(1, 2), dtype_policy="f32", folded=False)
+    assert_same_run(unfolded, loop, "golden chain, folded=False")
     y, st = scan
     want = torch.from_numpy(fx["out"]).double()
     assert O.max_rel(cpu(y.transpose(1, 2)), want) <= 2e-5
