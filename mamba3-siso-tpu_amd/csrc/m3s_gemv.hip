@@ -124,12 +124,12 @@ int32_t gemv_launch(const GvParams& p, hipStream_t s) {
 
 // ---- more rows: MFMA tiles ----------------------------------------------------------
 // From kGvMaxRows + 1 rows (a batch of decode tokens: 256 at the decode config) the
-// products run on v_mfma_f32_16x16x32_bf16. A workgroup of four waves takes a 64 x NC
-// output tile, wave w its rows 16 w .. 16 w + 15 and all NC columns, and walks K in steps
-// of kGmK = 64 (two MFMA K-blocks per step):
+// products run on v_mfma_f32_16x16x32_bf16. A workgroup of RW waves (four or eight) takes
+// a 16 RW x NC output tile, wave w its rows 16 w .. 16 w + 15 and all NC columns, and walks
+// K in steps of kGmK = 64 (two MFMA K-blocks per step):
 //  * the x rows are each wave's own A operand: per step and K-block one 16-byte piece per
 //    lane (row lane & 15, K slots 8 (lane >> 4) ..), read straight into registers;
-//  * the weight's kGmK x NC block of a step is shared by the four waves: staged in LDS as
+//  * the weight's kGmK x NC block of a step is shared by the RW waves: staged in LDS as
 //    it lies in memory (K rows, 16-byte pieces) and read as the B operand with
 //    ds_read_b64_tr_b16, which hands a lane four consecutive K of one column;
 //  * both are loaded kGmD steps ahead into a ring of registers (slot = step mod kGmD, so no
@@ -143,8 +143,6 @@ int32_t gemv_launch(const GvParams& p, hipStream_t s) {
 // through the buffer descriptors' range and are not stored. The row tiles of one column
 // tile are consecutive blocks of one XCD, so the weight block is fetched from HBM once and
 // from L2 after that. Fixed summation order: deterministic.
-constexpr int kGmThreads = 256;
-constexpr int kGmMT = 64;    // rows per workgroup (16 per wave)
 constexpr int kGmK = 64;     // K per step (kGmKB MFMA K-blocks of 32)
 constexpr int kGmKB = kGmK / 32;
 constexpr int kGmD = 4;      // steps loaded ahead (even: the LDS stage of step s0 + d is d & 1)
@@ -158,13 +156,14 @@ struct GmParams {
   uint32_t ex, ew;   // the operands' extents in bytes
 };
 
-template <int NC>
-__global__ void __launch_bounds__(kGmThreads) gemm_rows_kernel(const GmParams p) {
+template <int NC, int RW>
+__global__ void __launch_bounds__(64 * RW) gemm_rows_kernel(const GmParams p) {
+  constexpr int TH = 64 * RW, MT = 16 * RW;   // threads; rows per workgroup
   constexpr int CT = NC / 16;                  // 16-column tiles per wave
   constexpr int LD = NC + 8;                   // LDS row stride (bf16), 16 bytes of pad
   constexpr int WPR = NC / 8;                  // 16-byte weight pieces per K row
-  constexpr int WP = kGmK * WPR / kGmThreads;  // weight pieces per thread and step
-  static_assert(WP >= 1 && kGmK * WPR % kGmThreads == 0, "whole weight pieces per thread");
+  constexpr int WP = kGmK * WPR / TH;          // weight pieces per thread and step
+  static_assert(WP >= 1 && kGmK * WPR % TH == 0, "whole weight pieces per thread");
   __shared__ __attribute__((aligned(16))) bf16 sw[2][kGmK * LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // block -> (row tile, column tile): the row tiles of one column tile on one XCD
@@ -172,18 +171,18 @@ __global__ void __launch_bounds__(kGmThreads) gemm_rows_kernel(const GmParams p)
   const int lin = (bid & 7) * per + (bid >> 3);
   if (lin >= nb) return;   // the XCD groups are padded to equal size
   const int tn = lin / p.tiles_m, tm = lin % p.tiles_m;
-  const int row = tm * kGmMT + 16 * wave + (lane & 15), n0 = tn * NC;
+  const int row = tm * MT + 16 * wave + (lane & 15), n0 = tn * NC;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, p.ex), rw = make_rsrc(p.w, p.ew);
   // this lane's x pieces: row `row`, K slots 8 (lane >> 4) .. of each K-block; past M: out
   // of range
   const uint32_t ox = row < p.M ? (uint32_t)(row * p.ldx + 8 * (lane >> 4)) * 2 : p.ex;
-  // this thread's weight pieces: row (tid + 256 r) / WPR of the step, columns
-  // 8 ((tid + 256 r) % WPR) ..
+  // this thread's weight pieces: row (tid + TH r) / WPR of the step, columns
+  // 8 ((tid + TH r) % WPR) ..
   uint32_t ow[WP];
   int lo[WP];
 #pragma unroll
   for (int r = 0; r < WP; ++r) {
-    const int i = tid + r * kGmThreads, wr = i / WPR, wc = 8 * (i % WPR);
+    const int i = tid + r * TH, wr = i / WPR, wc = 8 * (i % WPR);
     ow[r] = n0 + wc < p.N ? (uint32_t)(wr * p.ldw + n0 + wc) * 2 : p.ew;
     lo[r] = wr * LD + wc;
   }
@@ -234,7 +233,7 @@ __global__ void __launch_bounds__(kGmThreads) gemm_rows_kernel(const GmParams p)
     }
   }
   // acc[j][e] = y[row0 + e][n0 + 16 j + (lane & 15)], row0 = the wave's row of 4 g
-  const int row0 = tm * kGmMT + 16 * wave + 4 * g;
+  const int row0 = tm * MT + 16 * wave + 4 * g;
 #pragma unroll
   for (int j = 0; j < CT; ++j) {
     const int col = n0 + 16 * j + (lane & 15);
@@ -245,14 +244,16 @@ __global__ void __launch_bounds__(kGmThreads) gemm_rows_kernel(const GmParams p)
   }
 }
 
-// Columns per workgroup: 64 when that still gives at least 128 workgroups, else 32.
-template <int NC>
+// Tile shapes: 64 rows x 64 columns when that gives 128 to 256 workgroups; 64 x 32 below;
+// above, 128 rows (eight waves sharing each weight block) x 64 columns, so that one wave
+// of workgroups covers the CUs without a partly filled second one.
+template <int NC, int RW>
 int32_t gemm_rows_launch(GmParams p, hipStream_t s) {
-  p.tiles_m = (p.M + kGmMT - 1) / kGmMT;
+  p.tiles_m = (p.M + 16 * RW - 1) / (16 * RW);
   p.tiles_n = (p.N + NC - 1) / NC;
   const int nb = p.tiles_m * p.tiles_n;
   const unsigned grid = (unsigned)(((nb + 7) >> 3) * 8);
-  hipLaunchKernelGGL((gemm_rows_kernel<NC>), dim3(grid), dim3(kGmThreads), 0, s, p);
+  hipLaunchKernelGGL((gemm_rows_kernel<NC, RW>), dim3(grid), dim3(64 * RW), 0, s, p);
   return launch_status("m3s_gemv");
 }
 
@@ -285,9 +286,10 @@ extern "C" int32_t m3s_gemv(const m3s_gemv_args* a, void* stream) {
     GmParams g{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w),
                static_cast<bf16*>(a->y), a->rows, a->k, a->n, 0, 0, a->ldx, a->ldw, a->ldy,
                (uint32_t)ex, (uint32_t)ew};
-    const int tm = (a->rows + kGmMT - 1) / kGmMT;
-    if ((int64_t)tm * ((a->n + 63) / 64) >= 128) return gemm_rows_launch<64>(g, s);
-    return gemm_rows_launch<32>(g, s);
+    const int64_t t64 = (int64_t)((a->rows + 63) / 64) * ((a->n + 63) / 64);
+    if (t64 > 256) return gemm_rows_launch<64, 8>(g, s);
+    if (t64 >= 128) return gemm_rows_launch<64, 4>(g, s);
+    return gemm_rows_launch<32, 4>(g, s);
   }
   GvParams p{static_cast<const bf16*>(a->x), static_cast<const bf16*>(a->w),
              static_cast<bf16*>(a->y), a->rows, a->k, a->n, a->ldx, a->ldw, a->ldy};
