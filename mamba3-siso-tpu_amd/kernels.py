@@ -616,6 +616,10 @@ def decode_scan(q, k, v, adt, dt, lam, angles, q_bias, k_bias, state, d_skip=Non
     kst = _state_buf(state.k, (batch, nheads, state_dim), dev)
     vst = _state_buf(state.v, (batch, nheads, headdim), dev)
     phist = _state_buf(state.phi, (batch, nheads, n_angles), dev)
+    if steps == 0:   # a scan of length 0: no output rows, the state as it was
+        y_dtype = v.dtype if v.dtype in (torch.bfloat16, torch.float32) else mt
+        return (torch.empty(batch, nheads, 0, headdim, device=dev, dtype=y_dtype),
+                SISOState(ssm=ssm, k=kst, v=vst, phi=phist))
     r = headdim // width
     if r > 1:   # sub-heads of `width` columns, as siso_decode
         ssm_k, vst_k = ssm.view(batch, nheads * r, width, state_dim), vst.view(batch, nheads * r, width)

@@ -274,3 +274,23 @@ def test_decode_scan_rejects_mismatched_shapes(m3):
     with pytest.raises(ValueError):
         m3.decode_scan(d["q"], d["k"], d["v"], d["adt"][:, :, :3], d["dt"], d["lam"], d["angles"],
                        d["q_bias"], d["k_bias"], dev_state(st))
+
+
+def test_decode_scan_of_no_steps_keeps_the_state(m3):
+    """A run of length 0 (``lax.scan`` with ``length=0`` in ``kernel_decode.py:474-533``):
+    an empty ``(B, H, 0, P)`` output and the carried state unchanged; then a real run on
+    that state still matches the step-by-step chain."""
+    _, d, st = chain_inputs(2, 3, 5, 128, 64, 32, "bf16", seed=43)
+    cut = {k_: (v_[:, :0] if k_ in ("q", "k", "angles") else
+                v_[:, :, :0] if k_ in ("v", "z", "adt", "dt", "lam") else v_) for k_, v_ in d.items()}
+    s0 = dev_state(st)
+    y, s1 = m3.decode_scan(cut["q"], cut["k"], cut["v"], cut["adt"], cut["dt"], cut["lam"],
+                           cut["angles"], cut["q_bias"], cut["k_bias"], s0, d_skip=cut["d_skip"],
+                           z=cut["z"])
+    assert tuple(y.shape) == (2, 3, 0, 64) and y.dtype == d["v"].dtype
+    for name, a, b in zip(("ssm", "k", "v", "phi"), s1, dev_state(st)):
+        assert torch.equal(a, b), f"{name} changed by an empty run"
+    args = (d["q"], d["k"], d["v"], d["adt"], d["dt"], d["lam"], d["angles"], d["q_bias"], d["k_bias"])
+    assert_same_run(m3.decode_scan(*args, s1, d_skip=d["d_skip"], z=d["z"]),
+                    m3.kernels.decode_loop(*args, dev_state(st), d_skip=d["d_skip"], z=d["z"]),
+                    "after an empty run")
