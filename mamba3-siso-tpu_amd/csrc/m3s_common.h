@@ -323,6 +323,14 @@ __device__ __forceinline__ float tanh_fast(float x) {
 __device__ __forceinline__ float heavy_tail_fast(float x) {
   return fmaxf(x, 0.f) + __builtin_amdgcn_rcpf(1.f - fminf(x, 0.f));
 }
+// The RMS norm's row scale rsqrt(ss / n + eps) (layer.py:190-198) from a row's sum of
+// squares: the mean as a product with 1 / n (exact when n is a power of two, as every
+// compiled d_state is) and the hardware reciprocal square root (about one ulp, as the
+// two roundings of 1 / sqrt are). One definition for every norm of the B and C rows (the
+// forward norms, their angle pass, the decode step), so they agree bit for bit.
+__device__ __forceinline__ float bc_rstd(float ss, float inv_n, float eps) {
+  return __builtin_amdgcn_rsqf(fmaf(ss, inv_n, eps));
+}
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 // silu from the hardware exp2 / reciprocal (~2 ulp): for gates whose product is rounded
 // to bf16 right after.

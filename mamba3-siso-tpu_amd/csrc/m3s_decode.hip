@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_kernel(const DecParams p) 
       }
       sq = group_sum<64>(sq);
       sk = group_sum<64>(sk);
-      const float rq = 1.f / sqrtf(sq / (float)N + p.eps), rk = 1.f / sqrtf(sk / (float)N + p.eps);
+      const float rq = bc_rstd(sq, 1.f / N, p.eps), rk = bc_rstd(sk, 1.f / N, p.eps);
 #pragma unroll
       for (int u = 0; u < JP; ++u) {
         const int j = tid + 64 * u;

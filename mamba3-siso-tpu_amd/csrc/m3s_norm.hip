@@ -55,7 +55,7 @@ struct NormThetaParams {
 struct NormFwdParams {
   NormRows in;
   int B, L, N, G, count;
-  float eps;
+  float eps, inv_n;   // inv_n = 1 / N
   void* y[2];
   float* rstd[2];
   NormThetaParams th;
@@ -145,7 +145,7 @@ __device__ __forceinline__ void norm_finish(const NormFwdParams& p, int b, int t
       for (int i = 0; i < VEC; ++i) ss += (float)xv[k][i] * (float)xv[k][i];
     }
     ss = group_sum_dyn(ss, G);
-    const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
+    const float rstd = bc_rstd(ss, p.inv_n, p.eps);
     if (act) {
       const float* w = p.in.w[which] + n0;
       VT yv;
@@ -289,7 +289,7 @@ __device__ __forceinline__ void norm_row(const NormFwdParams& p, int which, int 
     for (int i = 0; i < VEC; ++i) ss += x[i] * x[i];
   }
   ss = group_sum_dyn(ss, p.G);
-  const float rstd = 1.f / sqrtf(ss / (float)p.N + p.eps);
+  const float rstd = bc_rstd(ss, p.inv_n, p.eps);
   if (act) {
     const float* w = p.in.w[which] + n0;
     float y[VEC];
@@ -441,6 +441,7 @@ extern "C" int32_t m3s_norm_fwd(const m3s_norm_fwd_args* a, void* stream) {
     p.rstd[i] = a->rstd[i];
   }
   p.B = B; p.L = L; p.N = N; p.G = norm_group(N, vec); p.eps = a->eps; p.count = cnt;
+  p.inv_n = 1.f / (float)N;
   const bool theta = a->theta_table || a->theta_prefix || a->theta_chunk_totals ||
                      a->angles.ptr || a->dt_raw.ptr;
   size_t dyn = 0;
