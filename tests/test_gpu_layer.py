@@ -544,3 +544,48 @@ def test_gemv_tiles_match_float64(m3, dev, m, k, n, ldx, ldw):
     # the layer routes its decode batch through the same tiles
     if m3.kernels.MATMUL_TILE_ROWS[0] <= m <= m3.kernels.MATMUL_TILE_ROWS[1]:
         assert torch.equal(m3.kernels.matmul(xd, wd), got)
+
+
+def test_layer_forward_cfg2_full_size(m3):
+    """BASELINE configs[1] at its own size, the headline path end to end: B=8, L=8192,
+    d_model 1024 (H 32, N 128, P 64, chunk 128), init_params(seed=0), u ~ N(0, 1) in bf16;
+    the inference forward (raw mode: BCNorm with the angle pass, the preprocess inside the
+    scan), one sequence at a time, against the bf16 layer's rounding model (the reference's
+    storage points: the projection, the normalised B and C and y in bf16): y to the model
+    bars, the final state within north_star's 2e-2 max-abs and 5e-3 of max |ref| (measured
+    2.4e-3); and y against the float32 maths (no activation rounding) within 1e-2 of
+    max |ref|. The final state against those maths is printed, not bounded: the bf16
+    projection's dt shifts the decay of a whole sequence's contributions, about 4e-2 of
+    max |ref| at this length, for the reference's bf16 policy as for this one."""
+    cfg = m3.SISOConfig(d_model=1024, d_state=128, headdim=64, expand=2, chunk=128)
+    p_cpu = m3.init_params(cfg, 0)
+    params = m3.SISOParams(*(t.to(BF16).cuda() if f in ("in_proj", "out_proj") else t.cuda()
+                             for f, t in zip(p_cpu._fields, p_cpu)))
+    B, L = 8, 8192
+    u = torch.randn(B, L, 1024, generator=torch.Generator().manual_seed(0)).to(BF16)
+    print("[cfg2 layer] GPU forward", flush=True)
+    with torch.no_grad():
+        y, st = m3.mamba3_siso_layer(params, u.cuda(), cfg)
+    y, ssm, kf = cpu(y), cpu(st.ssm), cpu(st.k)
+    # the oracle with the weights the bf16 layer multiplies by (rounded once, as cast)
+    pd = params_dict(p_cpu, torch.float32)
+    pd["in_proj"], pd["out_proj"] = (pd[k_].to(BF16).float() for k_ in ("in_proj", "out_proj"))
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    with torch.no_grad():
+        for b in range(B):
+            print(f"[cfg2 layer] oracle sequence {b}", flush=True)
+            ub = u[b:b + 1].float()
+            ym, sm = O.layer_forward(pd, ub, d_state=128, headdim=64, expand=2, chunk=128,
+                                     mm_dtype=BF16, act_dtype=BF16)
+            report(f"cfg2 layer y[{b}] vs bf16 layer model", y[b:b + 1], ym)
+            report(f"cfg2 layer final ssm[{b}] vs bf16 layer model", ssm[b:b + 1], sm.ssm)
+            assert_p95(y[b:b + 1], ym, BF16_LAYER_MODEL_P95, f"y[{b}] vs bf16 layer model")
+            assert_bf16_bound(y[b:b + 1], ym, what=f"y[{b}] vs bf16 layer model")
+            assert_maxabs(ssm[b:b + 1], sm.ssm, STATE_MAXABS, f"final ssm[{b}] vs bf16 layer model")
+            assert_maxrel(ssm[b:b + 1], sm.ssm, 5e-3, f"final ssm[{b}] vs bf16 layer model")
+            assert_maxrel(kf[b:b + 1], sm.k, 5e-3, f"final k[{b}] vs bf16 layer model")
+            yr, sr = O.layer_forward(pd, ub, d_state=128, headdim=64, expand=2, chunk=128)
+            report(f"cfg2 layer y[{b}] vs float32", y[b:b + 1], yr)
+            report(f"cfg2 layer final ssm[{b}] vs float32", ssm[b:b + 1], sr.ssm)
+            report(f"bf16 layer model final ssm[{b}] vs float32 (no kernel)", sm.ssm, sr.ssm)
+            assert_maxrel(y[b:b + 1], yr, BF16_Y_MAXREL, f"y[{b}] vs float32")
