@@ -589,3 +589,45 @@ def test_layer_forward_cfg2_full_size(m3):
             report(f"cfg2 layer final ssm[{b}] vs float32", ssm[b:b + 1], sr.ssm)
             report(f"bf16 layer model final ssm[{b}] vs float32 (no kernel)", sm.ssm, sr.ssm)
             assert_maxrel(y[b:b + 1], yr, BF16_Y_MAXREL, f"y[{b}] vs float32")
+
+
+def test_layer_gradients_cfg3_full_size(m3):
+    """BASELINE configs[2] at its own size: the bf16 layer's forward and backward at B=8,
+    L=8192, d_model 1024, init_params(seed=0), u ~ N(0, 1) in bf16 (seed 0), float32
+    parameters cast per call as the layer does. The upstream gradient is N(0, 1) in bf16
+    (seed 2) on sequences 0 and 7 and zero on the others, so that the float32 oracle, run
+    with autograd through the bf16 layer's rounding model on those two sequences only,
+    gives every parameter's whole gradient: du of sequences 0 and 7 and the gradient of
+    each `SISOParams` field within 2e-2 of max |ref|; du of the other sequences exactly
+    zero."""
+    cfg = m3.SISOConfig(d_model=1024, d_state=128, headdim=64, expand=2, chunk=128)
+    p_cpu = m3.init_params(cfg, 0)
+    B, L, live = 8, 8192, (0, 7)
+    u = torch.randn(B, L, 1024, generator=torch.Generator().manual_seed(0)).to(BF16)
+    dy = torch.zeros(B, L, 1024, dtype=BF16)
+    g2 = torch.Generator().manual_seed(2)
+    for b in live:
+        dy[b] = torch.randn(L, 1024, generator=g2).to(BF16)
+    print("[cfg3 layer] GPU forward and backward", flush=True)
+    params = m3.SISOParams(*(t.cuda().requires_grad_(True) for t in p_cpu))
+    ud = u.cuda().requires_grad_(True)
+    y, _ = m3.mamba3_siso_layer(params, ud, cfg)
+    (y.float() * dy.cuda().float()).sum().backward()
+    du = cpu(ud.grad)
+    for b in range(B):
+        if b not in live:
+            assert float(du[b].abs().max()) == 0.0, f"du[{b}] without upstream gradient"
+    pd = {k_: v_.requires_grad_(True) for k_, v_ in params_dict(p_cpu, torch.float32).items()}
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    for b in live:
+        print(f"[cfg3 layer] oracle sequence {b}", flush=True)
+        ub = u[b:b + 1].float().requires_grad_(True)
+        yr, _ = O.layer_forward(pd, ub, d_state=128, headdim=64, expand=2, chunk=128,
+                                mm_dtype=BF16, act_dtype=BF16)
+        (yr * dy[b:b + 1].float()).sum().backward()
+        report(f"cfg3 layer du[{b}] vs bf16 layer model", du[b:b + 1], ub.grad)
+        assert_maxrel(du[b:b + 1], ub.grad, BF16_GRAD_MAXREL, f"du[{b}]")
+        del yr, ub
+    for f in p_cpu._fields:
+        report(f"cfg3 layer d{f} vs bf16 layer model", getattr(params, f).grad, pd[f].grad)
+        assert_maxrel(getattr(params, f).grad, pd[f].grad, BF16_GRAD_MAXREL, f"d{f}")
