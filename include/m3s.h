@@ -188,7 +188,9 @@ typedef struct m3s_decode_args {
  * 474-533: one lax.scan of decode_step over a known-length run, e.g. a fixed prompt suffix
  * or teacher forcing). Each (b, h) state stays on chip for all T steps and is read and
  * written once; every step's arithmetic is m3s_decode's, so the results equal T calls of
- * m3s_decode. Inputs carry a time axis; the state is updated in place. */
+ * m3s_decode. Inputs carry a time axis; the state is updated in place. steps must be at
+ * least 1 (a run of none has nothing to launch: the Python wrapper returns the state as it
+ * was). */
 typedef struct m3s_decode_scan_args {
   int32_t struct_size; /* sizeof(m3s_decode_scan_args) */
   int32_t batch, steps, nheads, headdim, state_dim, n_angles;
