@@ -520,6 +520,7 @@ def test_gemv_matches_float64(m3, dev, m, k, n, ldw):
 @pytest.mark.parametrize("m,k,n,ldx,ldw", [
     (256, 1024, 4480, 1024, 4480),   # the layer's in_proj at the decode batch (128-row tiles)
     (200, 128, 5000, 136, 5000),     # 128-row tiles, a partial one and ragged columns
+    (1000, 192, 2056, 192, 2056),    # 128-row tiles over several rounds, ragged rows and columns
     (256, 2048, 1024, 2048, 1024),   # its out_proj
     (64, 768, 3432, 768, 3432),      # the LM's in_proj, ragged 64-column tiles
     (5, 1536, 768, 1544, 776),       # five rows (a partial row tile), padded row strides
